@@ -1,0 +1,565 @@
+"""gpt-oss MoE experts with frozen MXFP4 weights on MI355X (drop-in module).
+
+Same public API as the reference's ``src/agent_factory_3/models/gpt_oss/
+quantization.py`` for the ``dequant_dtype="bf16"`` path:
+
+================================  ===========================================
+reference (quantization.py)       here
+================================  ===========================================
+``mxfp4_to_bf16`` 89-99           HIP dequant kernel (bit-exact)
+``FP4_VALUES`` 131-134            same table (e2m1 code -> value)
+``convert_moe_packed_tensors``    HIP dequant + transpose to [E, K, N]
+  137-172
+pack / unpack / store 232-287     same byte reinterpretation into bf16
+                                  containers (FSDP2-shardable)
+``DequantMoEMatmul`` 294-421      grouped GEMM with the MXFP4 -> bf16
+                                  conversion fused into the tile load
+                                  (no materialised bf16 weight), 15 inputs,
+                                  gradient for ``x`` only
+``SwiGLUFunction`` 424-444        HIP clamped SwiGLU fwd/bwd
+``Mxfp4Bf16DequantGptOssExperts`` same parameters/attributes/forward
+  451-544
+``routing_torch_dist`` 551-590    top-k routing (world size 1)
+``routing_replay`` 593-636        HIP routing kernels
+``mlp_forward`` 639-668           same control flow
+``replace_with_dequant_experts``  same module surgery
+  675-699
+================================  ===========================================
+
+New (not in the reference, which puts LoRA on attention only): per-expert
+LoRA on both projections (``enable_expert_lora``), with the PEFT convention
+``W_eff = W + (lora_alpha / r) * B @ A`` (model_trainer.py:665,711) and bf16
+adapters; its autograd function returns gradients for ``x``, ``A`` and ``B``.
+
+Every compute call goes to ``libaf3_mi355x.so``; there is no CPU or eager
+fallback.  Only ``dequant_dtype="bf16"`` is implemented (the fp8 mode of the
+reference is unused by its recipes).
+"""
+from __future__ import annotations
+
+import math
+from contextlib import contextmanager
+
+import torch
+from torch import nn
+
+from . import _capi
+from .kernels import mxfp4_to_bf16_hip, swiglu_backward_raw, swiglu_forward
+from .routing import (  # noqa: F401  (re-exported names of the routing layer)
+    ExptData, GatherIndx, RoutingData, ScatterIndx, compute_expt_data, compute_expt_data_torch,
+    dense_routing, routing, routing_replay,
+)
+
+GEMM_BLOCK_M = 128
+
+# Optional launch timer for the grouped GEMM (set by benchmark harnesses):
+# callable(tag: str, flops: int) -> context manager wrapping the launch.
+KERNEL_TIMER = None
+
+FP4_VALUES = [
+    +0.0, +0.5, +1.0, +1.5, +2.0, +3.0, +4.0, +6.0,
+    -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0,
+]
+
+
+@contextmanager
+def on_device(dev):
+    if isinstance(dev, torch.Tensor):
+        dev = dev.device
+    elif isinstance(dev, str):
+        dev = torch.device(dev)
+    if getattr(dev, "type", None) == "cuda":
+        with torch.cuda.device(dev):
+            yield
+            return
+    yield
+
+
+# ---------------------------------------------------------------------------
+# dequant
+# ---------------------------------------------------------------------------
+
+def mxfp4_to_bf16(blocks, scales):
+    """MXFP4 [..., G, 16] + scales [..., G] -> bf16 [..., G*32] (quantization.py:89-99)."""
+    return mxfp4_to_bf16_hip(blocks, scales)
+
+
+def convert_moe_packed_tensors(blocks, scales, *, dtype=torch.bfloat16, rows_per_chunk=None):
+    """Dequantize to a full weight, transposed to [E, K, N] (quantization.py:137-172).
+
+    Used by the dequantize-at-load fallback of the quantizer.
+    """
+    if dtype != torch.bfloat16:
+        raise TypeError("only bf16 dequantisation is implemented")
+    w = mxfp4_to_bf16_hip(blocks.to(torch.uint8), scales.to(torch.uint8))
+    return w.transpose(1, 2).contiguous()
+
+
+# ---------------------------------------------------------------------------
+# FSDP-compatible storage of the packed bytes (quantization.py:232-287)
+# ---------------------------------------------------------------------------
+
+def _pack_uint8_as_bf16(tensor):
+    """Reinterpret a uint8 tensor as bf16 (two bytes per element, odd length padded)."""
+    flat = tensor.contiguous().reshape(-1)
+    if flat.numel() % 2:
+        flat = torch.cat([flat, flat.new_zeros(1)])
+    return flat.view(torch.bfloat16)
+
+
+def _unpack_bf16_as_uint8(packed, shape):
+    """View bf16-packed bytes as a uint8 tensor of ``shape`` (no copy)."""
+    numel = math.prod(shape)
+    return packed.reshape(-1).view(torch.uint8)[:numel].reshape(shape)
+
+
+def _store_mxfp4_weights(blocks, scales, module, proj, target_device):
+    """Register ``{proj}_blocks`` / ``{proj}_scales`` as bf16-container Parameters."""
+    if getattr(target_device, "type", target_device) == "cpu":
+        target_device = "cuda"
+    blocks = blocks.to(target_device).contiguous()
+    scales = scales.to(target_device).contiguous()
+    for attr in (f"{proj}_blocks", f"{proj}_scales", proj):
+        if attr in module._parameters:
+            del module._parameters[attr]
+    setattr(module, f"_{proj}_shapes", (tuple(blocks.shape), tuple(scales.shape)))
+    module.register_parameter(f"{proj}_blocks", nn.Parameter(_pack_uint8_as_bf16(blocks), requires_grad=False))
+    module.register_parameter(f"{proj}_scales", nn.Parameter(_pack_uint8_as_bf16(scales), requires_grad=False))
+
+
+# ---------------------------------------------------------------------------
+# grouped GEMM (the matmul_ogs replacement)
+# ---------------------------------------------------------------------------
+
+def _expt_data(routing_data, n_rows, device):
+    if routing_data is None:
+        return dense_routing(n_rows, device), 1
+    ed = routing_data.expt_data
+    if ed is None or GEMM_BLOCK_M not in getattr(ed, "block_pid_map", {}):
+        ed = compute_expt_data(routing_data.expt_hist, routing_data.n_expts_tot, n_rows)
+        routing_data = RoutingData(routing_data.gate_scal, routing_data.expt_hist, routing_data.n_expts_tot,
+                                   routing_data.n_expts_act, ed)
+    return routing_data, routing_data.n_expts_act
+
+
+def _gather_ptr(gather_indx):
+    if gather_indx is None:
+        return None
+    g = gather_indx.src_indx
+    if g.dtype != torch.int32:
+        g = g.to(torch.int32)
+    return g.contiguous()
+
+
+def _weight_dims(blocks, trans_w):
+    """(E, N, K) of the GEMM from the MXFP4 block tensor [E, rows, G, 16]."""
+    if blocks.dim() == 3:
+        blocks = blocks.unsqueeze(0)
+    E, rows, G, _ = blocks.shape
+    return (E, G * 32, rows) if trans_w else (E, rows, G * 32)
+
+
+def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=None, trans_w=False,
+             lora_l=None, lora_b=None):
+    """Expert-sorted output rows of the grouped GEMM (no scatter).
+
+    ``trans_w=False``: ``Y[r] = X[a(r)] @ W[e]^T`` with W = dequant(blocks) [E, N, K]
+    (matmul_ogs(x, w.transpose(-1, -2)), quantization.py:361).
+    ``trans_w=True``:  ``Y[r] = X[a(r)] @ W[e]`` (matmul_ogs(grad, w), quantization.py:411).
+    Then ``(+ bias[e]) * gammas[r]`` and bf16 rounding.  ``lora_l``/``lora_b``
+    append the expert-LoRA term ``L[r] @ B[e]^T`` (trans 0) / ``L[r] @ B[e]``.
+    """
+    if not x.is_cuda:
+        raise RuntimeError("x must be a GPU tensor (the MI355X path has no CPU implementation)")
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"x must be bfloat16 (got {x.dtype})")
+    dev = x.device
+    x = x if x.stride(-1) == 1 and x.data_ptr() % 16 == 0 and x.stride(0) % 8 == 0 else x.contiguous()
+    E, N, K = _weight_dims(blocks, trans_w)
+    if x.shape[-1] != K:
+        raise ValueError(f"x has {x.shape[-1]} columns, weight reduction dim is {K}")
+    g = _gather_ptr(gather_indx)
+    R = g.shape[0] if g is not None else x.shape[0]
+    routing_data, k_act = _expt_data(routing_data, R, dev)
+    ed = routing_data.expt_data
+    pid_map = ed.block_pid_map[GEMM_BLOCK_M]
+    offs = ed.token_offs_raw
+    y = torch.empty(R, N, dtype=torch.bfloat16, device=dev)
+    if R == 0 or pid_map.numel() == 0:
+        return y
+    blocks = blocks if blocks.data_ptr() % 16 == 0 else blocks.clone()
+    b = None
+    if bias is not None:
+        b = bias.to(torch.float32).contiguous()
+    gm, gm_f32 = None, 0
+    if gammas is not None:
+        if gammas.dtype == torch.float32:
+            gm, gm_f32 = gammas.contiguous(), 1
+        else:
+            gm = gammas.to(torch.bfloat16).contiguous()
+    lr = 0
+    if lora_l is not None:
+        lr = lora_l.shape[-1]
+        lora_l = lora_l.contiguous()
+        lora_b = lora_b.to(torch.bfloat16).contiguous()
+    args = (x.data_ptr(), x.stride(0) if x.shape[0] > 1 else K, _capi.ptr(g), k_act if g is not None else 1,
+            blocks.data_ptr(), scales.data_ptr(), 1 if trans_w else 0, _capi.ptr(b), _capi.ptr(gm), gm_f32,
+            _capi.ptr(lora_l), lr, _capi.ptr(lora_b), lr, offs.data_ptr(), pid_map.data_ptr(), pid_map.numel(),
+            E, N, K, y.data_ptr(), N, _capi.stream_of(dev))
+    if KERNEL_TIMER is None:
+        _capi.call("af3_moe_gemm", *args)
+    else:
+        with KERNEL_TIMER("moe_gemm_dgrad" if trans_w else "moe_gemm_fwd", 2 * R * N * (K + lr)):
+            _capi.call("af3_moe_gemm", *args)
+    return y
+
+
+def moe_combine(rows, scatter_indx, n_expts_act):
+    """Sum each token's K expert rows (matmul_ogs scatter reduction)."""
+    src = scatter_indx.src_indx
+    src = (src if src.dtype == torch.int32 else src.to(torch.int32)).contiguous()
+    n_tokens = src.shape[0] // n_expts_act
+    N = rows.shape[-1]
+    out = torch.empty(n_tokens, N, dtype=torch.bfloat16, device=rows.device)
+    if n_tokens:
+        _capi.call("af3_moe_combine", rows.data_ptr(), rows.stride(0), src.data_ptr(), n_tokens, n_expts_act, N,
+                   out.data_ptr(), N, _capi.stream_of(rows.device))
+    return out
+
+
+def matmul_ogs(x, w_blocks_scales, bias, routing_data=None, gather_indx=None, scatter_indx=None, gammas=None,
+               trans_w=False):
+    """matmul_ogs semantics over MXFP4 weights: rows, then the scatter-sum if any."""
+    blocks, scales = w_blocks_scales
+    y = moe_rows(x, blocks, scales, bias, routing_data, gather_indx, gammas, trans_w)
+    if scatter_indx is None:
+        return y
+    k = routing_data.n_expts_act if routing_data is not None else 1
+    return moe_combine(y, scatter_indx, k)
+
+
+# ---------------------------------------------------------------------------
+# Autograd functions
+# ---------------------------------------------------------------------------
+
+class DequantMoEMatmul(torch.autograd.Function):
+    """MXFP4 grouped GEMM (quantization.py:294-421), dequant fused into the GEMM.
+
+    Weights are not saved: backward re-derives them from ``experts_module``
+    (FSDP re-gathers them for backward).  Returns a gradient for ``x`` only.
+    """
+
+    @staticmethod
+    def forward(ctx, x, blocks, scales, bias, routing_data, fwd_gather_indx, fwd_scatter_indx, fwd_gammas,
+                bwd_gather_indx, bwd_scatter_indx, bwd_gammas, dequant_dtype="bf16", n_expts_act=1,
+                experts_module=None, proj_name=None):
+        if dequant_dtype != "bf16":
+            raise NotImplementedError(f"dequant_dtype={dequant_dtype!r}: only 'bf16' is implemented")
+        with on_device(x.device):
+            out = matmul_ogs(x, (blocks, scales), bias, routing_data, fwd_gather_indx, fwd_scatter_indx,
+                             fwd_gammas, trans_w=False)
+        ctx.experts_module = experts_module
+        ctx.proj_name = proj_name
+        if experts_module is None:  # no module to re-derive from: keep the (view) tensors
+            ctx.weights = (blocks, scales)
+        ctx.routing_data = routing_data
+        ctx.bwd_gather_indx = bwd_gather_indx
+        ctx.bwd_scatter_indx = bwd_scatter_indx
+        ctx.bwd_gammas = bwd_gammas
+        ctx.dequant_dtype = dequant_dtype
+        ctx.n_expts_act = n_expts_act
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        if ctx.experts_module is not None:
+            blocks, scales = ctx.experts_module._get_uint8_weights(ctx.proj_name)
+        else:
+            blocks, scales = ctx.weights
+        with on_device(grad_output.device):
+            grad_x = matmul_ogs(grad_output.to(torch.bfloat16).contiguous(), (blocks, scales), None,
+                                ctx.routing_data, ctx.bwd_gather_indx, ctx.bwd_scatter_indx, ctx.bwd_gammas,
+                                trans_w=True)
+        return grad_x, None, None, None, None, None, None, None, None, None, None, None, None, None, None
+
+
+class SwiGLUFunction(torch.autograd.Function):
+    """gpt-oss clamped SwiGLU (quantization.py:424-444).
+
+    Saves the raw interleaved input (same bytes as the reference's clamped
+    gate + up pair) and clamps again in backward, so the forward writes only
+    its output.
+    """
+
+    @staticmethod
+    def forward(ctx, gate_up_raw, alpha, limit):
+        out = swiglu_forward(gate_up_raw, alpha, limit, save_for_bwd=False)
+        ctx.save_for_backward(gate_up_raw)
+        ctx.alpha = alpha
+        ctx.limit = limit
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        (gate_up_raw,) = ctx.saved_tensors
+        return swiglu_backward_raw(grad_output.contiguous(), gate_up_raw, ctx.alpha, ctx.limit), None, None
+
+
+def _lora_rows(x, gather, k_act, wl, trans_b, scale, ed, n_out, K):
+    dev = x.device
+    R = gather.shape[0] if gather is not None else x.shape[0]
+    out = torch.empty(R, n_out, dtype=torch.bfloat16, device=dev)
+    pid_map = ed.block_pid_map[GEMM_BLOCK_M]
+    if R and pid_map.numel():
+        E = wl.shape[0]
+        _capi.call("af3_lora_rows", x.data_ptr(), x.stride(0) if x.shape[0] > 1 else K, _capi.ptr(gather),
+                   k_act if gather is not None else 1, wl.data_ptr(), trans_b, float(scale),
+                   ed.token_offs_raw.data_ptr(), pid_map.data_ptr(), pid_map.numel(), E, n_out, K,
+                   out.data_ptr(), n_out, _capi.stream_of(dev))
+    return out
+
+
+def _lora_wgrad(a, a_gather, a_div, a_rowscale, b, b_gather, b_div, ed, E, M, N):
+    g = torch.empty(E, M, N, dtype=torch.bfloat16, device=a.device)
+    _capi.call("af3_lora_wgrad", a.data_ptr(), a.stride(0) if a.shape[0] > 1 else M, _capi.ptr(a_gather), a_div,
+               _capi.ptr(a_rowscale), b.data_ptr(), b.stride(0) if b.shape[0] > 1 else N, _capi.ptr(b_gather),
+               b_div, 1.0, ed.token_offs_raw.data_ptr(), E, M, N, g.data_ptr(), _capi.stream_of(a.device))
+    return g
+
+
+class LoraDequantMoEMatmul(torch.autograd.Function):
+    """Frozen-MXFP4 grouped GEMM plus a trainable per-expert LoRA term.
+
+    Forward (trans 0 weights ``W[e]`` = dequant(blocks[e]) of shape [N, K]):
+        L[r]   = bf16(s * X[a(r)] @ A[e]^T)              A: [E, r, K]
+        Y_r[r] = bf16(gamma[r] * (X[a(r)] @ W[e]^T + L[r] @ B[e]^T + bias[e]))   B: [E, N, r]
+        Y      = scatter-sum(Y_r) if fwd_scatter_indx else Y_r
+    Backward with dZ[r] = gamma_b[r] * dY[b(r)] (b = backward gather):
+        u[r]  = s * dY[b(r)] @ B[e]                      (without gamma)
+        dX_r  = gamma_b[r] * (dY[b(r)] @ W[e] + u[r] @ A[e]);  dX = scatter-sum(dX_r) if bwd scatter
+        dA[e] = sum_r gamma_b[r] u[r]^T X[a(r)]
+        dB[e] = sum_r gamma_b[r] dY[b(r)]^T L[r]
+    which are the gradients of W_eff = W + s * B @ A.
+    """
+
+    @staticmethod
+    def forward(ctx, x, lora_A, lora_B, scaling, blocks, scales, bias, routing_data, fwd_gather_indx,
+                fwd_scatter_indx, fwd_gammas, bwd_gather_indx, bwd_scatter_indx, bwd_gammas, experts_module=None,
+                proj_name=None):
+        dev = x.device
+        E, N, K = _weight_dims(blocks, False)
+        xg = x if x.stride(-1) == 1 and x.data_ptr() % 16 == 0 and x.stride(0) % 8 == 0 else x.contiguous()
+        g = _gather_ptr(fwd_gather_indx)
+        R = g.shape[0] if g is not None else xg.shape[0]
+        routing_data, k_act = _expt_data(routing_data, R, dev)
+        ed = routing_data.expt_data
+        A = lora_A.to(torch.bfloat16).contiguous()
+        B = lora_B.to(torch.bfloat16).contiguous()
+        r = A.shape[1]
+        with on_device(dev):
+            L = _lora_rows(xg, g, k_act, A, 0, scaling, ed, r, K)
+            y = moe_rows(xg, blocks, scales, bias, routing_data, fwd_gather_indx, fwd_gammas, False, L, B)
+            if fwd_scatter_indx is not None:
+                y = moe_combine(y, fwd_scatter_indx, k_act)
+        ctx.save_for_backward(xg, A, B, L)
+        ctx.scaling = float(scaling)
+        ctx.experts_module = experts_module
+        ctx.proj_name = proj_name
+        if experts_module is None:
+            ctx.weights = (blocks, scales)
+        ctx.routing_data = routing_data
+        ctx.fwd_gather = g
+        ctx.k_act = k_act
+        ctx.bwd_gather_indx = bwd_gather_indx
+        ctx.bwd_scatter_indx = bwd_scatter_indx
+        ctx.bwd_gammas = bwd_gammas
+        ctx.lora_dtypes = (lora_A.dtype, lora_B.dtype)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        xg, A, B, L = ctx.saved_tensors
+        if ctx.experts_module is not None:
+            blocks, scales = ctx.experts_module._get_uint8_weights(ctx.proj_name)
+        else:
+            blocks, scales = ctx.weights
+        E, N, K = _weight_dims(blocks, False)
+        r = A.shape[1]
+        ed = ctx.routing_data.expt_data
+        k_act = ctx.k_act
+        dY = grad_output.to(torch.bfloat16).contiguous()
+        bg = _gather_ptr(ctx.bwd_gather_indx)
+        gam = ctx.bwd_gammas
+        if gam is not None:
+            gam = gam.to(torch.bfloat16).contiguous()
+        with on_device(dY.device):
+            u = _lora_rows(dY, bg, k_act, B, 1, ctx.scaling, ed, r, N)
+            dx = moe_rows(dY, blocks, scales, None, ctx.routing_data, ctx.bwd_gather_indx, gam, True, u, A)
+            if ctx.bwd_scatter_indx is not None:
+                dx = moe_combine(dx, ctx.bwd_scatter_indx, k_act)
+            dA = _lora_wgrad(u, None, 1, gam, xg, ctx.fwd_gather, k_act if ctx.fwd_gather is not None else 1,
+                             ed, E, r, K)
+            dB = _lora_wgrad(dY, bg, k_act if bg is not None else 1, gam, L, None, 1, ed, E, N, r)
+        dA = dA.to(ctx.lora_dtypes[0])
+        dB = dB.to(ctx.lora_dtypes[1])
+        return (dx, dA, dB) + (None,) * 13
+
+
+# ---------------------------------------------------------------------------
+# Expert module
+# ---------------------------------------------------------------------------
+
+class Mxfp4Bf16DequantGptOssExperts(nn.Module):
+    """MoE experts with frozen MXFP4 weights (quantization.py:451-544)."""
+
+    def __init__(self, config):
+        super().__init__()
+        self.num_experts = config.num_local_experts
+        self.intermediate_size = config.intermediate_size
+        self.hidden_size = config.hidden_size
+        self.gate_up_proj = nn.Parameter(
+            torch.zeros(self.num_experts, 2 * self.intermediate_size, self.hidden_size // 32, 16,
+                        dtype=torch.uint8), requires_grad=False)
+        self.gate_up_proj_bias = nn.Parameter(
+            torch.zeros(self.num_experts, 2 * self.intermediate_size, dtype=torch.bfloat16), requires_grad=False)
+        self.down_proj = nn.Parameter(
+            torch.zeros(self.num_experts, self.hidden_size, self.intermediate_size // 32, 16, dtype=torch.uint8),
+            requires_grad=False)
+        self.down_proj_bias = nn.Parameter(
+            torch.zeros(self.num_experts, self.hidden_size, dtype=torch.bfloat16), requires_grad=False)
+        self.alpha = 1.702
+        self.limit = getattr(config, "swiglu_limit", 7.0)
+        self.dequant_dtype = getattr(config, "dequant_dtype", "bf16")
+        self.expert_lora_r = 0
+        self.expert_lora_scaling = 0.0
+
+    def _get_uint8_weights(self, proj):
+        """uint8 views of the bf16-packed blocks/scales (valid while FSDP has them gathered)."""
+        shapes = getattr(self, f"_{proj}_shapes", None)
+        blocks_param = getattr(self, f"{proj}_blocks")
+        scales_param = getattr(self, f"{proj}_scales")
+        if shapes is not None:
+            blocks_shape, scales_shape = shapes
+            return _unpack_bf16_as_uint8(blocks_param, blocks_shape), _unpack_bf16_as_uint8(scales_param,
+                                                                                            scales_shape)
+        return blocks_param, scales_param
+
+    def _proj(self, x, proj, bias, routing_data, fg, fs, fgam, bg, bs, bgam):
+        blocks, scales = self._get_uint8_weights(proj)
+        if self.expert_lora_r:
+            return LoraDequantMoEMatmul.apply(
+                x, getattr(self, f"{proj}_lora_A"), getattr(self, f"{proj}_lora_B"), self.expert_lora_scaling,
+                blocks, scales, bias, routing_data, fg, fs, fgam, bg, bs, bgam, self, proj)
+        return DequantMoEMatmul.apply(x, blocks, scales, bias, routing_data, fg, fs, fgam, bg, bs, bgam,
+                                      self.dequant_dtype, routing_data.n_expts_act, self, proj)
+
+    def forward(self, hidden_states: torch.Tensor, routing_data, gather_idx, scatter_idx) -> torch.Tensor:
+        gate_up_raw = self._proj(hidden_states, "gate_up_proj", self.gate_up_proj_bias.float(), routing_data,
+                                 gather_idx, None, None, None, scatter_idx, None)
+        intermediate = SwiGLUFunction.apply(gate_up_raw, self.alpha, self.limit)
+        return self._proj(intermediate, "down_proj", self.down_proj_bias.float(), routing_data,
+                          None, scatter_idx, routing_data.gate_scal, gather_idx, None, routing_data.gate_scal)
+
+
+def enable_expert_lora(experts: Mxfp4Bf16DequantGptOssExperts, r: int = 16, lora_alpha: float = 32.0,
+                       init: str = "peft", generator: torch.Generator | None = None,
+                       a_std: float = 0.1, b_std: float = 0.0316):
+    """Attach trainable bf16 LoRA adapters to both expert projections.
+
+    Parameters (per expert e): ``gate_up_proj_lora_A [E, r, H]``,
+    ``gate_up_proj_lora_B [E, 2I, r]`` (rows in the interleaved gate/up order
+    of the frozen weight), ``down_proj_lora_A [E, r, I]``,
+    ``down_proj_lora_B [E, H, r]``.  Scaling ``lora_alpha / r``.
+    ``init="peft"``: A kaiming-uniform(a=sqrt(5)), B = 0 (PEFT default);
+    ``init="normal"``: A ~ N(0, a_std^2), B ~ N(0, b_std^2).
+    """
+    if r % 8 or r <= 0 or r > 64:
+        raise ValueError("expert LoRA rank must be a positive multiple of 8, at most 64")
+    dev = experts.gate_up_proj_bias.device
+    E, H, I2 = experts.num_experts, experts.hidden_size, 2 * experts.intermediate_size
+    I = experts.intermediate_size
+    shapes = {"gate_up_proj_lora_A": (E, r, H), "gate_up_proj_lora_B": (E, I2, r),
+              "down_proj_lora_A": (E, r, I), "down_proj_lora_B": (E, H, r)}
+    for name, shp in shapes.items():
+        t = torch.empty(shp, dtype=torch.float32)
+        if name.endswith("_A"):
+            if init == "peft":
+                bound = 1.0 / math.sqrt(shp[-1])  # kaiming_uniform_(a=sqrt(5)) on [r, fan_in]
+                t.uniform_(-bound, bound, generator=generator)
+            else:
+                t.normal_(0.0, a_std, generator=generator)
+        else:
+            if init == "peft":
+                t.zero_()
+            else:
+                t.normal_(0.0, b_std, generator=generator)
+        experts.register_parameter(name, nn.Parameter(t.to(device=dev, dtype=torch.bfloat16)))
+    experts.expert_lora_r = r
+    experts.expert_lora_scaling = float(lora_alpha) / r
+    return experts
+
+
+# ---------------------------------------------------------------------------
+# Routing entry points and the MLP forward
+# ---------------------------------------------------------------------------
+
+def routing_torch_dist(logits, n_expts_act):
+    """Top-k routing under torch.distributed (quantization.py:551-590).
+
+    Expert-parallel masking is not part of this single-GPU build: at world
+    size 1 this is plain top-k routing.
+    """
+    import torch.distributed as dist
+    if dist.is_available() and dist.is_initialized() and dist.get_world_size() > 1:
+        raise NotImplementedError("expert-parallel routing (world size > 1) is not implemented")
+    return routing(logits, n_expts_act)
+
+
+def mlp_forward(self, hidden_states, router_indices=None):
+    """MoE MLP forward with optional routing replay (quantization.py:639-668)."""
+    import torch.distributed as dist
+    if dist.is_available() and dist.is_initialized() and hasattr(self, "_is_hooked"):
+        route = routing_torch_dist
+    else:
+        route = routing
+    batch_size = hidden_states.shape[0]
+    hidden_states = hidden_states.reshape(-1, self.router.hidden_dim)
+    router_logits = nn.functional.linear(hidden_states, self.router.weight, self.router.bias)
+    with on_device(router_logits.device):
+        if router_indices is not None:
+            expt_indx = router_indices.reshape(-1, self.router.top_k).to(device=router_logits.device,
+                                                                         dtype=torch.int32)
+            routing_data, gather_idx, scatter_idx = routing_replay(router_logits, expt_indx, self.router.top_k)
+        else:
+            routing_data, gather_idx, scatter_idx = route(router_logits, self.router.top_k)
+    routed_out = self.experts(hidden_states, routing_data, gather_idx, scatter_idx=scatter_idx)
+    routed_out = routed_out.reshape(batch_size, -1, self.router.hidden_dim)
+    return routed_out, router_logits
+
+
+def replace_with_dequant_experts(model, quantization_config=None, modules_to_not_convert=None):
+    """Swap GptOssExperts for the MXFP4 module and re-bind GptOssMLP.forward (quantization.py:675-699)."""
+    if quantization_config is not None and getattr(quantization_config, "dequantize", False):
+        return model
+    dequant_dtype = getattr(quantization_config, "dequant_dtype", "bf16")
+    model.config.dequant_dtype = dequant_dtype
+    try:
+        from transformers.quantizers.quantizers_utils import should_convert_module
+    except ImportError:  # pragma: no cover - transformers always ships it
+        def should_convert_module(name, patterns=None):
+            return not patterns or not any(p in name for p in patterns)
+    from types import MethodType
+    replaced = False
+    for module_name, module in list(model.named_modules()):
+        if not should_convert_module(module_name, modules_to_not_convert):
+            continue
+        if module.__class__.__name__ == "GptOssExperts":
+            with torch.device("meta"):
+                model.set_submodule(module_name, Mxfp4Bf16DequantGptOssExperts(model.config))
+            replaced = True
+        if module.__class__.__name__ == "GptOssMLP":
+            module.forward = MethodType(mlp_forward, module)
+    if not replaced:
+        import warnings
+        warnings.warn("No expert modules found for MXFP4 dequant conversion.")
+    return model

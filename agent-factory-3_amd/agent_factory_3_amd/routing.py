@@ -1,0 +1,183 @@
+"""Routing metadata for the grouped expert GEMMs (HIP-backed).
+
+Own restatement of the routing objects the reference imports from the
+un-vendored ``triton_kernels`` package (``quantization.py:42-48``) and of the
+routing functions built on them:
+
+* ``GatherIndx(src_indx, dst_indx)``, ``ScatterIndx(src_indx, dst_indx)``,
+  ``RoutingData(gate_scal, expt_hist, n_expts_tot, n_expts_act, expt_data)``
+  with the field order used at ``quantization.py:586-590,632-636``;
+* ``ExptData`` / ``compute_expt_data`` (``compute_expt_data_torch`` at
+  ``quantization.py:588,627``): raw and padded expert offsets and the
+  ``block_pid_map`` that drives the ragged GEMM grid;
+* ``routing_replay`` (``quantization.py:593-636``) and top-k ``routing``
+  (``routing_torch_dist`` at world size 1, ``quantization.py:551-590``).
+
+All index work runs in HIP kernels on the caller's stream (no host sync).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _capi
+
+# block sizes (rows per GEMM tile) for which tile maps are built
+BLOCK_MS = (128,)
+
+
+@dataclass
+class GatherIndx:
+    """Row gather: sorted row i reads token ``src_indx[i] // n_expts_act``."""
+    src_indx: torch.Tensor
+    dst_indx: torch.Tensor
+
+
+@dataclass
+class ScatterIndx:
+    """Row scatter: token t sums sorted rows ``src_indx[t*k + j]``."""
+    src_indx: torch.Tensor
+    dst_indx: torch.Tensor
+
+
+@dataclass
+class ExptData:
+    hist: torch.Tensor                      # [E] int32 rows per expert
+    token_offs_raw: torch.Tensor            # [E+1] int32 exclusive scan of hist
+    token_offs_pad: dict = field(default_factory=dict)  # BM -> [E+1] int32 scan of ceil(hist/BM)
+    block_pid_map: dict = field(default_factory=dict)   # BM -> [max_tiles] int32 (b<<16)|e or -1
+
+
+@dataclass
+class RoutingData:
+    gate_scal: torch.Tensor | None
+    expt_hist: torch.Tensor | None
+    n_expts_tot: int
+    n_expts_act: int
+    expt_data: ExptData | None = None
+
+
+def max_tiles(n_gates: int, n_expts_tot: int, block_m: int) -> int:
+    """Upper bound of sum_e ceil(hist[e]/block_m) given sum_e hist[e] = n_gates."""
+    return min(n_gates, (n_gates + block_m - 1) // block_m + n_expts_tot) if n_gates > 0 else 0
+
+
+_BMS_CACHE: dict = {}
+
+
+def _block_ms_on(dev) -> torch.Tensor:
+    key = (str(dev), BLOCK_MS)
+    t = _BMS_CACHE.get(key)
+    if t is None:
+        t = torch.tensor(BLOCK_MS, dtype=torch.int32).to(dev)
+        _BMS_CACHE[key] = t
+    return t
+
+
+def compute_expt_data(hist: torch.Tensor, n_expts_tot: int, n_gates: int,
+                      token_offs_raw: torch.Tensor | None = None) -> ExptData:
+    """Tile metadata from the expert histogram (compute_expt_data_torch semantics)."""
+    dev = hist.device
+    hist = hist.to(torch.int32).contiguous()
+    if token_offs_raw is None:
+        token_offs_raw = torch.zeros(n_expts_tot + 1, dtype=torch.int32, device=dev)
+        token_offs_raw[1:] = torch.cumsum(hist, 0)
+    bms = _block_ms_on(dev)
+    mt = max(max_tiles(n_gates, n_expts_tot, bm) for bm in BLOCK_MS)
+    offs_pad = torch.empty(len(BLOCK_MS), n_expts_tot + 1, dtype=torch.int32, device=dev)
+    pid_map = torch.empty(len(BLOCK_MS), max(mt, 1), dtype=torch.int32, device=dev)
+    _capi.call("af3_expt_data", hist.data_ptr(), n_expts_tot, bms.data_ptr(), len(BLOCK_MS), mt,
+               offs_pad.data_ptr(), pid_map.data_ptr(), _capi.stream_of(dev))
+    ed = ExptData(hist, token_offs_raw)
+    for i, bm in enumerate(BLOCK_MS):
+        ed.token_offs_pad[bm] = offs_pad[i]
+        ed.block_pid_map[bm] = pid_map[i, :mt]
+    return ed
+
+
+# the reference's name (triton_kernels.routing.compute_expt_data_torch)
+def compute_expt_data_torch(hist, n_expts_tot, n_gates):
+    return compute_expt_data(hist, n_expts_tot, n_gates)
+
+
+def _bf16_logits(logits: torch.Tensor) -> torch.Tensor:
+    if not logits.is_cuda:
+        raise RuntimeError("router logits must be a GPU tensor (the MI355X path has no CPU implementation)")
+    if logits.dtype != torch.bfloat16:
+        logits = logits.to(torch.bfloat16)
+    if logits.stride(-1) != 1:
+        logits = logits.contiguous()
+    return logits
+
+
+def _run_routing(logits: torch.Tensor, n_expts_act: int, expt_indx: torch.Tensor | None):
+    out_dtype = logits.dtype
+    lg = _bf16_logits(logits)
+    T, E = lg.shape
+    K = int(n_expts_act)
+    R = T * K
+    dev = lg.device
+    gate_scal = torch.empty(R, dtype=torch.bfloat16, device=dev)
+    hist = torch.empty(E, dtype=torch.int32, device=dev)
+    topk_indx = torch.empty(R, dtype=torch.int32, device=dev)
+    gate_indx = torch.empty(R, dtype=torch.int32, device=dev)
+    offs = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    ws_n = _capi.workspace_bytes(T, E, K)
+    ws = torch.empty(ws_n, dtype=torch.uint8, device=dev)
+    stream = _capi.stream_of(dev)
+    ld = lg.stride(0) if T > 1 else E
+    if expt_indx is not None:
+        ei = expt_indx.to(device=dev, dtype=torch.int32).contiguous()
+        if ei.shape != (T, K):
+            raise ValueError(f"expt_indx shape {tuple(ei.shape)} != ({T}, {K})")
+        _capi.call("af3_routing_replay", lg.data_ptr(), ld, ei.data_ptr(), T, E, K, gate_scal.data_ptr(),
+                   hist.data_ptr(), topk_indx.data_ptr(), gate_indx.data_ptr(), offs.data_ptr(), ws.data_ptr(),
+                   ws_n, stream)
+    else:
+        _capi.call("af3_routing_topk", lg.data_ptr(), ld, T, E, K, gate_scal.data_ptr(), hist.data_ptr(),
+                   topk_indx.data_ptr(), gate_indx.data_ptr(), offs.data_ptr(), ws.data_ptr(), ws_n, stream)
+    expt_data = compute_expt_data(hist, E, R, token_offs_raw=offs)
+    if out_dtype != torch.bfloat16 and out_dtype.is_floating_point:
+        gate_scal = gate_scal.to(out_dtype)
+    return (
+        RoutingData(gate_scal, hist, E, K, expt_data),
+        GatherIndx(src_indx=topk_indx, dst_indx=gate_indx),
+        ScatterIndx(src_indx=gate_indx, dst_indx=topk_indx),
+    )
+
+
+def routing_replay(logits: torch.Tensor, expt_indx: torch.Tensor, n_expts_act: int):
+    """Routing structures from given expert ids (quantization.py:593-636).
+
+    Args:
+        logits: [T, E] router logits (softmax over the K selected only)
+        expt_indx: [T, K] int expert ids per token
+        n_expts_act: K
+    Returns:
+        (RoutingData, GatherIndx, ScatterIndx)
+    """
+    return _run_routing(logits, n_expts_act, expt_indx)
+
+
+def routing(logits: torch.Tensor, n_expts_act: int, sm_first: bool = False, expt_indx=None,
+            simulated_ep: int = 1, n_rows=None):
+    """Top-k routing with the call signature of triton_kernels.routing.routing.
+
+    Top-``n_expts_act`` logits per token (ties to the lower expert id), softmax
+    over the selected ones, ids of a token ordered by expert id
+    (quantization.py:564-576).  ``expt_indx`` given -> replay.
+    """
+    if sm_first:
+        raise NotImplementedError("sm_first=True is not used on the gpt-oss path")
+    if simulated_ep != 1:
+        raise NotImplementedError("simulated expert parallelism is not supported (single GPU)")
+    if n_rows is not None:
+        logits = logits[:n_rows]
+    return _run_routing(logits, n_expts_act, expt_indx)
+
+
+def dense_routing(n_rows: int, device) -> RoutingData:
+    """Single-expert routing (matmul_ogs with routing_data=None)."""
+    hist = torch.tensor([n_rows], dtype=torch.int32, device=device)
+    return RoutingData(None, hist, 1, 1, compute_expt_data(hist, 1, n_rows))

@@ -1,0 +1,107 @@
+// Shared device/host helpers for the gfx950 MXFP4 MoE expert path.
+//
+// Storage conventions used by every kernel in this library:
+//   * bf16 tensors travel as raw 16-bit patterns (uint16_t); arithmetic is fp32.
+//   * MXFP4 weights are two e2m1 nibbles per byte (low nibble = even element)
+//     in 16-byte blocks of 32 elements, with one e8m0 scale byte per block.
+//   * Element/byte offsets that can exceed 2^31 are computed in int64.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define AF3_ABI_VERSION 1
+
+// ---------------------------------------------------------------------------
+// error reporting (host side)
+// ---------------------------------------------------------------------------
+namespace af3 {
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace af3
+
+// argument errors are negative, HIP errors positive (the hipError_t value)
+#define AF3_EINVAL (-1)
+#define AF3_EUNSUPPORTED (-2)
+
+#define AF3_REQUIRE(cond, ...)            \
+  do {                                    \
+    if (!(cond)) {                        \
+      af3::set_error(__VA_ARGS__);        \
+      return AF3_EINVAL;                  \
+    }                                     \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+typedef __attribute__((ext_vector_type(2))) __bf16 af3_bf16x2;
+typedef __attribute__((ext_vector_type(8))) __bf16 af3_bf16x8;
+typedef __attribute__((ext_vector_type(16))) float af3_f32x16;
+typedef __attribute__((ext_vector_type(4))) unsigned int af3_u32x4;
+
+__device__ __forceinline__ float af3_bf16_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even (hardware v_cvt_pk_bf16_f32 on gfx950)
+__device__ __forceinline__ uint32_t af3_f32_to_bf16(float f) {
+  __bf16 b = (__bf16)f;
+  return (uint32_t)__builtin_bit_cast(unsigned short, b);
+}
+
+__device__ __forceinline__ uint32_t af3_pack_bf16x2(float lo, float hi) {
+  return af3_f32_to_bf16(lo) | (af3_f32_to_bf16(hi) << 16);
+}
+
+// One e2m1 nibble + e8m0 scale byte -> bf16 bits, integer-only.
+// Restates kernels.py:120-158 (_convert_nibble_to_bf16): normal e2m1
+// (ee>0) gives bf16 exponent ee-1+S and mantissa bit6 = m; the e2m1
+// subnormal (ee=0, m=1) gives exponent S-1; |n|==0, exponent > 254 and
+// exponent < 1 all give a signed zero.
+__device__ __forceinline__ uint32_t af3_e2m1_to_bf16_bits(uint32_t nib, uint32_t scale) {
+  uint32_t sign = (nib >> 3) & 1u;
+  uint32_t ee = (nib >> 1) & 3u;
+  uint32_t m = nib & 1u;
+  int exp = ee ? (int)(ee - 1 + scale) : (int)scale - 1;
+  uint32_t mant = ee ? (m << 6) : 0u;
+  uint32_t r = (sign << 15) | ((uint32_t)exp << 7) | mant;
+  bool zero = ((nib & 7u) == 0u) || exp > 254 || exp < 1;
+  return zero ? (sign << 15) : (r & 0xFFFFu);
+}
+
+// Four packed bytes (8 nibbles) with one scale -> 8 bf16 (4 dwords, element
+// order lo0,hi0,lo1,hi1,...), exact for every scale byte 0..255.
+// Scales in [2, 252] keep every exponent inside bf16's normal range, where the
+// gfx950 hardware converter (v_cvt_scalef32_pk_bf16_fp4: fp4 pair * 2^(S-127))
+// is exact; other scales take the integer restatement above so that the
+// overflow/underflow flush-to-zero rule is honoured bit for bit.
+__device__ __forceinline__ void af3_dequant_u32(uint32_t v, uint32_t scale, uint32_t out[4]) {
+  if (scale - 2u <= 250u) {
+    float sc = __uint_as_float(scale << 23);
+    out[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, sc, 0));
+    out[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, sc, 1));
+    out[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, sc, 2));
+    out[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, sc, 3));
+  } else {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      uint32_t byte = (v >> (8 * b)) & 0xFFu;
+      out[b] = af3_e2m1_to_bf16_bits(byte & 0xFu, scale) |
+               (af3_e2m1_to_bf16_bits(byte >> 4, scale) << 16);
+    }
+  }
+}
+
+// integer-only variant of af3_dequant_u32 (used as the in-kernel cross-check
+// path and for the exhaustive known-answer entry point)
+__device__ __forceinline__ void af3_dequant_u32_int(uint32_t v, uint32_t scale, uint32_t out[4]) {
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    uint32_t byte = (v >> (8 * b)) & 0xFFu;
+    out[b] = af3_e2m1_to_bf16_bits(byte & 0xFu, scale) |
+             (af3_e2m1_to_bf16_bits(byte >> 4, scale) << 16);
+  }
+}
+
+__host__ __device__ __forceinline__ int64_t af3_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -1,0 +1,707 @@
+// Grouped (per-expert) GEMMs of the gpt-oss MoE expert path on bf16 MFMA.
+//
+// Reference behaviour (the reference calls triton_kernels.matmul_ogs after
+// materialising the bf16 weights of every expert, quantization.py:358-362 and
+// 409-418; matmul_ogs semantics: for each expert e,
+//   Y[rows(e)] = X[gather(rows(e))] @ W[e] (+ bias[e]) (* gammas[rows(e)])
+// followed by a scatter-sum over the K slots of each token):
+//   A6  gate_up forward  quantization.py:516-525   trans_w = 0, gather, bias
+//   A8  down forward     quantization.py:532-541   trans_w = 0, bias, gammas
+//   A9  down dX          quantization.py:409-418   trans_w = 1, gather, gammas
+//   A11 gate_up dX       quantization.py:409-418   trans_w = 1 (then combine)
+// Here the MXFP4 weight is never materialised: each k-step of the B tile is
+// read packed from HBM and converted to bf16 on its way into LDS.
+//
+// One kernel template covers every GEMM of the path.  C[m][n] = sum_k A(m,k) *
+// B(n,k) with a 64-deep k-step staged through LDS as [rows][64] bf16 tiles
+// (k contiguous, 16-byte chunks XOR-swizzled by row), read by
+// v_mfma_f32_32x32x16_bf16.  Operands are produced by loaders:
+//   RowsBf16   A[m][k] / B[n][k] with k contiguous (optionally row-gathered)
+//   RowsFp4    B = MXFP4 W[e][n][k/32][16]     (nibbles packed along k)
+//   ColsBf16   operand stored [k][rows]: 8x8 register transpose before LDS
+//   ColsFp4    B = MXFP4 W[e][k][n/32][16]     (nibbles packed along n)
+// Grid modes:
+//   row tiles  blockIdx.x -> block_pid_map entry (expert e, BM-row block b) of
+//              the expert-sorted rows; blockIdx.y -> BN-column block.  An
+//              optional second k segment (the expert LoRA term) is appended.
+//   wgrad      blockIdx.x -> (expert, m block, n block); the k range is the
+//              expert's rows: G[e] = A(rows(e))^T B(rows(e)).
+#include "af3_common.h"
+
+namespace {
+
+constexpr int kBK = 64;
+constexpr int kThreads = 256;
+
+enum Kind { ROWS_BF16 = 0, ROWS_FP4 = 1, COLS_BF16 = 2, COLS_FP4 = 3, NONE = 4 };
+
+struct Operand {
+  const void* ptr;         // bf16 elements or MXFP4 blocks
+  const uint8_t* scales;   // MXFP4 scales
+  int64_t ld;              // row stride: elements (bf16) / bytes (fp4 blocks)
+  int64_t sld;             // scale row stride (bytes)
+  int64_t estride;         // per-expert stride (elements / bytes), 0 = shared
+  int64_t sestride;        // per-expert scale stride
+  const int32_t* gather;   // optional row indirection (index / gdiv)
+  int gdiv;
+  const uint16_t* rowscale;  // optional bf16 per-row multiplier (COLS_BF16 A only)
+  int extent;              // number of valid tile rows along the operand's non-k axis (N or M)
+};
+
+struct Params {
+  Operand a, b;       // main segment
+  Operand ax, bx;     // extension segment (row tiles only)
+  int K;              // main reduction length (row tiles)
+  int kx;             // extension reduction length (0 = none)
+  const int32_t* offs;      // expert row offsets [E+1]
+  const int32_t* tile_map;  // block_pid_map (row tiles)
+  int E;
+  int n_mblk, n_nblk;       // wgrad tiling
+  const float* bias;        // [E][N] fp32
+  int64_t bias_estride;
+  const void* gammas;       // [rows] bf16 or fp32
+  int gammas_f32;
+  float scale;
+  uint16_t* c;
+  int64_t ldc;
+  int64_t c_estride;        // wgrad output per-expert stride
+  int M, N;                 // output extents (M used by wgrad; rows come from offs in row tiles)
+};
+
+__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
+
+// LDS offset (in bf16 elements) of the 16-byte chunk `ch` of tile row `row`
+__device__ __forceinline__ int lds_off(int row, int ch) { return row * kBK + ((ch ^ swz(row)) << 3); }
+
+__device__ __forceinline__ af3_u32x4 zero4() { return af3_u32x4{0u, 0u, 0u, 0u}; }
+
+__device__ __forceinline__ uint32_t perm_lo(uint32_t a, uint32_t b) {  // lo16(a) | lo16(b) << 16
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t perm_hi(uint32_t a, uint32_t b) {  // hi16(a) | hi16(b) << 16
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// in[j] = row j (k index) holding 8 consecutive tile-row values; out[i] =
+// tile row i holding 8 consecutive k values.
+__device__ __forceinline__ void transpose8x8(const af3_u32x4 in[8], af3_u32x4 out[8]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      uint32_t a = in[2 * p][q], b = in[2 * p + 1][q];
+      lo[p] = perm_lo(a, b);
+      hi[p] = perm_hi(a, b);
+    }
+    out[2 * q] = af3_u32x4{lo[0], lo[1], lo[2], lo[3]};
+    out[2 * q + 1] = af3_u32x4{hi[0], hi[1], hi[2], hi[3]};
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Loaders.  TR = tile rows (BM for A, BN for B).  `row0` is the first tile row
+// in the operand's row space (expert-sorted row for gathered/row operands,
+// column for cols operands); k ranges over [k0, k0+64) limited by `kend`.
+// ---------------------------------------------------------------------------
+template <int TR, int KIND>
+struct Loader;
+
+// k-contiguous bf16 rows
+template <int TR>
+struct Loader<TR, ROWS_BF16> {
+  static constexpr int kUnits = TR * 8;
+  static constexpr int kUPT = (kUnits + kThreads - 1) / kThreads;
+  const uint16_t* rp[kUPT];
+  af3_u32x4 v[kUPT];
+  int kend;
+
+  __device__ void init(const Operand& op, int e, int row0, int nvalid, int kend_) {
+    kend = kend_;
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      int u = threadIdx.x + i * kThreads;
+      int r = u >> 3;
+      rp[i] = nullptr;
+      if (u < kUnits && r < nvalid) {
+        int64_t src = row0 + r;
+        if (op.gather) src = op.gather[src] / op.gdiv;
+        rp[i] = (const uint16_t*)op.ptr + e * op.estride + src * op.ld;
+      }
+    }
+  }
+  __device__ void load(int k0) {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      int u = threadIdx.x + i * kThreads;
+      int k = k0 + ((u & 7) << 3);
+      v[i] = (rp[i] && k < kend) ? *(const af3_u32x4*)(rp[i] + k) : zero4();
+    }
+  }
+  __device__ void store(uint16_t* lds) {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      int u = threadIdx.x + i * kThreads;
+      if (u < kUnits) *(af3_u32x4*)(lds + lds_off(u >> 3, u & 7)) = v[i];
+    }
+  }
+};
+
+// MXFP4 rows packed along k: W[e][n][k/32][16]
+template <int TR>
+struct Loader<TR, ROWS_FP4> {
+  static constexpr int kUnits = TR * 2;  // two 32-element groups per 64-deep k-step
+  static constexpr int kUPT = (kUnits + kThreads - 1) / kThreads;
+  const uint8_t* bp[kUPT];
+  const uint8_t* sp[kUPT];
+  af3_u32x4 v[kUPT];
+  uint32_t s[kUPT];
+  int kend;
+
+  __device__ void init(const Operand& op, int e, int row0, int nvalid, int kend_) {
+    kend = kend_;
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      int u = threadIdx.x + i * kThreads;
+      int r = u >> 1;
+      bp[i] = nullptr;
+      sp[i] = nullptr;
+      if (u < kUnits && r < nvalid) {
+        int64_t n = row0 + r;
+        bp[i] = (const uint8_t*)op.ptr + e * op.estride + n * op.ld;
+        sp[i] = op.scales + e * op.sestride + n * op.sld;
+      }
+    }
+  }
+  __device__ void load(int k0) {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      int u = threadIdx.x + i * kThreads;
+      int k = k0 + ((u & 1) << 5);
+      bool ok = bp[i] && k < kend;
+      v[i] = ok ? *(const af3_u32x4*)(bp[i] + (k >> 1)) : zero4();
+      s[i] = ok ? (uint32_t)sp[i][k >> 5] : 127u;
+    }
+  }
+  __device__ void store(uint16_t* lds) {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      int u = threadIdx.x + i * kThreads;
+      if (u >= kUnits) continue;
+      int r = u >> 1, ch0 = (u & 1) << 2;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t o[4];
+        af3_dequant_u32(v[i][q], s[i], o);
+        *(af3_u32x4*)(lds + lds_off(r, ch0 + q)) = af3_u32x4{o[0], o[1], o[2], o[3]};
+      }
+    }
+  }
+};
+
+// bf16 operand stored [k][rows] (rows contiguous): unit = 8 k x 8 rows
+template <int TR>
+struct Loader<TR, COLS_BF16> {
+  static constexpr int kUnits = 8 * (TR / 8);
+  static constexpr int kUPT = (kUnits + kThreads - 1) / kThreads;
+  const uint16_t* base;
+  const int32_t* gather;
+  const uint16_t* rowscale;
+  int64_t ld;
+  int gdiv, kb, kend, col0, ncols;
+  af3_u32x4 v[kUPT][8];
+
+  __device__ void init(const Operand& op, int e, int col0_, int ncols_, int kb_, int kend_) {
+    base = (const uint16_t*)op.ptr + e * op.estride;
+    gather = op.gather;
+    gdiv = op.gdiv;
+    rowscale = op.rowscale;
+    ld = op.ld;
+    kb = kb_;
+    kend = kend_;
+    col0 = col0_;
+    ncols = ncols_;
+  }
+  __device__ void load(int k0) {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      int u = threadIdx.x + i * kThreads;
+      int ko = u & 7, co = u >> 3;
+      int c = co * 8;
+      bool cok = u < kUnits && c < ncols;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        int k = k0 + ko * 8 + j;
+        af3_u32x4 x = zero4();
+        if (cok && k < kend) {
+          int64_t r = kb + k;
+          int64_t src = gather ? (int64_t)(gather[r] / gdiv) : r;
+          x = *(const af3_u32x4*)(base + src * ld + col0 + c);
+          if (rowscale) {
+            float sc = af3_bf16_to_f32(rowscale[r]);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              x[q] = af3_pack_bf16x2(af3_bf16_to_f32(x[q] & 0xFFFFu) * sc, af3_bf16_to_f32(x[q] >> 16) * sc);
+          }
+        }
+        v[i][j] = x;
+      }
+    }
+  }
+  __device__ void store(uint16_t* lds) {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      int u = threadIdx.x + i * kThreads;
+      if (u >= kUnits) continue;
+      int ko = u & 7, co = u >> 3;
+      af3_u32x4 t[8];
+      transpose8x8(v[i], t);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) *(af3_u32x4*)(lds + lds_off(co * 8 + j, ko)) = t[j];
+    }
+  }
+};
+
+// MXFP4 operand packed along the tile-row axis: W[e][k][n/32][16]
+template <int TR>
+struct Loader<TR, COLS_FP4> {
+  static constexpr int kUnits = 8 * (TR / 8);
+  static constexpr int kUPT = (kUnits + kThreads - 1) / kThreads;
+  const uint8_t* bbase;
+  const uint8_t* sbase;
+  int64_t ld, sld;
+  int kend, col0, ncols;
+  uint32_t w[kUPT][8];
+  uint32_t s[kUPT][8];
+
+  __device__ void init(const Operand& op, int e, int col0_, int ncols_, int kb_, int kend_) {
+    bbase = (const uint8_t*)op.ptr + e * op.estride;
+    sbase = op.scales + e * op.sestride;
+    ld = op.ld;
+    sld = op.sld;
+    kend = kend_;
+    col0 = col0_;
+    ncols = ncols_;
+  }
+  __device__ void load(int k0) {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      int u = threadIdx.x + i * kThreads;
+      int ko = u & 7, co = u >> 3;
+      int c = col0 + co * 8;  // first of 8 columns = 4 packed bytes
+      bool cok = u < kUnits && co * 8 < ncols;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        int k = k0 + ko * 8 + j;
+        bool ok = cok && k < kend;
+        w[i][j] = ok ? *(const uint32_t*)(bbase + (int64_t)k * ld + (c >> 1)) : 0u;
+        s[i][j] = ok ? (uint32_t)sbase[(int64_t)k * sld + (c >> 5)] : 127u;
+      }
+    }
+  }
+  __device__ void store(uint16_t* lds) {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      int u = threadIdx.x + i * kThreads;
+      if (u >= kUnits) continue;
+      int ko = u & 7, co = u >> 3;
+      af3_u32x4 x[8], t[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        uint32_t o[4];
+        af3_dequant_u32(w[i][j], s[i][j], o);
+        x[j] = af3_u32x4{o[0], o[1], o[2], o[3]};
+      }
+      transpose8x8(x, t);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) *(af3_u32x4*)(lds + lds_off(co * 8 + j, ko)) = t[j];
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// MFMA compute on one LDS k-step
+// ---------------------------------------------------------------------------
+template <int TM, int TN>
+__device__ __forceinline__ void mma_kstep(const uint16_t* As, const uint16_t* Bs, int wm0, int wn0,
+                                          af3_f32x16 acc[TM][TN]) {
+  const int lane = threadIdx.x & 63;
+  const int lr = lane & 31, lk = lane >> 5;
+#pragma unroll
+  for (int ks = 0; ks < kBK / 16; ++ks) {
+    af3_bf16x8 af[TM], bf[TN];
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+      af[tm] = *(const af3_bf16x8*)(As + lds_off(wm0 + tm * 32 + lr, ks * 2 + lk));
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+      bf[tn] = *(const af3_bf16x8*)(Bs + lds_off(wn0 + tn * 32 + lr, ks * 2 + lk));
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+        acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[tm], bf[tn], acc[tm][tn], 0, 0, 0);
+  }
+}
+
+template <class LA, class LB, int TM, int TN>
+__device__ __forceinline__ void run_segment(LA& la, LB& lb, int k_len, uint16_t* As, uint16_t* Bs, int wm0, int wn0,
+                                            af3_f32x16 acc[TM][TN]) {
+  const int nk = (k_len + kBK - 1) / kBK;
+  if (nk <= 0) return;
+  la.load(0);
+  lb.load(0);
+  for (int kt = 0; kt < nk; ++kt) {
+    __syncthreads();
+    la.store(As);
+    lb.store(Bs);
+    __syncthreads();
+    if (kt + 1 < nk) {
+      la.load((kt + 1) * kBK);
+      lb.load((kt + 1) * kBK);
+    }
+    mma_kstep<TM, TN>(As, Bs, wm0, wn0, acc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// row-tile kernel: main GEMMs and the skinny LoRA row products
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int WM, int WN, int AK, int BK_, int AXK, int BXK>
+__global__ __launch_bounds__(kThreads) void rowtile_kernel(Params p) {
+  static_assert(WM * WN == 4, "four waves");
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  __shared__ __attribute__((aligned(16))) uint16_t As[BM * kBK];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[BN * kBK];
+
+  const int32_t ent = p.tile_map[blockIdx.x];
+  if (ent < 0) return;
+  const int e = ent & 0xFFFF, blk = ent >> 16;
+  const int row_lo = p.offs[e] + blk * BM;
+  const int nrows = min(BM, p.offs[e + 1] - row_lo);
+  if (nrows <= 0) return;
+  const int n0 = blockIdx.y * BN;
+  const int ncols = min(BN, p.N - n0);
+
+  const int wave = threadIdx.x >> 6;
+  const int wm0 = (wave / WN) * (BM / WM), wn0 = (wave % WN) * (BN / WN);
+  af3_f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  {
+    Loader<BM, AK> la;
+    Loader<BN, BK_> lb;
+    la.init(p.a, 0, row_lo, nrows, p.K);
+    if constexpr (BK_ == ROWS_BF16 || BK_ == ROWS_FP4)
+      lb.init(p.b, e, n0, ncols, p.K);
+    else
+      lb.init(p.b, e, n0, ncols, 0, p.K);
+    run_segment<Loader<BM, AK>, Loader<BN, BK_>, TM, TN>(la, lb, p.K, As, Bs, wm0, wn0, acc);
+  }
+  if constexpr (AXK != NONE) {
+    if (p.kx > 0) {
+      Loader<BM, AXK> la;
+      Loader<BN, BXK> lb;
+      la.init(p.ax, 0, row_lo, nrows, p.kx);
+      if constexpr (BXK == ROWS_BF16)
+        lb.init(p.bx, e, n0, ncols, p.kx);
+      else
+        lb.init(p.bx, e, n0, ncols, 0, p.kx);
+      run_segment<Loader<BM, AXK>, Loader<BN, BXK>, TM, TN>(la, lb, p.kx, As, Bs, wm0, wn0, acc);
+    }
+  }
+
+  // epilogue: (acc + bias) * gamma * scale -> bf16
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int col = wn0 + tn * 32 + (lane & 31);
+      if (col >= ncols) continue;
+      const int n = n0 + col;
+      const float bv = p.bias ? p.bias[e * p.bias_estride + n] : 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = wm0 + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        if (row >= nrows) continue;
+        const int64_t gr = row_lo + row;
+        float v = acc[tm][tn][r] + bv;
+        if (p.gammas)
+          v *= p.gammas_f32 ? ((const float*)p.gammas)[gr] : af3_bf16_to_f32(((const uint16_t*)p.gammas)[gr]);
+        v *= p.scale;
+        p.c[gr * p.ldc + n] = (uint16_t)af3_f32_to_bf16(v);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// weight-gradient kernel: G[e][m][n] = scale * sum_{r in rows(e)} A[r][m] B[r][n]
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(kThreads) void wgrad_kernel(Params p) {
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  __shared__ __attribute__((aligned(16))) uint16_t As[BM * kBK];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[BN * kBK];
+
+  const int per_e = p.n_mblk * p.n_nblk;
+  const int e = blockIdx.x / per_e;
+  const int rem = blockIdx.x - e * per_e;
+  const int m0 = (rem / p.n_nblk) * BM, n0 = (rem % p.n_nblk) * BN;
+  const int kb = p.offs[e], kend = p.offs[e + 1] - kb;
+  const int mcols = min(BM, p.M - m0), ncols = min(BN, p.N - n0);
+
+  const int wave = threadIdx.x >> 6;
+  const int wm0 = (wave / WN) * (BM / WM), wn0 = (wave % WN) * (BN / WN);
+  af3_f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  Loader<BM, COLS_BF16> la;
+  Loader<BN, COLS_BF16> lb;
+  la.init(p.a, 0, m0, mcols, kb, kend);
+  lb.init(p.b, 0, n0, ncols, kb, kend);
+  run_segment<Loader<BM, COLS_BF16>, Loader<BN, COLS_BF16>, TM, TN>(la, lb, kend, As, Bs, wm0, wn0, acc);
+
+  const int lane = threadIdx.x & 63;
+  uint16_t* out = p.c + e * p.c_estride;
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int col = wn0 + tn * 32 + (lane & 31);
+      if (col >= ncols) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = wm0 + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        if (row >= mcols) continue;
+        out[(int64_t)(m0 + row) * p.ldc + n0 + col] = (uint16_t)af3_f32_to_bf16(acc[tm][tn][r] * p.scale);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// combine: out[t] = sum_j rows[src[t*K + j]] (fp32 sum, bf16 out), -1 skipped
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ rows, int64_t ld_rows,
+                                                      const int32_t* __restrict__ src, int K, int N,
+                                                      uint16_t* __restrict__ out, int64_t ld_out, int vec_per_row,
+                                                      int64_t n_vec) {
+  int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (v >= n_vec) return;
+  int64_t t = v / vec_per_row;
+  int c = (int)(v - t * vec_per_row) * 8;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int j = 0; j < K; ++j) {
+    int32_t r = src[t * K + j];
+    if (r < 0) continue;
+    af3_u32x4 x = *(const af3_u32x4*)(rows + (int64_t)r * ld_rows + c);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      acc[2 * q] += af3_bf16_to_f32(x[q] & 0xFFFFu);
+      acc[2 * q + 1] += af3_bf16_to_f32(x[q] >> 16);
+    }
+  }
+  af3_u32x4 o;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) o[q] = af3_pack_bf16x2(acc[2 * q], acc[2 * q + 1]);
+  *(af3_u32x4*)(out + t * ld_out + c) = o;
+}
+
+Operand make_bf16(const uint16_t* ptr, int64_t ld, int64_t estride, const int32_t* gather, int gdiv,
+                  const uint16_t* rowscale = nullptr) {
+  Operand o{};
+  o.ptr = ptr;
+  o.ld = ld;
+  o.estride = estride;
+  o.gather = gather;
+  o.gdiv = gdiv > 0 ? gdiv : 1;
+  o.rowscale = rowscale;
+  return o;
+}
+
+inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// exported entry points
+// ---------------------------------------------------------------------------
+
+// Grouped GEMM through frozen MXFP4 expert weights (A6/A8/A9/A11).
+//   trans_w = 0: Y[r][n] = sum_k X[a(r)][k] W[e][n][k]   W blocks [E][N][K/32][16]
+//   trans_w = 1: Y[r][n] = sum_k X[a(r)][k] W[e][k][n]   W blocks [E][K][N/32][16]
+//   optional extension (expert LoRA):  + sum_j L[r][j] Bx[e][n][j] (trans 0) or Bx[e][j][n] (trans 1)
+//   then v = (acc + bias[e][n]) * gammas[r] -> bf16 Y[r][n]
+// a(r) = gather ? gather[r] / gather_div : r.  Rows r are expert-sorted; expert
+// e owns rows [token_offs[e], token_offs[e+1]); block_pid_map is the BM=128
+// map of af3_expt_data; grid.x = max_tiles.
+extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
+                            const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
+                            const void* gammas, int gammas_f32, const uint16_t* lora_l, int64_t ld_l, const uint16_t* lora_b,
+                            int lora_r, const int32_t* token_offs, const int32_t* block_pid_map, int max_tiles,
+                            int n_expts, int N, int K, uint16_t* y, int64_t ldy, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  AF3_REQUIRE(N > 0 && K > 0 && n_expts > 0 && max_tiles >= 0, "moe_gemm: bad sizes N=%d K=%d E=%d", N, K, n_expts);
+  if (max_tiles == 0) return 0;
+  AF3_REQUIRE(x && w_blocks && w_scales && token_offs && block_pid_map && y, "moe_gemm: null pointer");
+  AF3_REQUIRE(K % 32 == 0 && N % 32 == 0, "moe_gemm: N and K must be multiples of 32 (N=%d K=%d)", N, K);
+  AF3_REQUIRE(ldx % 8 == 0 && al16(x), "moe_gemm: x must be 16-byte aligned with ld % 8 == 0");
+  AF3_REQUIRE(lora_r >= 0 && lora_r <= 64, "moe_gemm: lora rank %d unsupported (max 64)", lora_r);
+  AF3_REQUIRE(lora_r == 0 || (lora_l && lora_b && ld_l % 8 == 0 && lora_r % 8 == 0 && al16(lora_l) && al16(lora_b)),
+              "moe_gemm: LoRA operands must be 16-byte aligned, rank % 8 == 0");
+  AF3_REQUIRE(al16(w_blocks), "moe_gemm: weight blocks must be 16-byte aligned");
+  Params p{};
+  const int G_k = K / 32, G_n = N / 32;
+  p.a = make_bf16(x, ldx, 0, gather_indx, gather_div);
+  p.b.ptr = w_blocks;
+  p.b.scales = w_scales;
+  if (trans_w == 0) {
+    p.b.ld = (int64_t)G_k * 16;
+    p.b.sld = G_k;
+    p.b.estride = (int64_t)N * G_k * 16;
+    p.b.sestride = (int64_t)N * G_k;
+  } else {
+    p.b.ld = (int64_t)G_n * 16;
+    p.b.sld = G_n;
+    p.b.estride = (int64_t)K * G_n * 16;
+    p.b.sestride = (int64_t)K * G_n;
+  }
+  p.K = K;
+  p.kx = lora_r;
+  if (lora_r) {
+    p.ax = make_bf16(lora_l, ld_l, 0, nullptr, 1);
+    // trans 0: Bx[e] is [N][r] (k contiguous); trans 1: Bx[e] is [r][N] (n contiguous)
+    p.bx = trans_w == 0 ? make_bf16(lora_b, lora_r, (int64_t)N * lora_r, nullptr, 1)
+                        : make_bf16(lora_b, N, (int64_t)N * lora_r, nullptr, 1);
+  }
+  p.offs = token_offs;
+  p.tile_map = block_pid_map;
+  p.E = n_expts;
+  p.bias = bias;
+  p.bias_estride = N;
+  p.gammas = gammas;
+  p.gammas_f32 = gammas_f32;
+  p.scale = 1.0f;
+  p.c = y;
+  p.ldc = ldy;
+  p.N = N;
+  dim3 grid(max_tiles, (N + 127) / 128);
+  if (trans_w == 0)
+    hipLaunchKernelGGL((rowtile_kernel<128, 128, 2, 2, ROWS_BF16, ROWS_FP4, ROWS_BF16, ROWS_BF16>), grid,
+                       dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((rowtile_kernel<128, 128, 2, 2, ROWS_BF16, COLS_FP4, ROWS_BF16, COLS_BF16>), grid,
+                       dim3(kThreads), 0, stream, p);
+  return af3::check_launch("moe_gemm");
+}
+
+// Skinny per-expert row product for the LoRA terms (BM = 128 map):
+//   trans_b = 0: out[r][j] = scale * sum_k X[a(r)][k] Wl[e][j][k]   Wl [E][n_out][K]
+//   trans_b = 1: out[r][j] = scale * sum_k X[a(r)][k] Wl[e][k][j]   Wl [E][K][n_out]
+extern "C" int af3_lora_rows(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
+                             const uint16_t* wl, int trans_b, float scale, const int32_t* token_offs,
+                             const int32_t* block_pid_map, int max_tiles, int n_expts, int n_out, int K,
+                             uint16_t* out, int64_t ld_out, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  AF3_REQUIRE(n_out > 0 && n_out <= 64 && K > 0, "lora_rows: bad sizes n_out=%d K=%d", n_out, K);
+  if (max_tiles == 0) return 0;
+  AF3_REQUIRE(K % 8 == 0 && n_out % 8 == 0 && ldx % 8 == 0 && al16(x) && al16(wl),
+              "lora_rows: operands must be 16-byte aligned with sizes % 8 == 0");
+  Params p{};
+  p.a = make_bf16(x, ldx, 0, gather_indx, gather_div);
+  p.b = trans_b == 0 ? make_bf16(wl, K, (int64_t)n_out * K, nullptr, 1)
+                     : make_bf16(wl, n_out, (int64_t)n_out * K, nullptr, 1);
+  p.K = K;
+  p.offs = token_offs;
+  p.tile_map = block_pid_map;
+  p.E = n_expts;
+  p.scale = scale;
+  p.c = out;
+  p.ldc = ld_out;
+  p.N = n_out;
+  if (n_out <= 32) {
+    dim3 grid(max_tiles, 1);
+    if (trans_b == 0)
+      hipLaunchKernelGGL((rowtile_kernel<128, 32, 4, 1, ROWS_BF16, ROWS_BF16, NONE, NONE>), grid, dim3(kThreads), 0,
+                         stream, p);
+    else
+      hipLaunchKernelGGL((rowtile_kernel<128, 32, 4, 1, ROWS_BF16, COLS_BF16, NONE, NONE>), grid, dim3(kThreads), 0,
+                         stream, p);
+  } else {
+    dim3 grid(max_tiles, 1);
+    if (trans_b == 0)
+      hipLaunchKernelGGL((rowtile_kernel<128, 64, 2, 2, ROWS_BF16, ROWS_BF16, NONE, NONE>), grid, dim3(kThreads), 0,
+                         stream, p);
+    else
+      hipLaunchKernelGGL((rowtile_kernel<128, 64, 2, 2, ROWS_BF16, COLS_BF16, NONE, NONE>), grid, dim3(kThreads), 0,
+                         stream, p);
+  }
+  return af3::check_launch("lora_rows");
+}
+
+// Per-expert weight gradient over the expert's rows:
+//   G[e][m][n] = scale * sum_{r in rows(e)} (rs(r) * A[a(r)][m]) * B[b(r)][n]
+// with a(r) = a_gather ? a_gather[r] / a_div : r (same for b) and rs the
+// optional bf16 per-row multiplier.  G is bf16 [E][M][N] row-major.
+extern "C" int af3_lora_wgrad(const uint16_t* a, int64_t lda, const int32_t* a_gather, int a_div,
+                              const uint16_t* a_rowscale, const uint16_t* b, int64_t ldb, const int32_t* b_gather,
+                              int b_div, float scale, const int32_t* token_offs, int n_expts, int M, int N,
+                              uint16_t* g, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  AF3_REQUIRE(M > 0 && N > 0 && n_expts > 0, "lora_wgrad: bad sizes");
+  AF3_REQUIRE(M % 8 == 0 && N % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && al16(a) && al16(b),
+              "lora_wgrad: operands must be 16-byte aligned with sizes % 8 == 0");
+  Params p{};
+  p.a = make_bf16(a, lda, 0, a_gather, a_div, a_rowscale);
+  p.b = make_bf16(b, ldb, 0, b_gather, b_div);
+  p.offs = token_offs;
+  p.E = n_expts;
+  p.scale = scale;
+  p.c = g;
+  p.ldc = N;
+  p.c_estride = (int64_t)M * N;
+  p.M = M;
+  p.N = N;
+  if (N <= 32) {  // tall output (e.g. dB: [N_out][r])
+    p.n_mblk = (M + 127) / 128;
+    p.n_nblk = 1;
+    hipLaunchKernelGGL((wgrad_kernel<128, 32, 4, 1>), dim3(n_expts * p.n_mblk), dim3(kThreads), 0, stream, p);
+  } else if (M <= 32) {  // wide output (e.g. dA: [r][K])
+    p.n_mblk = 1;
+    p.n_nblk = (N + 127) / 128;
+    hipLaunchKernelGGL((wgrad_kernel<32, 128, 1, 4>), dim3(n_expts * p.n_nblk), dim3(kThreads), 0, stream, p);
+  } else {
+    p.n_mblk = (M + 127) / 128;
+    p.n_nblk = (N + 127) / 128;
+    hipLaunchKernelGGL((wgrad_kernel<128, 128, 2, 2>), dim3(n_expts * p.n_mblk * p.n_nblk), dim3(kThreads), 0,
+                       stream, p);
+  }
+  return af3::check_launch("lora_wgrad");
+}
+
+// out[t][:] = sum_{j<K} rows[src[t*K+j]][:]  (the scatter-sum of matmul_ogs)
+extern "C" int af3_moe_combine(const uint16_t* rows, int64_t ld_rows, const int32_t* src_indx, int64_t n_tokens,
+                               int K, int N, uint16_t* out, int64_t ld_out, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  AF3_REQUIRE(n_tokens >= 0 && K > 0 && N > 0, "moe_combine: bad sizes");
+  if (n_tokens == 0) return 0;
+  AF3_REQUIRE(N % 8 == 0 && ld_rows % 8 == 0 && ld_out % 8 == 0 && al16(rows) && al16(out),
+              "moe_combine: rows/out must be 16-byte aligned with N % 8 == 0");
+  int vpr = N / 8;
+  int64_t nv = n_tokens * vpr;
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)af3_cdiv(nv, 256)), dim3(256), 0, stream, rows, ld_rows, src_indx,
+                     K, N, out, ld_out, vpr, nv);
+  return af3::check_launch("moe_combine");
+}

@@ -1,0 +1,321 @@
+// Token -> expert permutation (routing metadata) for the grouped expert GEMMs.
+//
+// Reference behaviour:
+//   routing_replay   quantization.py:593-636: softmax over the K gathered
+//                    logits of each token; stable sort of the flat [T*K]
+//                    expert ids; gate_indx = inverse permutation; gate_scal =
+//                    softmax weights in sorted order; hist = bincount.
+//   top-k routing    quantization.py:551-590 (routing_torch_dist at world size
+//                    1, the torch restatement of triton_kernels' routing):
+//                    top-K logits per token by a stable descending sort (ties
+//                    go to the lower expert id), softmax over those K, then
+//                    the K (id, weight) pairs of a token sorted by expert id.
+//   expt data        triton_kernels.routing.compute_expt_data_torch (called at
+//                    quantization.py:588,627): token_offs_raw = exclusive scan
+//                    of hist; per block size BM, token_offs_pad = exclusive
+//                    scan of ceil(hist/BM) and block_pid_map[i] = (b<<16)|e for
+//                    the b-th BM-row block of expert e, -1 for unused slots.
+//
+// The sort is a stable counting sort: per 256-entry chunk histograms, a scan
+// over (expert, chunk), then a scatter where each entry's rank among equal ids
+// earlier in its chunk keeps the order of the flat index.  Entries whose
+// expert id is outside [0, E) are dropped (gate_indx = -1), the same shape the
+// reference gives expert-parallel-masked entries.
+#include "af3_common.h"
+
+namespace {
+
+constexpr int kChunk = 256;
+
+__device__ __forceinline__ uint32_t bf16_bits_rne(float f) { return af3_f32_to_bf16(f); }
+
+// one thread per token: ids/weights of its K slots (replay form)
+__global__ void replay_token_kernel(const uint16_t* __restrict__ logits, int64_t ld, const int32_t* __restrict__ idx,
+                                    int64_t T, int E, int K, int32_t* __restrict__ ids,
+                                    uint16_t* __restrict__ scal) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= T) return;
+  float v[16];
+  int e[16];
+  float mx = -INFINITY;
+  for (int j = 0; j < K; ++j) {
+    e[j] = idx[t * K + j];
+    bool ok = e[j] >= 0 && e[j] < E;
+    v[j] = ok ? af3_bf16_to_f32(logits[t * ld + e[j]]) : -INFINITY;
+    mx = fmaxf(mx, v[j]);
+  }
+  float den = 0.f;
+  for (int j = 0; j < K; ++j) {
+    v[j] = (e[j] >= 0 && e[j] < E) ? expf(v[j] - mx) : 0.f;
+    den += v[j];
+  }
+  for (int j = 0; j < K; ++j) {
+    bool ok = e[j] >= 0 && e[j] < E;
+    ids[t * K + j] = ok ? e[j] : -1;
+    scal[t * K + j] = (uint16_t)bf16_bits_rne(v[j] / den);
+  }
+}
+
+// one thread per token: top-K selection + softmax + sort of the K by expert id
+__global__ void topk_token_kernel(const uint16_t* __restrict__ logits, int64_t ld, int64_t T, int E, int K,
+                                  int32_t* __restrict__ ids, uint16_t* __restrict__ scal) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= T) return;
+  float v[16];
+  int e[16];
+  for (int j = 0; j < K; ++j) {
+    v[j] = -INFINITY;
+    e[j] = E;  // sentinel larger than any id
+  }
+  const uint16_t* row = logits + t * ld;
+  for (int x = 0; x < E; ++x) {
+    float f = af3_bf16_to_f32(row[x]);
+    // strict > keeps the earlier (lower) id on ties, matching a stable sort of -logits
+    if (f > v[K - 1] || (e[K - 1] == E)) {
+      int p = K - 1;
+      while (p > 0 && (f > v[p - 1] || e[p - 1] == E)) {
+        v[p] = v[p - 1];
+        e[p] = e[p - 1];
+        --p;
+      }
+      v[p] = f;
+      e[p] = x;
+    }
+  }
+  float mx = v[0];
+  float w[16], den = 0.f;
+  for (int j = 0; j < K; ++j) {
+    w[j] = expf(v[j] - mx);
+    den += w[j];
+  }
+  // softmax output is rounded to the logits dtype (bf16) before reordering
+  uint16_t wb[16];
+  for (int j = 0; j < K; ++j) wb[j] = (uint16_t)bf16_bits_rne(w[j] / den);
+  // insertion sort of the K pairs by expert id (ids are distinct)
+  for (int a = 1; a < K; ++a) {
+    int ek = e[a];
+    uint16_t wk = wb[a];
+    int b = a - 1;
+    while (b >= 0 && e[b] > ek) {
+      e[b + 1] = e[b];
+      wb[b + 1] = wb[b];
+      --b;
+    }
+    e[b + 1] = ek;
+    wb[b + 1] = wk;
+  }
+  for (int j = 0; j < K; ++j) {
+    ids[t * K + j] = e[j];
+    scal[t * K + j] = wb[j];
+  }
+}
+
+// per-chunk histogram: counts[c * E + e]
+__global__ void chunk_hist_kernel(const int32_t* __restrict__ ids, int64_t R, int E, int32_t* __restrict__ counts) {
+  extern __shared__ int32_t sh[];
+  for (int e = threadIdx.x; e < E; e += blockDim.x) sh[e] = 0;
+  __syncthreads();
+  int64_t i = (int64_t)blockIdx.x * kChunk + threadIdx.x;
+  if (i < R) {
+    int e = ids[i];
+    if (e >= 0) atomicAdd(&sh[e], 1);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) counts[(int64_t)blockIdx.x * E + e] = sh[e];
+}
+
+// single block: hist, token_offs_raw, per-(chunk,expert) base offsets
+__global__ void scan_kernel(int32_t* __restrict__ counts, int n_chunks, int E, int32_t* __restrict__ hist,
+                            int32_t* __restrict__ offs) {
+  extern __shared__ int32_t tot[];  // E + 1
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int32_t run = 0;
+    for (int c = 0; c < n_chunks; ++c) {
+      int32_t v = counts[(int64_t)c * E + e];
+      counts[(int64_t)c * E + e] = run;
+      run += v;
+    }
+    tot[e] = run;
+    hist[e] = run;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int32_t run = 0;
+    for (int e = 0; e < E; ++e) {
+      int32_t v = tot[e];
+      tot[e] = run;
+      offs[e] = run;
+      run += v;
+    }
+    offs[E] = run;
+    tot[E] = run;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int32_t b = tot[e];
+    for (int c = 0; c < n_chunks; ++c) counts[(int64_t)c * E + e] += b;
+  }
+}
+
+// stable scatter of each chunk into expert-sorted order
+__global__ void scatter_kernel(const int32_t* __restrict__ ids, const uint16_t* __restrict__ scal, int64_t R, int E,
+                               const int32_t* __restrict__ base, int32_t* __restrict__ topk_indx,
+                               int32_t* __restrict__ gate_indx, uint16_t* __restrict__ gate_scal) {
+  __shared__ int32_t sid[kChunk];
+  int64_t i = (int64_t)blockIdx.x * kChunk + threadIdx.x;
+  int e = (i < R) ? ids[i] : -1;
+  sid[threadIdx.x] = e;
+  __syncthreads();
+  if (i >= R) return;
+  if (e < 0) {
+    gate_indx[i] = -1;
+    return;
+  }
+  int rank = 0;
+  for (int j = 0; j < (int)threadIdx.x; ++j) rank += (sid[j] == e);
+  int32_t pos = base[(int64_t)blockIdx.x * E + e] + rank;
+  topk_indx[pos] = (int32_t)i;
+  gate_indx[i] = pos;
+  gate_scal[pos] = scal[i];
+}
+
+// sorted slots past the number of valid entries (only when some ids were dropped)
+__global__ void fill_tail_kernel(const int32_t* __restrict__ offs, int E, int64_t R, int32_t* __restrict__ topk_indx,
+                                 uint16_t* __restrict__ gate_scal) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= R) return;
+  if (i >= offs[E]) {
+    topk_indx[i] = -1;
+    gate_scal[i] = 0;
+  }
+}
+
+// ---- expert data: padded tile offsets and block -> (block, expert) map -----
+__global__ void tile_scan_kernel(const int32_t* __restrict__ hist, int E, const int32_t* __restrict__ block_ms,
+                                 int n_bm, int32_t* __restrict__ offs_pad /* n_bm x (E+1) */) {
+  int b = threadIdx.x;
+  if (b >= n_bm) return;
+  int bm = block_ms[b];
+  int32_t run = 0;
+  for (int e = 0; e < E; ++e) {
+    offs_pad[b * (E + 1) + e] = run;
+    run += (hist[e] + bm - 1) / bm;
+  }
+  offs_pad[b * (E + 1) + E] = run;
+}
+
+__global__ void tile_map_kernel(const int32_t* __restrict__ offs_pad, int E, int max_tiles,
+                                int32_t* __restrict__ map /* n_bm x max_tiles */) {
+  int b = blockIdx.y;
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= max_tiles) return;
+  const int32_t* op = offs_pad + b * (E + 1);
+  int32_t val = -1;
+  if (i < op[E]) {
+    // largest e with op[e] <= i (experts with zero tiles have op[e] == op[e+1])
+    int lo = 0, hi = E - 1;
+    while (lo < hi) {
+      int mid = (lo + hi + 1) >> 1;
+      if (op[mid] <= i)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    val = ((i - op[lo]) << 16) | lo;
+  }
+  map[(int64_t)b * max_tiles + i] = val;
+}
+
+}  // namespace
+
+extern "C" size_t af3_routing_workspace_bytes(int64_t n_tokens, int n_expts_tot, int n_expts_act) {
+  int64_t R = n_tokens * n_expts_act;
+  int64_t n_chunks = af3_cdiv(R, kChunk);
+  size_t b = 0;
+  b += (size_t)R * 4;                       // ids
+  b = (b + 255) & ~(size_t)255;
+  b += (size_t)R * 2;                       // scal
+  b = (b + 255) & ~(size_t)255;
+  b += (size_t)n_chunks * n_expts_tot * 4;  // counts
+  return b + 256;
+}
+
+static int routing_common(bool topk, const uint16_t* logits, int64_t ld, const int32_t* expt_indx, int64_t T, int E,
+                          int K, uint16_t* gate_scal, int32_t* hist, int32_t* topk_indx, int32_t* gate_indx,
+                          int32_t* token_offs_raw, void* workspace, size_t ws_bytes, hipStream_t stream) {
+  AF3_REQUIRE(T >= 0 && E > 0 && K > 0, "routing: bad sizes T=%lld E=%d K=%d", (long long)T, E, K);
+  AF3_REQUIRE(K <= 16, "routing: K=%d > 16 unsupported", K);
+  AF3_REQUIRE(E <= 0x7fff, "routing: E=%d too large", E);
+  AF3_REQUIRE(!topk || K <= E, "routing: K=%d > E=%d", K, E);
+  AF3_REQUIRE(ld >= E, "routing: logits leading dim %lld < E", (long long)ld);
+  AF3_REQUIRE(ws_bytes >= af3_routing_workspace_bytes(T, E, K), "routing: workspace too small");
+  const int64_t R = T * K;
+  AF3_REQUIRE(R < 0x7fffffffLL, "routing: T*K too large");
+  char* ws = (char*)workspace;
+  size_t o = 0;
+  int32_t* ids = (int32_t*)(ws + o);
+  o += (size_t)R * 4;
+  o = (o + 255) & ~(size_t)255;
+  uint16_t* scal = (uint16_t*)(ws + o);
+  o += (size_t)R * 2;
+  o = (o + 255) & ~(size_t)255;
+  int32_t* counts = (int32_t*)(ws + o);
+  const int n_chunks = (int)af3_cdiv(R, kChunk);
+
+  if (T > 0) {
+    dim3 g((unsigned)af3_cdiv(T, 128));
+    if (topk)
+      hipLaunchKernelGGL(topk_token_kernel, g, dim3(128), 0, stream, logits, ld, T, E, K, ids, scal);
+    else
+      hipLaunchKernelGGL(replay_token_kernel, g, dim3(128), 0, stream, logits, ld, expt_indx, T, E, K, ids, scal);
+    int rc = af3::check_launch("routing/token");
+    if (rc) return rc;
+    hipLaunchKernelGGL(chunk_hist_kernel, dim3(n_chunks), dim3(kChunk), E * 4, stream, ids, R, E, counts);
+    rc = af3::check_launch("routing/hist");
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(256), (E + 1) * 4, stream, counts, n_chunks, E, hist,
+                     token_offs_raw);
+  int rc = af3::check_launch("routing/scan");
+  if (rc) return rc;
+  if (T > 0) {
+    hipLaunchKernelGGL(scatter_kernel, dim3(n_chunks), dim3(kChunk), 0, stream, ids, scal, R, E, counts, topk_indx,
+                       gate_indx, gate_scal);
+    rc = af3::check_launch("routing/scatter");
+    if (rc) return rc;
+    hipLaunchKernelGGL(fill_tail_kernel, dim3((unsigned)af3_cdiv(R, 256)), dim3(256), 0, stream, token_offs_raw, E,
+                       R, topk_indx, gate_scal);
+    rc = af3::check_launch("routing/tail");
+  }
+  return rc;
+}
+
+extern "C" int af3_routing_replay(const uint16_t* logits, int64_t ld_logits, const int32_t* expt_indx, int64_t n_tokens,
+                                  int n_expts_tot, int n_expts_act, uint16_t* gate_scal, int32_t* hist,
+                                  int32_t* topk_indx, int32_t* gate_indx, int32_t* token_offs_raw, void* workspace,
+                                  size_t ws_bytes, void* stream) {
+  AF3_REQUIRE(expt_indx || n_tokens == 0, "routing_replay: null expt_indx");
+  return routing_common(false, logits, ld_logits, expt_indx, n_tokens, n_expts_tot, n_expts_act, gate_scal, hist,
+                        topk_indx, gate_indx, token_offs_raw, workspace, ws_bytes, (hipStream_t)stream);
+}
+
+extern "C" int af3_routing_topk(const uint16_t* logits, int64_t ld_logits, int64_t n_tokens, int n_expts_tot,
+                                int n_expts_act, uint16_t* gate_scal, int32_t* hist, int32_t* topk_indx,
+                                int32_t* gate_indx, int32_t* token_offs_raw, void* workspace, size_t ws_bytes,
+                                void* stream) {
+  return routing_common(true, logits, ld_logits, nullptr, n_tokens, n_expts_tot, n_expts_act, gate_scal, hist,
+                        topk_indx, gate_indx, token_offs_raw, workspace, ws_bytes, (hipStream_t)stream);
+}
+
+extern "C" int af3_expt_data(const int32_t* hist, int n_expts_tot, const int32_t* block_ms_dev, int n_block_ms,
+                             int max_tiles, int32_t* token_offs_pad, int32_t* block_pid_map, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  AF3_REQUIRE(n_expts_tot > 0 && n_block_ms > 0 && n_block_ms <= 64 && max_tiles >= 0, "expt_data: bad sizes");
+  hipLaunchKernelGGL(tile_scan_kernel, dim3(1), dim3(64), 0, stream, hist, n_expts_tot, block_ms_dev, n_block_ms,
+                     token_offs_pad);
+  int rc = af3::check_launch("expt_data/scan");
+  if (rc || max_tiles == 0) return rc;
+  hipLaunchKernelGGL(tile_map_kernel, dim3((unsigned)af3_cdiv(max_tiles, 256), n_block_ms), dim3(256), 0, stream,
+                     token_offs_pad, n_expts_tot, max_tiles, block_pid_map);
+  return af3::check_launch("expt_data/map");
+}

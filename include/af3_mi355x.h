@@ -1,0 +1,131 @@
+/*
+ * af3_mi355x.h — C ABI of libaf3_mi355x.so, the gfx950 (MI355X) HIP
+ * implementation of agent-factory-3's MXFP4 MoE expert hot path.
+ *
+ * Conventions (every entry point):
+ *   - pointers are device pointers; bf16 tensors are passed as uint16_t* bit
+ *     patterns; MXFP4 weights as packed uint8 blocks + uint8 e8m0 scales;
+ *   - `stream` is a hipStream_t (torch.cuda.current_stream().cuda_stream);
+ *     work is enqueued on it, nothing synchronises the host;
+ *   - the library never allocates, frees or keeps pointers: callers own all
+ *     outputs and workspaces;
+ *   - return 0 on success, a negative value for an argument error, or a
+ *     positive hipError_t; af3_last_error() gives the message (per thread).
+ *
+ * Reference citations are file:line in ycchen-tw/agent-factory-3,
+ * src/agent_factory_3/models/gpt_oss/.
+ */
+#ifndef AF3_MI355X_H
+#define AF3_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ABI version (1). */
+int af3_abi_version(void);
+
+/* Message of the last failing call on this host thread. */
+const char* af3_last_error(void);
+
+/* MXFP4 -> bf16.  Replaces kernels.py:206-235 (mxfp4_to_bf16_triton) and the
+ * quantization.py:89-99 wrapper mxfp4_to_bf16.  blocks [n_groups][16] u8,
+ * scales [n_groups] u8, out [n_groups][32] bf16; bit-exact with
+ * kernels.py:120-158 for every (nibble, scale) pair. */
+int af3_mxfp4_to_bf16(const uint8_t* blocks, const uint8_t* scales, uint16_t* out, int64_t n_groups,
+                      void* stream);
+
+/* Clamped SwiGLU forward.  Replaces kernels.py:451-490 (_swiglu_forward_triton).
+ * gate_up [M][ld_in] interleaved (gate even, up odd), out [M][ld_out];
+ * gate_save/up_save (both or neither) receive the clamped gate/up. */
+int af3_swiglu_fwd(const uint16_t* gate_up, int64_t ld_in, uint16_t* out, int64_t ld_out, uint16_t* gate_save,
+                   uint16_t* up_save, int64_t ld_save, int64_t M, int64_t N, float alpha, float limit,
+                   void* stream);
+
+/* Clamped SwiGLU backward from saved clamped gate/up.  Replaces
+ * kernels.py:556-582 (_swiglu_backward); grad_gu [M][ld_gu] interleaved. */
+int af3_swiglu_bwd(const uint16_t* grad_out, int64_t ld_grad, const uint16_t* gate, const uint16_t* up,
+                   int64_t ld_save, uint16_t* grad_gu, int64_t ld_gu, int64_t M, int64_t N, float alpha,
+                   float limit, void* stream);
+
+/* Same backward from the raw interleaved pre-activation (clamps internally);
+ * used by SwiGLUFunction (quantization.py:424-444) so the forward need not
+ * store gate/up. */
+int af3_swiglu_bwd_raw(const uint16_t* grad_out, int64_t ld_grad, const uint16_t* gate_up, int64_t ld_in,
+                       uint16_t* grad_gu, int64_t ld_gu, int64_t M, int64_t N, float alpha, float limit,
+                       void* stream);
+
+/* Workspace bytes needed by af3_routing_replay / af3_routing_topk. */
+size_t af3_routing_workspace_bytes(int64_t n_tokens, int n_expts_tot, int n_expts_act);
+
+/* Routing from given expert ids.  Replaces quantization.py:593-636
+ * (routing_replay).  logits [T][ld] bf16, expt_indx [T][K] int32 ->
+ * gate_scal [T*K] bf16 (softmax over the K gathered logits, expert-sorted),
+ * hist [E], topk_indx [T*K] (sorted row -> flat t*K+j), gate_indx [T*K]
+ * (flat -> sorted row), token_offs_raw [E+1].  Ids outside [0,E) are dropped
+ * (gate_indx = -1, trailing sorted slots topk_indx = -1). */
+int af3_routing_replay(const uint16_t* logits, int64_t ld_logits, const int32_t* expt_indx, int64_t n_tokens,
+                       int n_expts_tot, int n_expts_act, uint16_t* gate_scal, int32_t* hist, int32_t* topk_indx,
+                       int32_t* gate_indx, int32_t* token_offs_raw, void* workspace, size_t ws_bytes,
+                       void* stream);
+
+/* Top-K routing.  Replaces triton_kernels.routing.routing as called at
+ * quantization.py:651,664 (torch restatement: routing_torch_dist,
+ * quantization.py:551-590 at world size 1).  Same outputs as above. */
+int af3_routing_topk(const uint16_t* logits, int64_t ld_logits, int64_t n_tokens, int n_expts_tot,
+                     int n_expts_act, uint16_t* gate_scal, int32_t* hist, int32_t* topk_indx, int32_t* gate_indx,
+                     int32_t* token_offs_raw, void* workspace, size_t ws_bytes, void* stream);
+
+/* Tile metadata.  Replaces triton_kernels.routing.compute_expt_data_torch
+ * (quantization.py:588,627).  block_ms_dev [n_block_ms] (device) ->
+ * token_offs_pad [n_block_ms][E+1], block_pid_map [n_block_ms][max_tiles]
+ * with entries (block << 16) | expert or -1. */
+int af3_expt_data(const int32_t* hist, int n_expts_tot, const int32_t* block_ms_dev, int n_block_ms, int max_tiles,
+                  int32_t* token_offs_pad, int32_t* block_pid_map, void* stream);
+
+/* Grouped GEMM through frozen MXFP4 expert weights, dequant fused into the
+ * tile load.  Replaces mxfp4_to_bf16 + matmul_ogs at quantization.py:358-362
+ * (trans_w = 0; forward, A6/A8) and quantization.py:409-418 (trans_w = 1;
+ * dX backward, A9/A11), without the scatter (see af3_moe_combine).
+ *   trans_w 0: Y[r][n] = sum_k X[a(r)][k] W[e][n][k],  blocks [E][N][K/32][16]
+ *   trans_w 1: Y[r][n] = sum_k X[a(r)][k] W[e][k][n],  blocks [E][K][N/32][16]
+ *   + sum_j L[r][j] Bx[e][n][j] (trans 0) / Bx[e][j][n] (trans 1)  if lora_r > 0
+ *   Y = bf16((acc + bias[e][n]) * gammas[r])   (bias fp32 [E][N], gammas bf16 or fp32)
+ * a(r) = gather_indx ? gather_indx[r] / gather_div : r; rows r of expert e
+ * are [token_offs[e], token_offs[e+1]); block_pid_map is the BM = 128 map;
+ * launches max_tiles x ceil(N/128) workgroups. */
+int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
+                 const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
+                 const void* gammas, int gammas_f32, const uint16_t* lora_l, int64_t ld_l, const uint16_t* lora_b,
+                 int lora_r, const int32_t* token_offs, const int32_t* block_pid_map, int max_tiles, int n_expts,
+                 int N, int K, uint16_t* y, int64_t ldy, void* stream);
+
+/* Scatter-sum over each token's K expert rows (the k-reduction matmul_ogs
+ * performs for scatter_indx, quantization.py:532-541 and 409-418):
+ * out[t] = bf16(sum_j rows[src_indx[t*K+j]]) in fp32; -1 entries skipped. */
+int af3_moe_combine(const uint16_t* rows, int64_t ld_rows, const int32_t* src_indx, int64_t n_tokens, int K, int N,
+                    uint16_t* out, int64_t ld_out, void* stream);
+
+/* Expert-LoRA skinny row product (no counterpart in the reference, which has
+ * no expert LoRA; convention dW = scale * B @ A of model_trainer.py:665,711):
+ *   trans_b 0: out[r][j] = scale * sum_k X[a(r)][k] Wl[e][j][k]
+ *   trans_b 1: out[r][j] = scale * sum_k X[a(r)][k] Wl[e][k][j]        */
+int af3_lora_rows(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div, const uint16_t* wl,
+                  int trans_b, float scale, const int32_t* token_offs, const int32_t* block_pid_map, int max_tiles,
+                  int n_expts, int n_out, int K, uint16_t* out, int64_t ld_out, void* stream);
+
+/* Expert-LoRA weight gradient over each expert's rows (no counterpart in the
+ * reference):  G[e][m][n] = scale * sum_{r in rows(e)} rs(r) A[a(r)][m] B[b(r)][n]
+ * rs = optional bf16 per-row multiplier; G bf16 [E][M][N]. */
+int af3_lora_wgrad(const uint16_t* a, int64_t lda, const int32_t* a_gather, int a_div, const uint16_t* a_rowscale,
+                   const uint16_t* b, int64_t ldb, const int32_t* b_gather, int b_div, float scale,
+                   const int32_t* token_offs, int n_expts, int M, int N, uint16_t* g, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AF3_MI355X_H */

@@ -1,0 +1,90 @@
+"""PyTorch-eager CPU baseline of the MoE expert layer (reported baseline, not the target).
+
+The reference's eager path restated for the CPU: transformers-style MXFP4
+dequant (LUT + ldexp, quantization.py:137-163) of every expert's weights,
+then the per-expert bf16 matmul loop of GptOssExperts.forward
+(transformers/models/gpt_oss/modeling_gpt_oss.py, expert loop over routed
+tokens) with gpt-oss's clamped SwiGLU, the expert-LoRA deltas, and torch
+autograd for the backward.  Test/bench infrastructure only.
+
+``run_sample`` times a bounded sample (the rows of a few experts, fwd + bwd,
+plus the dequant of those experts) and scales it to the whole layer:
+    t_layer = t_dequant_per_expert * E * 2   (forward and backward re-dequant,
+                                              as DequantMoEMatmul does)
+            + t_loop_per_row * T * K
+"""
+from __future__ import annotations
+
+import os
+import time
+
+import torch
+
+from . import mxfp4 as _mx
+
+ALPHA, LIMIT = 1.702, 7.0
+
+
+def _swiglu(gu):
+    gate, up = gu[..., 0::2], gu[..., 1::2]
+    gate = gate.clamp(max=LIMIT)
+    up = up.clamp(min=-LIMIT, max=LIMIT)
+    return (up + 1) * (gate * torch.sigmoid(gate * ALPHA))
+
+
+def threads() -> int:
+    n = len(os.sched_getaffinity(0))
+    cap = int(os.environ.get("OMP_NUM_THREADS", n))
+    return max(1, min(n, cap, 16))
+
+
+def run_sample(inp, ranks=(0, 10, 60, 110)) -> dict:
+    """inp: workloads.LayerInputs on the CPU.  ``ranks`` picks sample experts by popularity."""
+    torch.set_num_threads(threads())
+    E = inp.gu_blocks.shape[0]
+    K = inp.k
+    ids = inp.expt_indx.long()
+    hist = torch.bincount(ids.flatten(), minlength=E)
+    order = torch.argsort(-hist, stable=True)
+    experts = [int(order[r]) for r in ranks if r < E and int(hist[order[r]]) > 0]
+    T, H = inp.x.shape
+    gam = torch.softmax(torch.take_along_dim(inp.logits, ids, 1), dim=-1)
+    lora = inp.lora
+    s = (lora["alpha"] / lora["r"]) if lora else 0.0
+
+    # dequant of the sample experts (both projections)
+    t0 = time.perf_counter()
+    W = {}
+    for e in experts:
+        W[e] = (_mx.dequant_lut_ldexp(inp.gu_blocks[e], inp.gu_scales[e]),
+                _mx.dequant_lut_ldexp(inp.dn_blocks[e], inp.dn_scales[e]))
+    t_deq = (time.perf_counter() - t0) / max(1, len(experts))
+
+    # per-expert loop, forward + backward (torch autograd), bf16 eager
+    rows = 0
+    t0 = time.perf_counter()
+    for e in experts:
+        tok, slot = torch.nonzero(ids == e, as_tuple=True)
+        rows += tok.numel()
+        xe = inp.x[tok].clone().requires_grad_(True)
+        Wgu, Wdn = W[e]
+        params = []
+        gu = xe @ Wgu.T + inp.gu_bias[e]
+        if lora:
+            A, B = (lora["Agu"][e].clone().requires_grad_(True), lora["Bgu"][e].clone().requires_grad_(True))
+            params += [A, B]
+            gu = gu + ((xe @ A.T) @ B.T) * s
+        act = _swiglu(gu)
+        y = act @ Wdn.T + inp.dn_bias[e]
+        if lora:
+            A2, B2 = (lora["Adn"][e].clone().requires_grad_(True), lora["Bdn"][e].clone().requires_grad_(True))
+            params += [A2, B2]
+            y = y + ((act @ A2.T) @ B2.T) * s
+        y = y * gam[tok, slot, None]
+        y.backward(inp.dy[tok])
+    t_loop = time.perf_counter() - t0
+    per_row = t_loop / max(1, rows)
+    t_layer = t_deq * E * 2 + per_row * T * K
+    return dict(tokens_per_s=T / t_layer, t_layer_s=t_layer, dequant_s_per_expert=t_deq,
+                loop_s_per_row=per_row, sample_experts=experts, sample_rows=rows, threads=torch.get_num_threads(),
+                sample_wall_s=t_deq * len(experts) + t_loop)

@@ -1,0 +1,148 @@
+"""Grouped GEMM / combine / expert-LoRA HIP kernels vs the oracle (A6, A8, A9, A11, A13)."""
+import pytest
+import torch
+
+from agent_factory_3_amd import quantization as Q
+from agent_factory_3_amd import routing as R
+from oracle import moe, mxfp4
+from oracle import routing as O
+
+pytestmark = pytest.mark.gpu
+RTOL, ATOL = 2e-2, 1e-2
+
+
+def _close(gpu, ref, rtol=RTOL, atol=ATOL):
+    a, b = gpu.float().cpu().double(), ref.float().double()
+    ok = (a - b).abs() <= atol + rtol * b.abs()
+    return bool(ok.all()), float((~ok).float().mean())
+
+
+def _problem(T=300, E=6, K=4, H=128, N=192, seed=0, scale_lo=118, scale_hi=124, skew=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    logits = torch.randn(T, E, generator=g).to(torch.bfloat16)
+    if skew:  # expert 0 popular (>128 rows), expert E-1 idle
+        logits[:, 0] += 3.0
+        logits[:, E - 1] -= 50.0
+    blocks = torch.randint(0, 256, (E, N, H // 32, 16), generator=g).to(torch.uint8)
+    scales = torch.randint(scale_lo, scale_hi + 1, (E, N, H // 32), generator=g).to(torch.uint8)
+    bias = (torch.randn(E, N, generator=g) * 0.1).to(torch.bfloat16)
+    return g, x, logits, blocks, scales, bias
+
+
+def _route(logits, K, dev):
+    ref = O.routing_topk(logits, K)
+    out = R.routing(logits.to(dev), K)
+    return ref, out
+
+
+def test_gate_up_forward_gather_bias(dev):
+    g, x, logits, blocks, scales, bias = _problem()
+    ref, (rd, gi, si) = _route(logits, 4, dev)
+    assert int(ref["hist"][0]) > 128 and int(ref["hist"][-1]) == 0
+    y = Q.moe_rows(x.to(dev), blocks.to(dev), scales.to(dev), bias.float().to(dev), rd, gi)
+    W = mxfp4.dequant_f32(blocks, scales)
+    yr = moe.rows(x, W, ref["offs"], ref["topk_indx"], 4, bias=bias)
+    ok, frac = _close(y, yr)
+    assert ok, frac
+
+
+def test_down_forward_gammas_and_combine(dev):
+    g, x, logits, blocks, scales, bias = _problem(H=192, N=128, seed=1)
+    K = 4
+    ref, (rd, gi, si) = _route(logits, K, dev)
+    R_ = x.shape[0] * K
+    act = torch.randn(R_, 192, generator=g).to(torch.bfloat16)
+    y = Q.matmul_ogs(act.to(dev), (blocks.to(dev), scales.to(dev)), bias.float().to(dev), rd, None, si,
+                     rd.gate_scal)
+    W = mxfp4.dequant_f32(blocks, scales)
+    yr = moe.rows(act, W, ref["offs"], None, 1, bias=bias, gammas=ref["gate_scal"])
+    ok, frac = _close(y, moe.combine(yr, ref["gate_indx"], K))
+    assert ok, frac
+
+
+@pytest.mark.parametrize("gather", [True, False])
+def test_dgrad_transposed_weights(dev, gather):
+    g, x, logits, blocks, scales, bias = _problem(H=160, N=224, seed=2)  # W [E, 224, 160]
+    K = 4
+    ref, (rd, gi, si) = _route(logits, K, dev)
+    R_ = x.shape[0] * K
+    rows_in = torch.randn(x.shape[0] if gather else R_, 224, generator=g).to(torch.bfloat16)
+    gam = rd.gate_scal if gather else None
+    y = Q.moe_rows(rows_in.to(dev), blocks.to(dev), scales.to(dev), None, rd, gi if gather else None, gam,
+                   trans_w=True)
+    W = mxfp4.dequant_f32(blocks, scales)
+    yr = moe.rows(rows_in, W, ref["offs"], ref["topk_indx"] if gather else None, K,
+                  gammas=ref["gate_scal"] if gather else None, trans=True)
+    assert y.shape == (R_, 160)
+    ok, frac = _close(y, yr)
+    assert ok, frac
+
+
+@pytest.mark.parametrize("trans", [False, True])
+def test_lora_extension_segment(dev, trans):
+    g, x, logits, blocks, scales, bias = _problem(H=128, N=192, seed=3)
+    K, r = 4, 16
+    ref, (rd, gi, si) = _route(logits, K, dev)
+    E = blocks.shape[0]
+    W = mxfp4.dequant_f32(blocks, scales)
+    L = (torch.randn(x.shape[0] * K, r, generator=g) * 0.5).to(torch.bfloat16)
+    if not trans:
+        Bx = (torch.randn(E, 192, r, generator=g) * 0.5).to(torch.bfloat16)
+        y = Q.moe_rows(x.to(dev), blocks.to(dev), scales.to(dev), bias.float().to(dev), rd, gi, None, False,
+                       L.to(dev), Bx.to(dev))
+        yr = moe.rows(x, W, ref["offs"], ref["topk_indx"], K, bias=bias, lora_l=L, lora_b=Bx)
+    else:
+        xin = torch.randn(x.shape[0], 192, generator=g).to(torch.bfloat16)
+        Ax = (torch.randn(E, r, 128, generator=g) * 0.5).to(torch.bfloat16)
+        y = Q.moe_rows(xin.to(dev), blocks.to(dev), scales.to(dev), None, rd, gi, rd.gate_scal, True,
+                       L.to(dev), Ax.to(dev))
+        yr = moe.rows(xin, W, ref["offs"], ref["topk_indx"], K, gammas=ref["gate_scal"], trans=True,
+                      lora_l=L, lora_b=Ax)
+    ok, frac = _close(y, yr)
+    assert ok, frac
+
+
+@pytest.mark.parametrize("trans,r", [(False, 16), (True, 16), (False, 32), (True, 32)])
+def test_lora_rows(dev, trans, r):
+    g, x, logits, blocks, scales, bias = _problem(seed=4)
+    K = 4
+    ref, (rd, gi, si) = _route(logits, K, dev)
+    E, Kd = blocks.shape[0], 128
+    Wl = (torch.randn(E, Kd, r, generator=g) if trans else torch.randn(E, r, Kd, generator=g)).to(torch.bfloat16)
+    out = Q._lora_rows(x.to(dev), gi.src_indx, K, Wl.to(dev), 1 if trans else 0, 2.0, rd.expt_data, r, Kd)
+    refo = moe.lora_rows(x, Wl, ref["offs"], ref["topk_indx"], K, 2.0, trans=trans)
+    ok, frac = _close(out, refo)
+    assert ok, frac
+
+
+@pytest.mark.parametrize("M,N,gather_b,rowscale", [(192, 16, False, True), (16, 128, True, False),
+                                                   (192, 32, True, True), (32, 160, False, False)])
+def test_lora_wgrad(dev, M, N, gather_b, rowscale):
+    g, x, logits, blocks, scales, bias = _problem(seed=5)
+    K = 4
+    ref, (rd, gi, si) = _route(logits, K, dev)
+    R_ = x.shape[0] * K
+    a = torch.randn(R_, M, generator=g).to(torch.bfloat16)
+    b = torch.randn(x.shape[0] if gather_b else R_, N, generator=g).to(torch.bfloat16)
+    E = blocks.shape[0]
+    rs = rd.gate_scal if rowscale else None
+    out = Q._lora_wgrad(a.to(dev), None, 1, rs, b.to(dev), gi.src_indx if gather_b else None, K if gather_b else 1,
+                        rd.expt_data, E, M, N)
+    refo = moe.wgrad(a, b, ref["offs"], a_rowscale=ref["gate_scal"] if rowscale else None,
+                     b_gather=ref["topk_indx"] if gather_b else None, b_div=K)
+    assert int(ref["hist"][-1]) == 0 and out[-1].abs().max() == 0     # idle expert -> zero gradient
+    ok, frac = _close(out, refo, rtol=RTOL, atol=5e-2)
+    assert ok, frac
+
+
+def test_dense_routing_none(dev):
+    """matmul_ogs with routing_data=None: one expert, plain GEMM."""
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(70, 64, generator=g).to(torch.bfloat16)
+    blocks = torch.randint(0, 256, (96, 2, 16), generator=g).to(torch.uint8)
+    scales = torch.randint(120, 126, (96, 2), generator=g).to(torch.uint8)
+    y = Q.matmul_ogs(x.to(dev), (blocks.to(dev), scales.to(dev)), None)
+    W = mxfp4.dequant_f32(blocks, scales)
+    ok, frac = _close(y, (x.float() @ W.T).to(torch.bfloat16))
+    assert ok, frac

@@ -1,0 +1,147 @@
+"""Expert layer through the drop-in module API (A12/A13) vs the oracle.
+
+Stage-wise parity uses identical inputs per stage; the end-to-end checks use a
+well-conditioned scale range so that bf16 rounding of the pre-activation does
+not move values across the clamp boundary.
+"""
+from pathlib import Path
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from agent_factory_3_amd import quantization as Q
+from agent_factory_3_amd import routing as R
+from agent_factory_3_amd import workloads
+from oracle import moe, mxfp4
+from oracle import routing as O
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).parent / "golden" / "tiny_moe.npz"
+
+
+def _rel(a, b):
+    a, b = a.float().cpu().double(), b.float().cpu().double()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def _frac_bad(gpu, ref, rtol=2e-2, atol=1e-2):
+    a, b = gpu.float().cpu().double(), ref.float().double()
+    return float(((a - b).abs() > atol + rtol * b.abs()).float().mean())
+
+
+def _params(inp):
+    return dict(Wgu=mxfp4.dequant_f32(inp.gu_blocks, inp.gu_scales), bgu=inp.gu_bias,
+                Wdn=mxfp4.dequant_f32(inp.dn_blocks, inp.dn_scales), bdn=inp.dn_bias)
+
+
+def _run_module(inp, dev, lora):
+    m = workloads.make_experts(inp if lora else _strip_lora(inp), dev)
+    rd, gi, si = R.routing_replay(inp.logits.to(dev), inp.expt_indx.to(dev), inp.k)
+    x = inp.x.to(dev).requires_grad_(True)
+    y = m(x, rd, gi, si)
+    y.backward(inp.dy.to(dev))
+    return m, x, y
+
+
+def _strip_lora(inp):
+    return workloads.LayerInputs(inp.x, inp.logits, inp.expt_indx, inp.gu_blocks, inp.gu_scales, inp.gu_bias,
+                                 inp.dn_blocks, inp.dn_scales, inp.dn_bias, inp.dy, None, inp.k)
+
+
+@pytest.mark.parametrize("lora", [False, True])
+def test_layer_fwd_bwd_matches_oracle(dev, lora):
+    inp = workloads.layer(3, T=256, E=6, H=128, I=96, lora_r=16, scale_lo=118, scale_hi=121, zipf=False)
+    inp.lora = dict(inp.lora, Bgu=inp.lora["Bgu"] * 30, Bdn=inp.lora["Bdn"] * 30)  # make the LoRA term visible
+    m, x, y = _run_module(inp, dev, lora)
+    rt = O.routing_replay(inp.logits, inp.expt_indx, inp.k)
+    p = _params(inp)
+    lo = None
+    if lora:
+        lo = dict(Agu=inp.lora["Agu"], Bgu=inp.lora["Bgu"], Adn=inp.lora["Adn"], Bdn=inp.lora["Bdn"],
+                  s=inp.lora["alpha"] / inp.lora["r"])
+    st = moe.layer_forward(inp.x, p, rt, inp.k, lora=lo)
+    gr = moe.layer_backward(inp.x, p, rt, inp.k, st, inp.dy, lora=lo)
+    assert _rel(y, st["Y"]) < 1e-2 and _frac_bad(y, st["Y"]) < 1e-3
+    assert _rel(x.grad, gr["dX"]) < 2e-2 and _frac_bad(x.grad, gr["dX"]) < 1e-2
+    if lora:
+        for pn, key in (("gate_up_proj_lora_A", "dAgu"), ("gate_up_proj_lora_B", "dBgu"),
+                        ("down_proj_lora_A", "dAdn"), ("down_proj_lora_B", "dBdn")):
+            assert _rel(getattr(m, pn).grad, gr[key]) < 3e-2, pn
+
+
+def test_stagewise_official_distribution(dev):
+    """cfg3-shaped scales/codes (saturating SwiGLU): each stage on identical inputs."""
+    inp = workloads.layer(3, T=512, E=8, H=128, I=128, lora_r=0, zipf=False)
+    rt = O.routing_replay(inp.logits, inp.expt_indx, 4)
+    rd, gi, si = R.routing_replay(inp.logits.to(dev), inp.expt_indx.to(dev), 4)
+    p = _params(inp)
+    gu = Q.moe_rows(inp.x.to(dev), inp.gu_blocks.to(dev), inp.gu_scales.to(dev), inp.gu_bias.float().to(dev), rd,
+                    gi)
+    gu_ref = moe.rows(inp.x, p["Wgu"], rt["offs"], rt["topk_indx"], 4, bias=inp.gu_bias)
+    assert _frac_bad(gu, gu_ref) == 0.0
+    act = Q.SwiGLUFunction.apply(gu, 1.702, 7.0)
+    from oracle import swiglu
+    assert _frac_bad(act, swiglu.forward(gu.cpu())[0]) == 0.0
+    y = Q.matmul_ogs(act, (inp.dn_blocks.to(dev), inp.dn_scales.to(dev)), inp.dn_bias.float().to(dev), rd, None,
+                     si, rd.gate_scal)
+    y_ref = moe.combine(moe.rows(act.cpu(), p["Wdn"], rt["offs"], None, 1, bias=inp.dn_bias,
+                                 gammas=rt["gate_scal"]), rt["gate_indx"], 4)
+    assert _frac_bad(y, y_ref) == 0.0
+    dact = Q.moe_rows(inp.dy.to(dev), inp.dn_blocks.to(dev), inp.dn_scales.to(dev), None, rd, gi, rd.gate_scal,
+                      trans_w=True)
+    dact_ref = moe.rows(inp.dy, p["Wdn"], rt["offs"], rt["topk_indx"], 4, gammas=rt["gate_scal"], trans=True)
+    assert _frac_bad(dact, dact_ref) == 0.0
+    dx = Q.matmul_ogs(dact, (inp.gu_blocks.to(dev), inp.gu_scales.to(dev)), None, rd, None, si, None, trans_w=True)
+    dx_ref = moe.combine(moe.rows(dact.cpu(), p["Wgu"], rt["offs"], None, 1, trans=True), rt["gate_indx"], 4)
+    assert _frac_bad(dx, dx_ref) == 0.0
+
+
+def test_golden_tiny_layer(dev):
+    z = np.load(GOLDEN, allow_pickle=False)
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16)  # noqa: E731
+    inp = workloads.LayerInputs(bf(z["x"]), bf(z["logits"]), torch.from_numpy(z["ids"]),
+                                torch.from_numpy(z["gu_blocks"]), torch.from_numpy(z["gu_scales"]), bf(z["gu_bias"]),
+                                torch.from_numpy(z["dn_blocks"]), torch.from_numpy(z["dn_scales"]), bf(z["dn_bias"]),
+                                bf(z["dy"]), None, 2)
+    m, x, y = _run_module(inp, dev, False)
+    Y, dX = torch.from_numpy(z["Y"]), torch.from_numpy(z["dX"])
+    rms = float(Y.pow(2).mean().sqrt())
+    assert ((y.float().cpu().double() - Y).abs() <= 2e-2 * Y.abs() + 2e-2 * rms).all()
+    assert _rel(x.grad, dX) < 2e-2
+
+
+def test_mlp_forward_topk_and_replay(dev):
+    inp = workloads.layer(2, T=64, E=8, H=64, I=64, lora_r=0, zipf=False, scale_lo=120, scale_hi=123)
+    experts = workloads.make_experts(inp, dev)
+    g = torch.Generator().manual_seed(1)
+    router = SimpleNamespace(hidden_dim=64, top_k=4,
+                             weight=(torch.randn(8, 64, generator=g) * 0.2).to(torch.bfloat16).to(dev),
+                             bias=torch.zeros(8, dtype=torch.bfloat16, device=dev))
+    mlp = SimpleNamespace(router=router, experts=experts)
+    hs = inp.x.view(2, 32, 64).to(dev)
+    out, logits = Q.mlp_forward(mlp, hs)
+    ids = O.topk_ids(logits.cpu(), 4)[0]
+    out2, _ = Q.mlp_forward(mlp, hs, router_indices=ids.view(2, 32, 4).to(dev))
+    assert out.shape == (2, 32, 64) and torch.equal(out, out2)
+    rt = O.routing_topk(logits.cpu(), 4)
+    ref = moe.layer_forward(inp.x, _params(inp), rt, 4)["Y"]
+    assert _rel(out.view(64, 64), ref) < 1e-2
+
+
+def test_dequant_matmul_function_without_module(dev):
+    inp = workloads.layer(2, T=64, E=4, H=64, I=64, lora_r=0, zipf=False, scale_lo=120, scale_hi=123)
+    rd, gi, si = R.routing_replay(inp.logits.to(dev), inp.expt_indx.to(dev), 4)
+    x = inp.x.to(dev).requires_grad_(True)
+    y = Q.DequantMoEMatmul.apply(x, inp.gu_blocks.to(dev), inp.gu_scales.to(dev), inp.gu_bias.float().to(dev), rd,
+                                 gi, None, None, None, si, None, "bf16", 4, None, None)
+    dy = torch.randn(y.shape, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16)
+    y.backward(dy.to(dev))
+    rt = O.routing_replay(inp.logits, inp.expt_indx, 4)
+    W = mxfp4.dequant_f32(inp.gu_blocks, inp.gu_scales)
+    dxr = moe.rows(dy, W, rt["offs"], None, 1, trans=True)
+    assert _rel(x.grad, moe.combine(dxr, rt["gate_indx"], 4)) < 1e-2
+    with pytest.raises(NotImplementedError):
+        Q.DequantMoEMatmul.apply(x, inp.gu_blocks.to(dev), inp.gu_scales.to(dev), None, rd, gi, None, None, None,
+                                 si, None, "fp8", 4, None, None)

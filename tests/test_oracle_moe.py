@@ -1,0 +1,104 @@
+"""Pins oracle.moe (CPU): per-expert loops vs float64 dense math and autograd."""
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from oracle import moe, mxfp4, routing
+
+GOLDEN = Path(__file__).parent / "golden" / "tiny_moe.npz"
+
+
+def _bf16(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16)
+
+
+def _rel(a, b):
+    a, b = a.double(), b.double()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def _tiny():
+    z = np.load(GOLDEN, allow_pickle=False)
+    p = dict(Wgu=mxfp4.dequant_f32(z["gu_blocks"], z["gu_scales"]), bgu=_bf16(z["gu_bias"]),
+             Wdn=mxfp4.dequant_f32(z["dn_blocks"], z["dn_scales"]), bdn=_bf16(z["dn_bias"]))
+    return z, p
+
+
+def test_oracle_layer_matches_golden_dense_math():
+    z, p = _tiny()
+    x, logits, dy = _bf16(z["x"]), _bf16(z["logits"]), _bf16(z["dy"])
+    ids = torch.from_numpy(z["ids"])
+    rt = routing.routing_replay(logits, ids, 2)
+    st = moe.layer_forward(x, p, rt, 2)
+    g = moe.layer_backward(x, p, rt, 2, st, dy)
+    Y, dX = torch.from_numpy(z["Y"]), torch.from_numpy(z["dX"])
+    assert _rel(st["Y"], Y) < 1e-2
+    # bf16 rounding of the intermediates: error relative to the output's scale
+    rms = float(Y.pow(2).mean().sqrt())
+    assert ((st["Y"].double() - Y).abs() <= 2e-2 * Y.abs() + 2e-2 * rms).all()
+    assert _rel(g["dX"], dX) < 2e-2
+
+
+def _rand_layer(seed=1, T=40, H=64, I=64, E=5, K=2, r=8):
+    gen = torch.Generator().manual_seed(seed)
+    bl = lambda *s: torch.randint(0, 256, s, generator=gen).to(torch.uint8)  # noqa: E731
+    sc = lambda *s: torch.randint(121, 125, s, generator=gen).to(torch.uint8)  # noqa: E731
+    p = dict(Wgu=mxfp4.dequant_f32(bl(E, 2 * I, H // 32, 16), sc(E, 2 * I, H // 32)),
+             bgu=(torch.randn(E, 2 * I, generator=gen) * 0.1).to(torch.bfloat16),
+             Wdn=mxfp4.dequant_f32(bl(E, H, I // 32, 16), sc(E, H, I // 32)),
+             bdn=(torch.randn(E, H, generator=gen) * 0.1).to(torch.bfloat16))
+    x = torch.randn(T, H, generator=gen).to(torch.bfloat16)
+    logits = torch.randn(T, E, generator=gen).to(torch.bfloat16)
+    dy = torch.randn(T, H, generator=gen).to(torch.bfloat16)
+    lora = dict(Agu=(torch.randn(E, r, H, generator=gen) * 0.3).to(torch.bfloat16),
+                Bgu=(torch.randn(E, 2 * I, r, generator=gen) * 0.3).to(torch.bfloat16),
+                Adn=(torch.randn(E, r, I, generator=gen) * 0.3).to(torch.bfloat16),
+                Bdn=(torch.randn(E, H, r, generator=gen) * 0.3).to(torch.bfloat16), s=2.0)
+    return p, x, logits, dy, lora
+
+
+def _autograd_dense(p, x, logits, dy, lora, K):
+    ids, scal = routing.topk_ids(logits, K)
+    leaves = {k: v.double().requires_grad_(True) for k, v in lora.items() if k != "s"}
+    xd = x.double().requires_grad_(True)
+    Y = moe.dense_reference(xd, p, ids, scal, lora=dict(leaves, s=lora["s"]))
+    Y.backward(dy.double())
+    return Y.detach(), xd.grad, {k: v.grad for k, v in leaves.items()}
+
+
+def test_oracle_lora_layer_formulas_exact_in_float64():
+    """With float64 intermediates the sorted/per-expert oracle equals float64
+    autograd of the dense layer to rounding: pins every gradient formula."""
+    p, x, logits, dy, lora = _rand_layer()
+    K = 2
+    rt = routing.routing_topk(logits, K)
+    st = moe.layer_forward(x, p, rt, K, lora=lora, rd=torch.float64)
+    g = moe.layer_backward(x, p, rt, K, st, dy, lora=lora, rd=torch.float64)
+    Y, dX, grads = _autograd_dense(p, x, logits, dy, lora, K)
+    assert _rel(st["Y"], Y) < 1e-12
+    assert _rel(g["dX"], dX) < 1e-12
+    for name, key in (("dAgu", "Agu"), ("dBgu", "Bgu"), ("dAdn", "Adn"), ("dBdn", "Bdn")):
+        assert _rel(g[name], grads[key]) < 1e-12, name
+
+
+def test_oracle_lora_layer_bf16_close_to_exact():
+    """bf16 intermediates (the GPU's rounding points) stay near the exact math;
+    the clamp boundary amplifies rounding, hence the loose bound."""
+    p, x, logits, dy, lora = _rand_layer()
+    K = 2
+    rt = routing.routing_topk(logits, K)
+    st = moe.layer_forward(x, p, rt, K, lora=lora)
+    g = moe.layer_backward(x, p, rt, K, st, dy, lora=lora)
+    Y, dX, grads = _autograd_dense(p, x, logits, dy, lora, K)
+    assert _rel(st["Y"], Y) < 1e-2
+    assert _rel(g["dX"], dX) < 0.1
+    for name, key in (("dAgu", "Agu"), ("dBgu", "Bgu"), ("dAdn", "Adn"), ("dBdn", "Bdn")):
+        assert _rel(g[name], grads[key]) < 0.1, name
+
+
+def test_combine_skips_dropped_slots():
+    rows = torch.arange(12, dtype=torch.float32).view(6, 2).to(torch.bfloat16)
+    gi = torch.tensor([5, -1, 0, 2, 1, 3], dtype=torch.int32)
+    out = moe.combine(rows, gi, 2)
+    assert out.float().tolist() == [[10.0, 11.0], [4.0, 6.0], [8.0, 10.0]]
