@@ -20,6 +20,10 @@ BF16 = torch.bfloat16
 F32 = torch.float32
 
 
+def _rnd(t, rd):
+    return t.to(rd) if rd == torch.float64 else t.to(F32).to(rd)
+
+
 def rows(x, W, offs, gather=None, k=1, bias=None, gammas=None, trans=False, lora_l=None, lora_b=None, rd=BF16):
     """Expert-sorted bf16 rows.
 
@@ -86,7 +90,7 @@ def lora_rows(x, A_or_B, offs, gather=None, k=1, scale=1.0, trans=False, rd=BF16
 
 
 def wgrad(a, b, offs, a_gather=None, a_div=1, a_rowscale=None, b_gather=None, b_div=1, rd=BF16):
-    """G[e] = sum_{r in e} (rs[r] * a[a(r)])^T b[b(r)]  -> bf16 [E, Ma, Nb]."""
+    """G[e] = sum_{r in e} bf16(rs[r] * a[a(r)])^T b[b(r)]  -> bf16 [E, Ma, Nb]."""
     E = offs.numel() - 1
     acc = torch.float64 if rd == torch.float64 else F32
     af, bf = a.to(acc), b.to(acc)
@@ -99,13 +103,11 @@ def wgrad(a, b, offs, a_gather=None, a_div=1, a_rowscale=None, b_gather=None, b_
         ib = (b_gather[lo:hi].long() // b_div) if b_gather is not None else torch.arange(lo, hi)
         ae = af[ia]
         if a_rowscale is not None:
-            ae = ae * a_rowscale[lo:hi, None].to(acc)
+            # the row-scaled operand is a bf16 tensor (the product rounds it
+            # before the matrix core, as autograd of a bf16 multiply does)
+            ae = _rnd(ae * a_rowscale[lo:hi, None].to(acc), rd).to(acc)
         G[e] = ae.T @ bf[ib]
     return G.to(rd)
-
-
-def _rnd(t, rd):
-    return t.to(rd) if rd == torch.float64 else t.to(F32).to(rd)
 
 
 def layer_forward(x, p, rt, k, alpha=_sw.ALPHA, limit=_sw.LIMIT, lora=None, rd=BF16):

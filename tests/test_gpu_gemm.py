@@ -11,6 +11,26 @@ pytestmark = pytest.mark.gpu
 RTOL, ATOL = 2e-2, 1e-2
 
 
+
+def _frac_bad_combined(gpu, ref_rows, gate_indx, k, rtol=2e-2, atol=1e-2):
+    """Combined (k-summed) outputs: the rows are rounded to bf16 before the sum
+    (matmul_ogs' scatter), so a one-ulp row difference may dominate a sum that
+    cancels; allow two bf16 ulps (2^-7 relative) of each contributing row."""
+    gi = gate_indx.view(-1, k).long()
+    rr = ref_rows.float().double().abs()
+    slack = torch.zeros(gi.shape[0], rr.shape[1], dtype=torch.float64)
+    for j in range(k):
+        ok = gi[:, j] >= 0
+        slack[ok] += rr[gi[ok, j]]
+    ref = torch.zeros_like(slack)
+    rf = ref_rows.float().double()
+    for j in range(k):
+        ok = gi[:, j] >= 0
+        ref[ok] += rf[gi[ok, j]]
+    a = gpu.detach().float().cpu().double()
+    bad = (a - ref).abs() > atol + rtol * ref.abs() + 2.0 ** -7 * slack
+    return float(bad.float().mean())
+
 def _close(gpu, ref, rtol=RTOL, atol=ATOL):
     a, b = gpu.float().cpu().double(), ref.float().double()
     ok = (a - b).abs() <= atol + rtol * b.abs()
@@ -57,8 +77,11 @@ def test_down_forward_gammas_and_combine(dev):
                      rd.gate_scal)
     W = mxfp4.dequant_f32(blocks, scales)
     yr = moe.rows(act, W, ref["offs"], None, 1, bias=bias, gammas=ref["gate_scal"])
-    ok, frac = _close(y, moe.combine(yr, ref["gate_indx"], K))
-    assert ok, frac
+    assert _frac_bad_combined(y, yr, ref["gate_indx"], K) == 0.0
+    # the combine kernel alone, on identical rows: fp32 sum of bf16 rows, one rounding
+    rows_dev = Q.moe_rows(act.to(dev), blocks.to(dev), scales.to(dev), bias.float().to(dev), rd, None, rd.gate_scal)
+    out = Q.moe_combine(rows_dev, si, K)
+    assert torch.equal(out.cpu(), moe.combine(rows_dev.cpu(), ref["gate_indx"], K))
 
 
 @pytest.mark.parametrize("gather", [True, False])

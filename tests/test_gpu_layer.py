@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 import torch
 
+from agent_factory_3_amd import kernels
 from agent_factory_3_amd import quantization as Q
 from agent_factory_3_amd import routing as R
 from agent_factory_3_amd import workloads
@@ -21,8 +22,28 @@ pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).parent / "golden" / "tiny_moe.npz"
 
 
+
+def _frac_bad_combined(gpu, ref_rows, gate_indx, k, rtol=2e-2, atol=1e-2):
+    """Combined (k-summed) outputs: the rows are rounded to bf16 before the sum
+    (matmul_ogs' scatter), so a one-ulp row difference may dominate a sum that
+    cancels; allow two bf16 ulps (2^-7 relative) of each contributing row."""
+    gi = gate_indx.view(-1, k).long()
+    rr = ref_rows.float().double().abs()
+    slack = torch.zeros(gi.shape[0], rr.shape[1], dtype=torch.float64)
+    for j in range(k):
+        ok = gi[:, j] >= 0
+        slack[ok] += rr[gi[ok, j]]
+    ref = torch.zeros_like(slack)
+    rf = ref_rows.float().double()
+    for j in range(k):
+        ok = gi[:, j] >= 0
+        ref[ok] += rf[gi[ok, j]]
+    a = gpu.detach().float().cpu().double()
+    bad = (a - ref).abs() > atol + rtol * ref.abs() + 2.0 ** -7 * slack
+    return float(bad.float().mean())
+
 def _rel(a, b):
-    a, b = a.float().cpu().double(), b.float().cpu().double()
+    a, b = a.detach().float().cpu().double(), b.detach().float().cpu().double()
     return float((a - b).norm() / b.norm().clamp_min(1e-30))
 
 
@@ -86,16 +107,17 @@ def test_stagewise_official_distribution(dev):
     assert _frac_bad(act, swiglu.forward(gu.cpu())[0]) == 0.0
     y = Q.matmul_ogs(act, (inp.dn_blocks.to(dev), inp.dn_scales.to(dev)), inp.dn_bias.float().to(dev), rd, None,
                      si, rd.gate_scal)
-    y_ref = moe.combine(moe.rows(act.cpu(), p["Wdn"], rt["offs"], None, 1, bias=inp.dn_bias,
-                                 gammas=rt["gate_scal"]), rt["gate_indx"], 4)
-    assert _frac_bad(y, y_ref) == 0.0
+    y_rows = moe.rows(act.cpu(), p["Wdn"], rt["offs"], None, 1, bias=inp.dn_bias, gammas=rt["gate_scal"])
+    assert _frac_bad_combined(y, y_rows, rt["gate_indx"], 4) == 0.0
     dact = Q.moe_rows(inp.dy.to(dev), inp.dn_blocks.to(dev), inp.dn_scales.to(dev), None, rd, gi, rd.gate_scal,
                       trans_w=True)
     dact_ref = moe.rows(inp.dy, p["Wdn"], rt["offs"], rt["topk_indx"], 4, gammas=rt["gate_scal"], trans=True)
     assert _frac_bad(dact, dact_ref) == 0.0
-    dx = Q.matmul_ogs(dact, (inp.gu_blocks.to(dev), inp.gu_scales.to(dev)), None, rd, None, si, None, trans_w=True)
-    dx_ref = moe.combine(moe.rows(dact.cpu(), p["Wgu"], rt["offs"], None, 1, trans=True), rt["gate_indx"], 4)
-    assert _frac_bad(dx, dx_ref) == 0.0
+    dgu = kernels.swiglu_backward_raw(dact, gu, 1.702, 7.0)
+    assert _frac_bad(dgu, swiglu.backward_from_raw(dact.cpu(), gu.cpu())) == 0.0
+    dx = Q.matmul_ogs(dgu, (inp.gu_blocks.to(dev), inp.gu_scales.to(dev)), None, rd, None, si, None, trans_w=True)
+    dx_rows = moe.rows(dgu.cpu(), p["Wgu"], rt["offs"], None, 1, trans=True)
+    assert _frac_bad_combined(dx, dx_rows, rt["gate_indx"], 4) == 0.0
 
 
 def test_golden_tiny_layer(dev):
