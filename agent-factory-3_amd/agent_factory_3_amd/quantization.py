@@ -135,7 +135,7 @@ def _expt_data(routing_data, n_rows, device):
     if routing_data is None:
         return dense_routing(n_rows, device), 1
     ed = routing_data.expt_data
-    if ed is None or GEMM_BLOCK_M not in getattr(ed, "block_pid_map", {}):
+    if ed is None or not all(bm in getattr(ed, "block_pid_map", {}) for bm in (GEMM_BLOCK_M, WGRAD_CHUNK)):
         ed = compute_expt_data(routing_data.expt_hist, routing_data.n_expts_tot, n_rows)
         routing_data = RoutingData(routing_data.gate_scal, routing_data.expt_hist, routing_data.n_expts_tot,
                                    routing_data.n_expts_act, ed)
@@ -319,11 +319,21 @@ def _lora_rows(x, gather, k_act, wl, trans_b, scale, ed, n_out, K):
     return out
 
 
+WGRAD_CHUNK = 512
+
+
 def _lora_wgrad(a, a_gather, a_div, a_rowscale, b, b_gather, b_div, ed, E, M, N):
-    g = torch.empty(E, M, N, dtype=torch.bfloat16, device=a.device)
+    dev = a.device
+    g = torch.empty(E, M, N, dtype=torch.bfloat16, device=dev)
+    cmap = ed.block_pid_map[WGRAD_CHUNK]
+    coffs = ed.token_offs_pad[WGRAD_CHUNK]
+    nch = cmap.numel()
+    ws_n = int(_capi.load().af3_lora_wgrad_workspace_bytes(nch, M, N))
+    ws = torch.empty(ws_n // 4, dtype=torch.float32, device=dev)
     _capi.call("af3_lora_wgrad", a.data_ptr(), a.stride(0) if a.shape[0] > 1 else M, _capi.ptr(a_gather), a_div,
                _capi.ptr(a_rowscale), b.data_ptr(), b.stride(0) if b.shape[0] > 1 else N, _capi.ptr(b_gather),
-               b_div, 1.0, ed.token_offs_raw.data_ptr(), E, M, N, g.data_ptr(), _capi.stream_of(a.device))
+               b_div, 1.0, ed.token_offs_raw.data_ptr(), E, M, N, cmap.data_ptr(), coffs.data_ptr(), nch,
+               WGRAD_CHUNK, ws.data_ptr(), ws_n, g.data_ptr(), _capi.stream_of(dev))
     return g
 
 

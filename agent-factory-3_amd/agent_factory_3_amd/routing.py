@@ -23,8 +23,9 @@ import torch
 
 from . import _capi
 
-# block sizes (rows per GEMM tile) for which tile maps are built
-BLOCK_MS = (128,)
+# block sizes for which tile maps are built: 128-row GEMM tiles and the
+# 512-row chunks of the LoRA weight-gradient reduction
+BLOCK_MS = (128, 512)
 
 
 @dataclass

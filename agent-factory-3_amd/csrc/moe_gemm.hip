@@ -65,6 +65,8 @@ struct Params {
   uint16_t* c;
   int64_t ldc;
   int64_t c_estride;        // wgrad output per-expert stride
+  int chunk_rows;           // wgrad rows per chunk
+  float* partials;          // wgrad fp32 partials [chunk][M][N]
   int M, N;                 // output extents (M used by wgrad; rows come from offs in row tiles)
 };
 
@@ -442,19 +444,25 @@ __global__ __launch_bounds__(kThreads) void rowtile_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------
-// weight-gradient kernel: G[e][m][n] = scale * sum_{r in rows(e)} A[r][m] B[r][n]
+// weight-gradient kernels: G[e][m][n] = scale * sum_{r in rows(e)} A[r][m] B[r][n]
+// Pass 1: blockIdx.x -> chunk (expert e, chunk_rows-row block b) of the
+// expert-sorted rows (the chunk map has the block_pid_map format),
+// blockIdx.y -> (m block, n block); writes the fp32 partial of its rows.
+// Pass 2: per expert, sums its chunks' partials in chunk order (deterministic).
 // ---------------------------------------------------------------------------
 template <int BM, int BN, int WM, int WN>
-__global__ __launch_bounds__(kThreads) void wgrad_kernel(Params p) {
+__global__ __launch_bounds__(kThreads) void wgrad_partial_kernel(Params p) {
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
   __shared__ __attribute__((aligned(16))) uint16_t As[BM * kBK];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[BN * kBK];
 
-  const int per_e = p.n_mblk * p.n_nblk;
-  const int e = blockIdx.x / per_e;
-  const int rem = blockIdx.x - e * per_e;
-  const int m0 = (rem / p.n_nblk) * BM, n0 = (rem % p.n_nblk) * BN;
-  const int kb = p.offs[e], kend = p.offs[e + 1] - kb;
+  const int32_t ent = p.tile_map[blockIdx.x];
+  if (ent < 0) return;
+  const int e = ent & 0xFFFF, blk = ent >> 16;
+  const int kb = p.offs[e] + blk * p.chunk_rows;
+  const int kend = min(p.chunk_rows, p.offs[e + 1] - kb);
+  if (kend <= 0) return;
+  const int m0 = (blockIdx.y / p.n_nblk) * BM, n0 = (blockIdx.y % p.n_nblk) * BN;
   const int mcols = min(BM, p.M - m0), ncols = min(BN, p.N - n0);
 
   const int wave = threadIdx.x >> 6;
@@ -474,7 +482,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(Params p) {
   run_segment<Loader<BM, COLS_BF16>, Loader<BN, COLS_BF16>, TM, TN>(la, lb, kend, As, Bs, wm0, wn0, acc);
 
   const int lane = threadIdx.x & 63;
-  uint16_t* out = p.c + e * p.c_estride;
+  float* out = p.partials + (int64_t)blockIdx.x * p.M * p.N;
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm) {
 #pragma unroll
@@ -485,10 +493,32 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(Params p) {
       for (int r = 0; r < 16; ++r) {
         const int row = wm0 + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
         if (row >= mcols) continue;
-        out[(int64_t)(m0 + row) * p.ldc + n0 + col] = (uint16_t)af3_f32_to_bf16(acc[tm][tn][r] * p.scale);
+        out[(int64_t)(m0 + row) * p.N + n0 + col] = acc[tm][tn][r];
       }
     }
   }
+}
+
+// one thread per 4 output elements of one expert
+__global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restrict__ partials,
+                                                           const int32_t* __restrict__ chunk_offs, int64_t MN,
+                                                           float scale, uint16_t* __restrict__ g) {
+  const int e = blockIdx.y;
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= MN) return;
+  const int c0 = chunk_offs[e], c1 = chunk_offs[e + 1];
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  for (int c = c0; c < c1; ++c) {
+    const float4 v = *(const float4*)(partials + (int64_t)c * MN + i);
+    a0 += v.x;
+    a1 += v.y;
+    a2 += v.z;
+    a3 += v.w;
+  }
+  uint2 o;
+  o.x = af3_pack_bf16x2(a0 * scale, a1 * scale);
+  o.y = af3_pack_bf16x2(a2 * scale, a3 * scale);
+  *(uint2*)(g + (int64_t)e * MN + i) = o;
 }
 
 // ---------------------------------------------------------------------------
@@ -654,41 +684,61 @@ extern "C" int af3_lora_rows(const uint16_t* x, int64_t ldx, const int32_t* gath
 // Per-expert weight gradient over the expert's rows:
 //   G[e][m][n] = scale * sum_{r in rows(e)} (rs(r) * A[a(r)][m]) * B[b(r)][n]
 // with a(r) = a_gather ? a_gather[r] / a_div : r (same for b) and rs the
-// optional bf16 per-row multiplier.  G is bf16 [E][M][N] row-major.
+// optional bf16 per-row multiplier.  G is bf16 [E][M][N] row-major.  The rows
+// are split into chunk_rows-row chunks described by chunk_map / chunk_offs
+// (block_pid_map / token_offs_pad of af3_expt_data for that block size); each
+// chunk writes an fp32 partial into `partials`, then the partials of an expert
+// are summed in chunk order.
+extern "C" size_t af3_lora_wgrad_workspace_bytes(int max_chunks, int M, int N) {
+  return (size_t)(max_chunks > 0 ? max_chunks : 1) * (size_t)M * (size_t)N * sizeof(float);
+}
+
 extern "C" int af3_lora_wgrad(const uint16_t* a, int64_t lda, const int32_t* a_gather, int a_div,
                               const uint16_t* a_rowscale, const uint16_t* b, int64_t ldb, const int32_t* b_gather,
                               int b_div, float scale, const int32_t* token_offs, int n_expts, int M, int N,
-                              uint16_t* g, void* stream_) {
+                              const int32_t* chunk_map, const int32_t* chunk_offs, int max_chunks, int chunk_rows,
+                              float* partials, size_t partial_bytes, uint16_t* g, void* stream_) {
   hipStream_t stream = (hipStream_t)stream_;
-  AF3_REQUIRE(M > 0 && N > 0 && n_expts > 0, "lora_wgrad: bad sizes");
-  AF3_REQUIRE(M % 8 == 0 && N % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && al16(a) && al16(b),
+  AF3_REQUIRE(M > 0 && N > 0 && n_expts > 0 && max_chunks >= 0 && chunk_rows > 0, "lora_wgrad: bad sizes");
+  AF3_REQUIRE(M % 8 == 0 && N % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && al16(a) && al16(b) && al16(g),
               "lora_wgrad: operands must be 16-byte aligned with sizes % 8 == 0");
+  AF3_REQUIRE(partial_bytes >= af3_lora_wgrad_workspace_bytes(max_chunks, M, N) && partials && al16(partials),
+              "lora_wgrad: partials workspace too small");
   Params p{};
   p.a = make_bf16(a, lda, 0, a_gather, a_div, a_rowscale);
   p.b = make_bf16(b, ldb, 0, b_gather, b_div);
   p.offs = token_offs;
+  p.tile_map = chunk_map;
   p.E = n_expts;
   p.scale = scale;
-  p.c = g;
-  p.ldc = N;
-  p.c_estride = (int64_t)M * N;
   p.M = M;
   p.N = N;
-  if (N <= 32) {  // tall output (e.g. dB: [N_out][r])
-    p.n_mblk = (M + 127) / 128;
-    p.n_nblk = 1;
-    hipLaunchKernelGGL((wgrad_kernel<128, 32, 4, 1>), dim3(n_expts * p.n_mblk), dim3(kThreads), 0, stream, p);
-  } else if (M <= 32) {  // wide output (e.g. dA: [r][K])
-    p.n_mblk = 1;
-    p.n_nblk = (N + 127) / 128;
-    hipLaunchKernelGGL((wgrad_kernel<32, 128, 1, 4>), dim3(n_expts * p.n_nblk), dim3(kThreads), 0, stream, p);
-  } else {
-    p.n_mblk = (M + 127) / 128;
-    p.n_nblk = (N + 127) / 128;
-    hipLaunchKernelGGL((wgrad_kernel<128, 128, 2, 2>), dim3(n_expts * p.n_mblk * p.n_nblk), dim3(kThreads), 0,
-                       stream, p);
+  p.chunk_rows = chunk_rows;
+  p.partials = partials;
+  if (max_chunks > 0) {
+    if (N <= 32) {  // tall output (e.g. dB: [N_out][r])
+      p.n_mblk = (M + 127) / 128;
+      p.n_nblk = 1;
+      hipLaunchKernelGGL((wgrad_partial_kernel<128, 32, 4, 1>), dim3(max_chunks, p.n_mblk), dim3(kThreads), 0,
+                         stream, p);
+    } else if (M <= 32) {  // wide output (e.g. dA: [r][K])
+      p.n_mblk = 1;
+      p.n_nblk = (N + 127) / 128;
+      hipLaunchKernelGGL((wgrad_partial_kernel<32, 128, 1, 4>), dim3(max_chunks, p.n_nblk), dim3(kThreads), 0,
+                         stream, p);
+    } else {
+      p.n_mblk = (M + 127) / 128;
+      p.n_nblk = (N + 127) / 128;
+      hipLaunchKernelGGL((wgrad_partial_kernel<128, 128, 2, 2>), dim3(max_chunks, p.n_mblk * p.n_nblk),
+                         dim3(kThreads), 0, stream, p);
+    }
+    int rc = af3::check_launch("lora_wgrad/partial");
+    if (rc) return rc;
   }
-  return af3::check_launch("lora_wgrad");
+  const int64_t MN = (int64_t)M * N;  // multiple of 64: M % 8 == 0 and N % 8 == 0
+  hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((unsigned)af3_cdiv(MN / 4, 256), n_expts), dim3(256), 0, stream,
+                     partials, chunk_offs, MN, scale, g);
+  return af3::check_launch("lora_wgrad/reduce");
 }
 
 // out[t][:] = sum_{j<K} rows[src[t*K+j]][:]  (the scatter-sum of matmul_ogs)

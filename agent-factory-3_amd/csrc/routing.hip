@@ -110,8 +110,9 @@ __global__ void topk_token_kernel(const uint16_t* __restrict__ logits, int64_t l
   }
 }
 
-// per-chunk histogram: counts[c * E + e]
-__global__ void chunk_hist_kernel(const int32_t* __restrict__ ids, int64_t R, int E, int32_t* __restrict__ counts) {
+// per-chunk histogram: counts[e * n_chunks + c]
+__global__ void chunk_hist_kernel(const int32_t* __restrict__ ids, int64_t R, int E, int n_chunks,
+                                  int32_t* __restrict__ counts) {
   extern __shared__ int32_t sh[];
   for (int e = threadIdx.x; e < E; e += blockDim.x) sh[e] = 0;
   __syncthreads();
@@ -121,45 +122,62 @@ __global__ void chunk_hist_kernel(const int32_t* __restrict__ ids, int64_t R, in
     if (e >= 0) atomicAdd(&sh[e], 1);
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x) counts[(int64_t)blockIdx.x * E + e] = sh[e];
+  for (int e = threadIdx.x; e < E; e += blockDim.x) counts[(int64_t)e * n_chunks + blockIdx.x] = sh[e];
 }
 
-// single block: hist, token_offs_raw, per-(chunk,expert) base offsets
-__global__ void scan_kernel(int32_t* __restrict__ counts, int n_chunks, int E, int32_t* __restrict__ hist,
-                            int32_t* __restrict__ offs) {
-  extern __shared__ int32_t tot[];  // E + 1
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    int32_t run = 0;
-    for (int c = 0; c < n_chunks; ++c) {
-      int32_t v = counts[(int64_t)c * E + e];
-      counts[(int64_t)c * E + e] = run;
-      run += v;
+// one block per expert: exclusive scan of its per-chunk counts (in place) and hist[e]
+__global__ __launch_bounds__(256) void chunk_scan_kernel(int32_t* __restrict__ counts, int n_chunks,
+                                                         int32_t* __restrict__ hist) {
+  __shared__ int32_t sh[256];
+  const int e = blockIdx.x, t = threadIdx.x;
+  int32_t* row = counts + (int64_t)e * n_chunks;
+  int32_t carry = 0;
+  for (int base = 0; base < n_chunks; base += 256) {
+    const int c = base + t;
+    const int32_t v = c < n_chunks ? row[c] : 0;
+    sh[t] = v;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+      int32_t add = t >= off ? sh[t - off] : 0;
+      __syncthreads();
+      sh[t] += add;
+      __syncthreads();
     }
-    tot[e] = run;
-    hist[e] = run;
+    if (c < n_chunks) row[c] = carry + sh[t] - v;
+    carry += sh[255];
+    __syncthreads();
   }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int32_t run = 0;
-    for (int e = 0; e < E; ++e) {
-      int32_t v = tot[e];
-      tot[e] = run;
-      offs[e] = run;
-      run += v;
+  if (t == 0) hist[e] = carry;
+}
+
+// single block: token_offs_raw = exclusive scan of hist over experts
+__global__ __launch_bounds__(1024) void expert_scan_kernel(const int32_t* __restrict__ hist, int E,
+                                                           int32_t* __restrict__ offs) {
+  __shared__ int32_t sh[1024];
+  const int t = threadIdx.x;
+  int32_t carry = 0;
+  for (int base = 0; base < E; base += 1024) {
+    const int e = base + t;
+    const int32_t v = e < E ? hist[e] : 0;
+    sh[t] = v;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+      int32_t add = t >= off ? sh[t - off] : 0;
+      __syncthreads();
+      sh[t] += add;
+      __syncthreads();
     }
-    offs[E] = run;
-    tot[E] = run;
+    if (e < E) offs[e] = carry + sh[t] - v;
+    carry += sh[1023];
+    __syncthreads();
   }
-  __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    int32_t b = tot[e];
-    for (int c = 0; c < n_chunks; ++c) counts[(int64_t)c * E + e] += b;
-  }
+  if (t == 0) offs[E] = carry;
 }
 
 // stable scatter of each chunk into expert-sorted order
-__global__ void scatter_kernel(const int32_t* __restrict__ ids, const uint16_t* __restrict__ scal, int64_t R, int E,
-                               const int32_t* __restrict__ base, int32_t* __restrict__ topk_indx,
+__global__ void scatter_kernel(const int32_t* __restrict__ ids, const uint16_t* __restrict__ scal, int64_t R,
+                               int n_chunks, const int32_t* __restrict__ offs, const int32_t* __restrict__ base,
+                               int32_t* __restrict__ topk_indx,
                                int32_t* __restrict__ gate_indx, uint16_t* __restrict__ gate_scal) {
   __shared__ int32_t sid[kChunk];
   int64_t i = (int64_t)blockIdx.x * kChunk + threadIdx.x;
@@ -173,10 +191,14 @@ __global__ void scatter_kernel(const int32_t* __restrict__ ids, const uint16_t* 
   }
   int rank = 0;
   for (int j = 0; j < (int)threadIdx.x; ++j) rank += (sid[j] == e);
-  int32_t pos = base[(int64_t)blockIdx.x * E + e] + rank;
+  int32_t pos = offs[e] + base[(int64_t)e * n_chunks + blockIdx.x] + rank;
   topk_indx[pos] = (int32_t)i;
   gate_indx[i] = pos;
   gate_scal[pos] = scal[i];
+}
+
+__global__ void zero_kernel(int32_t* __restrict__ p, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0;
 }
 
 // sorted slots past the number of valid entries (only when some ids were dropped)
@@ -246,6 +268,7 @@ static int routing_common(bool topk, const uint16_t* logits, int64_t ld, const i
   AF3_REQUIRE(T >= 0 && E > 0 && K > 0, "routing: bad sizes T=%lld E=%d K=%d", (long long)T, E, K);
   AF3_REQUIRE(K <= 16, "routing: K=%d > 16 unsupported", K);
   AF3_REQUIRE(E <= 0x7fff, "routing: E=%d too large", E);
+  AF3_REQUIRE(E * 4 <= 48 * 1024, "routing: E=%d exceeds the per-chunk LDS histogram", E);
   AF3_REQUIRE(!topk || K <= E, "routing: K=%d > E=%d", K, E);
   AF3_REQUIRE(ld >= E, "routing: logits leading dim %lld < E", (long long)ld);
   AF3_REQUIRE(ws_bytes >= af3_routing_workspace_bytes(T, E, K), "routing: workspace too small");
@@ -270,17 +293,23 @@ static int routing_common(bool topk, const uint16_t* logits, int64_t ld, const i
       hipLaunchKernelGGL(replay_token_kernel, g, dim3(128), 0, stream, logits, ld, expt_indx, T, E, K, ids, scal);
     int rc = af3::check_launch("routing/token");
     if (rc) return rc;
-    hipLaunchKernelGGL(chunk_hist_kernel, dim3(n_chunks), dim3(kChunk), E * 4, stream, ids, R, E, counts);
+    hipLaunchKernelGGL(chunk_hist_kernel, dim3(n_chunks), dim3(kChunk), E * 4, stream, ids, R, E, n_chunks, counts);
     rc = af3::check_launch("routing/hist");
     if (rc) return rc;
+    hipLaunchKernelGGL(chunk_scan_kernel, dim3(E), dim3(256), 0, stream, counts, n_chunks, hist);
+    rc = af3::check_launch("routing/chunk_scan");
+    if (rc) return rc;
+  } else {
+    hipLaunchKernelGGL(zero_kernel, dim3(1), dim3(256), 0, stream, hist, E);
+    int rc = af3::check_launch("routing/zero");
+    if (rc) return rc;
   }
-  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(256), (E + 1) * 4, stream, counts, n_chunks, E, hist,
-                     token_offs_raw);
-  int rc = af3::check_launch("routing/scan");
+  hipLaunchKernelGGL(expert_scan_kernel, dim3(1), dim3(1024), 0, stream, hist, E, token_offs_raw);
+  int rc = af3::check_launch("routing/expert_scan");
   if (rc) return rc;
   if (T > 0) {
-    hipLaunchKernelGGL(scatter_kernel, dim3(n_chunks), dim3(kChunk), 0, stream, ids, scal, R, E, counts, topk_indx,
-                       gate_indx, gate_scal);
+    hipLaunchKernelGGL(scatter_kernel, dim3(n_chunks), dim3(kChunk), 0, stream, ids, scal, R, n_chunks, token_offs_raw,
+                       counts, topk_indx, gate_indx, gate_scal);
     rc = af3::check_launch("routing/scatter");
     if (rc) return rc;
     hipLaunchKernelGGL(fill_tail_kernel, dim3((unsigned)af3_cdiv(R, 256)), dim3(256), 0, stream, token_offs_raw, E,

@@ -69,52 +69,46 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def bandwidth_extras(torch, dev, kernels, workloads, reps=20):
+def _batched_us(torch, fn, sets, reps):
+    """Average per-launch time of ``reps`` rounds over rotating buffer sets,
+    one event pair around the whole batch (per-launch event pairs would add
+    their own overhead to microsecond kernels)."""
+    for args in sets:
+        fn(*args)
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        for args in sets:
+            fn(*args)
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) * 1e3 / (reps * len(sets))
+
+
+def bandwidth_extras(torch, dev, kernels, workloads, reps=50):
     """cfg 0 dequant and cfg 1 SwiGLU fwd/bwd: algorithmic GB/s per launch."""
     res = {}
+
+    def rec(name, us, byts):
+        gbs = byts / (us * 1e-6) / 1e9
+        res[name] = {"GBps": gbs, "us": us, "bytes": byts, "frac_hbm_peak": gbs / HBM_PEAK_GBS}
+
     blocks, scales = workloads.cfg0()
-    nset = 8  # 8 x 42 MB > 256 MB MALL: each launch reads cold data
-    bs = [(blocks.to(dev), scales.to(dev)) for _ in range(nset)]
-    for b, s in bs:
-        kernels.mxfp4_to_bf16_hip(b, s)
-    torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps * nset)]
-    i = 0
-    for _ in range(reps):
-        for b, s in bs:
-            ev[i][0].record()
-            kernels.mxfp4_to_bf16_hip(b, s)
-            ev[i][1].record()
-            i += 1
-    torch.cuda.synchronize()
-    ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
-    byts = 8294400 + 518400 + 33177600
-    res["dequant_cfg0"] = {"GBps": byts / (ms * 1e-3) / 1e9, "us": ms * 1e3, "bytes": byts,
-                           "frac_hbm_peak": byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
-    del bs
+    # 8 x 42 MB > 256 MB MALL: each launch reads cold data
+    sets = [(blocks.to(dev), scales.to(dev)) for _ in range(8)]
+    rec("dequant_cfg0", _batched_us(torch, kernels.mxfp4_to_bf16_hip, sets, reps), 8294400 + 518400 + 33177600)
+    del sets
     gu, dout = workloads.cfg1()
-    sets = [(gu.to(dev), dout.to(dev)) for _ in range(2)]
     M, N2 = gu.shape
     N = N2 // 2
-    for name, fn, byts in (
-            ("swiglu_fwd_cfg1", lambda g, d: kernels.swiglu_forward(g, 1.702, 7.0), M * N2 * 2 + M * N * 2),
-            ("swiglu_bwd_cfg1", lambda g, d: kernels.swiglu_backward_raw(d, g, 1.702, 7.0),
-             M * N * 2 + M * N2 * 2 + M * N2 * 2)):
-        for g, d in sets:
-            fn(g, d)
-        torch.cuda.synchronize()
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps * 2)]
-        i = 0
-        for _ in range(reps):
-            for g, d in sets:
-                ev[i][0].record()
-                fn(g, d)
-                ev[i][1].record()
-                i += 1
-        torch.cuda.synchronize()
-        ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
-        res[name] = {"GBps": byts / (ms * 1e-3) / 1e9, "us": ms * 1e3, "bytes": byts,
-                     "frac_hbm_peak": byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    sets = [(gu.to(dev), dout.to(dev)) for _ in range(2)]
+    rec("swiglu_fwd_cfg1", _batched_us(torch, lambda g, d: kernels.swiglu_forward(g, 1.702, 7.0), sets, reps),
+        M * N2 * 2 + M * N * 2)
+    rec("swiglu_bwd_cfg1",
+        _batched_us(torch, lambda g, d: kernels.swiglu_backward_raw(d, g, 1.702, 7.0), sets, reps),
+        M * N * 2 + M * N2 * 2 + M * N2 * 2)
     return res
 
 

@@ -118,11 +118,17 @@ int af3_lora_rows(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, in
                   int n_expts, int n_out, int K, uint16_t* out, int64_t ld_out, void* stream);
 
 /* Expert-LoRA weight gradient over each expert's rows (no counterpart in the
- * reference):  G[e][m][n] = scale * sum_{r in rows(e)} rs(r) A[a(r)][m] B[b(r)][n]
- * rs = optional bf16 per-row multiplier; G bf16 [E][M][N]. */
+ * reference):  G[e][m][n] = scale * sum_{r in rows(e)} bf16(rs(r) A[a(r)][m]) B[b(r)][n]
+ * rs = optional bf16 per-row multiplier; G bf16 [E][M][N].  Rows are split
+ * into chunk_rows-row chunks (chunk_map / chunk_offs = block_pid_map /
+ * token_offs_pad of af3_expt_data for BM = chunk_rows); per-chunk fp32
+ * partials go to `partials`, then are summed per expert in chunk order. */
+size_t af3_lora_wgrad_workspace_bytes(int max_chunks, int M, int N);
 int af3_lora_wgrad(const uint16_t* a, int64_t lda, const int32_t* a_gather, int a_div, const uint16_t* a_rowscale,
                    const uint16_t* b, int64_t ldb, const int32_t* b_gather, int b_div, float scale,
-                   const int32_t* token_offs, int n_expts, int M, int N, uint16_t* g, void* stream);
+                   const int32_t* token_offs, int n_expts, int M, int N, const int32_t* chunk_map,
+                   const int32_t* chunk_offs, int max_chunks, int chunk_rows, float* partials, size_t partial_bytes,
+                   uint16_t* g, void* stream);
 
 #ifdef __cplusplus
 }
