@@ -51,6 +51,9 @@ from .routing import (  # noqa: F401  (re-exported names of the routing layer)
 )
 
 GEMM_BLOCK_M = 128
+# Grouped-GEMM tile selection (tuning knob): rows per tile (128 or 256; the
+# LoRA row products always use 128) and the C library's tile_cfg (0 = default).
+GEMM_TILE = {"block_m": 256, "tile_cfg": 0}
 
 # Optional launch timer for the grouped GEMM (set by benchmark harnesses):
 # callable(tag: str, flops: int) -> context manager wrapping the launch.
@@ -135,7 +138,7 @@ def _expt_data(routing_data, n_rows, device):
     if routing_data is None:
         return dense_routing(n_rows, device), 1
     ed = routing_data.expt_data
-    if ed is None or not all(bm in getattr(ed, "block_pid_map", {}) for bm in (GEMM_BLOCK_M, WGRAD_CHUNK)):
+    if ed is None or not all(bm in getattr(ed, "block_pid_map", {}) for bm in (128, 256, WGRAD_CHUNK)):
         ed = compute_expt_data(routing_data.expt_hist, routing_data.n_expts_tot, n_rows)
         routing_data = RoutingData(routing_data.gate_scal, routing_data.expt_hist, routing_data.n_expts_tot,
                                    routing_data.n_expts_act, ed)
@@ -182,7 +185,8 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
     R = g.shape[0] if g is not None else x.shape[0]
     routing_data, k_act = _expt_data(routing_data, R, dev)
     ed = routing_data.expt_data
-    pid_map = ed.block_pid_map[GEMM_BLOCK_M]
+    bm = GEMM_TILE["block_m"] if K % 64 == 0 else 128
+    pid_map = ed.block_pid_map[bm]
     offs = ed.token_offs_raw
     y = torch.empty(R, N, dtype=torch.bfloat16, device=dev)
     if R == 0 or pid_map.numel() == 0:
@@ -204,8 +208,9 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
         lora_b = lora_b.to(torch.bfloat16).contiguous()
     args = (x.data_ptr(), x.stride(0) if x.shape[0] > 1 else K, _capi.ptr(g), k_act if g is not None else 1,
             blocks.data_ptr(), scales.data_ptr(), 1 if trans_w else 0, _capi.ptr(b), _capi.ptr(gm), gm_f32,
-            _capi.ptr(lora_l), lr, _capi.ptr(lora_b), lr, offs.data_ptr(), pid_map.data_ptr(), pid_map.numel(),
-            E, N, K, y.data_ptr(), N, _capi.stream_of(dev))
+            _capi.ptr(lora_l), lr, _capi.ptr(lora_b), lr, offs.data_ptr(), pid_map.data_ptr(),
+            ed.token_offs_pad[bm].data_ptr(), pid_map.numel(), bm, GEMM_TILE["tile_cfg"], E, N, K, y.data_ptr(), N,
+            _capi.stream_of(dev))
     if KERNEL_TIMER is None:
         _capi.call("af3_moe_gemm", *args)
     else:

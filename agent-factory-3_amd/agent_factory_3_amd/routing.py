@@ -23,9 +23,9 @@ import torch
 
 from . import _capi
 
-# block sizes for which tile maps are built: 128-row GEMM tiles and the
-# 512-row chunks of the LoRA weight-gradient reduction
-BLOCK_MS = (128, 512)
+# block sizes for which tile maps are built: 128- and 256-row GEMM tiles and
+# the 512-row chunks of the LoRA weight-gradient reduction
+BLOCK_MS = (128, 256, 512)
 
 
 @dataclass

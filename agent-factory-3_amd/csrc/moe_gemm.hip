@@ -55,6 +55,7 @@ struct Params {
   int kx;             // extension reduction length (0 = none)
   const int32_t* offs;      // expert row offsets [E+1]
   const int32_t* tile_map;  // block_pid_map (row tiles)
+  const int32_t* tile_offs; // token_offs_pad of the same block size ([E] = number of m-tiles)
   int E;
   int n_mblk, n_nblk;       // wgrad tiling
   const float* bias;        // [E][N] fp32
@@ -106,23 +107,23 @@ __device__ __forceinline__ void transpose8x8(const af3_u32x4 in[8], af3_u32x4 ou
 // in the operand's row space (expert-sorted row for gathered/row operands,
 // column for cols operands); k ranges over [k0, k0+64) limited by `kend`.
 // ---------------------------------------------------------------------------
-template <int TR, int KIND>
+template <int TR, int KIND, int NT = kThreads>
 struct Loader;
 
 // k-contiguous bf16 rows
-template <int TR>
-struct Loader<TR, ROWS_BF16> {
+template <int TR, int NT>
+struct Loader<TR, ROWS_BF16, NT> {
   static constexpr int kUnits = TR * 8;
-  static constexpr int kUPT = (kUnits + kThreads - 1) / kThreads;
+  static constexpr int kUPT = (kUnits + NT - 1) / NT;
   const uint16_t* rp[kUPT];
   af3_u32x4 v[kUPT];
   int kend;
 
-  __device__ void init(const Operand& op, int e, int row0, int nvalid, int kend_) {
+  __device__ __forceinline__ void init(const Operand& op, int e, int row0, int nvalid, int kend_) {
     kend = kend_;
 #pragma unroll
     for (int i = 0; i < kUPT; ++i) {
-      int u = threadIdx.x + i * kThreads;
+      int u = threadIdx.x + i * NT;
       int r = u >> 3;
       rp[i] = nullptr;
       if (u < kUnits && r < nvalid) {
@@ -132,39 +133,39 @@ struct Loader<TR, ROWS_BF16> {
       }
     }
   }
-  __device__ void load(int k0) {
+  __device__ __forceinline__ void load(int k0) {
 #pragma unroll
     for (int i = 0; i < kUPT; ++i) {
-      int u = threadIdx.x + i * kThreads;
+      int u = threadIdx.x + i * NT;
       int k = k0 + ((u & 7) << 3);
       v[i] = (rp[i] && k < kend) ? *(const af3_u32x4*)(rp[i] + k) : zero4();
     }
   }
-  __device__ void store(uint16_t* lds) {
+  __device__ __forceinline__ void store(uint16_t* lds) {
 #pragma unroll
     for (int i = 0; i < kUPT; ++i) {
-      int u = threadIdx.x + i * kThreads;
+      int u = threadIdx.x + i * NT;
       if (u < kUnits) *(af3_u32x4*)(lds + lds_off(u >> 3, u & 7)) = v[i];
     }
   }
 };
 
 // MXFP4 rows packed along k: W[e][n][k/32][16]
-template <int TR>
-struct Loader<TR, ROWS_FP4> {
+template <int TR, int NT>
+struct Loader<TR, ROWS_FP4, NT> {
   static constexpr int kUnits = TR * 2;  // two 32-element groups per 64-deep k-step
-  static constexpr int kUPT = (kUnits + kThreads - 1) / kThreads;
+  static constexpr int kUPT = (kUnits + NT - 1) / NT;
   const uint8_t* bp[kUPT];
   const uint8_t* sp[kUPT];
   af3_u32x4 v[kUPT];
   uint32_t s[kUPT];
   int kend;
 
-  __device__ void init(const Operand& op, int e, int row0, int nvalid, int kend_) {
+  __device__ __forceinline__ void init(const Operand& op, int e, int row0, int nvalid, int kend_) {
     kend = kend_;
 #pragma unroll
     for (int i = 0; i < kUPT; ++i) {
-      int u = threadIdx.x + i * kThreads;
+      int u = threadIdx.x + i * NT;
       int r = u >> 1;
       bp[i] = nullptr;
       sp[i] = nullptr;
@@ -175,20 +176,20 @@ struct Loader<TR, ROWS_FP4> {
       }
     }
   }
-  __device__ void load(int k0) {
+  __device__ __forceinline__ void load(int k0) {
 #pragma unroll
     for (int i = 0; i < kUPT; ++i) {
-      int u = threadIdx.x + i * kThreads;
+      int u = threadIdx.x + i * NT;
       int k = k0 + ((u & 1) << 5);
       bool ok = bp[i] && k < kend;
       v[i] = ok ? *(const af3_u32x4*)(bp[i] + (k >> 1)) : zero4();
       s[i] = ok ? (uint32_t)sp[i][k >> 5] : 127u;
     }
   }
-  __device__ void store(uint16_t* lds) {
+  __device__ __forceinline__ void store(uint16_t* lds) {
 #pragma unroll
     for (int i = 0; i < kUPT; ++i) {
-      int u = threadIdx.x + i * kThreads;
+      int u = threadIdx.x + i * NT;
       if (u >= kUnits) continue;
       int r = u >> 1, ch0 = (u & 1) << 2;
 #pragma unroll
@@ -202,10 +203,11 @@ struct Loader<TR, ROWS_FP4> {
 };
 
 // bf16 operand stored [k][rows] (rows contiguous): unit = 8 k x 8 rows
-template <int TR>
-struct Loader<TR, COLS_BF16> {
-  static constexpr int kUnits = 8 * (TR / 8);
-  static constexpr int kUPT = (kUnits + kThreads - 1) / kThreads;
+template <int TR, int NT>
+struct Loader<TR, COLS_BF16, NT> {
+  static constexpr int kCO = TR / 8;  // 8-column groups per k-row
+  static constexpr int kUnits = 8 * kCO;
+  static constexpr int kUPT = (kUnits + NT - 1) / NT;
   const uint16_t* base;
   const int32_t* gather;
   const uint16_t* rowscale;
@@ -213,7 +215,7 @@ struct Loader<TR, COLS_BF16> {
   int gdiv, kb, kend, col0, ncols;
   af3_u32x4 v[kUPT][8];
 
-  __device__ void init(const Operand& op, int e, int col0_, int ncols_, int kb_, int kend_) {
+  __device__ __forceinline__ void init(const Operand& op, int e, int col0_, int ncols_, int kb_, int kend_) {
     base = (const uint16_t*)op.ptr + e * op.estride;
     gather = op.gather;
     gdiv = op.gdiv;
@@ -224,11 +226,11 @@ struct Loader<TR, COLS_BF16> {
     col0 = col0_;
     ncols = ncols_;
   }
-  __device__ void load(int k0) {
+  __device__ __forceinline__ void load(int k0) {
 #pragma unroll
     for (int i = 0; i < kUPT; ++i) {
-      int u = threadIdx.x + i * kThreads;
-      int ko = u & 7, co = u >> 3;
+      int u = threadIdx.x + i * NT;
+      int ko = u / kCO, co = u % kCO;
       int c = co * 8;
       bool cok = u < kUnits && c < ncols;
 #pragma unroll
@@ -250,12 +252,12 @@ struct Loader<TR, COLS_BF16> {
       }
     }
   }
-  __device__ void store(uint16_t* lds) {
+  __device__ __forceinline__ void store(uint16_t* lds) {
 #pragma unroll
     for (int i = 0; i < kUPT; ++i) {
-      int u = threadIdx.x + i * kThreads;
+      int u = threadIdx.x + i * NT;
       if (u >= kUnits) continue;
-      int ko = u & 7, co = u >> 3;
+      int ko = u / kCO, co = u % kCO;
       af3_u32x4 t[8];
       transpose8x8(v[i], t);
 #pragma unroll
@@ -265,10 +267,11 @@ struct Loader<TR, COLS_BF16> {
 };
 
 // MXFP4 operand packed along the tile-row axis: W[e][k][n/32][16]
-template <int TR>
-struct Loader<TR, COLS_FP4> {
-  static constexpr int kUnits = 8 * (TR / 8);
-  static constexpr int kUPT = (kUnits + kThreads - 1) / kThreads;
+template <int TR, int NT>
+struct Loader<TR, COLS_FP4, NT> {
+  static constexpr int kCO = TR / 8;  // 8-column groups per k-row
+  static constexpr int kUnits = 8 * kCO;
+  static constexpr int kUPT = (kUnits + NT - 1) / NT;
   const uint8_t* bbase;
   const uint8_t* sbase;
   int64_t ld, sld;
@@ -276,7 +279,7 @@ struct Loader<TR, COLS_FP4> {
   uint32_t w[kUPT][8];
   uint32_t s[kUPT][8];
 
-  __device__ void init(const Operand& op, int e, int col0_, int ncols_, int kb_, int kend_) {
+  __device__ __forceinline__ void init(const Operand& op, int e, int col0_, int ncols_, int kb_, int kend_) {
     bbase = (const uint8_t*)op.ptr + e * op.estride;
     sbase = op.scales + e * op.sestride;
     ld = op.ld;
@@ -285,11 +288,11 @@ struct Loader<TR, COLS_FP4> {
     col0 = col0_;
     ncols = ncols_;
   }
-  __device__ void load(int k0) {
+  __device__ __forceinline__ void load(int k0) {
 #pragma unroll
     for (int i = 0; i < kUPT; ++i) {
-      int u = threadIdx.x + i * kThreads;
-      int ko = u & 7, co = u >> 3;
+      int u = threadIdx.x + i * NT;
+      int ko = u / kCO, co = u % kCO;
       int c = col0 + co * 8;  // first of 8 columns = 4 packed bytes
       bool cok = u < kUnits && co * 8 < ncols;
 #pragma unroll
@@ -301,12 +304,12 @@ struct Loader<TR, COLS_FP4> {
       }
     }
   }
-  __device__ void store(uint16_t* lds) {
+  __device__ __forceinline__ void store(uint16_t* lds) {
 #pragma unroll
     for (int i = 0; i < kUPT; ++i) {
-      int u = threadIdx.x + i * kThreads;
+      int u = threadIdx.x + i * NT;
       if (u >= kUnits) continue;
-      int ko = u & 7, co = u >> 3;
+      int ko = u / kCO, co = u % kCO;
       af3_u32x4 x[8], t[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -363,6 +366,482 @@ __device__ __forceinline__ void run_segment(LA& la, LB& lb, int k_len, uint16_t*
       lb.load((kt + 1) * kBK);
     }
     mma_kstep<TM, TN>(As, Bs, wm0, wn0, acc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// A operand through direct global->LDS loads (global_load_lds_dwordx4):
+// k-contiguous bf16 rows, optionally gathered.  One wave instruction fills 8
+// LDS tile rows (1 KiB, lane l -> bytes [16 l, 16 l + 16)); lane l fetches the
+// logical chunk (l % 8) ^ swz(row) of row l / 8, which realises the swizzled
+// layout of lds_off.  Requires K % 64 == 0.  Padding rows (>= nvalid) read the
+// tile's first row; their results are never stored.
+// ---------------------------------------------------------------------------
+template <int TR, int NW>
+struct DmaRows {
+  static_assert(TR % (8 * NW) == 0, "tile rows must split evenly over the waves");
+  static constexpr int kIPW = TR / 8 / NW;  // 1 KiB instructions per wave per k-step
+  const uint16_t* rp[kIPW];
+
+  __device__ __forceinline__ void init(const Operand& op, int row0, int nvalid) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint16_t* base = (const uint16_t*)op.ptr;
+    int64_t src0 = row0;
+    if (op.gather) src0 = op.gather[row0] / op.gdiv;
+#pragma unroll
+    for (int i = 0; i < kIPW; ++i) {
+      const int row = (wave * kIPW + i) * 8 + (lane >> 3);
+      int64_t src = src0;
+      if (row < nvalid) {
+        src = row0 + row;
+        if (op.gather) src = op.gather[src] / op.gdiv;
+      }
+      rp[i] = base + src * op.ld + (((lane & 7) ^ swz(row)) << 3);
+    }
+  }
+  __device__ __forceinline__ void issue(uint16_t* lds, int k0) {
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < kIPW; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(rp[i] + k0),
+                                       (__attribute__((address_space(3))) void*)(lds + (wave * kIPW + i) * 8 * kBK),
+                                       16, 0, 0);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// main grouped GEMM through MXFP4 weights: double-buffered LDS (one barrier
+// per k-step), A by direct loads, B (MXFP4, dequantised in registers) by the
+// loaders above, optional LoRA extension segment, epilogue as rowtile_kernel.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int WM, int WN, int BK_, int BXK>
+__global__ __launch_bounds__(WM * WN * 64) void gemm2_kernel(Params p) {
+  constexpr int NW = WM * WN, NT = NW * 64;
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  static_assert(TM >= 1 && TN >= 1, "wave tile at least 32x32");
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * (BM + BN) * kBK];
+  uint16_t* const A0 = lds;
+  uint16_t* const B0 = lds + BM * kBK;
+  uint16_t* const A1 = lds + (BM + BN) * kBK;
+  uint16_t* const B1 = A1 + BM * kBK;
+
+  // 1-D grid over (valid m-tile, n-tile) work items, n-tile fastest.  The
+  // hardware deals consecutive workgroups to the 8 XCDs in turn, so workgroup
+  // b is remapped to work item (b % 8) * (W8 / 8) + b / 8: each XCD walks a
+  // contiguous range and keeps an m-tile's activation rows in its own L2
+  // while it sweeps that tile's n-tiles.
+  const int NN = p.n_nblk;
+  const int W = p.tile_offs[p.E] * NN;  // number of valid m-tiles from the device-side scan
+  const int b = blockIdx.x;
+  if (b >= W) return;
+  const int W8 = W & ~7;
+  const int w = b < W8 ? (b & 7) * (W8 >> 3) + (b >> 3) : b;
+  const int32_t ent = p.tile_map[w / NN];
+  if (ent < 0) return;
+  const int e = ent & 0xFFFF, blk = ent >> 16;
+  const int row_lo = p.offs[e] + blk * BM;
+  const int nrows = min(BM, p.offs[e + 1] - row_lo);
+  if (nrows <= 0) return;
+  const int n0 = (w % NN) * BN;
+  const int ncols = min(BN, p.N - n0);
+
+  const int wave = threadIdx.x >> 6;
+  const int wm0 = (wave / WN) * (BM / WM), wn0 = (wave % WN) * (BN / WN);
+  af3_f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  {
+    DmaRows<BM, NW> la;
+    la.init(p.a, row_lo, nrows);
+    Loader<BN, BK_, NT> lb;
+    if constexpr (BK_ == ROWS_FP4)
+      lb.init(p.b, e, n0, ncols, p.K);
+    else
+      lb.init(p.b, e, n0, ncols, 0, p.K);
+    const int nk = p.K / kBK;
+    la.issue(A0, 0);
+    lb.load(0);
+    lb.store(B0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      uint16_t* const Ac = (kt & 1) ? A1 : A0;
+      uint16_t* const Bc = (kt & 1) ? B1 : B0;
+      uint16_t* const An = (kt & 1) ? A0 : A1;
+      uint16_t* const Bn = (kt & 1) ? B0 : B1;
+      const bool more = kt + 1 < nk;
+      if (more) {
+        la.issue(An, (kt + 1) * kBK);
+        lb.load((kt + 1) * kBK);
+      }
+      mma_kstep<TM, TN>(Ac, Bc, wm0, wn0, acc);
+      if (more) lb.store(Bn);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+  }
+  if constexpr (BXK != NONE) {
+    if (p.kx > 0) {
+      Loader<BM, ROWS_BF16, NT> la;
+      Loader<BN, BXK, NT> lb;
+      la.init(p.ax, 0, row_lo, nrows, p.kx);
+      if constexpr (BXK == ROWS_BF16)
+        lb.init(p.bx, e, n0, ncols, p.kx);
+      else
+        lb.init(p.bx, e, n0, ncols, 0, p.kx);
+      run_segment<Loader<BM, ROWS_BF16, NT>, Loader<BN, BXK, NT>, TM, TN>(la, lb, p.kx, A0, B0, wm0, wn0, acc);
+    }
+  }
+
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int col = wn0 + tn * 32 + (lane & 31);
+      if (col >= ncols) continue;
+      const int n = n0 + col;
+      const float bv = p.bias ? p.bias[e * p.bias_estride + n] : 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = wm0 + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        if (row >= nrows) continue;
+        const int64_t gr = row_lo + row;
+        float v = acc[tm][tn][r] + bv;
+        if (p.gammas)
+          v *= p.gammas_f32 ? ((const float*)p.gammas)[gr] : af3_bf16_to_f32(((const uint16_t*)p.gammas)[gr]);
+        p.c[gr * p.ldc + n] = (uint16_t)af3_f32_to_bf16(v);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Prefetching B loaders for gemm3: every global load is unconditional (rows /
+// columns past the tile edge are clamped to valid ones; their results land in
+// output columns that are never stored), so each wave issues exactly kOps
+// vector-memory instructions per load() and the k-loop can wait for an older
+// stage with an exact vmcnt.  Addresses live in the loader; the raw data of a
+// k-step lives in a separate Data object so two k-steps can be in flight.
+// ---------------------------------------------------------------------------
+template <int TR, int NT>
+struct PfRowsFp4 {  // W[e][n][k/32][16], nibbles along k
+  static constexpr int kUnits = TR * 2;
+  static_assert(kUnits % NT == 0, "units must split evenly over the threads");
+  static constexpr int kUPT = kUnits / NT;
+  static constexpr int kOps = 2 * kUPT;  // dwordx4 + ubyte per unit
+  struct Data {
+    af3_u32x4 v[kUPT];
+    uint32_t s[kUPT];
+  };
+  const uint8_t* bp[kUPT];
+  const uint8_t* sp[kUPT];
+
+  __device__ __forceinline__ void init(const Operand& op, int e, int row0, int nvalid) {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      const int u = threadIdx.x + i * NT;
+      const int64_t n = row0 + min(u >> 1, nvalid - 1);
+      bp[i] = (const uint8_t*)op.ptr + e * op.estride + n * op.ld + ((u & 1) << 4);
+      sp[i] = op.scales + e * op.sestride + n * op.sld + (u & 1);
+    }
+  }
+  __device__ __forceinline__ void load(Data& d, int k0) const {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      d.v[i] = *(const af3_u32x4*)(bp[i] + (k0 >> 1));
+      d.s[i] = (uint32_t)sp[i][k0 >> 5];
+    }
+  }
+  __device__ __forceinline__ void store(const Data& d, uint16_t* lds) const {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      const int u = threadIdx.x + i * NT;
+      const int r = u >> 1, ch0 = (u & 1) << 2;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t o[4];
+        af3_dequant_u32(d.v[i][q], d.s[i], o);
+        *(af3_u32x4*)(lds + lds_off(r, ch0 + q)) = af3_u32x4{o[0], o[1], o[2], o[3]};
+      }
+    }
+  }
+};
+
+template <int TR, int NT>
+struct PfColsFp4 {  // W[e][k][n/32][16], nibbles along n: unit = 8 k x 8 n
+  static constexpr int kCO = TR / 8;
+  static constexpr int kUnits = 8 * kCO;
+  static_assert(kUnits % NT == 0 || NT % kUnits == 0, "units and threads must divide");
+  // with fewer units than threads the extra threads load a duplicate unit (so
+  // every wave issues the same instructions) and store nothing
+  static constexpr int kUPT = kUnits >= NT ? kUnits / NT : 1;
+  static constexpr int kOps = 16 * kUPT;  // 8 dwords + 8 scale bytes per unit
+  struct Data {
+    uint32_t w[kUPT][8];
+    uint32_t s[kUPT][8];
+  };
+  const uint8_t* bp[kUPT];
+  const uint8_t* sp[kUPT];
+  int64_t ld, sld;
+
+  __device__ __forceinline__ void init(const Operand& op, int e, int col0, int ncols) {
+    ld = op.ld;
+    sld = op.sld;
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      const int u = (threadIdx.x + i * NT) % kUnits;
+      const int ko = u / kCO, co = u % kCO;
+      const int c = col0 + min(co * 8, ncols - 8);
+      bp[i] = (const uint8_t*)op.ptr + e * op.estride + (int64_t)(ko * 8) * ld + (c >> 1);
+      sp[i] = op.scales + e * op.sestride + (int64_t)(ko * 8) * sld + (c >> 5);
+    }
+  }
+  __device__ __forceinline__ void load(Data& d, int k0) const {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        d.w[i][j] = *(const uint32_t*)(bp[i] + (int64_t)(k0 + j) * ld);
+        d.s[i][j] = (uint32_t)sp[i][(int64_t)(k0 + j) * sld];
+      }
+  }
+  __device__ __forceinline__ void store(const Data& d, uint16_t* lds) const {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      const int u = threadIdx.x + i * NT;
+      if (kUnits < NT && u >= kUnits) continue;
+      const int ko = u / kCO, co = u % kCO;
+      af3_u32x4 x[8], t[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        uint32_t o[4];
+        af3_dequant_u32(d.w[i][j], d.s[i][j], o);
+        x[j] = af3_u32x4{o[0], o[1], o[2], o[3]};
+      }
+      transpose8x8(x, t);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) *(af3_u32x4*)(lds + lds_off(co * 8 + j, ko)) = t[j];
+    }
+  }
+};
+
+template <int TR, int NT>
+struct PfRowsBf16 {  // k-contiguous bf16 rows, optionally gathered (A operand)
+  static constexpr int kUnits = TR * 8;
+  static_assert(kUnits % NT == 0, "units must split evenly over the threads");
+  static constexpr int kUPT = kUnits / NT;
+  struct Data {
+    af3_u32x4 v[kUPT];
+  };
+  const uint16_t* rp[kUPT];
+
+  // rows past nvalid read the tile's first row (results never stored)
+  __device__ __forceinline__ void init(const Operand& op, int row0, int nvalid) {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      const int u = threadIdx.x + i * NT;
+      int64_t src = row0 + min(u >> 3, nvalid - 1);
+      if (op.gather) src = op.gather[src] / op.gdiv;
+      rp[i] = (const uint16_t*)op.ptr + src * op.ld + ((u & 7) << 3);
+    }
+  }
+  __device__ __forceinline__ void load(Data& d, int k0) const {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) d.v[i] = *(const af3_u32x4*)(rp[i] + k0);
+  }
+  __device__ __forceinline__ void store(const Data& d, uint16_t* lds) const {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      const int u = threadIdx.x + i * NT;
+      *(af3_u32x4*)(lds + lds_off(u >> 3, u & 7)) = d.v[i];
+    }
+  }
+};
+
+template <int KIND, int TR, int NT>
+struct PfLoader;
+template <int TR, int NT>
+struct PfLoader<ROWS_FP4, TR, NT> {
+  using type = PfRowsFp4<TR, NT>;
+};
+template <int TR, int NT>
+struct PfLoader<COLS_FP4, TR, NT> {
+  using type = PfColsFp4<TR, NT>;
+};
+
+// s_waitcnt with vmcnt(n) and lgkmcnt(0) (expcnt not waited)
+#define AF3_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4))
+
+// MFMA over one LDS k-step with the fragments of sub-step s+1 read while the
+// MFMAs of sub-step s issue.
+template <int TM, int TN>
+__device__ __forceinline__ void mma_kstep_pf(const uint16_t* As, const uint16_t* Bs, int wm0, int wn0,
+                                             af3_f32x16 acc[TM][TN]) {
+  const int lane = threadIdx.x & 63;
+  const int lr = lane & 31, lk = lane >> 5;
+  af3_bf16x8 af[2][TM], bf[2][TN];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) af[0][tm] = *(const af3_bf16x8*)(As + lds_off(wm0 + tm * 32 + lr, lk));
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) bf[0][tn] = *(const af3_bf16x8*)(Bs + lds_off(wn0 + tn * 32 + lr, lk));
+#pragma unroll
+  for (int ks = 0; ks < kBK / 16; ++ks) {
+    const int cur = ks & 1, nxt = cur ^ 1;
+    if (ks + 1 < kBK / 16) {
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+        af[nxt][tm] = *(const af3_bf16x8*)(As + lds_off(wm0 + tm * 32 + lr, (ks + 1) * 2 + lk));
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+        bf[nxt][tn] = *(const af3_bf16x8*)(Bs + lds_off(wn0 + tn * 32 + lr, (ks + 1) * 2 + lk));
+    }
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+        acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][tm], bf[cur][tn], acc[tm][tn], 0, 0, 0);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// gemm3: main grouped GEMM with a two-k-step-deep prefetch.  A (activations)
+// goes global->LDS directly into one of three LDS stages two k-steps ahead; B
+// (MXFP4) is loaded two k-steps ahead into one of two register sets and
+// dequantised into one of two LDS stages one k-step ahead.  One barrier per
+// k-step; before it each wave waits (exact vmcnt) for everything except the
+// loads it issued in the current step.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int WM, int WN, int BK_, int BXK>
+__global__ __launch_bounds__(WM * WN * 64) void gemm3_kernel(Params p) {
+  constexpr int NW = WM * WN, NT = NW * 64;
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  using LB = typename PfLoader<BK_, BN, NT>::type;
+  constexpr int kStageA = BM * kBK, kStageB = BN * kBK;
+  __shared__ __attribute__((aligned(16))) uint16_t Ab[2 * kStageA];
+  __shared__ __attribute__((aligned(16))) uint16_t Bb[2 * kStageB];
+
+  const int NN = p.n_nblk;
+  const int W = p.tile_offs[p.E] * NN;
+  const int b = blockIdx.x;
+  if (b >= W) return;
+  const int W8 = W & ~7;
+  const int w = b < W8 ? (b & 7) * (W8 >> 3) + (b >> 3) : b;
+  const int32_t ent = p.tile_map[w / NN];
+  if (ent < 0) return;
+  const int e = ent & 0xFFFF, blk = ent >> 16;
+  const int row_lo = p.offs[e] + blk * BM;
+  const int nrows = min(BM, p.offs[e + 1] - row_lo);
+  if (nrows <= 0) return;
+  const int n0 = (w % NN) * BN;
+  const int ncols = min(BN, p.N - n0);
+
+  const int wave = threadIdx.x >> 6;
+  const int wm0 = (wave / WN) * (BM / WM), wn0 = (wave % WN) * (BN / WN);
+  af3_f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  {
+    using LA = PfRowsBf16<BM, NT>;
+    LA la;
+    la.init(p.a, row_lo, nrows);
+    LB lb;
+    lb.init(p.b, e, n0, ncols);
+    typename LA::Data a0, a1;
+    typename LB::Data b0, b1;
+    const int nk = p.K / kBK;
+    la.load(a0, 0);
+    lb.load(b0, 0);
+    if (nk > 1) {
+      la.load(a1, kBK);
+      lb.load(b1, kBK);
+    }
+    la.store(a0, Ab);
+    lb.store(b0, Bb);
+    __syncthreads();
+
+    // steady state: step kt computes stage kt & 1, stores k-step kt + 1 (loaded
+    // one step earlier) into the other stage and loads k-step kt + 2 into the
+    // register set it just freed; two steps per iteration keep the register
+    // sets static.
+    auto step_pf = [&](int kt, typename LA::Data& acur, typename LB::Data& bcur, const typename LA::Data& anxt,
+                       const typename LB::Data& bnxt) {
+      la.load(acur, (kt + 2) * kBK);
+      lb.load(bcur, (kt + 2) * kBK);
+      mma_kstep_pf<TM, TN>(Ab + (kt & 1) * kStageA, Bb + (kt & 1) * kStageB, wm0, wn0, acc);
+      __syncthreads();
+      la.store(anxt, Ab + ((kt + 1) & 1) * kStageA);
+      lb.store(bnxt, Bb + ((kt + 1) & 1) * kStageB);
+      __syncthreads();
+    };
+    const int n_pf = nk - 2;
+    int kt = 0;
+    for (; kt + 1 < n_pf; kt += 2) {
+      step_pf(kt, a0, b0, a1, b1);
+      step_pf(kt + 1, a1, b1, a0, b0);
+    }
+    if (kt < n_pf) {  // odd count: kt even
+      step_pf(kt, a0, b0, a1, b1);
+      ++kt;
+    }
+    for (; kt < nk; ++kt) {
+      mma_kstep_pf<TM, TN>(Ab + (kt & 1) * kStageA, Bb + (kt & 1) * kStageB, wm0, wn0, acc);
+      __syncthreads();
+      if (kt + 1 < nk) {
+        if (kt & 1) {
+          la.store(a0, Ab + ((kt + 1) & 1) * kStageA);
+          lb.store(b0, Bb + ((kt + 1) & 1) * kStageB);
+        } else {
+          la.store(a1, Ab + ((kt + 1) & 1) * kStageA);
+          lb.store(b1, Bb + ((kt + 1) & 1) * kStageB);
+        }
+      }
+      __syncthreads();
+    }
+  }
+  if constexpr (BXK != NONE) {
+    if (p.kx > 0) {
+      Loader<BM, ROWS_BF16, NT> la;
+      Loader<BN, BXK, NT> lb;
+      la.init(p.ax, 0, row_lo, nrows, p.kx);
+      if constexpr (BXK == ROWS_BF16)
+        lb.init(p.bx, e, n0, ncols, p.kx);
+      else
+        lb.init(p.bx, e, n0, ncols, 0, p.kx);
+      run_segment<Loader<BM, ROWS_BF16, NT>, Loader<BN, BXK, NT>, TM, TN>(la, lb, p.kx, Ab, Bb, wm0, wn0, acc);
+    }
+  }
+
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int col = wn0 + tn * 32 + (lane & 31);
+      if (col >= ncols) continue;
+      const int n = n0 + col;
+      const float bv = p.bias ? p.bias[e * p.bias_estride + n] : 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = wm0 + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        if (row >= nrows) continue;
+        const int64_t gr = row_lo + row;
+        float v = acc[tm][tn][r] + bv;
+        if (p.gammas)
+          v *= p.gammas_f32 ? ((const float*)p.gammas)[gr] : af3_bf16_to_f32(((const uint16_t*)p.gammas)[gr]);
+        p.c[gr * p.ldc + n] = (uint16_t)af3_f32_to_bf16(v);
+      }
+    }
   }
 }
 
@@ -569,29 +1048,53 @@ inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // exported entry points
 // ---------------------------------------------------------------------------
 
+template <int BM, int BN, int WM, int WN>
+static void launch_gemm3(bool trans, int max_tiles, int N, hipStream_t stream, Params p) {
+  p.n_nblk = (N + BN - 1) / BN;
+  dim3 grid(max_tiles * p.n_nblk);
+  if (!trans)
+    hipLaunchKernelGGL((gemm3_kernel<BM, BN, WM, WN, ROWS_FP4, ROWS_BF16>), grid, dim3(WM * WN * 64), 0, stream, p);
+  else
+    hipLaunchKernelGGL((gemm3_kernel<BM, BN, WM, WN, COLS_FP4, COLS_BF16>), grid, dim3(WM * WN * 64), 0, stream, p);
+}
+
+template <int BM, int BN, int WM, int WN>
+static void launch_gemm2(bool trans, int max_tiles, int N, hipStream_t stream, Params p) {
+  p.n_nblk = (N + BN - 1) / BN;
+  dim3 grid(max_tiles * p.n_nblk);
+  if (!trans)
+    hipLaunchKernelGGL((gemm2_kernel<BM, BN, WM, WN, ROWS_FP4, ROWS_BF16>), grid, dim3(WM * WN * 64), 0, stream, p);
+  else
+    hipLaunchKernelGGL((gemm2_kernel<BM, BN, WM, WN, COLS_FP4, COLS_BF16>), grid, dim3(WM * WN * 64), 0, stream, p);
+}
+
 // Grouped GEMM through frozen MXFP4 expert weights (A6/A8/A9/A11).
 //   trans_w = 0: Y[r][n] = sum_k X[a(r)][k] W[e][n][k]   W blocks [E][N][K/32][16]
 //   trans_w = 1: Y[r][n] = sum_k X[a(r)][k] W[e][k][n]   W blocks [E][K][N/32][16]
 //   optional extension (expert LoRA):  + sum_j L[r][j] Bx[e][n][j] (trans 0) or Bx[e][j][n] (trans 1)
 //   then v = (acc + bias[e][n]) * gammas[r] -> bf16 Y[r][n]
 // a(r) = gather ? gather[r] / gather_div : r.  Rows r are expert-sorted; expert
-// e owns rows [token_offs[e], token_offs[e+1]); block_pid_map is the BM=128
-// map of af3_expt_data; grid.x = max_tiles.
+// e owns rows [token_offs[e], token_offs[e+1]); block_pid_map is the map of
+// af3_expt_data for BM = block_m; grid.x = max_tiles.  tile_cfg selects the
+// block tile (0 = default for block_m; see the table below).
 extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
                             const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
-                            const void* gammas, int gammas_f32, const uint16_t* lora_l, int64_t ld_l, const uint16_t* lora_b,
-                            int lora_r, const int32_t* token_offs, const int32_t* block_pid_map, int max_tiles,
-                            int n_expts, int N, int K, uint16_t* y, int64_t ldy, void* stream_) {
+                            const void* gammas, int gammas_f32, const uint16_t* lora_l, int64_t ld_l,
+                            const uint16_t* lora_b, int lora_r, const int32_t* token_offs, const int32_t* block_pid_map,
+                            const int32_t* tile_offs, int max_tiles, int block_m, int tile_cfg, int n_expts, int N,
+                            int K, uint16_t* y, int64_t ldy, void* stream_) {
   hipStream_t stream = (hipStream_t)stream_;
   AF3_REQUIRE(N > 0 && K > 0 && n_expts > 0 && max_tiles >= 0, "moe_gemm: bad sizes N=%d K=%d E=%d", N, K, n_expts);
   if (max_tiles == 0) return 0;
-  AF3_REQUIRE(x && w_blocks && w_scales && token_offs && block_pid_map && y, "moe_gemm: null pointer");
+  AF3_REQUIRE(x && w_blocks && w_scales && token_offs && block_pid_map && tile_offs && y, "moe_gemm: null pointer");
+  AF3_REQUIRE((int64_t)max_tiles * ((N + 127) / 128) < 0x7fffffffLL, "moe_gemm: grid too large");
   AF3_REQUIRE(K % 32 == 0 && N % 32 == 0, "moe_gemm: N and K must be multiples of 32 (N=%d K=%d)", N, K);
   AF3_REQUIRE(ldx % 8 == 0 && al16(x), "moe_gemm: x must be 16-byte aligned with ld % 8 == 0");
   AF3_REQUIRE(lora_r >= 0 && lora_r <= 64, "moe_gemm: lora rank %d unsupported (max 64)", lora_r);
   AF3_REQUIRE(lora_r == 0 || (lora_l && lora_b && ld_l % 8 == 0 && lora_r % 8 == 0 && al16(lora_l) && al16(lora_b)),
               "moe_gemm: LoRA operands must be 16-byte aligned, rank % 8 == 0");
   AF3_REQUIRE(al16(w_blocks), "moe_gemm: weight blocks must be 16-byte aligned");
+  AF3_REQUIRE(block_m == 128 || block_m == 256, "moe_gemm: block_m must be 128 or 256 (got %d)", block_m);
   Params p{};
   const int G_k = K / 32, G_n = N / 32;
   p.a = make_bf16(x, ldx, 0, gather_indx, gather_div);
@@ -618,6 +1121,7 @@ extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gathe
   }
   p.offs = token_offs;
   p.tile_map = block_pid_map;
+  p.tile_offs = tile_offs;
   p.E = n_expts;
   p.bias = bias;
   p.bias_estride = N;
@@ -627,13 +1131,47 @@ extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gathe
   p.c = y;
   p.ldc = ldy;
   p.N = N;
-  dim3 grid(max_tiles, (N + 127) / 128);
-  if (trans_w == 0)
-    hipLaunchKernelGGL((rowtile_kernel<128, 128, 2, 2, ROWS_BF16, ROWS_FP4, ROWS_BF16, ROWS_BF16>), grid,
-                       dim3(kThreads), 0, stream, p);
-  else
-    hipLaunchKernelGGL((rowtile_kernel<128, 128, 2, 2, ROWS_BF16, COLS_FP4, ROWS_BF16, COLS_BF16>), grid,
-                       dim3(kThreads), 0, stream, p);
+  const bool trans = trans_w != 0;
+  // tile configurations: (BM, BN, waves)
+  //   1: 128x128, 2x2    2: 128x256, 2x2    3: 256x128, 2x2
+  //   4: 256x256, 2x4    5: 128x256, 2x4    6: 256x256, 2x2
+  //   7: 256x256, 2x2 two-deep prefetch     10: 128x256, 2x2 two-deep prefetch
+  //   11: 128x128, 2x2 two-deep prefetch    12: 256x128, 2x2 two-deep prefetch
+  //   9: single-buffered 128x128 (reference kernel)
+  int cfg = tile_cfg;
+  if (cfg == 0) cfg = block_m == 256 ? 4 : 2;
+  const bool bm_ok = (cfg == 3 || cfg == 4 || cfg == 6 || cfg == 7 || cfg == 12) ? block_m == 256 : block_m == 128;
+  AF3_REQUIRE(bm_ok, "moe_gemm: tile_cfg %d does not match block_m %d", cfg, block_m);
+  if (K % kBK != 0) cfg = 9;  // direct A loads need whole 64-deep k-steps
+  if (cfg == 9 && block_m != 128) {
+    af3::set_error("moe_gemm: K %% 64 != 0 needs block_m 128");
+    return AF3_EINVAL;
+  }
+  switch (cfg) {
+    case 1: launch_gemm2<128, 128, 2, 2>(trans, max_tiles, N, stream, p); break;
+    case 2: launch_gemm2<128, 256, 2, 2>(trans, max_tiles, N, stream, p); break;
+    case 3: launch_gemm2<256, 128, 2, 2>(trans, max_tiles, N, stream, p); break;
+    case 4: launch_gemm2<256, 256, 2, 4>(trans, max_tiles, N, stream, p); break;
+    case 5: launch_gemm2<128, 256, 2, 4>(trans, max_tiles, N, stream, p); break;
+    case 6: launch_gemm2<256, 256, 2, 2>(trans, max_tiles, N, stream, p); break;
+    case 7: launch_gemm3<256, 256, 2, 2>(trans, max_tiles, N, stream, p); break;
+    case 10: launch_gemm3<128, 256, 2, 2>(trans, max_tiles, N, stream, p); break;
+    case 11: launch_gemm3<128, 128, 2, 2>(trans, max_tiles, N, stream, p); break;
+    case 12: launch_gemm3<256, 128, 2, 2>(trans, max_tiles, N, stream, p); break;
+    case 9: {
+      dim3 grid(max_tiles, (N + 127) / 128);
+      if (!trans)
+        hipLaunchKernelGGL((rowtile_kernel<128, 128, 2, 2, ROWS_BF16, ROWS_FP4, ROWS_BF16, ROWS_BF16>), grid,
+                           dim3(kThreads), 0, stream, p);
+      else
+        hipLaunchKernelGGL((rowtile_kernel<128, 128, 2, 2, ROWS_BF16, COLS_FP4, ROWS_BF16, COLS_BF16>), grid,
+                           dim3(kThreads), 0, stream, p);
+      break;
+    }
+    default:
+      af3::set_error("moe_gemm: unknown tile_cfg %d", tile_cfg);
+      return AF3_EINVAL;
+  }
   return af3::check_launch("moe_gemm");
 }
 

@@ -95,13 +95,16 @@ int af3_expt_data(const int32_t* hist, int n_expts_tot, const int32_t* block_ms_
  *   + sum_j L[r][j] Bx[e][n][j] (trans 0) / Bx[e][j][n] (trans 1)  if lora_r > 0
  *   Y = bf16((acc + bias[e][n]) * gammas[r])   (bias fp32 [E][N], gammas bf16 or fp32)
  * a(r) = gather_indx ? gather_indx[r] / gather_div : r; rows r of expert e
- * are [token_offs[e], token_offs[e+1]); block_pid_map is the BM = 128 map;
- * launches max_tiles x ceil(N/128) workgroups. */
+ * are [token_offs[e], token_offs[e+1]); block_pid_map / tile_offs are the
+ * af3_expt_data map and token_offs_pad for BM = block_m (128 or 256); the
+ * number of valid m-tiles is read from tile_offs[n_expts] on the device.
+ * tile_cfg picks the block tile (0 = default for block_m). */
 int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
                  const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
                  const void* gammas, int gammas_f32, const uint16_t* lora_l, int64_t ld_l, const uint16_t* lora_b,
-                 int lora_r, const int32_t* token_offs, const int32_t* block_pid_map, int max_tiles, int n_expts,
-                 int N, int K, uint16_t* y, int64_t ldy, void* stream);
+                 int lora_r, const int32_t* token_offs, const int32_t* block_pid_map, const int32_t* tile_offs,
+                 int max_tiles, int block_m, int tile_cfg, int n_expts, int N, int K, uint16_t* y, int64_t ldy,
+                 void* stream);
 
 /* Scatter-sum over each token's K expert rows (the k-reduction matmul_ogs
  * performs for scatter_indx, quantization.py:532-541 and 409-418):
