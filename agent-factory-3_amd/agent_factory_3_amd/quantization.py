@@ -537,6 +537,9 @@ def mlp_forward(self, hidden_states, router_indices=None):
         route = routing_torch_dist
     else:
         route = routing
+    if router_indices is None:  # indices set by enable_routing_replay's decoder wrapper
+        from .routing_replay import current_router_indices
+        router_indices = current_router_indices(self)
     batch_size = hidden_states.shape[0]
     hidden_states = hidden_states.reshape(-1, self.router.hidden_dim)
     router_logits = nn.functional.linear(hidden_states, self.router.weight, self.router.bias)
@@ -578,3 +581,60 @@ def replace_with_dequant_experts(model, quantization_config=None, modules_to_not
         import warnings
         warnings.warn("No expert modules found for MXFP4 dequant conversion.")
     return model
+
+
+# ---------------------------------------------------------------------------
+# transformers weight-loading conversions (quantization.py:175-221)
+# ---------------------------------------------------------------------------
+try:
+    from transformers.core_model_loading import ConversionOps as _ConversionOps
+    from transformers.quantizers.quantizers_utils import get_module_from_name as _get_module_from_name
+except ImportError:  # pragma: no cover - only the HF loading integration needs these
+    _ConversionOps = object
+    _get_module_from_name = None
+
+
+def _first(v):
+    return v[0] if isinstance(v, list) else v
+
+
+class Mxfp4Fp8DequantQuantize(_ConversionOps):
+    """Quantize-on-load is not supported (checkpoints are pre-quantized)."""
+
+    def __init__(self, hf_quantizer):
+        self.hf_quantizer = hf_quantizer
+
+    def convert(self, input_dict, model=None, missing_keys=None, full_layer_name=None, **kwargs):
+        return {}
+
+
+class Mxfp4Fp8DequantDequantize(_ConversionOps):
+    """dequantize=True fallback: load the full bf16 weight ([E, K, N], transposed)."""
+
+    def __init__(self, hf_quantizer):
+        self.hf_quantizer = hf_quantizer
+
+    def convert(self, input_dict, model=None, full_layer_name=None, missing_keys=None, **kwargs):
+        blocks = _first(input_dict["_blocks"])
+        scales = _first(input_dict["_scales"])
+        if not blocks.is_cuda:
+            blocks, scales = blocks.cuda(), scales.cuda()
+        return {full_layer_name: convert_moe_packed_tensors(blocks, scales)}
+
+
+class Mxfp4Fp8DequantDeserialize(_ConversionOps):
+    """Keep the checkpoint's MXFP4 blocks/scales as-is (bf16-container Parameters)."""
+
+    def __init__(self, hf_quantizer):
+        self.hf_quantizer = hf_quantizer
+
+    def convert(self, input_dict, model=None, full_layer_name=None, missing_keys=None, **kwargs):
+        blocks = _first(input_dict["_blocks"])
+        scales = _first(input_dict["_scales"])
+        module, _ = _get_module_from_name(model, full_layer_name)
+        proj = "gate_up_proj" if "gate_up_proj" in full_layer_name else "down_proj"
+        _store_mxfp4_weights(blocks, scales, module, proj, blocks.device)
+        if missing_keys is not None:
+            missing_keys.discard(f"{full_layer_name}")
+        module._is_hf_initialized = True
+        return {}
