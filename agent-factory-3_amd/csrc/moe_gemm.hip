@@ -26,6 +26,8 @@
 //              optional second k segment (the expert LoRA term) is appended.
 //   wgrad      blockIdx.x -> (expert, m block, n block); the k range is the
 //              expert's rows: G[e] = A(rows(e))^T B(rows(e)).
+#include <type_traits>
+
 #include "af3_common.h"
 
 namespace {
@@ -69,6 +71,7 @@ struct Params {
   int chunk_rows;           // wgrad rows per chunk
   float* partials;          // wgrad fp32 partials [chunk][M][N]
   int M, N;                 // output extents (M used by wgrad; rows come from offs in row tiles)
+  int group_m;              // work-item grouping (m-tiles per group), gemm4
 };
 
 __device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
@@ -846,6 +849,365 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm3_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------
+// gemm4: forward grouped GEMM through MXFP4 weights packed along k
+// (W[e][n][k/32][16]).  256 threads = 4 waves in a 2x2 arrangement of 128x128
+// wave tiles over a 256x256 output tile.
+//   * A (activation rows, optionally gathered) goes global->LDS directly
+//     (global_load_lds_dwordx4) into a 3-stage ring of [256][64] bf16 tiles
+//     (16-byte chunks XOR-swizzled by row, as lds_off);
+//   * B stays packed in LDS: per 64-deep k-step the two MXFP4 blocks (32 B)
+//     of each of the 256 weight rows, also loaded global->LDS, 3-stage ring;
+//   * the e8m0 scale bytes of the tile's weight rows are loaded once per
+//     work item;
+//   * each wave dequantises its own 128 columns in registers
+//     (v_cvt_scalef32_pk_bf16_fp4) straight into MFMA B fragments, so the bf16
+//     weight never exists in LDS or HBM.
+// k is permuted inside a k-step so that a lane's B fragment is one whole MXFP4
+// block: lane (r, h) of v_mfma_f32_32x32x16_bf16 feeds k = 32 h + 8 s + (0..7)
+// at sub-step s, i.e. A chunk 4 h + s and dword s of block 2 kt + h.  Both
+// operands use the same permutation, so the dot products are unchanged.
+// Loads run two k-steps ahead; each wave waits for its own loads of the
+// current stage (exact vmcnt: 10 DMA instructions per wave per stage), then
+// one barrier per k-step publishes the stage and frees the oldest one.
+// Rows / columns past the tile's valid extent are loaded from valid addresses
+// and their 32x32 MFMA sub-tiles are skipped (wave-uniform), so a short tail
+// tile of an expert costs about its valid rows, not 256.
+// ---------------------------------------------------------------------------
+constexpr int kG4Stages = 3;
+constexpr int kG4Rows = 256;               // BM = BN
+constexpr int kG4AStage = kG4Rows * kBK;   // bf16 elements per A stage (32 KB)
+constexpr int kG4BStage = kG4Rows * 32;    // bytes per packed-B stage (8 KB)
+constexpr int kG4MaxG = 128;               // scale bytes per weight row (K <= 4096)
+constexpr int kG4LdsBytes = kG4Stages * (kG4AStage * 2 + kG4BStage) + kG4Rows * kG4MaxG;  // 152 KB
+static_assert(kG4LdsBytes >= 256 * 512 + 1024, "the epilogue reuses the LDS for the bf16 tile + row gammas");
+static_assert(kG4LdsBytes <= 160 * 1024, "gfx950 LDS per workgroup");
+
+// Epilogue of a 256x256 tile computed by 4 waves (2x2) of 4x4 32x32 MFMA
+// sub-tiles: v = (acc + bias[n]) * gamma[row] -> bf16, staged through LDS as
+// a [256][256] bf16 tile (16-byte chunks XOR-swizzled so the two row groups
+// of an MFMA output store hit disjoint banks), then written out with one
+// 16-byte store per chunk (a wave writes two whole 512-byte rows at a time).
+// `lds` must hold >= 129 KB; every wave must have finished reading its
+// operands from it.
+__device__ __forceinline__ int g4_c_off(int row, int col) {  // byte offset of C[row][col] in the LDS tile
+  return row * 512 + ((((col >> 3) ^ (((row >> 2) & 1) << 2))) << 4) + ((col & 7) << 1);
+}
+
+__device__ __forceinline__ void g4_epilogue(const Params& p, uint8_t* lds, af3_f32x16 acc[4][4], int e, int row_lo,
+                                            int nrows, int n0, int ncols, int wm0, int wn0) {
+  const int lane = threadIdx.x & 63;
+  const int lr = lane & 31, lh = lane >> 5;
+  float* const gl = (float*)(lds + 256 * 512);  // per-row gammas
+  __syncthreads();
+  {
+    const int t = threadIdx.x;
+    float gv = 1.f;
+    if (p.gammas && t < nrows) {
+      const int64_t gr = row_lo + t;
+      gv = p.gammas_f32 ? ((const float*)p.gammas)[gr] : af3_bf16_to_f32(((const uint16_t*)p.gammas)[gr]);
+    }
+    gl[t] = gv;
+  }
+  float bv[4];
+#pragma unroll
+  for (int tn = 0; tn < 4; ++tn) {
+    const int col = wn0 + tn * 32 + lr;
+    bv[tn] = (p.bias && col < ncols) ? p.bias[e * p.bias_estride + n0 + col] : 0.f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int tm = 0; tm < 4; ++tm) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row0 = wm0 + tm * 32 + j * 8 + lh * 4;
+      const float4 g = *(const float4*)(gl + row0);
+      const float gq[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+      for (int tn = 0; tn < 4; ++tn) {
+        const int col = wn0 + tn * 32 + lr;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float v = (acc[tm][tn][j * 4 + q] + bv[tn]) * gq[q];
+          *(uint16_t*)(lds + g4_c_off(row0 + q, col)) = (uint16_t)af3_f32_to_bf16(v);
+        }
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll 4
+  for (int i = 0; i < 32; ++i) {
+    const int id = i * 256 + threadIdx.x;
+    const int row = id >> 5, ch = id & 31;
+    if (row < nrows && ch * 8 < ncols) {
+      const af3_u32x4 v = *(const af3_u32x4*)(lds + row * 512 + ((ch ^ (((row >> 2) & 1) << 2)) << 4));
+      *(af3_u32x4*)(p.c + (int64_t)(row_lo + row) * p.ldc + n0 + ch * 8) = v;
+    }
+  }
+}
+
+// byte offset of (weight row n, block h) inside a packed-B stage: four rows
+// share a 128-byte line, the block bit is flipped every 8 rows, so the 16
+// lanes of an MFMA fragment read hit 16 distinct 16-byte bank groups
+__device__ __forceinline__ int g4_b_off(int n, int h) {
+  return (n >> 2) * 128 + (((h << 2) | (n & 3)) ^ (((n >> 3) & 1) << 2)) * 16;
+}
+
+// The k-loop's global->LDS copies are issued through inline assembly so that
+// the compiler's wait-count insertion, which cannot tell the LDS stages apart
+// and would wait for every copy in flight before any LDS read, leaves them
+// alone; the loop waits for them explicitly (vmcnt) and publishes a stage with
+// a bare s_barrier.  All three are compiler memory barriers.
+__device__ __forceinline__ void g4_dma16(const void* gptr, uint32_t lds_byte_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_byte_addr)
+               : "memory", "m0");
+}
+#define AF3_ASM_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
+#define AF3_ASM_BARRIER() asm volatile("s_barrier" ::: "memory")
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+__device__ __forceinline__ af3_bf16x8 g4_cvt(uint32_t v, float sc) {
+  af3_u32x4 o;
+  o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, sc, 0));
+  o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, sc, 1));
+  o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, sc, 2));
+  o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, sc, 3));
+  return __builtin_bit_cast(af3_bf16x8, o);
+}
+
+__device__ __forceinline__ af3_bf16x8 g4_int(uint32_t v, uint32_t scale) {
+  uint32_t o[4];
+  af3_dequant_u32_int(v, scale, o);
+  return __builtin_bit_cast(af3_bf16x8, af3_u32x4{o[0], o[1], o[2], o[3]});
+}
+
+// B fragment of sub-step s: dword s of the lane's MXFP4 block -> 8 bf16.
+// EXACT (work items whose tile holds a scale byte outside [2, 252], which
+// normal quantisers never produce): the integer restatement for those lanes.
+template <bool EXACT>
+__device__ __forceinline__ af3_bf16x8 g4_bfrag(uint32_t v, uint32_t sc, float scf) {
+  if constexpr (EXACT) {
+    if (sc - 2u > 250u) return g4_int(v, sc);
+  }
+  return g4_cvt(v, scf);
+}
+
+// one 64-deep k-step of a wave's 128x128 tile; FULL: every sub-tile live.
+// Instruction order is fixed by scheduling barriers: each MFMA is followed
+// by one conversion of the next sub-step's B fragments (and, every sixth
+// MFMA, one of the ten global->LDS copies of the k-step two ahead), so the
+// conversions and copy issues run in the MFMA shadow instead of stalling the
+// matrix pipe; the 4 A-fragment LDS reads of sub-step s + 1 are issued ahead
+// of the MFMAs of sub-step s.
+template <bool FULL, bool EXACT, class Dma>
+__device__ __forceinline__ void g4_kstep(const uint16_t* as, const af3_u32x4 bp[4], const uint32_t sc[4], int wm0,
+                                         int tm_live, int tn_live, af3_f32x16 acc[4][4], Dma&& dma) {
+  const int lane = threadIdx.x & 63;
+  const int lr = lane & 31, lh = lane >> 5;
+  float scf[4];
+#pragma unroll
+  for (int tn = 0; tn < 4; ++tn) scf[tn] = __uint_as_float(sc[tn] << 23);
+  af3_bf16x8 af[2][4], bf[2][4];
+#pragma unroll
+  for (int tm = 0; tm < 4; ++tm) af[0][tm] = *(const af3_bf16x8*)(as + lds_off(wm0 + tm * 32 + lr, lh * 4));
+#pragma unroll
+  for (int tn = 0; tn < 4; ++tn) bf[0][tn] = g4_bfrag<EXACT>(bp[tn][0], sc[tn], scf[tn]);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int c = s & 1, nx = c ^ 1;
+    __builtin_amdgcn_sched_barrier(0);
+    if (s + 1 < 4) {
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm)
+        af[nx][tm] = *(const af3_bf16x8*)(as + lds_off(wm0 + tm * 32 + lr, lh * 4 + s + 1));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int tm = i >> 2, tn = i & 3;
+      if (FULL || (tm < tm_live && tn < tn_live))
+        acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[c][tm], bf[c][tn], acc[tm][tn], 0, 0, 0);
+      if (s + 1 < 4 && (i & 3) == 3)
+        bf[nx][i >> 2] = g4_bfrag<EXACT>(bp[i >> 2][s + 1], sc[i >> 2], scf[i >> 2]);
+      const int q = s * 16 + i;
+      if (q % 6 == 2 && q / 6 < 10) dma(q / 6);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
+template <int BXK>
+__global__ __launch_bounds__(256) void gemm4_fwd_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kG4LdsBytes];
+  uint16_t* const As = (uint16_t*)lds;                          // 3 x 32 KB
+  uint8_t* const Bs = lds + kG4Stages * kG4AStage * 2;          // 3 x 8 KB
+  uint8_t* const Ss = Bs + kG4Stages * kG4BStage;               // <= 32 KB
+
+  const int NN = p.n_nblk;
+  const int W = p.tile_offs[p.E] * NN;  // valid work items (device-side tile count)
+  const int b = blockIdx.x;
+  if (b >= W) return;
+  // XCD-aware order: consecutive workgroups go to the 8 XCDs in turn, so
+  // workgroup b takes work item (b % 8) * (W8 / 8) + b / 8 and each XCD walks a
+  // contiguous range.  Inside the range, items go in groups of G m-tiles x all
+  // n-tiles with the m-tile fastest, so the ~32 items an XCD runs at once
+  // share G activation tiles and 32 / G weight tiles through its L2 (with the
+  // n-tile fastest every m-tile would re-read the whole expert weight, which
+  // does not fit in the L2).
+  const int W8 = W & ~7;
+  const int w = b < W8 ? (b & 7) * (W8 >> 3) + (b >> 3) : b;
+  const int Mt = W / NN;
+  const int GM = p.group_m > 0 ? p.group_m : 1;
+  const int first_m = (w / (GM * NN)) * GM;
+  const int gsz = min(GM, Mt - first_m);
+  const int local = w - first_m * NN;
+  const int mt = first_m + local % gsz, nt = local / gsz;
+  const int32_t ent = p.tile_map[mt];
+  if (ent < 0) return;
+  const int e = ent & 0xFFFF, blk = ent >> 16;
+  const int row_lo = p.offs[e] + blk * kG4Rows;
+  const int nrows = min(kG4Rows, p.offs[e + 1] - row_lo);
+  if (nrows <= 0) return;
+  const int n0 = nt * kG4Rows;
+  const int ncols = min(kG4Rows, p.N - n0);
+  const int G = p.K >> 5;
+  const int nk = p.K / kBK;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar)
+  const int lr = lane & 31, lh = lane >> 5;
+  const int wm0 = (wave >> 1) * 128, wn0 = (wave & 1) * 128;
+  const int tm_live = min(4, max(0, (nrows - wm0 + 31) >> 5));
+  const int tn_live = min(4, max(0, (ncols - wn0 + 31) >> 5));
+  const bool full = tm_live == 4 && tn_live == 4;
+
+  // DMA sources: A rows (8 instructions per wave per stage, 8 rows each)
+  const uint16_t* arow[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = (wave * 8 + i) * 8 + (lane >> 3);
+    int64_t src = row_lo + (row < nrows ? row : 0);
+    if (p.a.gather) src = p.a.gather[src] / p.a.gdiv;
+    arow[i] = (const uint16_t*)p.a.ptr + src * p.a.ld + (((lane & 7) ^ swz(row)) << 3);
+  }
+  // packed B (2 instructions per wave per stage, 32 weight rows each)
+  const uint8_t* bsrc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int row4 = (wave * 2 + j) * 8 + (lane >> 3);
+    const int lc = (lane & 7) ^ (((row4 >> 1) & 1) << 2);
+    int nn = row4 * 4 + (lc & 3);
+    if (nn >= ncols) nn = 0;
+    bsrc[j] = (const uint8_t*)p.b.ptr + e * p.b.estride + (int64_t)(n0 + nn) * p.b.ld + (lc >> 2) * 16;
+  }
+  // scales of the tile's weight rows: [ncols][G] bytes, contiguous in memory
+  {
+    const uint8_t* sbase = p.b.scales + e * p.b.sestride + (int64_t)n0 * G;
+    const int nbytes = ncols * G;  // multiple of 32: ncols % 32 == 0
+    const int ninstr = (nbytes + 1023) >> 10;
+    for (int i = wave; i < ninstr; i += 4) {
+      int off = i * 1024 + lane * 16;
+      const int src = off < nbytes ? off : 0;
+      g4_dma16(sbase + src, __builtin_amdgcn_readfirstlane(lds_addr(Ss + i * 1024)));
+    }
+  }
+  // copy j (0..9) of k-step kt: 8 A instructions (8 rows each), 2 packed-B
+  auto issue_one = [&](int kt, int j) {
+    const int st = kt % kG4Stages;
+    if (j < 8) {
+      const uint32_t abase = __builtin_amdgcn_readfirstlane(lds_addr(As + st * kG4AStage + wave * 8 * 8 * kBK));
+      g4_dma16(arow[j] + kt * kBK, abase + j * 8 * kBK * 2);
+    } else {
+      const uint32_t bbase = __builtin_amdgcn_readfirstlane(lds_addr(Bs + st * kG4BStage + wave * 2 * 1024));
+      g4_dma16(bsrc[j - 8] + kt * 32, bbase + (j - 8) * 1024);
+    }
+  };
+  auto issue = [&](int kt) {
+#pragma unroll
+    for (int j = 0; j < 10; ++j) issue_one(kt, j);
+  };
+
+  af3_f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  issue(0);
+  if (nk > 1) issue(1);
+  // does the tile hold a scale byte outside [2, 252]?  (then the whole work
+  // item takes the exact integer dequantisation)
+  bool odd = false;
+  {
+    AF3_ASM_WAIT_VM(0);
+    AF3_ASM_BARRIER();
+    const int nbytes = ncols * G;
+    for (int i = threadIdx.x * 16; i < nbytes; i += 256 * 16) {
+      const af3_u32x4 v = *(const af3_u32x4*)(Ss + i);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) odd |= ((v[q] >> (8 * j)) & 0xFFu) - 2u > 250u;
+    }
+  }
+  odd = __syncthreads_or(odd);
+
+  auto kloop = [&](auto full_c, auto exact_c) {
+    constexpr bool FULL = decltype(full_c)::value, EXACT = decltype(exact_c)::value;
+    for (int kt = 0; kt < nk; ++kt) {
+      if (kt + 1 < nk)
+        AF3_ASM_WAIT_VM(10);
+      else
+        AF3_ASM_WAIT_VM(0);
+      AF3_ASM_BARRIER();
+      const bool pf = kt + 2 < nk;
+      const int st = kt % kG4Stages;
+      const uint16_t* as = As + st * kG4AStage;
+      const uint8_t* bs = Bs + st * kG4BStage;
+      af3_u32x4 bp[4];
+      uint32_t sc[4];
+#pragma unroll
+      for (int tn = 0; tn < 4; ++tn) {
+        const int n = wn0 + tn * 32 + lr;
+        bp[tn] = *(const af3_u32x4*)(bs + g4_b_off(n, lh));
+        sc[tn] = Ss[n * G + 2 * kt + lh];
+      }
+      g4_kstep<FULL, EXACT>(as, bp, sc, wm0, tm_live, tn_live, acc, [&](int j) {
+        if (pf) issue_one(kt + 2, j);
+      });
+    }
+  };
+  if (odd)
+    kloop(std::false_type{}, std::true_type{});
+  else if (full)
+    kloop(std::true_type{}, std::false_type{});
+  else
+    kloop(std::false_type{}, std::false_type{});
+
+  if constexpr (BXK != NONE) {
+    if (p.kx > 0) {  // expert-LoRA segment: + L[r] . Bx[e][n]^T, both bf16 through LDS
+      Loader<kG4Rows, ROWS_BF16, 256> la, lb;
+      la.init(p.ax, 0, row_lo, nrows, p.kx);
+      lb.init(p.bx, e, n0, ncols, p.kx);
+      for (int k0 = 0; k0 < p.kx; k0 += kBK) {
+        la.load(k0);
+        lb.load(k0);
+        __syncthreads();
+        la.store(As);
+        lb.store(As + kG4AStage);
+        __syncthreads();
+        mma_kstep<4, 4>(As, As + kG4AStage, wm0, wn0, acc);
+      }
+    }
+  }
+
+  g4_epilogue(p, lds, acc, e, row_lo, nrows, n0, ncols, wm0, wn0);
+}
+
+// ---------------------------------------------------------------------------
 // row-tile kernel: main GEMMs and the skinny LoRA row products
 // ---------------------------------------------------------------------------
 template <int BM, int BN, int WM, int WN, int AK, int BK_, int AXK, int BXK>
@@ -1058,6 +1420,12 @@ static void launch_gemm3(bool trans, int max_tiles, int N, hipStream_t stream, P
     hipLaunchKernelGGL((gemm3_kernel<BM, BN, WM, WN, COLS_FP4, COLS_BF16>), grid, dim3(WM * WN * 64), 0, stream, p);
 }
 
+static void launch_gemm4_fwd(int max_tiles, int N, hipStream_t stream, Params p) {
+  p.n_nblk = (N + kG4Rows - 1) / kG4Rows;
+  dim3 grid(max_tiles * p.n_nblk);
+  hipLaunchKernelGGL((gemm4_fwd_kernel<ROWS_BF16>), grid, dim3(256), 0, stream, p);
+}
+
 template <int BM, int BN, int WM, int WN>
 static void launch_gemm2(bool trans, int max_tiles, int N, hipStream_t stream, Params p) {
   p.n_nblk = (N + BN - 1) / BN;
@@ -1138,9 +1506,18 @@ extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gathe
   //   7: 256x256, 2x2 two-deep prefetch     10: 128x256, 2x2 two-deep prefetch
   //   11: 128x128, 2x2 two-deep prefetch    12: 256x128, 2x2 two-deep prefetch
   //   9: single-buffered 128x128 (reference kernel)
-  int cfg = tile_cfg;
-  if (cfg == 0) cfg = block_m == 256 ? 4 : 2;
-  const bool bm_ok = (cfg == 3 || cfg == 4 || cfg == 6 || cfg == 7 || cfg == 12) ? block_m == 256 : block_m == 128;
+  //   20: gemm4 forward (256x256, 4 waves of 128x128, packed MXFP4 in LDS,
+  //       three-stage global->LDS ring); tile_cfg / 100 = m-tiles per group
+  //       of the work order (default 4).  Default for trans_w 0 when its
+  //       alignment / size requirements hold.
+  int cfg = tile_cfg % 100;
+  const int group_m = tile_cfg / 100 > 0 ? tile_cfg / 100 : 4;
+  if (cfg == 0) {
+    const bool g4_ok = !trans && block_m == 256 && K % kBK == 0 && K / 32 <= kG4MaxG && al16(w_scales) && al16(y) &&
+                       ldy % 8 == 0;
+    cfg = g4_ok ? 20 : (block_m == 256 ? 4 : 2);
+  }
+  const bool bm_ok = (cfg == 3 || cfg == 4 || cfg == 6 || cfg == 7 || cfg == 12 || cfg == 20) ? block_m == 256 : block_m == 128;
   AF3_REQUIRE(bm_ok, "moe_gemm: tile_cfg %d does not match block_m %d", cfg, block_m);
   if (K % kBK != 0) cfg = 9;  // direct A loads need whole 64-deep k-steps
   if (cfg == 9 && block_m != 128) {
@@ -1158,6 +1535,14 @@ extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gathe
     case 10: launch_gemm3<128, 256, 2, 2>(trans, max_tiles, N, stream, p); break;
     case 11: launch_gemm3<128, 128, 2, 2>(trans, max_tiles, N, stream, p); break;
     case 12: launch_gemm3<256, 128, 2, 2>(trans, max_tiles, N, stream, p); break;
+    case 20:
+      p.group_m = group_m;
+      AF3_REQUIRE(!trans && block_m == 256 && K % kBK == 0 && K / 32 <= kG4MaxG && al16(w_scales) && al16(y) &&
+                      ldy % 8 == 0,
+                  "moe_gemm: tile_cfg 20 needs trans_w 0, block_m 256, K %% 64 == 0, K <= %d, 16-byte aligned scales/y",
+                  kG4MaxG * 32);
+      launch_gemm4_fwd(max_tiles, N, stream, p);
+      break;
     case 9: {
       dim3 grid(max_tiles, (N + 127) / 128);
       if (!trans)
