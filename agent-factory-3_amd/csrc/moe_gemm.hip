@@ -893,14 +893,22 @@ __device__ __forceinline__ int g4_c_off(int row, int col) {  // byte offset of C
   return row * 512 + ((((col >> 3) ^ (((row >> 2) & 1) << 2))) << 4) + ((col & 7) << 1);
 }
 
-__device__ __forceinline__ void g4_epilogue(const Params& p, uint8_t* lds, af3_f32x16 acc[4][4], int e, int row_lo,
+// Column of MFMA sub-tile tn, lane column lr inside a wave's 128 columns:
+// plain (32 consecutive columns per sub-tile) or PAIRED (sub-tiles 2t and
+// 2t + 1 hold the even / odd columns of 64 consecutive columns).
+template <bool PAIRED>
+__device__ __forceinline__ int g4_col(int tn, int lr) {
+  return PAIRED ? 64 * (tn >> 1) + 2 * lr + (tn & 1) : tn * 32 + lr;
+}
+
+template <bool PAIRED = false, int TM = 4, int TN = 4, int NT = 256>
+__device__ __forceinline__ void g4_epilogue(const Params& p, uint8_t* lds, af3_f32x16 acc[TM][TN], int e, int row_lo,
                                             int nrows, int n0, int ncols, int wm0, int wn0) {
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
   float* const gl = (float*)(lds + 256 * 512);  // per-row gammas
   __syncthreads();
-  {
-    const int t = threadIdx.x;
+  for (int t = threadIdx.x; t < 256; t += NT) {
     float gv = 1.f;
     if (p.gammas && t < nrows) {
       const int64_t gr = row_lo + t;
@@ -908,23 +916,23 @@ __device__ __forceinline__ void g4_epilogue(const Params& p, uint8_t* lds, af3_f
     }
     gl[t] = gv;
   }
-  float bv[4];
+  float bv[TN];
 #pragma unroll
-  for (int tn = 0; tn < 4; ++tn) {
-    const int col = wn0 + tn * 32 + lr;
+  for (int tn = 0; tn < TN; ++tn) {
+    const int col = wn0 + g4_col<PAIRED>(tn, lr);
     bv[tn] = (p.bias && col < ncols) ? p.bias[e * p.bias_estride + n0 + col] : 0.f;
   }
   __syncthreads();
 #pragma unroll
-  for (int tm = 0; tm < 4; ++tm) {
+  for (int tm = 0; tm < TM; ++tm) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int row0 = wm0 + tm * 32 + j * 8 + lh * 4;
       const float4 g = *(const float4*)(gl + row0);
       const float gq[4] = {g.x, g.y, g.z, g.w};
 #pragma unroll
-      for (int tn = 0; tn < 4; ++tn) {
-        const int col = wn0 + tn * 32 + lr;
+      for (int tn = 0; tn < TN; ++tn) {
+        const int col = wn0 + g4_col<PAIRED>(tn, lr);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const float v = (acc[tm][tn][j * 4 + q] + bv[tn]) * gq[q];
@@ -935,8 +943,8 @@ __device__ __forceinline__ void g4_epilogue(const Params& p, uint8_t* lds, af3_f
   }
   __syncthreads();
 #pragma unroll 4
-  for (int i = 0; i < 32; ++i) {
-    const int id = i * 256 + threadIdx.x;
+  for (int i = 0; i < 32 * 256 / NT; ++i) {
+    const int id = i * NT + threadIdx.x;
     const int row = id >> 5, ch = id & 31;
     if (row < nrows && ch * 8 < ncols) {
       const af3_u32x4 v = *(const af3_u32x4*)(lds + row * 512 + ((ch ^ (((row >> 2) & 1) << 2)) << 4));
@@ -963,6 +971,8 @@ __device__ __forceinline__ void g4_dma16(const void* gptr, uint32_t lds_byte_add
 }
 #define AF3_ASM_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
 #define AF3_ASM_BARRIER() asm volatile("s_barrier" ::: "memory")
+// the same after this wave's own LDS stores have completed
+#define AF3_ASM_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
@@ -993,52 +1003,58 @@ __device__ __forceinline__ af3_bf16x8 g4_bfrag(uint32_t v, uint32_t sc, float sc
   return g4_cvt(v, scf);
 }
 
-// one 64-deep k-step of a wave's 128x128 tile; FULL: every sub-tile live.
-// Instruction order is fixed by scheduling barriers: each MFMA is followed
-// by one conversion of the next sub-step's B fragments (and, every sixth
-// MFMA, one of the ten global->LDS copies of the k-step two ahead), so the
-// conversions and copy issues run in the MFMA shadow instead of stalling the
-// matrix pipe; the 4 A-fragment LDS reads of sub-step s + 1 are issued ahead
-// of the MFMAs of sub-step s.
-template <bool FULL, bool EXACT, class Dma>
-__device__ __forceinline__ void g4_kstep(const uint16_t* as, const af3_u32x4 bp[4], const uint32_t sc[4], int wm0,
-                                         int tm_live, int tn_live, af3_f32x16 acc[4][4], Dma&& dma) {
+// one 64-deep k-step of a wave's (32 TM) x (32 TN) tile; FULL: every
+// sub-tile live.  Instruction order is fixed by scheduling barriers: the
+// conversions of the next sub-step's B fragments and the k-step's DPW
+// global->LDS copies are spread between the MFMAs, and the A-fragment LDS
+// reads of sub-step s + 1 are issued ahead of the MFMAs of sub-step s.
+template <int TM, int TN, int DPW, bool FULL, bool EXACT, class Dma>
+__device__ __forceinline__ void g4_kstep(const uint16_t* as, const af3_u32x4 bp[TN], const uint32_t sc[TN], int wm0,
+                                         int tm_live, int tn_live, af3_f32x16 acc[TM][TN], Dma&& dma) {
+  constexpr int NM = TM * TN * 4;          // MFMAs per k-step
+  constexpr int GAP = NM / (DPW + 1);      // MFMAs between copies
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
-  float scf[4];
+  float scf[TN];
 #pragma unroll
-  for (int tn = 0; tn < 4; ++tn) scf[tn] = __uint_as_float(sc[tn] << 23);
-  af3_bf16x8 af[2][4], bf[2][4];
+  for (int tn = 0; tn < TN; ++tn) scf[tn] = __uint_as_float(sc[tn] << 23);
+  af3_bf16x8 af[2][TM], bf[2][TN];
 #pragma unroll
-  for (int tm = 0; tm < 4; ++tm) af[0][tm] = *(const af3_bf16x8*)(as + lds_off(wm0 + tm * 32 + lr, lh * 4));
+  for (int tm = 0; tm < TM; ++tm) af[0][tm] = *(const af3_bf16x8*)(as + lds_off(wm0 + tm * 32 + lr, lh * 4));
 #pragma unroll
-  for (int tn = 0; tn < 4; ++tn) bf[0][tn] = g4_bfrag<EXACT>(bp[tn][0], sc[tn], scf[tn]);
+  for (int tn = 0; tn < TN; ++tn) bf[0][tn] = g4_bfrag<EXACT>(bp[tn][0], sc[tn], scf[tn]);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const int c = s & 1, nx = c ^ 1;
     __builtin_amdgcn_sched_barrier(0);
     if (s + 1 < 4) {
 #pragma unroll
-      for (int tm = 0; tm < 4; ++tm)
+      for (int tm = 0; tm < TM; ++tm)
         af[nx][tm] = *(const af3_bf16x8*)(as + lds_off(wm0 + tm * 32 + lr, lh * 4 + s + 1));
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int tm = i >> 2, tn = i & 3;
+    for (int i = 0; i < TM * TN; ++i) {
+      const int tm = i / TN, tn = i % TN;
       if (FULL || (tm < tm_live && tn < tn_live))
         acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[c][tm], bf[c][tn], acc[tm][tn], 0, 0, 0);
-      if (s + 1 < 4 && (i & 3) == 3)
-        bf[nx][i >> 2] = g4_bfrag<EXACT>(bp[i >> 2][s + 1], sc[i >> 2], scf[i >> 2]);
-      const int q = s * 16 + i;
-      if (q % 6 == 2 && q / 6 < 10) dma(q / 6);
+      constexpr int CV = TM * TN / TN;  // conversion slot spacing: one fragment per TM MFMAs
+      if (s + 1 < 4 && (i % CV) == CV - 1) {
+        const int t = i / CV;
+        bf[nx][t] = g4_bfrag<EXACT>(bp[t][s + 1], sc[t], scf[t]);
+      }
+      const int q = s * TM * TN + i;
+      if (q % GAP == GAP / 2 && q / GAP < DPW) dma(q / GAP);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
 
-template <int BXK>
-__global__ __launch_bounds__(256) void gemm4_fwd_kernel(Params p) {
+template <int WM, int WN, int BXK>
+__global__ __launch_bounds__(WM * WN * 64) void gemm4_fwd_kernel(Params p) {
+  constexpr int NW = WM * WN, NT = NW * 64;
+  constexpr int TM = 256 / WM / 32, TN = 256 / WN / 32;
+  constexpr int API = 32 / NW, BPI = 8 / NW, DPW = API + BPI;  // copies per wave per k-step
   __shared__ __attribute__((aligned(16))) uint8_t lds[kG4LdsBytes];
   uint16_t* const As = (uint16_t*)lds;                          // 3 x 32 KB
   uint8_t* const Bs = lds + kG4Stages * kG4AStage * 2;          // 3 x 8 KB
@@ -1077,25 +1093,25 @@ __global__ __launch_bounds__(256) void gemm4_fwd_kernel(Params p) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar)
   const int lr = lane & 31, lh = lane >> 5;
-  const int wm0 = (wave >> 1) * 128, wn0 = (wave & 1) * 128;
-  const int tm_live = min(4, max(0, (nrows - wm0 + 31) >> 5));
-  const int tn_live = min(4, max(0, (ncols - wn0 + 31) >> 5));
-  const bool full = tm_live == 4 && tn_live == 4;
+  const int wm0 = (wave / WN) * (32 * TM), wn0 = (wave % WN) * (32 * TN);
+  const int tm_live = min(TM, max(0, (nrows - wm0 + 31) >> 5));
+  const int tn_live = min(TN, max(0, (ncols - wn0 + 31) >> 5));
+  const bool full = tm_live == TM && tn_live == TN;
 
-  // DMA sources: A rows (8 instructions per wave per stage, 8 rows each)
-  const uint16_t* arow[8];
+  // DMA sources: A rows (API instructions per wave per stage, 8 rows each)
+  const uint16_t* arow[API];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = (wave * 8 + i) * 8 + (lane >> 3);
+  for (int i = 0; i < API; ++i) {
+    const int row = (wave * API + i) * 8 + (lane >> 3);
     int64_t src = row_lo + (row < nrows ? row : 0);
     if (p.a.gather) src = p.a.gather[src] / p.a.gdiv;
     arow[i] = (const uint16_t*)p.a.ptr + src * p.a.ld + (((lane & 7) ^ swz(row)) << 3);
   }
-  // packed B (2 instructions per wave per stage, 32 weight rows each)
-  const uint8_t* bsrc[2];
+  // packed B (BPI instructions per wave per stage, 32 weight rows each)
+  const uint8_t* bsrc[BPI];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int row4 = (wave * 2 + j) * 8 + (lane >> 3);
+  for (int j = 0; j < BPI; ++j) {
+    const int row4 = (wave * BPI + j) * 8 + (lane >> 3);
     const int lc = (lane & 7) ^ (((row4 >> 1) & 1) << 2);
     int nn = row4 * 4 + (lc & 3);
     if (nn >= ncols) nn = 0;
@@ -1106,33 +1122,32 @@ __global__ __launch_bounds__(256) void gemm4_fwd_kernel(Params p) {
     const uint8_t* sbase = p.b.scales + e * p.b.sestride + (int64_t)n0 * G;
     const int nbytes = ncols * G;  // multiple of 32: ncols % 32 == 0
     const int ninstr = (nbytes + 1023) >> 10;
-    for (int i = wave; i < ninstr; i += 4) {
+    for (int i = wave; i < ninstr; i += NW) {
       int off = i * 1024 + lane * 16;
       const int src = off < nbytes ? off : 0;
-      g4_dma16(sbase + src, __builtin_amdgcn_readfirstlane(lds_addr(Ss + i * 1024)));
+      g4_dma16(sbase + src, __builtin_amdgcn_readfirstlane(lds_addr(Ss)) + (uint32_t)(i * 1024));
     }
   }
   // copy j (0..9) of k-step kt: 8 A instructions (8 rows each), 2 packed-B
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));  // LDS byte address of the block's area
   auto issue_one = [&](int kt, int j) {
     const int st = kt % kG4Stages;
-    if (j < 8) {
-      const uint32_t abase = __builtin_amdgcn_readfirstlane(lds_addr(As + st * kG4AStage + wave * 8 * 8 * kBK));
-      g4_dma16(arow[j] + kt * kBK, abase + j * 8 * kBK * 2);
-    } else {
-      const uint32_t bbase = __builtin_amdgcn_readfirstlane(lds_addr(Bs + st * kG4BStage + wave * 2 * 1024));
-      g4_dma16(bsrc[j - 8] + kt * 32, bbase + (j - 8) * 1024);
-    }
+    if (j < API)
+      g4_dma16(arow[j] + kt * kBK, lds0 + (uint32_t)(st * kG4AStage * 2 + (wave * API + j) * 8 * kBK * 2));
+    else
+      g4_dma16(bsrc[j - API] + kt * 32,
+               lds0 + (uint32_t)(kG4Stages * kG4AStage * 2 + st * kG4BStage + (wave * BPI + j - API) * 1024));
   };
   auto issue = [&](int kt) {
 #pragma unroll
-    for (int j = 0; j < 10; ++j) issue_one(kt, j);
+    for (int j = 0; j < DPW; ++j) issue_one(kt, j);
   };
 
-  af3_f32x16 acc[4][4];
+  af3_f32x16 acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
@@ -1145,7 +1160,7 @@ __global__ __launch_bounds__(256) void gemm4_fwd_kernel(Params p) {
     AF3_ASM_WAIT_VM(0);
     AF3_ASM_BARRIER();
     const int nbytes = ncols * G;
-    for (int i = threadIdx.x * 16; i < nbytes; i += 256 * 16) {
+    for (int i = threadIdx.x * 16; i < nbytes; i += NT * 16) {
       const af3_u32x4 v = *(const af3_u32x4*)(Ss + i);
 #pragma unroll
       for (int q = 0; q < 4; ++q)
@@ -1158,24 +1173,28 @@ __global__ __launch_bounds__(256) void gemm4_fwd_kernel(Params p) {
   auto kloop = [&](auto full_c, auto exact_c) {
     constexpr bool FULL = decltype(full_c)::value, EXACT = decltype(exact_c)::value;
     for (int kt = 0; kt < nk; ++kt) {
-      if (kt + 1 < nk)
-        AF3_ASM_WAIT_VM(10);
-      else
+      if (kt + 1 < nk) {
+        if constexpr (DPW == 10)
+          AF3_ASM_WAIT_VM(10);
+        else
+          AF3_ASM_WAIT_VM(5);
+      } else {
         AF3_ASM_WAIT_VM(0);
+      }
       AF3_ASM_BARRIER();
       const bool pf = kt + 2 < nk;
       const int st = kt % kG4Stages;
       const uint16_t* as = As + st * kG4AStage;
       const uint8_t* bs = Bs + st * kG4BStage;
-      af3_u32x4 bp[4];
-      uint32_t sc[4];
+      af3_u32x4 bp[TN];
+      uint32_t sc[TN];
 #pragma unroll
-      for (int tn = 0; tn < 4; ++tn) {
+      for (int tn = 0; tn < TN; ++tn) {
         const int n = wn0 + tn * 32 + lr;
         bp[tn] = *(const af3_u32x4*)(bs + g4_b_off(n, lh));
         sc[tn] = Ss[n * G + 2 * kt + lh];
       }
-      g4_kstep<FULL, EXACT>(as, bp, sc, wm0, tm_live, tn_live, acc, [&](int j) {
+      g4_kstep<TM, TN, DPW, FULL, EXACT>(as, bp, sc, wm0, tm_live, tn_live, acc, [&](int j) {
         if (pf) issue_one(kt + 2, j);
       });
     }
@@ -1189,7 +1208,7 @@ __global__ __launch_bounds__(256) void gemm4_fwd_kernel(Params p) {
 
   if constexpr (BXK != NONE) {
     if (p.kx > 0) {  // expert-LoRA segment: + L[r] . Bx[e][n]^T, both bf16 through LDS
-      Loader<kG4Rows, ROWS_BF16, 256> la, lb;
+      Loader<kG4Rows, ROWS_BF16, NT> la, lb;
       la.init(p.ax, 0, row_lo, nrows, p.kx);
       lb.init(p.bx, e, n0, ncols, p.kx);
       for (int k0 = 0; k0 < p.kx; k0 += kBK) {
@@ -1199,12 +1218,342 @@ __global__ __launch_bounds__(256) void gemm4_fwd_kernel(Params p) {
         la.store(As);
         lb.store(As + kG4AStage);
         __syncthreads();
-        mma_kstep<4, 4>(As, As + kG4AStage, wm0, wn0, acc);
+        mma_kstep<TM, TN>(As, As + kG4AStage, wm0, wn0, acc);
       }
     }
   }
 
-  g4_epilogue(p, lds, acc, e, row_lo, nrows, n0, ncols, wm0, wn0);
+  g4_epilogue<false, TM, TN, NT>(p, lds, acc, e, row_lo, nrows, n0, ncols, wm0, wn0);
+}
+
+// ---------------------------------------------------------------------------
+// gemm4 dgrad: grouped GEMM through MXFP4 weights packed along the OUTPUT
+// axis, W[e][k][n/32][16] with scales [e][k][n/32] (the input-gradient
+// products dX = dY . W of quantization.py:409-418).  Same block / wave tiling,
+// A ring, grouping and epilogue as gemm4 forward.  The packed weight bytes of a
+// k-step ([64 k][128 B] for 256 columns) and their scales are loaded
+// global->LDS four k-steps deep, then transposed in LDS to [column pair][k]
+// (one byte = the two nibbles of columns 2p, 2p+1 at one k) while the MFMAs of
+// the previous k-step run.  A lane then reads the 8 bytes of its column pair
+// for the 8 k of a sub-step plus the 8 scale bytes of those k, and one
+// v_cvt_scalef32_pk_bf16_fp4 per byte yields the (even, odd) column values:
+// the even values form the B fragment of one MFMA sub-tile and the odd values
+// that of its partner (sub-tiles 2t, 2t + 1 hold the even / odd columns of 64
+// consecutive columns), so no value is converted twice or discarded.
+// ---------------------------------------------------------------------------
+constexpr int kD4BStage = 64 * 128;  // packed-B staging per k-step [64 k][128 B]
+constexpr int kD4SStage = 64 * 16;   // scale staging per k-step [64 k][4 x (2 bytes + 2 zero bytes)]
+constexpr int kD4BRing = 4;
+constexpr int kD4TBuf = 128 * 64;    // transposed packed B [128 pairs][64 k]
+constexpr int kD4TsBuf = 8 * 64;     // transposed scales [8 blocks][64 k]
+constexpr int kD4OffB = kG4Stages * kG4AStage * 2;
+constexpr int kD4OffS = kD4OffB + kD4BRing * kD4BStage;
+constexpr int kD4OffT = kD4OffS + kD4BRing * kD4SStage;
+constexpr int kD4OffTs = kD4OffT + 2 * kD4TBuf;
+constexpr int kD4LdsBytes = kD4OffTs + 2 * kD4TsBuf + 16;  // ~149 KB
+static_assert(kD4LdsBytes >= 256 * 512 + 1024 && kD4LdsBytes <= 160 * 1024, "dgrad LDS budget");
+
+// byte offset of (column pair p, k) in a transposed buffer: 64 bytes per pair,
+// 8-byte k groups XOR-swizzled by p / 4 so 32 lanes reading one k group of 32
+// consecutive pairs hit 32 distinct 8-byte bank pairs
+__device__ __forceinline__ int d4_t_off(int p, int k) {
+  return p * 64 + ((((k >> 3) ^ ((p >> 2) & 7))) << 3) + (k & 7);
+}
+
+// scale bytes outside [2, 252] among the 4 bytes of x
+__device__ __forceinline__ bool d4_odd4(uint32_t x) {
+  const uint32_t lo = (x - 0x02020202u) & ~x & 0x80808080u;    // some byte < 2
+  const uint32_t nx = ~x;
+  const uint32_t hi = (nx - 0x03030303u) & ~nx & 0x80808080u;  // some byte > 252
+  return (lo | hi) != 0u;
+}
+
+// B fragments of the sub-tile pair (even, odd columns) for one sub-step from
+// the 8 packed bytes (w0: k 0..3, w1: k 4..7) and their 8 scale bytes.
+__device__ __forceinline__ void d4_frags(uint32_t w0, uint32_t w1, uint32_t s0, uint32_t s1, bool exact,
+                                         af3_bf16x8& ev, af3_bf16x8& od) {
+  uint32_t dw[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t src = i < 4 ? w0 : w1;
+    const uint32_t sb = ((i < 4 ? s0 : s1) >> (8 * (i & 3))) & 0xFFu;
+    const float sc = __uint_as_float(sb << 23);
+    switch (i & 3) {
+      case 0: dw[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, sc, 0)); break;
+      case 1: dw[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, sc, 1)); break;
+      case 2: dw[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, sc, 2)); break;
+      default: dw[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, sc, 3)); break;
+    }
+  }
+  if (exact) {  // wave-uniform: only work items with out-of-range scale bytes pay for this
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t src = i < 4 ? w0 : w1;
+      const uint32_t sb = ((i < 4 ? s0 : s1) >> (8 * (i & 3))) & 0xFFu;
+      const uint32_t byte = (src >> (8 * (i & 3))) & 0xFFu;
+      const uint32_t alt = af3_e2m1_to_bf16_bits(byte & 0xFu, sb) | (af3_e2m1_to_bf16_bits(byte >> 4, sb) << 16);
+      dw[i] = sb - 2u > 250u ? alt : dw[i];
+    }
+  }
+  af3_u32x4 e4, o4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    e4[j] = perm_lo(dw[2 * j], dw[2 * j + 1]);
+    o4[j] = perm_hi(dw[2 * j], dw[2 * j + 1]);
+  }
+  ev = __builtin_bit_cast(af3_bf16x8, e4);
+  od = __builtin_bit_cast(af3_bf16x8, o4);
+}
+
+template <int BXK>
+__global__ __launch_bounds__(256) void gemm4_dgrad_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kD4LdsBytes];
+  uint16_t* const As = (uint16_t*)lds;
+  uint8_t* const Bp = lds + kD4OffB;
+  uint8_t* const Sp = lds + kD4OffS;
+  uint8_t* const Tb = lds + kD4OffT;
+  uint8_t* const Ts = lds + kD4OffTs;
+
+  const int NN = p.n_nblk;
+  const int W = p.tile_offs[p.E] * NN;
+  const int b = blockIdx.x;
+  if (b >= W) return;
+  const int W8 = W & ~7;
+  const int w = b < W8 ? (b & 7) * (W8 >> 3) + (b >> 3) : b;
+  const int Mt = W / NN;
+  const int GM = p.group_m > 0 ? p.group_m : 1;
+  const int first_m = (w / (GM * NN)) * GM;
+  const int gsz = min(GM, Mt - first_m);
+  const int local = w - first_m * NN;
+  const int mt = first_m + local % gsz, nt = local / gsz;
+  const int32_t ent = p.tile_map[mt];
+  if (ent < 0) return;
+  const int e = ent & 0xFFFF, blk = ent >> 16;
+  const int row_lo = p.offs[e] + blk * kG4Rows;
+  const int nrows = min(kG4Rows, p.offs[e + 1] - row_lo);
+  if (nrows <= 0) return;
+  const int n0 = nt * kG4Rows;
+  const int ncols = min(kG4Rows, p.N - n0);  // multiple of 64
+  const int nk = p.K / kBK;
+
+  // 1 x 4 waves: wave w owns all 256 rows and the 64 columns 64 w .. 64 w + 63
+  // (sub-tile pair: even / odd columns), so every weight byte is converted by
+  // exactly one wave
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = lane & 31, lh = lane >> 5;
+  const int wn0 = wave * 64;
+  const int tm_live = min(8, (nrows + 31) >> 5);
+  const bool wave_live = wn0 < ncols;  // ncols is a multiple of 64
+  const bool full = tm_live == 8 && wave_live;
+
+  // DMA sources.  A rows: as gemm4 forward.
+  const uint16_t* arow[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = (wave * 8 + i) * 8 + (lane >> 3);
+    int64_t src = row_lo + (row < nrows ? row : 0);
+    if (p.a.gather) src = p.a.gather[src] / p.a.gdiv;
+    arow[i] = (const uint16_t*)p.a.ptr + src * p.a.ld + (((lane & 7) ^ swz(row)) << 3);
+  }
+  // packed weight rows of a k-step: instruction q covers k rows 8q..8q+7, 128 B each
+  const uint8_t* bsrc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int kr = (wave * 2 + j) * 8 + (lane >> 3);
+    int c16 = (lane & 7) * 16;
+    if (c16 >= (ncols >> 1)) c16 = 0;
+    bsrc[j] = (const uint8_t*)p.b.ptr + e * p.b.estride + (int64_t)kr * p.b.ld + (n0 >> 1) + c16;
+  }
+  // scales of a k-step: instruction `wave` covers k rows 16 wave .. + 15, 8 B each; a 2-byte
+  // global->LDS copy lands in a 4-byte LDS slot per lane (zero-extended)
+  const uint8_t* ssrc;
+  {
+    const int kr = wave * 16 + (lane >> 2);
+    int c2 = (lane & 3) * 2;
+    if (c2 >= (ncols >> 5)) c2 = 0;
+    ssrc = p.b.scales + e * p.b.sestride + (int64_t)kr * p.b.sld + (n0 >> 5) + c2;
+  }
+  const int64_t bstep = (int64_t)kBK * p.b.ld, sstep = (int64_t)kBK * p.b.sld;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+  auto issue_b = [&](int kb) {  // packed B + scales of k-step kb (3 instructions)
+    const int slot = kb % kD4BRing;
+    const uint32_t bb = lds0 + (uint32_t)(kD4OffB + slot * kD4BStage + wave * 2 * 1024);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) g4_dma16(bsrc[j] + kb * bstep, bb + j * 1024);
+    const uint32_t sb = lds0 + (uint32_t)(kD4OffS + slot * kD4SStage + wave * 256);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_ushort %0, off" ::"v"(ssrc + kb * sstep), "s"(sb)
+                 : "memory", "m0");
+  };
+  auto issue_a = [&](int ka, int j) {  // A instruction j (0..7) of k-step ka
+    g4_dma16(arow[j] + ka * kBK,
+             lds0 + (uint32_t)((ka % kG4Stages) * kG4AStage * 2 + (wave * 8 + j) * 8 * kBK * 2));
+  };
+  // per-k-step flag: index of the last k-step whose scales held a byte outside
+  // [2, 252] (written by the scale transposer, read after the next barrier)
+  int* const oddk = (int*)(lds + kD4OffTs + 2 * kD4TsBuf);
+  // transposer: thread t moves packed bytes of k rows 4 rg .. 4 rg + 3, column
+  // pairs 8 hg .. 8 hg + 7 (and threads < 128 four scale bytes)
+  const int hg = threadIdx.x & 15, rg = threadIdx.x >> 4;
+  int toff[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) toff[q] = d4_t_off(hg * 8 + q, rg * 4);
+  const int nbq = (threadIdx.x >> 4) & 7, kq = (threadIdx.x & 15) * 4;
+  const int sso = (nbq >> 1) * 4 + (nbq & 1);
+  auto transpose = [&](int kb) {
+    const int slot = kb % kD4BRing;
+    const uint8_t* st = Bp + slot * kD4BStage + rg * 4 * 128 + hg * 8;
+    uint8_t* tb = Tb + (kb & 1) * kD4TBuf;
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint2 v = *(const uint2*)(st + i * 128);
+      lo[i] = v.x;
+      hi[i] = v.y;
+    }
+    auto tr4 = [&](const uint32_t x[4], uint32_t o[4]) {
+      const uint32_t a0 = __builtin_amdgcn_perm(x[1], x[0], 0x05010400u);
+      const uint32_t a1 = __builtin_amdgcn_perm(x[1], x[0], 0x07030602u);
+      const uint32_t b0 = __builtin_amdgcn_perm(x[3], x[2], 0x05010400u);
+      const uint32_t b1 = __builtin_amdgcn_perm(x[3], x[2], 0x07030602u);
+      o[0] = __builtin_amdgcn_perm(b0, a0, 0x05040100u);
+      o[1] = __builtin_amdgcn_perm(b0, a0, 0x07060302u);
+      o[2] = __builtin_amdgcn_perm(b1, a1, 0x05040100u);
+      o[3] = __builtin_amdgcn_perm(b1, a1, 0x07060302u);
+    };
+    uint32_t ol[4], oh[4];
+    tr4(lo, ol);
+    tr4(hi, oh);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      *(uint32_t*)(tb + toff[q]) = ol[q];
+      *(uint32_t*)(tb + toff[4 + q]) = oh[q];
+    }
+    if (threadIdx.x < 128) {  // scales: [64 k][8] -> [8][64 k]
+      const uint8_t* ss = Sp + slot * kD4SStage + kq * 16 + sso;
+      const uint32_t v = (uint32_t)ss[0] | ((uint32_t)ss[16] << 8) | ((uint32_t)ss[32] << 16) | ((uint32_t)ss[48] << 24);
+      *(uint32_t*)(Ts + (kb & 1) * kD4TsBuf + nbq * 64 + kq) = v;
+      if (d4_odd4(v)) oddk[kb & 1] = kb;
+    }
+  };
+
+  af3_f32x16 acc[8][2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  // lane-fixed LDS byte offsets: A row (32 tm + lr) chunk c sits at
+  // 4096 tm + 128 lr + 16 (c ^ swz), swz = (lr ^ lr / 8 ^ 4 (tm & 1)) & 7
+  const int ax = (lr ^ (lr >> 3)) & 7;
+  const int pr = (wn0 >> 1) + lr;  // the lane's column pair
+  int foff[4], soff[4];
+#pragma unroll
+  for (int sub = 0; sub < 4; ++sub) {
+    const int c = lh * 4 + sub;
+    foff[sub] = d4_t_off(pr, c * 8);
+    soff[sub] = (pr >> 4) * 64 + c * 8;
+  }
+
+  // prologue: B(0); batch 0 = A(0) + B(1); batch 1 = A(1) + B(2)
+  auto issue_batch = [&](int j) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) issue_a(j, i);
+    issue_b(min(j + 1, nk - 1));
+  };
+  if (threadIdx.x < 2) oddk[threadIdx.x] = -1;
+  issue_b(0);
+  issue_batch(0);
+  if (nk > 1) issue_batch(1);
+  if (nk > 1)
+    AF3_ASM_WAIT_VM(22);
+  else
+    AF3_ASM_WAIT_VM(11);
+  AF3_ASM_LDS_BARRIER();
+  transpose(0);
+
+  auto kloop = [&](auto full_c) {
+    constexpr bool FULL = decltype(full_c)::value;
+    for (int kt = 0; kt < nk; ++kt) {
+      if (kt + 1 < nk)
+        AF3_ASM_WAIT_VM(11);
+      else
+        AF3_ASM_WAIT_VM(0);
+      AF3_ASM_LDS_BARRIER();
+      const bool pf = kt + 2 < nk;
+      const uint8_t* as = (const uint8_t*)As + (kt % kG4Stages) * kG4AStage * 2 + lr * 128;
+      const uint8_t* tb = Tb + (kt & 1) * kD4TBuf;
+      const uint8_t* tsb = Ts + (kt & 1) * kD4TsBuf;
+      const bool exact = __builtin_amdgcn_readfirstlane(oddk[kt & 1]) == kt;
+      af3_bf16x8 af[2][8], bf[2][2];
+      auto load_frags = [&](int sub, int slot) {
+        const int c = lh * 4 + sub;
+#pragma unroll
+        for (int tm = 0; tm < 8; ++tm)
+          af[slot][tm] = *(const af3_bf16x8*)(as + tm * 4096 + (((c ^ ax) ^ ((tm & 1) << 2)) << 4));
+        const uint2 wv = *(const uint2*)(tb + foff[sub]);
+        const uint2 sv = *(const uint2*)(tsb + soff[sub]);
+        d4_frags(wv.x, wv.y, sv.x, sv.y, exact, bf[slot][0], bf[slot][1]);
+      };
+      if (FULL || wave_live) load_frags(0, 0);
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        const int cur = sub & 1;
+        __builtin_amdgcn_sched_barrier(0);
+        if ((FULL || wave_live) && sub + 1 < 4) load_frags(sub + 1, cur ^ 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int tm = i >> 1, tn = i & 1;
+          if (FULL || (wave_live && tm < tm_live))
+            acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][tm], bf[cur][tn], acc[tm][tn], 0, 0, 0);
+          const int q = sub * 16 + i;
+          if (pf && q % 6 == 2 && q / 6 < 8) issue_a(kt + 2, q / 6);
+          if (pf && q == 50) issue_b(min(kt + 3, nk - 1));
+          if (q == 40 && kt + 1 < nk) transpose(kt + 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+  };
+  if (full)
+    kloop(std::true_type{});
+  else
+    kloop(std::false_type{});
+
+  if constexpr (BXK != NONE) {
+    if (p.kx > 0) {  // expert-LoRA segment: + L[r] . Bx[e][:, n] (Bx [r][N], n contiguous)
+      Loader<kG4Rows, ROWS_BF16, 256> la;
+      Loader<kG4Rows, COLS_BF16, 256> lb;
+      la.init(p.ax, 0, row_lo, nrows, p.kx);
+      lb.init(p.bx, e, n0, ncols, 0, p.kx);
+      for (int k0 = 0; k0 < p.kx; k0 += kBK) {
+        la.load(k0);
+        lb.load(k0);
+        __syncthreads();
+        la.store(As);
+        lb.store(As + kG4AStage);
+        __syncthreads();
+#pragma unroll
+        for (int ks = 0; ks < kBK / 16; ++ks) {
+          af3_bf16x8 af[8], bf[2];
+#pragma unroll
+          for (int tm = 0; tm < 8; ++tm) af[tm] = *(const af3_bf16x8*)(As + lds_off(tm * 32 + lr, ks * 2 + lh));
+#pragma unroll
+          for (int tn = 0; tn < 2; ++tn)
+            bf[tn] = *(const af3_bf16x8*)(As + kG4AStage + lds_off(wn0 + 2 * lr + tn, ks * 2 + lh));
+#pragma unroll
+          for (int tm = 0; tm < 8; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn)
+              acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[tm], bf[tn], acc[tm][tn], 0, 0, 0);
+        }
+      }
+    }
+  }
+  g4_epilogue<true, 8, 2>(p, lds, acc, e, row_lo, nrows, n0, ncols, 0, wn0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1420,10 +1769,17 @@ static void launch_gemm3(bool trans, int max_tiles, int N, hipStream_t stream, P
     hipLaunchKernelGGL((gemm3_kernel<BM, BN, WM, WN, COLS_FP4, COLS_BF16>), grid, dim3(WM * WN * 64), 0, stream, p);
 }
 
+static void launch_gemm4_dgrad(int max_tiles, int N, hipStream_t stream, Params p) {
+  p.n_nblk = (N + kG4Rows - 1) / kG4Rows;
+  dim3 grid(max_tiles * p.n_nblk);
+  hipLaunchKernelGGL((gemm4_dgrad_kernel<COLS_BF16>), grid, dim3(256), 0, stream, p);
+}
+
+template <int WM, int WN>
 static void launch_gemm4_fwd(int max_tiles, int N, hipStream_t stream, Params p) {
   p.n_nblk = (N + kG4Rows - 1) / kG4Rows;
   dim3 grid(max_tiles * p.n_nblk);
-  hipLaunchKernelGGL((gemm4_fwd_kernel<ROWS_BF16>), grid, dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((gemm4_fwd_kernel<WM, WN, ROWS_BF16>), grid, dim3(WM * WN * 64), 0, stream, p);
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -1507,17 +1863,25 @@ extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gathe
   //   11: 128x128, 2x2 two-deep prefetch    12: 256x128, 2x2 two-deep prefetch
   //   9: single-buffered 128x128 (reference kernel)
   //   20: gemm4 forward (256x256, 4 waves of 128x128, packed MXFP4 in LDS,
-  //       three-stage global->LDS ring); tile_cfg / 100 = m-tiles per group
-  //       of the work order (default 4).  Default for trans_w 0 when its
-  //       alignment / size requirements hold.
+  //       three-stage global->LDS ring)
+  //   22: gemm4 forward with 8 waves of 128x64 (two waves per SIMD, so one
+  //       wave's conversions / LDS reads overlap the other's MFMAs); default
+  //       for trans_w 0 when the alignment / size requirements hold
+  //   21: gemm4 dgrad (weights packed along n, transposed in LDS; 4 waves of
+  //       256x64); default for trans_w 1 when the requirements hold
+  //   tile_cfg / 100 = m-tiles per group of the 20/21/22 work order (default 4)
   int cfg = tile_cfg % 100;
   const int group_m = tile_cfg / 100 > 0 ? tile_cfg / 100 : 4;
   if (cfg == 0) {
-    const bool g4_ok = !trans && block_m == 256 && K % kBK == 0 && K / 32 <= kG4MaxG && al16(w_scales) && al16(y) &&
-                       ldy % 8 == 0;
-    cfg = g4_ok ? 20 : (block_m == 256 ? 4 : 2);
+    const bool g4_fwd = !trans && block_m == 256 && K % kBK == 0 && K / 32 <= kG4MaxG && al16(w_scales) && al16(y) &&
+                        ldy % 8 == 0;
+    const bool g4_dgrad = trans && block_m == 256 && K % kBK == 0 && N % 64 == 0 && al16(y) && ldy % 8 == 0 &&
+                          ((uintptr_t)w_scales & 1) == 0;
+    cfg = g4_fwd ? 22 : g4_dgrad ? 21 : (block_m == 256 ? 4 : 2);
   }
-  const bool bm_ok = (cfg == 3 || cfg == 4 || cfg == 6 || cfg == 7 || cfg == 12 || cfg == 20) ? block_m == 256 : block_m == 128;
+  const bool bm_ok =
+      (cfg == 3 || cfg == 4 || cfg == 6 || cfg == 7 || cfg == 12 || cfg == 20 || cfg == 21 || cfg == 22) ? block_m == 256
+                                                                                                       : block_m == 128;
   AF3_REQUIRE(bm_ok, "moe_gemm: tile_cfg %d does not match block_m %d", cfg, block_m);
   if (K % kBK != 0) cfg = 9;  // direct A loads need whole 64-deep k-steps
   if (cfg == 9 && block_m != 128) {
@@ -1536,12 +1900,22 @@ extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gathe
     case 11: launch_gemm3<128, 128, 2, 2>(trans, max_tiles, N, stream, p); break;
     case 12: launch_gemm3<256, 128, 2, 2>(trans, max_tiles, N, stream, p); break;
     case 20:
+    case 22:
       p.group_m = group_m;
       AF3_REQUIRE(!trans && block_m == 256 && K % kBK == 0 && K / 32 <= kG4MaxG && al16(w_scales) && al16(y) &&
                       ldy % 8 == 0,
                   "moe_gemm: tile_cfg 20 needs trans_w 0, block_m 256, K %% 64 == 0, K <= %d, 16-byte aligned scales/y",
                   kG4MaxG * 32);
-      launch_gemm4_fwd(max_tiles, N, stream, p);
+      if (cfg == 20)
+        launch_gemm4_fwd<2, 2>(max_tiles, N, stream, p);
+      else
+        launch_gemm4_fwd<2, 4>(max_tiles, N, stream, p);
+      break;
+    case 21:
+      p.group_m = group_m;
+      AF3_REQUIRE(trans && block_m == 256 && K % kBK == 0 && N % 64 == 0 && al16(y) && ldy % 8 == 0,
+                  "moe_gemm: tile_cfg 21 needs trans_w 1, block_m 256, K %% 64 == 0, N %% 64 == 0, 16-byte aligned y");
+      launch_gemm4_dgrad(max_tiles, N, stream, p);
       break;
     case 9: {
       dim3 grid(max_tiles, (N + 127) / 128);
