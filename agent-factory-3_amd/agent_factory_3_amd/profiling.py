@@ -1,0 +1,133 @@
+"""Summaries of rocprofv3 output for the MXFP4 MoE expert path.
+
+Command line (run from the repository root on the MI355X box)::
+
+    python -m agent_factory_3_amd.profiling ktrace  <run>_kernel_trace.csv
+    python -m agent_factory_3_amd.profiling traffic <fetch>_counter_collection.csv \\
+                                                     <write>_counter_collection.csv
+
+``ktrace`` turns a ``rocprofv3 --kernel-trace --output-format csv`` trace into
+a markdown table (one row per kernel name and grid size: calls, average /
+minimum / total duration).
+
+``traffic`` takes two ``rocprofv3 --pmc FETCH_SIZE`` / ``--pmc WRITE_SIZE``
+counter collections of ``bench.py --probe traffic`` (which runs one plain
+elementwise device copy of a known size, then the layer) and reports, per kernel, the
+HBM-side bytes per dispatch: each counter (KiB per dispatch) is scaled by
+the factor that makes the copy kernel's reading equal its known size.  The
+last line is a machine-readable JSON comment that ``bench.py`` reads for the
+``roofline.traffic`` field.
+"""
+from __future__ import annotations
+
+import collections
+import csv
+import json
+import re
+import sys
+
+# the calibration copy of ``bench.py --probe traffic`` (an elementwise
+# dst = src * 1 kernel, so it runs as a kernel and not on a copy engine):
+# bytes read == bytes written
+COPY_BYTES = 512 * 1024 * 1024
+COPY_KERNEL = "MulFunctor"
+
+
+def short_name(name: str) -> str:
+    s = name.replace("(anonymous namespace)::", "")
+    s = re.sub(r"^void ", "", s)
+    depth, out = 0, []
+    for ch in s:  # cut the argument list, keep template arguments
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            break
+        out.append(ch)
+    return "".join(out).strip()
+
+
+def ktrace(path: str) -> str:
+    rows = list(csv.DictReader(open(path)))
+    agg = collections.defaultdict(list)
+    for r in rows:
+        grid = r.get("Grid_Size_X") or r.get("Grid_Size") or ""
+        dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        agg[(short_name(r["Kernel_Name"]), grid)].append(dur)
+    tot = sum(sum(v) for v in agg.values()) or 1.0
+    lines = ["| kernel | grid | calls | avg us | min us | total us | % |", "|---|---:|---:|---:|---:|---:|---:|"]
+    for (k, g), v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| `{k}` | {g} | {len(v)} | {sum(v) / len(v):.2f} | {min(v):.2f} | {sum(v):.1f} | "
+                     f"{100 * sum(v) / tot:.2f} |")
+    return "\n".join(lines)
+
+
+def _counter_means(path: str, counter: str) -> dict:
+    """(kernel, grid) -> mean counter value per dispatch (counter rows summed per dispatch)."""
+    per_dispatch = collections.defaultdict(float)
+    key_of = {}
+    for r in csv.DictReader(open(path)):
+        if r["Counter_Name"] != counter:
+            continue
+        d = r["Dispatch_Id"]
+        per_dispatch[d] += float(r["Counter_Value"])
+        key_of[d] = (short_name(r["Kernel_Name"]), r.get("Grid_Size") or r.get("Grid_Size_X") or "")
+    agg = collections.defaultdict(list)
+    for d, v in per_dispatch.items():
+        agg[key_of[d]].append(v)
+    return {k: sum(v) / len(v) for k, v in agg.items()}
+
+
+def _copy_key(means: dict):
+    """The calibration copy kernel (largest reading among the matching names)."""
+    cands = [k for k in means if COPY_KERNEL in k[0]]
+    if not cands:
+        raise SystemExit(f"no {COPY_KERNEL} copy kernel found in the counter collection")
+    return max(cands, key=lambda k: means[k])
+
+
+def traffic(fetch_csv: str, write_csv: str) -> str:
+    fetch = _counter_means(fetch_csv, "FETCH_SIZE")
+    write = _counter_means(write_csv, "WRITE_SIZE")
+    cf, cw = _copy_key(fetch), _copy_key(write)
+    f_scale = COPY_BYTES / (fetch[cf] * 1024.0)
+    w_scale = COPY_BYTES / (write[cw] * 1024.0)
+    lines = [f"Calibration copy `{cf[0]}` (grid {cf[1]}): {COPY_BYTES} B read and written; FETCH_SIZE reads "
+             f"{fetch[cf]:.0f} KiB (scale {f_scale:.4f}), WRITE_SIZE reads {write[cw]:.0f} KiB "
+             f"(scale {w_scale:.4f}).", "",
+             "| kernel | grid | FETCH_SIZE KiB/dispatch | WRITE_SIZE KiB/dispatch | HBM bytes/dispatch (scaled) |",
+             "|---|---:|---:|---:|---:|"]
+    out = {}
+    for k in sorted(set(fetch) & set(write), key=lambda k: -(fetch[k] + write[k])):
+        b = fetch[k] * 1024.0 * f_scale + write[k] * 1024.0 * w_scale
+        out[f"{k[0]}|{k[1]}"] = {"fetch_kib": fetch[k], "write_kib": write[k], "bytes": b}
+        lines.append(f"| `{k[0]}` | {k[1]} | {fetch[k]:.0f} | {write[k]:.0f} | {b:.4g} |")
+    lines += ["", "<!-- traffic-json: " + json.dumps({"fetch_scale": f_scale, "write_scale": w_scale,
+                                                       "kernels": out}) + " -->"]
+    return "\n".join(lines)
+
+
+def read_traffic(md_path: str) -> dict | None:
+    """The JSON block written by ``traffic`` (None when absent)."""
+    try:
+        text = open(md_path).read()
+    except OSError:
+        return None
+    m = re.search(r"<!-- traffic-json: (.*) -->", text)
+    return json.loads(m.group(1)) if m else None
+
+
+def main(argv: list[str]) -> int:
+    if len(argv) >= 2 and argv[0] == "ktrace":
+        print(ktrace(argv[1]))
+        return 0
+    if len(argv) >= 3 and argv[0] == "traffic":
+        print(traffic(argv[1], argv[2]))
+        return 0
+    print(__doc__, file=sys.stderr)
+    return 2
+
+
+if __name__ == "__main__":
+    sys.exit(main(sys.argv[1:]))

@@ -119,7 +119,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cfg", type=int, default=4, choices=(2, 3, 4))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample", action="store_true",
+                    help="CPU baseline on a 4-expert sample scaled to the layer (default: the whole layer)")
     ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--probe", choices=("traffic",),
+                    help="traffic: one plain 512 MiB device copy (counter calibration) then one layer step, for "
+                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs; prints no JSON line")
+    ap.add_argument("--traffic-profile", default=str(ROOT / "profiles" / "traffic_cfg4.md"),
+                    help="rocprofv3 traffic summary (agent_factory_3_amd.profiling traffic) read for roofline.traffic")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -156,6 +163,17 @@ def main():
             with torch.no_grad():
                 m(x0, rd, gi, si)
 
+    if args.probe == "traffic":
+        from agent_factory_3_amd.profiling import COPY_BYTES
+        src = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.mul(src, 1.0, out=dst)  # an elementwise kernel (a plain dst.copy_ may run on a copy engine)
+        torch.cuda.synchronize()
+        step()
+        torch.cuda.synchronize()
+        log("traffic probe done")
+        return
+
     log(f"warmup {args.warmup}")
     for _ in range(args.warmup):
         step()
@@ -189,6 +207,17 @@ def main():
     achieved = avg_flops / (avg_ms * 1e-3) / 1e12
     flops = workloads.layer_flops(T, k, backward=backward, lora_r=lora_r)
 
+    # HBM bytes per launch of the dominant kernel from the committed rocprofv3
+    # FETCH_SIZE / WRITE_SIZE summary (same kernel, same workload)
+    traffic = None
+    from agent_factory_3_amd.profiling import read_traffic
+    tj = read_traffic(args.traffic_profile)
+    kname = {"moe_gemm_dgrad": "gemm4_dgrad_kernel", "moe_gemm_fwd": "gemm4_fwd_kernel"}.get(dom_tag)
+    if tj and kname:
+        vals = [v["bytes"] for k, v in tj["kernels"].items() if kname in k.split("|")[0]]
+        if vals:
+            traffic = sum(vals) / len(vals)
+
     extra = {"gemm": {t: {"launches_per_step": v["n"] / args.steps, "avg_us": v["ms"] / v["n"] * 1e3,
                           "tflops": v["work"] / (v["ms"] * 1e-3) / 1e12} for t, v in ks.items()},
              "gemm_ms_per_step": gemm_ms,
@@ -203,12 +232,19 @@ def main():
     if not args.no_cpu_baseline and int(os.environ.get("RANK", "0")) == 0:
         log("CPU baseline sample")
         from oracle import cpu_baseline
-        r = cpu_baseline.run_sample(inp_cpu)
+        if args.cpu_sample:
+            r = cpu_baseline.run_sample(inp_cpu)
+            sample = (f"rows of experts {r['sample_experts']} ({r['sample_rows']} rows) fwd+bwd with LoRA, plus "
+                      f"their MXFP4 dequant; scaled to {E} experts dequantized twice and {T * k} rows "
+                      f"(sample wall {r['sample_wall_s']:.1f} s)")
+        else:
+            r = cpu_baseline.run_layer(inp_cpu)
+            sample = (f"the whole layer once: all {E} experts' MXFP4 weights dequantized (LUT + ldexp) for the "
+                      f"forward and again for the backward, then the per-expert bf16 loop over all {T * k} routed "
+                      f"rows, fwd+bwd with LoRA (wall {r['t_layer_s']:.1f} s)")
         cpu = {"value": r["tokens_per_s"], "unit": "tokens/s", "cores": r["threads"], "kind": "port",
-               "sample": (f"rows of experts {r['sample_experts']} ({r['sample_rows']} rows) fwd+bwd with LoRA, "
-                          f"plus their MXFP4 dequant; scaled to {E} experts dequantized twice and {T * k} rows "
-                          f"(sample wall {r['sample_wall_s']:.1f} s)"),
-               "dequant_s_per_expert": r["dequant_s_per_expert"], "loop_s_per_row": r["loop_s_per_row"]}
+               "sample": sample, "dequant_s_per_expert": r["dequant_s_per_expert"],
+               "loop_s_per_row": r["loop_s_per_row"]}
         log(f"cpu baseline {r['tokens_per_s']:.1f} tokens/s")
 
     line = {
@@ -230,7 +266,7 @@ def main():
                    "routing": "zipf1.1, 8 idle experts" if args.cfg == 4 else "top-k of N(0,1) logits",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": dom_tag, "achieved": achieved, "peak": BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None,
+                     "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS, "traffic": traffic,
                      "avg_launch_us": avg_ms * 1e3, "algorithmic_flops_per_launch": avg_flops},
         "cpu_baseline": cpu,
         "extra": extra,

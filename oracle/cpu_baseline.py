@@ -7,6 +7,10 @@ then the per-expert bf16 matmul loop of GptOssExperts.forward
 tokens) with gpt-oss's clamped SwiGLU, the expert-LoRA deltas, and torch
 autograd for the backward.  Test/bench infrastructure only.
 
+``run_layer`` times the whole layer once, unscaled: every expert's weights
+dequantized for the forward, the per-expert loop (forward + autograd
+backward) over all routed rows, and every expert's weights dequantized again
+for the backward (DequantMoEMatmul re-derives them, quantization.py:364-373).
 ``run_sample`` times a bounded sample (the rows of a few experts, fwd + bwd,
 plus the dequant of those experts) and scales it to the whole layer:
     t_layer = t_dequant_per_expert * E * 2   (forward and backward re-dequant,
@@ -36,6 +40,56 @@ def threads() -> int:
     n = len(os.sched_getaffinity(0))
     cap = int(os.environ.get("OMP_NUM_THREADS", n))
     return max(1, min(n, cap, 16))
+
+
+def _expert_step(inp, e, W, ids, gam, s):
+    """Forward + autograd backward of expert e's routed rows; returns the row count."""
+    lora = inp.lora
+    tok, slot = torch.nonzero(ids == e, as_tuple=True)
+    if tok.numel() == 0:
+        return 0
+    xe = inp.x[tok].clone().requires_grad_(True)
+    Wgu, Wdn = W
+    gu = xe @ Wgu.T + inp.gu_bias[e]
+    if lora:
+        A, B = (lora["Agu"][e].clone().requires_grad_(True), lora["Bgu"][e].clone().requires_grad_(True))
+        gu = gu + ((xe @ A.T) @ B.T) * s
+    act = _swiglu(gu)
+    y = act @ Wdn.T + inp.dn_bias[e]
+    if lora:
+        A2, B2 = (lora["Adn"][e].clone().requires_grad_(True), lora["Bdn"][e].clone().requires_grad_(True))
+        y = y + ((act @ A2.T) @ B2.T) * s
+    y = y * gam[tok, slot, None]
+    y.backward(inp.dy[tok])
+    return tok.numel()
+
+
+def run_layer(inp) -> dict:
+    """The whole layer once on the CPU (inp: workloads.LayerInputs on the CPU)."""
+    torch.set_num_threads(threads())
+    E = inp.gu_blocks.shape[0]
+    ids = inp.expt_indx.long()
+    T = inp.x.shape[0]
+    gam = torch.softmax(torch.take_along_dim(inp.logits, ids, 1), dim=-1)
+    s = (inp.lora["alpha"] / inp.lora["r"]) if inp.lora else 0.0
+
+    def dequant_all():
+        return [(_mx.dequant_lut_ldexp(inp.gu_blocks[e], inp.gu_scales[e]),
+                 _mx.dequant_lut_ldexp(inp.dn_blocks[e], inp.dn_scales[e])) for e in range(E)]
+
+    t0 = time.perf_counter()
+    W = dequant_all()
+    t1 = time.perf_counter()
+    rows = sum(_expert_step(inp, e, W[e], ids, gam, s) for e in range(E))
+    t2 = time.perf_counter()
+    del W
+    W = dequant_all()  # the backward re-dequant
+    t3 = time.perf_counter()
+    del W
+    t_layer = t3 - t0
+    t_deq = (t1 - t0) + (t3 - t2)
+    return dict(tokens_per_s=T / t_layer, t_layer_s=t_layer, dequant_s_per_expert=t_deq / (2 * E),
+                loop_s_per_row=(t2 - t1) / max(1, rows), rows=rows, threads=torch.get_num_threads())
 
 
 def run_sample(inp, ranks=(0, 10, 60, 110)) -> dict:
