@@ -18,6 +18,16 @@
 namespace af3 {
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
+
+// streaming expert-LoRA kernels (lora.hip); AF3_EUNSUPPORTED when the shape is
+// not covered (the entry points then use the general kernels)
+int lora_rows_fast(const uint16_t* x, int64_t ldx, const int32_t* gather, int gdiv, const uint16_t* wl, int trans_b,
+                   float scale, const int32_t* token_offs, const int32_t* block_pid_map, int max_tiles, int n_out,
+                   int K, uint16_t* out, int64_t ld_out, hipStream_t stream);
+int lora_wgrad_fast(const uint16_t* big, int64_t ld_big, const int32_t* big_gather, int big_div,
+                    const uint16_t* small, int64_t ld_small, const uint16_t* rowscale, int small_is_a, int W, int r,
+                    float scale, const int32_t* token_offs, const int32_t* chunk_map, const int32_t* chunk_offs,
+                    int max_chunks, int chunk_rows, int n_expts, float* partials, uint16_t* g, hipStream_t stream);
 }  // namespace af3
 
 // argument errors are negative, HIP errors positive (the hipError_t value)

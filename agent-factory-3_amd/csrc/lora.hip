@@ -1,0 +1,426 @@
+// Expert-LoRA kernels (rank 16 or 32) on the streaming path.
+//
+// The expert LoRA of this build (no reference counterpart: the reference puts
+// LoRA on attention only; convention W_eff = W + s * B @ A from PEFT as used at
+// model_trainer.py:665,711) needs, per projection:
+//   rows   out[r][j]  = s * sum_k X[a(r)][k] * Wl[e][j][k]      (L = s X A^T, u = s dY B)
+//   wgrad  G[e]       = sum_{r in e} rs(r) * Big[b(r)][:]^T  (x)  Small[r][:]
+//                        (dB = dY^T L  and  dA = u^T X)
+// Both are skinny (the rank is the narrow side) and bound by reading the wide
+// activation matrix once.  Both kernels stream that matrix through LDS with
+// global->LDS copies (inline assembly, explicit vmcnt waits) a few k-steps
+// ahead and keep the MFMA work on v_mfma_f32_32x32x16_bf16.  For the weight
+// gradient the reduction runs over rows, so both MFMA operands come out of
+// LDS through the gfx950 transposing read ds_read_b64_tr_b16: in a group of 16
+// lanes, lane q points at 4 consecutive 16-bit values of row q / 4, columns
+// 4 (q % 4) ..; lane i of the group receives the 4 values of column i of the
+// 4 rows.
+//
+// Entry points (host side) return AF3_EUNSUPPORTED for shapes they do not
+// cover; the callers in moe_gemm.hip then use the general kernels.
+#include "af3_common.h"
+
+namespace {
+
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+__device__ __forceinline__ void l_dma16(const void* gptr, uint32_t lds_byte_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_byte_addr)
+               : "memory", "m0");
+}
+#define L_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
+#define L_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+
+__device__ __forceinline__ uint32_t l_lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// two transposing reads (rows r0..r0+3 and r0+4..r0+7 of the caller's lane
+// pattern) -> the 8 consecutive-row values of one column
+__device__ __forceinline__ af3_bf16x8 l_tr8(const uint8_t* p0, const uint8_t* p1) {
+  const bf16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p0);
+  const bf16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p1);
+  return af3_bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+__device__ __forceinline__ int l_swz(int row) { return (row ^ (row >> 3)) & 7; }
+
+// ---------------------------------------------------------------------------
+// rows: out[r][j] = scale * sum_k X[a(r)][k] Wl[e][j][k]   (TRANS: Wl[e][k][j])
+// Block = 128 expert-sorted rows (tile map of 128-row blocks), 4 waves of
+// 32 rows x 32 columns.  X k-steps (128 rows x 64 k, 16-byte chunks swizzled
+// as the GEMMs) and the Wl k-step ([32 j][64 k], or [64 k][SR bytes] when
+// TRANS) go global->LDS through a 3-stage ring, two k-steps ahead.
+// ---------------------------------------------------------------------------
+struct LrParams {
+  const uint16_t* x;
+  int64_t ldx;
+  const int32_t* gather;
+  int gdiv;
+  const uint16_t* wl;
+  int64_t wl_estride;  // elements per expert
+  float scale;
+  const int32_t* offs;
+  const int32_t* tile_map;
+  int K, r;
+  uint16_t* out;
+  int64_t ld_out;
+};
+
+constexpr int kLrA = 128 * 64 * 2;  // A bytes per stage
+constexpr int kLrB = 64 * 64;       // B bytes per stage (<= 32 x 64 bf16)
+constexpr int kLrStage = kLrA + kLrB;
+
+template <bool TRANS, int SR>
+__global__ __launch_bounds__(256) void lrows_kernel(LrParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * kLrStage];
+  const int32_t ent = p.tile_map[blockIdx.x];
+  if (ent < 0) return;
+  const int e = ent & 0xFFFF, blk = ent >> 16;
+  const int row_lo = p.offs[e] + blk * 128;
+  const int nrows = min(128, p.offs[e + 1] - row_lo);
+  if (nrows <= 0) return;
+  const int nk = p.K / 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = lane & 31, lh = lane >> 5;
+  constexpr int NB = TRANS ? (64 * SR) / 1024 : 4;  // B copies per stage (block)
+  const bool has_b = wave < NB;
+
+  // A: 4 copies per wave (8 rows each)
+  const uint16_t* arow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = (wave * 4 + i) * 8 + (lane >> 3);
+    int64_t src = row_lo + (row < nrows ? row : 0);
+    if (p.gather) src = p.gather[src] / p.gdiv;
+    arow[i] = p.x + src * p.ldx + (((lane & 7) ^ l_swz(row)) << 3);
+  }
+  // B: copy `wave` (when has_b)
+  const uint8_t* bsrc;
+  {
+    const uint8_t* wb = (const uint8_t*)(p.wl + e * p.wl_estride);
+    if (TRANS) {  // [K][r] rows of SR bytes; copy w covers bytes [1024 w, 1024 w + 1024) of the k-step
+      const int off = (has_b ? wave : 0) * 1024 + lane * 16;
+      bsrc = wb + (int64_t)(off / SR) * (p.r * 2) + (off % SR);
+    } else {      // [r][K]: copy w covers j rows 8 w .. 8 w + 7 (128 B of k each)
+      int j = (has_b ? wave : 0) * 8 + (lane >> 3);
+      if (j >= p.r) j = 0;
+      bsrc = wb + (int64_t)j * p.K * 2 + ((((lane & 7) ^ l_swz(j))) << 4);
+    }
+  }
+  const int64_t bstep = TRANS ? (int64_t)64 * p.r * 2 : 128;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(l_lds_addr(lds));
+  auto issue = [&](int kt) {
+    const uint32_t st = lds0 + (uint32_t)((kt % 3) * kLrStage);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) l_dma16(arow[i] + kt * 64, st + (uint32_t)((wave * 4 + i) * 1024));
+    if (has_b) l_dma16(bsrc + kt * bstep, st + (uint32_t)(kLrA + wave * 1024));
+  };
+  af3_f32x16 acc;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) acc[q] = 0.f;
+
+  issue(0);
+  if (nk > 1) issue(1);
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 1 < nk) {
+      if (has_b)
+        L_WAIT_VM(5);
+      else
+        L_WAIT_VM(4);
+    } else {
+      L_WAIT_VM(0);
+    }
+    L_BARRIER();
+    if (kt + 2 < nk) issue(kt + 2);
+    const uint8_t* as = lds + (kt % 3) * kLrStage;
+    const uint8_t* bs = as + kLrA;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int row = wave * 32 + lr;
+      const af3_bf16x8 a = *(const af3_bf16x8*)(as + row * 128 + (((s * 2 + lh) ^ l_swz(row)) << 4));
+      af3_bf16x8 b;
+      if (TRANS) {  // [64 k][SR]: rows k = 16 s + 8 lh + (0..7), column j = lr
+        const int gi = lane >> 4, q = lane & 15;
+        const int kr = s * 16 + (gi >> 1) * 8 + (q >> 2);
+        const int col = (gi & 1) * 16 + 4 * (q & 3);
+        b = l_tr8(bs + kr * SR + col * 2, bs + (kr + 4) * SR + col * 2);
+      } else {
+        b = *(const af3_bf16x8*)(bs + lr * 128 + (((s * 2 + lh) ^ l_swz(lr)) << 4));
+      }
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+    }
+  }
+  const int j = lr;
+  if (j < p.r) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int row = wave * 32 + (q >> 2) * 8 + lh * 4 + (q & 3);
+      if (row < nrows) p.out[(int64_t)(row_lo + row) * p.ld_out + j] = (uint16_t)af3_f32_to_bf16(acc[q] * p.scale);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// wgrad partials: P[chunk] = sum_{r in chunk} Big[b(r)][c0 + (0..255)]^T (x) (rs(r) Small[r][0..r))
+// Block = (chunk of chunk_rows expert-sorted rows, 256 Big columns); 4 waves of
+// 64 columns x 32.  Per 64-row step: Big rows [64][256] (512 B rows, 16-byte
+// chunks XOR-swizzled by 2 (row & 3) so the transposing reads of 4 rows hit
+// distinct banks) and Small rows [64][SR bytes] go global->LDS (2 stages);
+// then each Small row is multiplied by rs(r) (0 past the chunk's rows) in place.
+// MODE 0 writes P as [W][r] (dB), MODE 1 as [r][W] (dA).
+// ---------------------------------------------------------------------------
+struct LwParams {
+  const uint16_t* big;
+  int64_t ld_big;
+  const int32_t* big_gather;
+  int big_div;
+  const uint16_t* small;  // [rows][r], compact
+  const uint16_t* rowscale;
+  const int32_t* offs;
+  const int32_t* chunk_map;
+  int chunk_rows;
+  int W, r, nbb;
+  float* partials;
+};
+
+constexpr int kLwBig = 64 * 512;
+constexpr int kLwSmall = 64 * 64;
+constexpr int kLwStage = kLwBig + kLwSmall;
+
+__device__ __forceinline__ int lw_big_off(int row, int col) {  // byte offset of Big[row][col] (col % 4 == 0)
+  return row * 512 + ((((col >> 3) ^ ((row & 3) << 1))) << 4) + ((col & 7) << 1);
+}
+
+template <int SR, int MODE>
+__global__ __launch_bounds__(256) void lwg_kernel(LwParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kLwStage];
+  const int chunk = blockIdx.x / p.nbb, bb = blockIdx.x % p.nbb;
+  const int32_t ent = p.chunk_map[chunk];
+  if (ent < 0) return;
+  const int e = ent & 0xFFFF, cb = ent >> 16;
+  const int kb = p.offs[e] + cb * p.chunk_rows;
+  const int kend = min(p.chunk_rows, p.offs[e + 1] - kb);
+  if (kend <= 0) return;
+  const int c0 = bb * 256;
+  const int ncols = min(256, p.W - c0);
+  const int nsteps = (kend + 63) / 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  constexpr int NS = (64 * SR) / 1024;  // Small copies per step (block)
+  const bool has_s = wave < NS;
+
+  // Big: 8 copies per wave, copy i covers rows 2 i, 2 i + 1
+  const uint16_t* brow[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int rr = (wave * 8 + i) * 2 + (lane >> 5);
+    const int lc = (lane & 31) ^ ((rr & 3) << 1);
+    const int col = lc * 8 < ncols ? c0 + lc * 8 : c0;
+    brow[i] = p.big + col;  // row part added per step (the gather differs per row)
+    (void)rr;
+  }
+  const uint8_t* ssrc = (const uint8_t*)p.small;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(l_lds_addr(lds));
+  auto issue = [&](int st_i) {
+    const uint32_t st = lds0 + (uint32_t)((st_i & 1) * kLwStage);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rr = (wave * 8 + i) * 2 + (lane >> 5);
+      const int rl = st_i * 64 + rr;
+      int64_t src = kb + (rl < kend ? rl : 0);
+      if (p.big_gather) src = p.big_gather[src] / p.big_div;
+      l_dma16(brow[i] + src * p.ld_big, st + (uint32_t)((wave * 8 + i) * 1024));
+    }
+    if (has_s) {
+      const int off = wave * 1024 + lane * 16;  // byte offset inside the step's Small rows
+      const int rr = off / SR;
+      const int rl = st_i * 64 + rr;
+      const int64_t srow = kb + (rl < kend ? rl : 0);
+      l_dma16(ssrc + srow * SR + (off % SR), st + (uint32_t)(kLwBig + wave * 1024));
+    }
+  };
+  af3_f32x16 acc[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int q = 0; q < 16; ++q) acc[t][q] = 0.f;
+
+  issue(0);
+  for (int st_i = 0; st_i < nsteps; ++st_i) {
+    if (st_i + 1 < nsteps) issue(st_i + 1);
+    if (st_i + 1 < nsteps) {
+      if (has_s)
+        L_WAIT_VM(9);
+      else
+        L_WAIT_VM(8);
+    } else {
+      L_WAIT_VM(0);
+    }
+    L_BARRIER();
+    uint8_t* bs = lds + (st_i & 1) * kLwStage;
+    uint8_t* ss = bs + kLwBig;
+    // row scale rs(r) -> bf16(rs(r) * operand A of the entry point) (the
+    // Small side in MODE 1, the Big side in MODE 0); rows past the chunk get 0
+    // on the Small side
+    {
+      constexpr int TPR = 256 / 64;  // threads per row
+      const int rr = threadIdx.x / TPR, part = threadIdx.x % TPR;
+      const int rl = st_i * 64 + rr;
+      const bool valid = rl < kend;
+      const float rs = (valid && p.rowscale) ? af3_bf16_to_f32(p.rowscale[kb + rl]) : 1.f;
+      constexpr int VPT = SR / 2 / TPR;  // Small values per thread (4 or 8)
+      const float ssc = valid ? (MODE == 1 ? rs : 1.f) : 0.f;
+      uint16_t* v = (uint16_t*)(ss + rr * SR) + part * VPT;
+#pragma unroll
+      for (int q = 0; q < VPT; ++q) v[q] = (uint16_t)af3_f32_to_bf16(af3_bf16_to_f32(v[q]) * ssc);
+      if (MODE == 0 && p.rowscale) {  // this thread's 64 Big values of row rr (order inside the row is irrelevant)
+        af3_u32x4* bv = (af3_u32x4*)(bs + rr * 512 + part * 128);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          af3_u32x4 w = bv[c];
+#pragma unroll
+          for (int h = 0; h < 4; ++h)
+            w[h] = af3_pack_bf16x2(af3_bf16_to_f32(w[h] & 0xFFFFu) * rs, af3_bf16_to_f32(w[h] >> 16) * rs);
+          bv[c] = w;
+        }
+      }
+    }
+    L_BARRIER();
+    const int gi = lane >> 4, q = lane & 15;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int kr = s * 16 + (gi >> 1) * 8 + (q >> 2);
+      const int scol = (gi & 1) * 16 + 4 * (q & 3);
+      const af3_bf16x8 b = l_tr8(ss + kr * SR + scol * 2, ss + (kr + 4) * SR + scol * 2);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int bcol = wave * 64 + t * 32 + (gi & 1) * 16 + 4 * (q & 3);
+        const af3_bf16x8 a = l_tr8(bs + lw_big_off(kr, bcol), bs + lw_big_off(kr + 4, bcol));
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[t], 0, 0, 0);
+      }
+    }
+    L_BARRIER();  // the stage is refilled by the next step's copies
+  }
+  // acc[t][q]: Big column c0 + 64 wave + 32 t + i (i = 8 (q / 4) + 4 lh + q % 4), Small column j = lane % 32
+  const int lr = lane & 31, lh = lane >> 5;
+  const int j = lr;
+  if (j >= p.r) return;
+  float* P = p.partials + (int64_t)chunk * p.W * p.r;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int qq = 0; qq < 16; ++qq) {
+      const int col = c0 + wave * 64 + t * 32 + (qq >> 2) * 8 + lh * 4 + (qq & 3);
+      if (col < c0 + ncols) {
+        if (MODE == 0)
+          P[(int64_t)col * p.r + j] = acc[t][qq];
+        else
+          P[(int64_t)j * p.W + col] = acc[t][qq];
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void lwg_reduce_kernel(const float* __restrict__ partials,
+                                                         const int32_t* __restrict__ chunk_offs, int64_t MN,
+                                                         float scale, uint16_t* __restrict__ g) {
+  const int e = blockIdx.y;
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= MN) return;
+  const int c0 = chunk_offs[e], c1 = chunk_offs[e + 1];
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  for (int c = c0; c < c1; ++c) {
+    const float4 v = *(const float4*)(partials + (int64_t)c * MN + i);
+    a0 += v.x;
+    a1 += v.y;
+    a2 += v.z;
+    a3 += v.w;
+  }
+  uint2 o;
+  o.x = af3_pack_bf16x2(a0 * scale, a1 * scale);
+  o.y = af3_pack_bf16x2(a2 * scale, a3 * scale);
+  *(uint2*)(g + (int64_t)e * MN + i) = o;
+}
+
+inline bool l_al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+namespace af3 {
+
+int lora_rows_fast(const uint16_t* x, int64_t ldx, const int32_t* gather, int gdiv, const uint16_t* wl, int trans_b,
+                   float scale, const int32_t* token_offs, const int32_t* block_pid_map, int max_tiles, int n_out,
+                   int K, uint16_t* out, int64_t ld_out, hipStream_t stream) {
+  if (!(n_out == 16 || n_out == 32) || K % 64 != 0 || ldx % 8 != 0 || !l_al16(x) || !l_al16(wl)) return AF3_EUNSUPPORTED;
+  LrParams p{};
+  p.x = x;
+  p.ldx = ldx;
+  p.gather = gather;
+  p.gdiv = gdiv > 0 ? gdiv : 1;
+  p.wl = wl;
+  p.wl_estride = (int64_t)n_out * K;
+  p.scale = scale;
+  p.offs = token_offs;
+  p.tile_map = block_pid_map;
+  p.K = K;
+  p.r = n_out;
+  p.out = out;
+  p.ld_out = ld_out;
+  const dim3 grid(max_tiles), block(256);
+  if (trans_b == 0)
+    hipLaunchKernelGGL((lrows_kernel<false, 64>), grid, block, 0, stream, p);
+  else if (n_out == 32)
+    hipLaunchKernelGGL((lrows_kernel<true, 64>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((lrows_kernel<true, 32>), grid, block, 0, stream, p);
+  return check_launch("lora_rows");
+}
+
+int lora_wgrad_fast(const uint16_t* big, int64_t ld_big, const int32_t* big_gather, int big_div,
+                    const uint16_t* small, int64_t ld_small, const uint16_t* rowscale, int small_is_a, int W, int r,
+                    float scale, const int32_t* token_offs, const int32_t* chunk_map, const int32_t* chunk_offs,
+                    int max_chunks, int chunk_rows, int n_expts, float* partials, uint16_t* g, hipStream_t stream) {
+  if (!(r == 16 || r == 32) || ld_small != r || W % 8 != 0 || ld_big % 8 != 0 || !l_al16(big) || !l_al16(small) ||
+      !l_al16(partials) || !l_al16(g))
+    return AF3_EUNSUPPORTED;
+  LwParams p{};
+  p.big = big;
+  p.ld_big = ld_big;
+  p.big_gather = big_gather;
+  p.big_div = big_div > 0 ? big_div : 1;
+  p.small = small;
+  p.rowscale = rowscale;
+  p.offs = token_offs;
+  p.chunk_map = chunk_map;
+  p.chunk_rows = chunk_rows;
+  p.W = W;
+  p.r = r;
+  p.nbb = (W + 255) / 256;
+  p.partials = partials;
+  if (max_chunks > 0) {
+    const dim3 grid((unsigned)max_chunks * p.nbb), block(256);
+    // small_is_a: G = Small^T Big ([r][W], the dA form); else G = Big^T Small ([W][r], dB)
+    if (r == 32) {
+      if (small_is_a)
+        hipLaunchKernelGGL((lwg_kernel<64, 1>), grid, block, 0, stream, p);
+      else
+        hipLaunchKernelGGL((lwg_kernel<64, 0>), grid, block, 0, stream, p);
+    } else {
+      if (small_is_a)
+        hipLaunchKernelGGL((lwg_kernel<32, 1>), grid, block, 0, stream, p);
+      else
+        hipLaunchKernelGGL((lwg_kernel<32, 0>), grid, block, 0, stream, p);
+    }
+    const int rc = check_launch("lora_wgrad/partial");
+    if (rc) return rc;
+  }
+  const int64_t MN = (int64_t)W * r;
+  hipLaunchKernelGGL(lwg_reduce_kernel, dim3((unsigned)af3_cdiv(MN / 4, 256), n_expts), dim3(256), 0, stream,
+                     partials, chunk_offs, MN, scale, g);
+  return check_launch("lora_wgrad/reduce");
+}
+
+}  // namespace af3

@@ -1946,6 +1946,11 @@ extern "C" int af3_lora_rows(const uint16_t* x, int64_t ldx, const int32_t* gath
   if (max_tiles == 0) return 0;
   AF3_REQUIRE(K % 8 == 0 && n_out % 8 == 0 && ldx % 8 == 0 && al16(x) && al16(wl),
               "lora_rows: operands must be 16-byte aligned with sizes % 8 == 0");
+  {
+    const int rc = af3::lora_rows_fast(x, ldx, gather_indx, gather_div, wl, trans_b, scale, token_offs, block_pid_map,
+                                       max_tiles, n_out, K, out, ld_out, stream);
+    if (rc != AF3_EUNSUPPORTED) return rc;
+  }
   Params p{};
   p.a = make_bf16(x, ldx, 0, gather_indx, gather_div);
   p.b = trans_b == 0 ? make_bf16(wl, K, (int64_t)n_out * K, nullptr, 1)
@@ -2001,6 +2006,16 @@ extern "C" int af3_lora_wgrad(const uint16_t* a, int64_t lda, const int32_t* a_g
               "lora_wgrad: operands must be 16-byte aligned with sizes % 8 == 0");
   AF3_REQUIRE(partial_bytes >= af3_lora_wgrad_workspace_bytes(max_chunks, M, N) && partials && al16(partials),
               "lora_wgrad: partials workspace too small");
+  {
+    int rc = AF3_EUNSUPPORTED;
+    if ((N == 16 || N == 32) && b_gather == nullptr)  // G = A^T B with B the rank side: [M][r]
+      rc = af3::lora_wgrad_fast(a, lda, a_gather, a_div, b, ldb, a_rowscale, 0, M, N, scale, token_offs, chunk_map,
+                                chunk_offs, max_chunks, chunk_rows, n_expts, partials, g, stream);
+    else if ((M == 16 || M == 32) && a_gather == nullptr)  // A the rank side: [r][N]
+      rc = af3::lora_wgrad_fast(b, ldb, b_gather, b_div, a, lda, a_rowscale, 1, N, M, scale, token_offs, chunk_map,
+                                chunk_offs, max_chunks, chunk_rows, n_expts, partials, g, stream);
+    if (rc != AF3_EUNSUPPORTED) return rc;
+  }
   Params p{};
   p.a = make_bf16(a, lda, 0, a_gather, a_div, a_rowscale);
   p.b = make_bf16(b, ldb, 0, b_gather, b_div);

@@ -139,20 +139,25 @@ def test_lora_rows(dev, trans, r):
     assert ok, frac
 
 
-@pytest.mark.parametrize("M,N,gather_b,rowscale", [(192, 16, False, True), (16, 128, True, False),
-                                                   (192, 32, True, True), (32, 160, False, False)])
-def test_lora_wgrad(dev, M, N, gather_b, rowscale):
+@pytest.mark.parametrize("M,N,gather_a,gather_b,rowscale", [
+    (192, 16, False, False, True), (16, 128, False, True, False), (192, 32, False, True, True),
+    (32, 160, False, False, False),
+    (320, 32, True, False, True),   # the dB form: wide operand gathered + row-scaled, rank side plain
+    (32, 384, False, True, True),   # the dA form: rank side row-scaled, wide operand gathered
+])
+def test_lora_wgrad(dev, M, N, gather_a, gather_b, rowscale):
     g, x, logits, blocks, scales, bias = _problem(seed=5)
     K = 4
     ref, (rd, gi, si) = _route(logits, K, dev)
     R_ = x.shape[0] * K
-    a = torch.randn(R_, M, generator=g).to(torch.bfloat16)
+    a = torch.randn(x.shape[0] if gather_a else R_, M, generator=g).to(torch.bfloat16)
     b = torch.randn(x.shape[0] if gather_b else R_, N, generator=g).to(torch.bfloat16)
     E = blocks.shape[0]
     rs = rd.gate_scal if rowscale else None
-    out = Q._lora_wgrad(a.to(dev), None, 1, rs, b.to(dev), gi.src_indx if gather_b else None, K if gather_b else 1,
-                        rd.expt_data, E, M, N)
-    refo = moe.wgrad(a, b, ref["offs"], a_rowscale=ref["gate_scal"] if rowscale else None,
+    out = Q._lora_wgrad(a.to(dev), gi.src_indx if gather_a else None, K if gather_a else 1, rs, b.to(dev),
+                        gi.src_indx if gather_b else None, K if gather_b else 1, rd.expt_data, E, M, N)
+    refo = moe.wgrad(a, b, ref["offs"], a_gather=ref["topk_indx"] if gather_a else None, a_div=K,
+                     a_rowscale=ref["gate_scal"] if rowscale else None,
                      b_gather=ref["topk_indx"] if gather_b else None, b_div=K)
     assert int(ref["hist"][-1]) == 0 and out[-1].abs().max() == 0     # idle expert -> zero gradient
     ok, frac = _close(out, refo, rtol=RTOL, atol=5e-2)
