@@ -1003,34 +1003,54 @@ __device__ __forceinline__ af3_bf16x8 g4_bfrag(uint32_t v, uint32_t sc, float sc
   return g4_cvt(v, scf);
 }
 
-// one 64-deep k-step of a wave's (32 TM) x (32 TN) tile; FULL: every
-// sub-tile live.  Instruction order is fixed by scheduling barriers: the
-// conversions of the next sub-step's B fragments and the k-step's DPW
-// global->LDS copies are spread between the MFMAs, and the A-fragment LDS
-// reads of sub-step s + 1 are issued ahead of the MFMAs of sub-step s.
+// one 64-deep k-step of a wave's (32 TM) x (32 TN) tile, software-pipelined
+// by one sub-step: af[1] / bf[1] enter holding the previous k-step's last
+// sub-step (zeros before the first k-step), whose MFMAs run first and cover
+// the LDS reads and B conversions of this k-step's sub-step 0; this k-step's
+// sub-step 3 leaves in af[1] / bf[1].  FULL: every sub-tile live.
+// Instruction order is fixed by scheduling barriers: the conversions of the
+// next sub-step's B fragments and the k-step's DPW global->LDS copies are
+// spread between the MFMAs, and the A-fragment LDS reads of sub-step s + 1
+// are issued ahead of the MFMAs of sub-step s.
 template <int TM, int TN, int DPW, bool FULL, bool EXACT, class Dma>
-__device__ __forceinline__ void g4_kstep(const uint16_t* as, const af3_u32x4 bp[TN], const uint32_t sc[TN], int wm0,
-                                         int tm_live, int tn_live, af3_f32x16 acc[TM][TN], Dma&& dma) {
-  constexpr int NM = TM * TN * 4;          // MFMAs per k-step
-  constexpr int GAP = NM / (DPW + 1);      // MFMAs between copies
+__device__ __forceinline__ void g4_kstep(const uint16_t* as, const uint8_t* bs, const uint8_t* ss, int G, int kt,
+                                         int wm0, int wn0, int tm_live, int tn_live, af3_f32x16 acc[TM][TN],
+                                         af3_bf16x8 af[2][TM], af3_bf16x8 bf[2][TN], Dma&& dma) {
+  constexpr int NM = TM * TN * 4;      // MFMAs per k-step
+  constexpr int GAP = NM / (DPW + 1);  // MFMAs between copies
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
+  af3_u32x4 bp[TN];
+  uint32_t sc[TN];
   float scf[TN];
+  // (partial tiles: no LDS reads or conversions for dead sub-tiles)
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) {
+    const int n = wn0 + tn * 32 + lr;
+    if (FULL || tn < tn_live) {
+      bp[tn] = *(const af3_u32x4*)(bs + g4_b_off(n, lh));
+      sc[tn] = ss[n * G + 2 * kt + lh];
+    } else {
+      bp[tn] = zero4();
+      sc[tn] = 127u;
+    }
+  }
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+    if (FULL || tm < tm_live) af[0][tm] = *(const af3_bf16x8*)(as + lds_off(wm0 + tm * 32 + lr, lh * 4));
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) scf[tn] = __uint_as_float(sc[tn] << 23);
-  af3_bf16x8 af[2][TM], bf[2][TN];
+  // sub-step -1 (the carried one) and sub-steps 0..2; the k-step's copies
+  // are spread over all of their MFMAs
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm) af[0][tm] = *(const af3_bf16x8*)(as + lds_off(wm0 + tm * 32 + lr, lh * 4));
-#pragma unroll
-  for (int tn = 0; tn < TN; ++tn) bf[0][tn] = g4_bfrag<EXACT>(bp[tn][0], sc[tn], scf[tn]);
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const int c = s & 1, nx = c ^ 1;
+  for (int s = -1; s < 3; ++s) {
+    const int c = s < 0 ? 1 : (s & 1);  // fragments used by this sub-step
+    const int nx = s < 0 ? 0 : (c ^ 1);  // fragments of sub-step s + 1
     __builtin_amdgcn_sched_barrier(0);
-    if (s + 1 < 4) {
+    if (s >= 0) {
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm)
-        af[nx][tm] = *(const af3_bf16x8*)(as + lds_off(wm0 + tm * 32 + lr, lh * 4 + s + 1));
+        if (FULL || tm < tm_live) af[nx][tm] = *(const af3_bf16x8*)(as + lds_off(wm0 + tm * 32 + lr, lh * 4 + s + 1));
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1038,12 +1058,11 @@ __device__ __forceinline__ void g4_kstep(const uint16_t* as, const af3_u32x4 bp[
       const int tm = i / TN, tn = i % TN;
       if (FULL || (tm < tm_live && tn < tn_live))
         acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[c][tm], bf[c][tn], acc[tm][tn], 0, 0, 0);
-      constexpr int CV = TM * TN / TN;  // conversion slot spacing: one fragment per TM MFMAs
-      if (s + 1 < 4 && (i % CV) == CV - 1) {
-        const int t = i / CV;
-        bf[nx][t] = g4_bfrag<EXACT>(bp[t][s + 1], sc[t], scf[t]);
+      if ((i % TM) == TM - 1) {  // one B fragment of sub-step s + 1 per TM MFMAs
+        const int t = i / TM;
+        if (FULL || t < tn_live) bf[nx][t] = g4_bfrag<EXACT>(bp[t][s + 1], sc[t], scf[t]);
       }
-      const int q = s * TM * TN + i;
+      const int q = (s + 1) * TM * TN + i;
       if (q % GAP == GAP / 2 && q / GAP < DPW) dma(q / GAP);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1172,39 +1191,60 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm4_fwd_kernel(Params p) {
 
   auto kloop = [&](auto full_c, auto exact_c) {
     constexpr bool FULL = decltype(full_c)::value, EXACT = decltype(exact_c)::value;
-    for (int kt = 0; kt < nk; ++kt) {
-      if (kt + 1 < nk) {
-        if constexpr (DPW == 10)
-          AF3_ASM_WAIT_VM(10);
-        else
-          AF3_ASM_WAIT_VM(5);
-      } else {
-        AF3_ASM_WAIT_VM(0);
-      }
-      AF3_ASM_BARRIER();
-      const bool pf = kt + 2 < nk;
-      const int st = kt % kG4Stages;
-      const uint16_t* as = As + st * kG4AStage;
-      const uint8_t* bs = Bs + st * kG4BStage;
-      af3_u32x4 bp[TN];
-      uint32_t sc[TN];
+    af3_bf16x8 af[2][TM], bf[2][TN];
+    const af3_bf16x8 zf = __builtin_bit_cast(af3_bf16x8, zero4());
 #pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        const int n = wn0 + tn * 32 + lr;
-        bp[tn] = *(const af3_u32x4*)(bs + g4_b_off(n, lh));
-        sc[tn] = Ss[n * G + 2 * kt + lh];
-      }
-      g4_kstep<TM, TN, DPW, FULL, EXACT>(as, bp, sc, wm0, tm_live, tn_live, acc, [&](int j) {
-        if (pf) issue_one(kt + 2, j);
-      });
+    for (int tm = 0; tm < TM; ++tm) af[1][tm] = zf;
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) bf[1][tn] = zf;
+    // k-step kt: its stage is complete once this wave's copies for it have
+    // landed (at most DPW newer ones outstanding) and every wave passed the
+    // barrier, which also orders the carried fragment reads of stage kt - 1
+    // before the copies into that stage (issued for kt + 2 during kt)
+    auto step = [&](int kt, bool last, auto&& dma) {
+      if (last)
+        AF3_ASM_WAIT_VM(0);
+      else if constexpr (DPW == 10)
+        AF3_ASM_WAIT_VM(10);
+      else
+        AF3_ASM_WAIT_VM(5);
+      AF3_ASM_LDS_BARRIER();
+      const int st = kt % kG4Stages;
+      g4_kstep<TM, TN, DPW, FULL, EXACT>(As + st * kG4AStage, Bs + st * kG4BStage, Ss, G, kt, wm0, wn0, tm_live,
+                                         tn_live, acc, af, bf, dma);
+    };
+    int kt = 0;
+    for (; kt + 2 < nk; ++kt) step(kt, false, [&](int j) { issue_one(kt + 2, j); });
+    for (; kt < nk; ++kt) step(kt, kt + 1 == nk, [](int) {});
+    // the last k-step's sub-step 3
+#pragma unroll
+    for (int i = 0; i < TM * TN; ++i) {
+      const int tm = i / TN, tn = i % TN;
+      if (FULL || (tm < tm_live && tn < tn_live))
+        acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[1][tm], bf[1][tn], acc[tm][tn], 0, 0, 0);
     }
   };
-  if (odd)
+  if (odd) {
     kloop(std::false_type{}, std::true_type{});
-  else if (full)
+  } else if (full) {
     kloop(std::true_type{}, std::false_type{});
-  else
+  } else if (tm_live > 0 && tn_live > 0) {
     kloop(std::false_type{}, std::false_type{});
+  } else {
+    // a wave with no live sub-tile (rows or columns past the end of a
+    // partial tile) only keeps the copy / barrier protocol of the k-loop, so
+    // the live wave sharing its SIMD runs alone
+    for (int kt = 0; kt < nk; ++kt) {
+      if (kt + 1 == nk)
+        AF3_ASM_WAIT_VM(0);
+      else if constexpr (DPW == 10)
+        AF3_ASM_WAIT_VM(10);
+      else
+        AF3_ASM_WAIT_VM(5);
+      AF3_ASM_LDS_BARRIER();
+      if (kt + 2 < nk) issue(kt + 2);
+    }
+  }
 
   if constexpr (BXK != NONE) {
     if (p.kx > 0) {  // expert-LoRA segment: + L[r] . Bx[e][n]^T, both bf16 through LDS
@@ -1270,8 +1310,9 @@ __device__ __forceinline__ bool d4_odd4(uint32_t x) {
 
 // B fragments of the sub-tile pair (even, odd columns) for one sub-step from
 // the 8 packed bytes (w0: k 0..3, w1: k 4..7) and their 8 scale bytes.
-__device__ __forceinline__ void d4_frags(uint32_t w0, uint32_t w1, uint32_t s0, uint32_t s1, bool exact,
-                                         af3_bf16x8& ev, af3_bf16x8& od) {
+template <bool EXACT>
+__device__ __forceinline__ void d4_frags(uint32_t w0, uint32_t w1, uint32_t s0, uint32_t s1, af3_bf16x8& ev,
+                                         af3_bf16x8& od) {
   uint32_t dw[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -1285,7 +1326,7 @@ __device__ __forceinline__ void d4_frags(uint32_t w0, uint32_t w1, uint32_t s0, 
       default: dw[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, sc, 3)); break;
     }
   }
-  if (exact) {  // wave-uniform: only work items with out-of-range scale bytes pay for this
+  if constexpr (EXACT) {  // k-steps with scale bytes outside [2, 252] only
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t src = i < 4 ? w0 : w1;
@@ -1474,28 +1515,25 @@ __global__ __launch_bounds__(256) void gemm4_dgrad_kernel(Params p) {
   AF3_ASM_LDS_BARRIER();
   transpose(0);
 
-  auto kloop = [&](auto full_c) {
+  // one k-step; EXACT k-steps (scale bytes outside [2, 252]) take a separate
+  // copy of the body so the common one carries no fix-up code
+  auto kstep = [&](auto full_c, auto exact_c, int kt) {
     constexpr bool FULL = decltype(full_c)::value;
-    for (int kt = 0; kt < nk; ++kt) {
-      if (kt + 1 < nk)
-        AF3_ASM_WAIT_VM(11);
-      else
-        AF3_ASM_WAIT_VM(0);
-      AF3_ASM_LDS_BARRIER();
+    constexpr bool EXACT = decltype(exact_c)::value;
+    {
       const bool pf = kt + 2 < nk;
       const uint8_t* as = (const uint8_t*)As + (kt % kG4Stages) * kG4AStage * 2 + lr * 128;
       const uint8_t* tb = Tb + (kt & 1) * kD4TBuf;
       const uint8_t* tsb = Ts + (kt & 1) * kD4TsBuf;
-      const bool exact = __builtin_amdgcn_readfirstlane(oddk[kt & 1]) == kt;
       af3_bf16x8 af[2][8], bf[2][2];
       auto load_frags = [&](int sub, int slot) {
         const int c = lh * 4 + sub;
 #pragma unroll
         for (int tm = 0; tm < 8; ++tm)
-          af[slot][tm] = *(const af3_bf16x8*)(as + tm * 4096 + (((c ^ ax) ^ ((tm & 1) << 2)) << 4));
+          if (FULL || tm < tm_live) af[slot][tm] = *(const af3_bf16x8*)(as + tm * 4096 + (((c ^ ax) ^ ((tm & 1) << 2)) << 4));
         const uint2 wv = *(const uint2*)(tb + foff[sub]);
         const uint2 sv = *(const uint2*)(tsb + soff[sub]);
-        d4_frags(wv.x, wv.y, sv.x, sv.y, exact, bf[slot][0], bf[slot][1]);
+        d4_frags<EXACT>(wv.x, wv.y, sv.x, sv.y, bf[slot][0], bf[slot][1]);
       };
       if (FULL || wave_live) load_frags(0, 0);
 #pragma unroll
@@ -1518,10 +1556,30 @@ __global__ __launch_bounds__(256) void gemm4_dgrad_kernel(Params p) {
       }
     }
   };
-  if (full)
-    kloop(std::true_type{});
-  else
-    kloop(std::false_type{});
+  // The common loop returns at the first k-step whose scales need the exact
+  // rule; the exact loop (fix-up on every k-step) finishes the tile.  The
+  // flag is block-uniform, so every wave leaves at the same k-step (and the
+  // repeated wait + barrier there is matched by all waves).
+  auto kloop = [&](auto full_c, auto exact_c, int kt) -> int {
+    for (; kt < nk; ++kt) {
+      if (kt + 1 < nk)
+        AF3_ASM_WAIT_VM(11);
+      else
+        AF3_ASM_WAIT_VM(0);
+      AF3_ASM_LDS_BARRIER();
+      if constexpr (!decltype(exact_c)::value)
+        if (__builtin_amdgcn_readfirstlane(oddk[kt & 1]) == kt) return kt;
+      kstep(full_c, exact_c, kt);
+    }
+    return nk;
+  };
+  if (full) {
+    const int kt = kloop(std::true_type{}, std::false_type{}, 0);
+    if (kt < nk) kloop(std::true_type{}, std::true_type{}, kt);
+  } else {
+    const int kt = kloop(std::false_type{}, std::false_type{}, 0);
+    if (kt < nk) kloop(std::false_type{}, std::true_type{}, kt);
+  }
 
   if constexpr (BXK != NONE) {
     if (p.kx > 0) {  // expert-LoRA segment: + L[r] . Bx[e][:, n] (Bx [r][N], n contiguous)
