@@ -33,6 +33,7 @@ _SIGNATURES = {
     "af3_routing_replay": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _sz, _p]),
     "af3_routing_topk": (_i32, [_p, _i64, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _sz, _p]),
     "af3_expt_data": (_i32, [_p, _i32, _p, _i32, _i32, _p, _p, _p]),
+    "af3_tile_order": (_i32, [_p, _i32, _i32, _p, _i32, _p, _p]),
     "af3_moe_gemm": (_i32, [_p, _i64, _p, _i32, _p, _p, _i32, _p, _p, _i32, _p, _i64, _p, _i32,
                             _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p]),
     "af3_moe_combine": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _p, _i64, _p]),

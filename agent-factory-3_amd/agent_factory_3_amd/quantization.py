@@ -186,7 +186,9 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
     routing_data, k_act = _expt_data(routing_data, R, dev)
     ed = routing_data.expt_data
     bm = GEMM_TILE["block_m"] if K % 64 == 0 else 128
-    pid_map = ed.block_pid_map[bm]
+    pid_map = getattr(ed, "gemm_order", {}).get(bm) if GEMM_TILE.get("order", True) else None
+    if pid_map is None:
+        pid_map = ed.block_pid_map[bm]
     offs = ed.token_offs_raw
     y = torch.empty(R, N, dtype=torch.bfloat16, device=dev)
     if R == 0 or pid_map.numel() == 0:

@@ -26,6 +26,7 @@ from . import _capi
 # block sizes for which tile maps are built: 128- and 256-row GEMM tiles and
 # the 512-row chunks of the LoRA weight-gradient reduction
 BLOCK_MS = (128, 256, 512)
+GEMM_ORDER_BMS = (256,)
 
 
 @dataclass
@@ -48,6 +49,10 @@ class ExptData:
     token_offs_raw: torch.Tensor            # [E+1] int32 exclusive scan of hist
     token_offs_pad: dict = field(default_factory=dict)  # BM -> [E+1] int32 scan of ceil(hist/BM)
     block_pid_map: dict = field(default_factory=dict)   # BM -> [max_tiles] int32 (b<<16)|e or -1
+    # BM -> the block_pid_map entries in grouped-GEMM work order (full tiles
+    # first, then partial tiles by decreasing rows); not part of the
+    # reference's ExptData, filled for GEMM_ORDER_BMS
+    gemm_order: dict = field(default_factory=dict)
 
 
 @dataclass
@@ -94,6 +99,13 @@ def compute_expt_data(hist: torch.Tensor, n_expts_tot: int, n_gates: int,
     for i, bm in enumerate(BLOCK_MS):
         ed.token_offs_pad[bm] = offs_pad[i]
         ed.block_pid_map[bm] = pid_map[i, :mt]
+    if n_expts_tot <= 4096:
+        for bm in GEMM_ORDER_BMS:
+            n = max_tiles(n_gates, n_expts_tot, bm)
+            order = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+            _capi.call("af3_tile_order", hist.data_ptr(), n_expts_tot, bm, ed.token_offs_pad[bm].data_ptr(), n,
+                       order.data_ptr(), _capi.stream_of(dev))
+            ed.gemm_order[bm] = order[:n]
     return ed
 
 

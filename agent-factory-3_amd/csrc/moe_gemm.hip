@@ -882,6 +882,36 @@ constexpr int kG4LdsBytes = kG4Stages * (kG4AStage * 2 + kG4BStage) + kG4Rows * 
 static_assert(kG4LdsBytes >= 256 * 512 + 1024, "the epilogue reuses the LDS for the bf16 tile + row gammas");
 static_assert(kG4LdsBytes <= 160 * 1024, "gfx950 LDS per workgroup");
 
+// Work item (m-tile, n-tile) of workgroup b.  Work goes in groups of GM
+// m-tiles x all NN n-tiles (m-tile fastest inside a group, so the ~32 items an
+// XCD runs at once share GM activation tiles and 32 / GM weight tiles through
+// its L2); the groups are dealt to the 8 XCDs in turn (workgroup b runs on XCD
+// b % 8), so with the m-tiles listed full tiles first and partial tiles by
+// decreasing rows every XCD receives the same mix of expensive and cheap work.
+// Returns false for workgroups past the work (the grid is rounded up to whole
+// groups per XCD).
+__device__ __forceinline__ bool g4_work_item(const Params& p, int& mt, int& nt) {
+  const int NN = p.n_nblk;
+  const int Mt = p.tile_offs[p.E];
+  const int GM = p.group_m > 0 ? p.group_m : 1;
+  const int per_group = GM * NN;
+  const int x = blockIdx.x & 7, j = blockIdx.x >> 3;
+  const int q = j / per_group, r = j - q * per_group;
+  const int first_m = (x + 8 * q) * GM;
+  if (first_m >= Mt) return false;
+  const int gsz = min(GM, Mt - first_m);
+  if (r >= gsz * NN) return false;
+  mt = first_m + r % gsz;
+  nt = r / gsz;
+  return true;
+}
+
+// grid of g4_work_item for up to max_tiles m-tiles
+static inline unsigned g4_grid(int max_tiles, int NN, int GM) {
+  const long long groups = (max_tiles + GM - 1) / GM;
+  return (unsigned)(8 * ((groups + 7) / 8) * GM * NN);
+}
+
 // Epilogue of a 256x256 tile computed by 4 waves (2x2) of 4x4 32x32 MFMA
 // sub-tiles: v = (acc + bias[n]) * gamma[row] -> bf16, staged through LDS as
 // a [256][256] bf16 tile (16-byte chunks XOR-swizzled so the two row groups
@@ -1079,25 +1109,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm4_fwd_kernel(Params p) {
   uint8_t* const Bs = lds + kG4Stages * kG4AStage * 2;          // 3 x 8 KB
   uint8_t* const Ss = Bs + kG4Stages * kG4BStage;               // <= 32 KB
 
-  const int NN = p.n_nblk;
-  const int W = p.tile_offs[p.E] * NN;  // valid work items (device-side tile count)
-  const int b = blockIdx.x;
-  if (b >= W) return;
-  // XCD-aware order: consecutive workgroups go to the 8 XCDs in turn, so
-  // workgroup b takes work item (b % 8) * (W8 / 8) + b / 8 and each XCD walks a
-  // contiguous range.  Inside the range, items go in groups of G m-tiles x all
-  // n-tiles with the m-tile fastest, so the ~32 items an XCD runs at once
-  // share G activation tiles and 32 / G weight tiles through its L2 (with the
-  // n-tile fastest every m-tile would re-read the whole expert weight, which
-  // does not fit in the L2).
-  const int W8 = W & ~7;
-  const int w = b < W8 ? (b & 7) * (W8 >> 3) + (b >> 3) : b;
-  const int Mt = W / NN;
-  const int GM = p.group_m > 0 ? p.group_m : 1;
-  const int first_m = (w / (GM * NN)) * GM;
-  const int gsz = min(GM, Mt - first_m);
-  const int local = w - first_m * NN;
-  const int mt = first_m + local % gsz, nt = local / gsz;
+  int mt, nt;
+  if (!g4_work_item(p, mt, nt)) return;
   const int32_t ent = p.tile_map[mt];
   if (ent < 0) return;
   const int e = ent & 0xFFFF, blk = ent >> 16;
@@ -1355,18 +1368,8 @@ __global__ __launch_bounds__(256) void gemm4_dgrad_kernel(Params p) {
   uint8_t* const Tb = lds + kD4OffT;
   uint8_t* const Ts = lds + kD4OffTs;
 
-  const int NN = p.n_nblk;
-  const int W = p.tile_offs[p.E] * NN;
-  const int b = blockIdx.x;
-  if (b >= W) return;
-  const int W8 = W & ~7;
-  const int w = b < W8 ? (b & 7) * (W8 >> 3) + (b >> 3) : b;
-  const int Mt = W / NN;
-  const int GM = p.group_m > 0 ? p.group_m : 1;
-  const int first_m = (w / (GM * NN)) * GM;
-  const int gsz = min(GM, Mt - first_m);
-  const int local = w - first_m * NN;
-  const int mt = first_m + local % gsz, nt = local / gsz;
+  int mt, nt;
+  if (!g4_work_item(p, mt, nt)) return;
   const int32_t ent = p.tile_map[mt];
   if (ent < 0) return;
   const int e = ent & 0xFFFF, blk = ent >> 16;
@@ -1615,6 +1618,336 @@ __global__ __launch_bounds__(256) void gemm4_dgrad_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------
+// gemm5 dgrad: the same products as gemm4 dgrad (weights packed along the
+// output axis, W[e][k][n/32][16], scales [e][k][n/32]) with no transposing
+// pass.  Each k-step stage holds, all copied global->LDS two k-steps ahead in
+// a three-stage ring and published by one barrier per k-step:
+//   A   [256 rows][64 k] bf16, 16-byte chunks XOR-swizzled by row (as gemm4);
+//   B   the packed weight rows [64 k][128 B] (256 columns), 16-byte chunk c of
+//       row k stored in slot c ^ (k & 7);
+//   S   the e8m0 scales as zero-extended dwords [8 column blocks][64 k] (the
+//       byte form of the LDS copy writes one dword per lane, which turns the
+//       [k][block] bytes of HBM into block-major dwords on the way in).
+// A lane's B fragment for one sub-step is one ds_read_b64_tr_b8 of the staged
+// rows: within each 16-lane group, output lane j byte b comes from source lane
+// 2b + j / 8, byte j % 8, so pointing source lanes 2b and 2b + 1 at row
+// (k0 + b), 8-byte halves 0 and 1 of the group's 16 column pairs, hands lane
+// j the byte of column pair (base + j) at the 8 rows k0 .. k0 + 7.  One
+// v_cvt_scalef32_pk_bf16_fp4 per byte yields the (even, odd) column values
+// (the cvt reads only the exponent field of its scale operand, so the scale
+// dword shifted left by 23 is the operand); the even values feed one MFMA
+// sub-tile and the odd values its partner, as in gemm4 dgrad.
+// k inside a k-step is permuted as in gemm4 forward: lane (r, h) at sub-step
+// s covers k = 32 h + 8 s + (0..7) (A chunk 4 h + s), so a lane's scales of a
+// sub-step are 8 consecutive dwords of its block.
+// Four waves (one per SIMD), wave w owns all 256 rows and columns 64 w ..
+// 64 w + 63.  The last sub-step of each k-step is carried: its fragments are
+// read before the barrier and its MFMAs run after it, covering the LDS reads
+// and the B conversion of the next k-step's first sub-step.
+// Scale bytes outside [2, 252] (never produced by normal quantisers) are
+// detected per wave and k-step from the staged scales; such k-steps rebuild
+// their B fragments with the integer rule after the fast conversion.
+// ---------------------------------------------------------------------------
+constexpr int kD5Stages = 3;
+constexpr int kD5AOff = 0;
+constexpr int kD5BOff = 256 * 64 * 2;           // 32 KB of A
+constexpr int kD5SOff = kD5BOff + 64 * 128;     // + 8 KB of packed B
+constexpr int kD5Stage = kD5SOff + 8 * 64 * 4;  // + 2 KB of scale dwords = 42 KB
+constexpr int kD5LdsBytes = kD5Stages * kD5Stage > 256 * 512 + 1024 ? kD5Stages * kD5Stage : 256 * 512 + 1024;
+static_assert(kD5LdsBytes <= 160 * 1024, "gemm5 dgrad LDS budget");
+
+typedef __attribute__((ext_vector_type(2))) int af3_i32x2;
+
+// (even, odd) column fragments of one sub-step from the 8 packed bytes (w0:
+// k 0..3, w1: k 4..7) and the 8 scale dwords of those k
+__device__ __forceinline__ void d5_cvt(uint32_t w0, uint32_t w1, const uint32_t s[8], af3_bf16x8& ev,
+                                       af3_bf16x8& od) {
+  uint32_t dw[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t src = i < 4 ? w0 : w1;
+    const float sc = __uint_as_float(s[i] << 23);
+    switch (i & 3) {
+      case 0: dw[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, sc, 0)); break;
+      case 1: dw[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, sc, 1)); break;
+      case 2: dw[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, sc, 2)); break;
+      default: dw[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, sc, 3)); break;
+    }
+  }
+  af3_u32x4 e4, o4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    e4[j] = perm_lo(dw[2 * j], dw[2 * j + 1]);
+    o4[j] = perm_hi(dw[2 * j], dw[2 * j + 1]);
+  }
+  ev = __builtin_bit_cast(af3_bf16x8, e4);
+  od = __builtin_bit_cast(af3_bf16x8, o4);
+}
+
+// the same with the integer rule (exact for every scale byte)
+__device__ __forceinline__ void d5_cvt_exact(uint32_t w0, uint32_t w1, const uint32_t s[8], af3_bf16x8& ev,
+                                             af3_bf16x8& od) {
+  uint32_t dw[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t byte = ((i < 4 ? w0 : w1) >> (8 * (i & 3))) & 0xFFu;
+    dw[i] = af3_e2m1_to_bf16_bits(byte & 0xFu, s[i]) | (af3_e2m1_to_bf16_bits(byte >> 4, s[i]) << 16);
+  }
+  af3_u32x4 e4, o4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    e4[j] = perm_lo(dw[2 * j], dw[2 * j + 1]);
+    o4[j] = perm_hi(dw[2 * j], dw[2 * j + 1]);
+  }
+  ev = __builtin_bit_cast(af3_bf16x8, e4);
+  od = __builtin_bit_cast(af3_bf16x8, o4);
+}
+
+template <int BXK>
+__global__ __launch_bounds__(256) void gemm5_dgrad_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kD5LdsBytes];
+
+  int mt, nt;
+  if (!g4_work_item(p, mt, nt)) return;
+  const int32_t ent = p.tile_map[mt];
+  if (ent < 0) return;
+  const int e = ent & 0xFFFF, blk = ent >> 16;
+  const int row_lo = p.offs[e] + blk * kG4Rows;
+  const int nrows = min(kG4Rows, p.offs[e + 1] - row_lo);
+  if (nrows <= 0) return;
+  const int n0 = nt * kG4Rows;
+  const int ncols = min(kG4Rows, p.N - n0);  // multiple of 64
+  const int nk = p.K / kBK;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = lane & 31, lh = lane >> 5;
+  const int wn0 = wave * 64;
+  const int tm_live = min(8, (nrows + 31) >> 5);
+  const bool wave_live = wn0 < ncols;
+  const bool full = tm_live == 8 && wave_live;
+
+  // ---- global -> LDS copy sources (12 instructions per wave per k-step) ----
+  const uint16_t* arow[8];  // A: rows (8 w + i) * 8 + lane / 8, chunk lane % 8 (swizzled)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = (wave * 8 + i) * 8 + (lane >> 3);
+    int64_t src = row_lo + (row < nrows ? row : 0);
+    if (p.a.gather) src = p.a.gather[src] / p.a.gdiv;
+    arow[i] = (const uint16_t*)p.a.ptr + src * p.a.ld + (((lane & 7) ^ swz(row)) << 3);
+  }
+  const uint8_t* bsrc[2];  // B: rows 8 q .. 8 q + 7 (q = 2 w + j), LDS slot lane % 8 holds chunk slot ^ (k & 7)
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int kr = (wave * 2 + j) * 8 + (lane >> 3);
+    int c = (lane & 7) ^ (kr & 7);
+    if (c * 32 >= ncols) c = 0;  // columns past the tile: any valid bytes (never read)
+    bsrc[j] = (const uint8_t*)p.b.ptr + e * p.b.estride + (int64_t)kr * p.b.ld + (n0 >> 1) + c * 16;
+  }
+  const uint8_t* ssrc[2];  // S: block q = 2 w + j, k row = lane
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    int q = wave * 2 + j;
+    if (q * 32 >= ncols) q = 0;
+    ssrc[j] = p.b.scales + e * p.b.sestride + (int64_t)lane * p.b.sld + (n0 >> 5) + q;
+  }
+  const int64_t bstep = (int64_t)kBK * p.b.ld, sstep = (int64_t)kBK * p.b.sld;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+  // copy j (0..11) of k-step kc: 0..7 A, 8..9 B, 10..11 S
+  auto issue_one = [&](int kc, int j) {
+    const uint32_t st = lds0 + (uint32_t)((kc % kD5Stages) * kD5Stage);
+    if (j < 8) {
+      g4_dma16(arow[j] + kc * kBK, st + (uint32_t)(kD5AOff + (wave * 8 + j) * 1024));
+    } else if (j < 10) {
+      g4_dma16(bsrc[j - 8] + kc * bstep, st + (uint32_t)(kD5BOff + (wave * 2 + j - 8) * 1024));
+    } else {
+      asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_ubyte %0, off" ::"v"(ssrc[j - 10] + kc * sstep),
+                   "s"(st + (uint32_t)(kD5SOff + (wave * 2 + j - 10) * 256))
+                   : "memory", "m0");
+    }
+  };
+  auto issue = [&](int kc) {
+#pragma unroll
+    for (int j = 0; j < 12; ++j) issue_one(kc, j);
+  };
+
+  // ---- lane-fixed LDS byte offsets inside a stage ----
+  const int ax = (lr ^ (lr >> 3)) & 7;
+  int aoff[2][4];  // A fragment of row group tm at sub-step s: aoff[tm & 1][s] + 4096 tm
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) aoff[t][s] = kD5AOff + lr * 128 + ((((lh * 4 + s) ^ ax) ^ (t << 2)) << 4);
+  // B transposed read: group g = lane / 16 (k half g / 2, column-pair half g % 2), i = lane % 16
+  const int gi = lane & 15, gg = lane >> 4;
+  const int boff = kD5BOff + (32 * (gg >> 1) + (gi >> 1)) * 128 + (((2 * wave + (gg & 1)) ^ (gi >> 1)) << 4) +
+                   (gi & 1) * 8;  // + 1024 s
+  const int soff = kD5SOff + ((2 * wave + (gg & 1)) * 64 + 32 * (gg >> 1)) * 4;  // + 32 s
+  const int coff = kD5SOff + (2 * wave * 64 + 2 * lane) * 4;  // the wave's 128 scale dwords, 2 per lane
+
+  af3_f32x16 acc[8][2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  issue(0);
+  if (nk > 1) issue(1);
+
+  auto kloop = [&](auto full_c) {
+    constexpr bool FULL = decltype(full_c)::value;
+    af3_bf16x8 af[2][8], bf[2][2];
+    // one k-step: iterations s = -1 (the carried sub-step of the previous
+    // k-step, skipped at kt = 0) and 0..2; iteration s runs the MFMAs of
+    // sub-step s while reading and converting the fragments of s + 1
+    auto kstep = [&](int kt, bool first, bool pf) {
+      const uint8_t* stg = lds + (kt % kD5Stages) * kD5Stage;
+      const int nxt_copy = kt + 2;
+      bool odd = false;
+#pragma unroll
+      for (int s = -1; s < 3; ++s) {
+        const int c = s < 0 ? 1 : (s & 1);   // fragments of sub-step s
+        const int nx = s < 0 ? 0 : (c ^ 1);  // fragments of sub-step s + 1
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t w0 = 0, w1 = 0;
+        uint32_t sc[8];
+        uint32_t chk0 = 2, chk1 = 2;
+        if (FULL || wave_live) {
+          const af3_i32x2 wv =
+              __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) af3_i32x2*)(stg + boff + 1024 * (s + 1)));
+          w0 = (uint32_t)wv[0];
+          w1 = (uint32_t)wv[1];
+          const af3_u32x4 s0 = *(const af3_u32x4*)(stg + soff + 32 * (s + 1));
+          const af3_u32x4 s1 = *(const af3_u32x4*)(stg + soff + 32 * (s + 1) + 16);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            sc[q] = s0[q];
+            sc[4 + q] = s1[q];
+          }
+          if (s < 0) {
+            const uint2 cv = *(const uint2*)(stg + coff);
+            chk0 = cv.x;
+            chk1 = cv.y;
+          }
+#pragma unroll
+          for (int tm = 0; tm < 8; ++tm)
+            if (FULL || tm < tm_live) af[nx][tm] = *(const af3_bf16x8*)(stg + aoff[tm & 1][s + 1] + 4096 * tm);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // 16 MFMAs of sub-step s; the copies of k-step kt + 2 (12 per wave
+        // per k-step, 3 per iteration) go after MFMAs 1, 6, 11; the B
+        // conversion of sub-step s + 1 after MFMAs 7..15
+        uint32_t dw[8];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int tm = i >> 1, tn = i & 1;
+          if (!(s < 0 && first) && (FULL || (wave_live && tm < tm_live)))
+            acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[c][tm], bf[c][tn], acc[tm][tn], 0, 0, 0);
+          if (pf && (i == 1 || i == 6 || i == 11)) issue_one(nxt_copy, (s + 1) * 3 + (i == 1 ? 0 : i == 6 ? 1 : 2));
+          if ((FULL || wave_live) && i >= 7 && i < 15) {
+            const int q = i - 7;
+            const uint32_t src = q < 4 ? w0 : w1;
+            const float scf = __uint_as_float(sc[q] << 23);
+            switch (q & 3) {
+              case 0: dw[q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, scf, 0)); break;
+              case 1: dw[q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, scf, 1)); break;
+              case 2: dw[q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, scf, 2)); break;
+              default: dw[q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, scf, 3)); break;
+            }
+          }
+          if ((FULL || wave_live) && i == 15) {
+            af3_u32x4 e4, o4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              e4[j] = perm_lo(dw[2 * j], dw[2 * j + 1]);
+              o4[j] = perm_hi(dw[2 * j], dw[2 * j + 1]);
+            }
+            // materialise the fast conversion here, ahead of the rare exact
+            // rebuild below (otherwise it is sunk past that branch)
+            asm volatile("" : "+v"(e4), "+v"(o4));
+            bf[nx][0] = __builtin_bit_cast(af3_bf16x8, e4);
+            bf[nx][1] = __builtin_bit_cast(af3_bf16x8, o4);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (FULL || wave_live) {
+          if (s < 0) {  // does this wave's part of k-step kt hold a scale byte outside [2, 252]?
+            const bool lane_odd = (chk0 - 2u > 250u) || (chk1 - 2u > 250u);
+            odd = __builtin_amdgcn_ballot_w64(lane_odd) != 0;
+          }
+          if (odd) d5_cvt_exact(w0, w1, sc, bf[nx][0], bf[nx][1]);
+        }
+      }
+    };
+    const af3_bf16x8 zf = __builtin_bit_cast(af3_bf16x8, zero4());
+#pragma unroll
+    for (int tm = 0; tm < 8; ++tm) af[1][tm] = zf;
+    bf[1][0] = bf[1][1] = zf;
+    if (nk > 1)
+      AF3_ASM_WAIT_VM(12);
+    else
+      AF3_ASM_WAIT_VM(0);
+    AF3_ASM_LDS_BARRIER();
+    kstep(0, true, nk > 2);
+#pragma nounroll
+    for (int kt = 1; kt < nk; ++kt) {
+      if (kt + 1 < nk)
+        AF3_ASM_WAIT_VM(12);
+      else
+        AF3_ASM_WAIT_VM(0);
+      AF3_ASM_LDS_BARRIER();
+      kstep(kt, false, kt + 2 < nk);
+    }
+    // the last k-step's sub-step 3
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int tm = i >> 1, tn = i & 1;
+      if (FULL || (wave_live && tm < tm_live))
+        acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[1][tm], bf[1][tn], acc[tm][tn], 0, 0, 0);
+    }
+  };
+  if (full)
+    kloop(std::true_type{});
+  else
+    kloop(std::false_type{});
+
+  if constexpr (BXK != NONE) {
+    if (p.kx > 0) {  // expert-LoRA segment: + L[r] . Bx[e][:, n] (Bx [r][N], n contiguous)
+      uint16_t* const As = (uint16_t*)lds;
+      Loader<kG4Rows, ROWS_BF16, 256> la;
+      Loader<kG4Rows, COLS_BF16, 256> lb;
+      la.init(p.ax, 0, row_lo, nrows, p.kx);
+      lb.init(p.bx, e, n0, ncols, 0, p.kx);
+      for (int k0 = 0; k0 < p.kx; k0 += kBK) {
+        la.load(k0);
+        lb.load(k0);
+        __syncthreads();
+        la.store(As);
+        lb.store(As + kG4AStage);
+        __syncthreads();
+#pragma unroll
+        for (int ks = 0; ks < kBK / 16; ++ks) {
+          af3_bf16x8 af[8], bf[2];
+#pragma unroll
+          for (int tm = 0; tm < 8; ++tm) af[tm] = *(const af3_bf16x8*)(As + lds_off(tm * 32 + lr, ks * 2 + lh));
+#pragma unroll
+          for (int tn = 0; tn < 2; ++tn)
+            bf[tn] = *(const af3_bf16x8*)(As + kG4AStage + lds_off(wn0 + 2 * lr + tn, ks * 2 + lh));
+#pragma unroll
+          for (int tm = 0; tm < 8; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn)
+              acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[tm], bf[tn], acc[tm][tn], 0, 0, 0);
+        }
+      }
+    }
+  }
+  g4_epilogue<true, 8, 2>(p, lds, acc, e, row_lo, nrows, n0, ncols, 0, wn0);
+}
+
+// ---------------------------------------------------------------------------
 // row-tile kernel: main GEMMs and the skinny LoRA row products
 // ---------------------------------------------------------------------------
 template <int BM, int BN, int WM, int WN, int AK, int BK_, int AXK, int BXK>
@@ -1829,14 +2162,20 @@ static void launch_gemm3(bool trans, int max_tiles, int N, hipStream_t stream, P
 
 static void launch_gemm4_dgrad(int max_tiles, int N, hipStream_t stream, Params p) {
   p.n_nblk = (N + kG4Rows - 1) / kG4Rows;
-  dim3 grid(max_tiles * p.n_nblk);
+  dim3 grid(g4_grid(max_tiles, p.n_nblk, p.group_m));
   hipLaunchKernelGGL((gemm4_dgrad_kernel<COLS_BF16>), grid, dim3(256), 0, stream, p);
+}
+
+static void launch_gemm5_dgrad(int max_tiles, int N, hipStream_t stream, Params p) {
+  p.n_nblk = (N + kG4Rows - 1) / kG4Rows;
+  dim3 grid(g4_grid(max_tiles, p.n_nblk, p.group_m));
+  hipLaunchKernelGGL((gemm5_dgrad_kernel<COLS_BF16>), grid, dim3(256), 0, stream, p);
 }
 
 template <int WM, int WN>
 static void launch_gemm4_fwd(int max_tiles, int N, hipStream_t stream, Params p) {
   p.n_nblk = (N + kG4Rows - 1) / kG4Rows;
-  dim3 grid(max_tiles * p.n_nblk);
+  dim3 grid(g4_grid(max_tiles, p.n_nblk, p.group_m));
   hipLaunchKernelGGL((gemm4_fwd_kernel<WM, WN, ROWS_BF16>), grid, dim3(WM * WN * 64), 0, stream, p);
 }
 
@@ -1926,20 +2265,23 @@ extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gathe
   //       wave's conversions / LDS reads overlap the other's MFMAs); default
   //       for trans_w 0 when the alignment / size requirements hold
   //   21: gemm4 dgrad (weights packed along n, transposed in LDS; 4 waves of
-  //       256x64); default for trans_w 1 when the requirements hold
+  //       256x64)
+  //   23: gemm5 dgrad (packed weight rows read with transposing LDS loads, one
+  //       three-stage ring for A, B and scales; 4 waves of 256x64); default
+  //       for trans_w 1 when the requirements hold
   //   tile_cfg / 100 = m-tiles per group of the 20/21/22 work order (default 4)
   int cfg = tile_cfg % 100;
   const int group_m = tile_cfg / 100 > 0 ? tile_cfg / 100 : 4;
   if (cfg == 0) {
     const bool g4_fwd = !trans && block_m == 256 && K % kBK == 0 && K / 32 <= kG4MaxG && al16(w_scales) && al16(y) &&
                         ldy % 8 == 0;
-    const bool g4_dgrad = trans && block_m == 256 && K % kBK == 0 && N % 64 == 0 && al16(y) && ldy % 8 == 0 &&
-                          ((uintptr_t)w_scales & 1) == 0;
-    cfg = g4_fwd ? 22 : g4_dgrad ? 21 : (block_m == 256 ? 4 : 2);
+    const bool g4_dgrad = trans && block_m == 256 && K % kBK == 0 && N % 64 == 0 && al16(y) && ldy % 8 == 0;
+    cfg = g4_fwd ? 22 : g4_dgrad ? 23 : (block_m == 256 ? 4 : 2);
   }
   const bool bm_ok =
-      (cfg == 3 || cfg == 4 || cfg == 6 || cfg == 7 || cfg == 12 || cfg == 20 || cfg == 21 || cfg == 22) ? block_m == 256
-                                                                                                       : block_m == 128;
+      (cfg == 3 || cfg == 4 || cfg == 6 || cfg == 7 || cfg == 12 || cfg == 20 || cfg == 21 || cfg == 22 || cfg == 23)
+          ? block_m == 256
+          : block_m == 128;
   AF3_REQUIRE(bm_ok, "moe_gemm: tile_cfg %d does not match block_m %d", cfg, block_m);
   if (K % kBK != 0) cfg = 9;  // direct A loads need whole 64-deep k-steps
   if (cfg == 9 && block_m != 128) {
@@ -1970,10 +2312,17 @@ extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gathe
         launch_gemm4_fwd<2, 4>(max_tiles, N, stream, p);
       break;
     case 21:
+    case 23:
       p.group_m = group_m;
-      AF3_REQUIRE(trans && block_m == 256 && K % kBK == 0 && N % 64 == 0 && al16(y) && ldy % 8 == 0,
-                  "moe_gemm: tile_cfg 21 needs trans_w 1, block_m 256, K %% 64 == 0, N %% 64 == 0, 16-byte aligned y");
-      launch_gemm4_dgrad(max_tiles, N, stream, p);
+      AF3_REQUIRE(trans && block_m == 256 && K % kBK == 0 && N % 64 == 0 && al16(y) && ldy % 8 == 0 &&
+                      (cfg != 21 || ((uintptr_t)w_scales & 1) == 0),
+                  "moe_gemm: tile_cfg %d needs trans_w 1, block_m 256, K %% 64 == 0, N %% 64 == 0, 16-byte aligned y"
+                  " (and 2-byte aligned scales for 21)",
+                  cfg);
+      if (cfg == 21)
+        launch_gemm4_dgrad(max_tiles, N, stream, p);
+      else
+        launch_gemm5_dgrad(max_tiles, N, stream, p);
       break;
     case 9: {
       dim3 grid(max_tiles, (N + 127) / 128);

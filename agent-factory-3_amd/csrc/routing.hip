@@ -248,6 +248,74 @@ __global__ void tile_map_kernel(const int32_t* __restrict__ offs_pad, int E, int
   map[(int64_t)b * max_tiles + i] = val;
 }
 
+// ---- grouped-GEMM tile order: full tiles first (expert order), then the
+// experts' partial last tiles by decreasing row count (ties: lower expert first)
+constexpr int kSchedMaxE = 4096;
+constexpr int kSchedMaxBM = 512;
+
+__global__ __launch_bounds__(1024) void tile_order_kernel(const int32_t* __restrict__ hist, int E, int bm,
+                                                          int max_tiles, int32_t* __restrict__ order) {
+  __shared__ int32_t nfull[kSchedMaxE];
+  __shared__ int32_t tail[kSchedMaxE];
+  __shared__ int32_t start[kSchedMaxBM + 1];  // tails of size s start at start[s]
+  __shared__ int32_t part[1024];
+  const int t = threadIdx.x;
+  for (int e = t; e < E; e += 1024) {
+    const int h = hist[e];
+    nfull[e] = h / bm;
+    tail[e] = h % bm;
+  }
+  for (int s = t; s <= kSchedMaxBM; s += 1024) start[s] = 0;
+  __syncthreads();
+  for (int e = t; e < E; e += 1024)
+    if (tail[e]) atomicAdd(&start[tail[e]], 1);
+  // exclusive prefix of full-tile counts over experts: thread t owns experts
+  // [t * per, (t + 1) * per)
+  const int per = (E + 1023) / 1024;
+  int32_t run = 0;
+  for (int i = 0; i < per; ++i) {
+    const int e = t * per + i;
+    if (e < E) run += nfull[e];
+  }
+  part[t] = run;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int32_t v = t >= off ? part[t - off] : 0;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
+  }
+  const int32_t total_full = part[1023];
+  if (t == 0) {  // descending exclusive scan of the tail-size histogram
+    int32_t acc = 0;
+    for (int s = bm - 1; s >= 1; --s) {
+      const int32_t c = start[s];
+      start[s] = acc;
+      acc += c;
+    }
+  }
+  __syncthreads();
+  int32_t pos = part[t] - run;
+  for (int i = 0; i < per; ++i) {
+    const int e = t * per + i;
+    if (e >= E) break;
+    for (int b = 0; b < nfull[e]; ++b) order[pos + b] = (b << 16) | e;
+    pos += nfull[e];
+    const int s = tail[e];
+    if (s) {
+      int rank = start[s];
+      for (int f = 0; f < e; ++f) rank += tail[f] == s;
+      order[total_full + rank] = (nfull[e] << 16) | e;
+    }
+  }
+}
+
+__global__ void tile_order_pad_kernel(const int32_t* __restrict__ offs_pad, int E, int max_tiles,
+                                      int32_t* __restrict__ order) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < max_tiles && i >= offs_pad[E]) order[i] = -1;
+}
+
 }  // namespace
 
 extern "C" size_t af3_routing_workspace_bytes(int64_t n_tokens, int n_expts_tot, int n_expts_act) {
@@ -347,4 +415,24 @@ extern "C" int af3_expt_data(const int32_t* hist, int n_expts_tot, const int32_t
   hipLaunchKernelGGL(tile_map_kernel, dim3((unsigned)af3_cdiv(max_tiles, 256), n_block_ms), dim3(256), 0, stream,
                      token_offs_pad, n_expts_tot, max_tiles, block_pid_map);
   return af3::check_launch("expt_data/map");
+}
+
+// Order of the BM-row tiles for the grouped GEMM's work list (same entries as
+// the block_pid_map of af3_expt_data for this BM, permuted): full tiles in
+// expert order, then each expert's partial last tile by decreasing rows.
+extern "C" int af3_tile_order(const int32_t* hist, int n_expts_tot, int block_m, const int32_t* token_offs_pad,
+                              int max_tiles, int32_t* order, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  AF3_REQUIRE(n_expts_tot > 0 && n_expts_tot <= kSchedMaxE, "tile_order: E=%d outside [1, %d]", n_expts_tot,
+              kSchedMaxE);
+  AF3_REQUIRE(block_m > 0 && block_m <= kSchedMaxBM && max_tiles >= 0, "tile_order: bad block_m %d / max_tiles %d",
+              block_m, max_tiles);
+  AF3_REQUIRE(max_tiles == 0 || (hist && token_offs_pad && order), "tile_order: null pointer");
+  if (max_tiles == 0) return 0;
+  hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(1024), 0, stream, hist, n_expts_tot, block_m, max_tiles, order);
+  int rc = af3::check_launch("tile_order");
+  if (rc) return rc;
+  hipLaunchKernelGGL(tile_order_pad_kernel, dim3((unsigned)af3_cdiv(max_tiles, 256)), dim3(256), 0, stream,
+                     token_offs_pad, n_expts_tot, max_tiles, order);
+  return af3::check_launch("tile_order/pad");
 }

@@ -86,6 +86,16 @@ int af3_routing_topk(const uint16_t* logits, int64_t ld_logits, int64_t n_tokens
 int af3_expt_data(const int32_t* hist, int n_expts_tot, const int32_t* block_ms_dev, int n_block_ms, int max_tiles,
                   int32_t* token_offs_pad, int32_t* block_pid_map, void* stream);
 
+/* Work order of the block_m-row tiles for af3_moe_gemm: the entries of the
+ * af3_expt_data block_pid_map for this block_m (token_offs_pad = its padded
+ * tile offsets), permuted so that full tiles come first in expert order and
+ * each expert's partial last tile follows by decreasing row count, -1 past
+ * the tile count.  No counterpart in the reference (its block_pid_map,
+ * compute_expt_data_torch, is in expert order and that order is kept there);
+ * the grouped GEMM takes either map.  n_expts_tot <= 4096, block_m <= 512. */
+int af3_tile_order(const int32_t* hist, int n_expts_tot, int block_m, const int32_t* token_offs_pad, int max_tiles,
+                   int32_t* order, void* stream);
+
 /* Grouped GEMM through frozen MXFP4 expert weights, dequant fused into the
  * tile load.  Replaces mxfp4_to_bf16 + matmul_ogs at quantization.py:358-362
  * (trans_w = 0; forward, A6/A8) and quantization.py:409-418 (trans_w = 1;

@@ -65,3 +65,30 @@ def test_out_of_range_ids_are_dropped(dev):
     gx = gi.dst_indx.cpu().tolist()
     assert gx[3] == -1 and gx[4] == -1
     assert gi.src_indx.cpu().tolist()[4:] == [-1, -1]
+
+
+@pytest.mark.parametrize("T,E,bm", [(5000, 128, 256), (300, 6, 256), (64, 8, 128), (16384, 128, 256)])
+def test_tile_order_is_sorted_permutation_of_map(dev, T, E, bm):
+    """af3_tile_order: the block_pid_map entries for bm, full tiles first in
+    expert order, then partial last tiles by decreasing rows (ties: lower
+    expert), -1 padding; the grouped GEMM accepts either list."""
+    from agent_factory_3_amd import _capi, workloads
+    g = torch.Generator().manual_seed(T + E)
+    ids = workloads.zipf_routing(g, T, E, 4, n_idle=8) if E >= 64 else \
+        torch.stack([torch.randperm(E, generator=g)[:4] for _ in range(T)]).sort(dim=1).values.to(torch.int32)
+    hist = torch.bincount(ids.reshape(-1).long(), minlength=E).to(torch.int32)
+    ed = R.compute_expt_data(hist.to(dev), E, T * 4)
+    n = R.max_tiles(T * 4, E, bm)
+    order = torch.empty(n, dtype=torch.int32, device=dev)
+    _capi.call("af3_tile_order", ed.hist.data_ptr(), E, bm, ed.token_offs_pad[bm].data_ptr(), n, order.data_ptr(),
+               _capi.stream_of(dev))
+    got = order.cpu().tolist()
+    full = [(b << 16) | e for e in range(E) for b in range(int(hist[e]) // bm)]
+    tails = sorted([e for e in range(E) if int(hist[e]) % bm], key=lambda e: (-(int(hist[e]) % bm), e))
+    want = full + [((int(hist[e]) // bm) << 16) | e for e in tails]
+    want += [-1] * (n - len(want))
+    assert got == want
+    pm = ed.block_pid_map[bm].cpu().tolist()
+    assert sorted(v for v in got if v >= 0) == sorted(v for v in pm if v >= 0)
+    if bm == 256:
+        assert ed.gemm_order[256].cpu().tolist() == got
