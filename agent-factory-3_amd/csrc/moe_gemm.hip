@@ -1703,66 +1703,135 @@ __device__ __forceinline__ void d5_cvt_exact(uint32_t w0, uint32_t w1, const uin
   od = __builtin_bit_cast(af3_bf16x8, o4);
 }
 
-template <int BXK>
-__global__ __launch_bounds__(256) void gemm5_dgrad_kernel(Params p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kD5LdsBytes];
+// Epilogue of gemm5: the RM x CN tile of 4 waves (wave w owns columns
+// CN / 4 * w .. + CN / 4, all RM rows; its MFMA sub-tile pairs hold the even /
+// odd columns of 64 consecutive columns): v = (acc + bias[n]) * gamma[row] -> bf16, staged
+// through LDS as [RM][CN] bf16 rows (16-byte chunks XOR-swizzled by row bit 2
+// so the two row groups of an MFMA output store hit disjoint banks), then one
+// 16-byte global store per chunk.
+template <int RM, int CN>
+__device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f32x16 (&acc)[RM / 32][CN / 128],
+                                            int e, int row_lo, int nrows, int n0, int ncols, int wn0) {
+  constexpr int TM = RM / 32, TN = CN / 128, RB = CN * 2;
+  const int lane = threadIdx.x & 63;
+  const int lr = lane & 31, lh = lane >> 5;
+  float* const gl = (float*)(lds + RM * RB);
+  auto coff = [&](int row, int col) { return row * RB + ((((col >> 3) ^ (((row >> 2) & 1) << 2))) << 4) + ((col & 7) << 1); };
+  __syncthreads();
+  for (int t = threadIdx.x; t < RM; t += 256) {
+    float gv = 1.f;
+    if (p.gammas && t < nrows) {
+      const int64_t gr = row_lo + t;
+      gv = p.gammas_f32 ? ((const float*)p.gammas)[gr] : af3_bf16_to_f32(((const uint16_t*)p.gammas)[gr]);
+    }
+    gl[t] = gv;
+  }
+  float bv[TN];
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) {
+    const int col = wn0 + 64 * (tn >> 1) + 2 * lr + (tn & 1);
+    bv[tn] = (p.bias && col < ncols) ? p.bias[e * p.bias_estride + n0 + col] : 0.f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row0 = tm * 32 + j * 8 + lh * 4;
+      const float4 g = *(const float4*)(gl + row0);
+      const float gq[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const int col = wn0 + 64 * (tn >> 1) + 2 * lr + (tn & 1);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *(uint16_t*)(lds + coff(row0 + q, col)) =
+              (uint16_t)af3_f32_to_bf16((acc[tm][tn][j * 4 + q] + bv[tn]) * gq[q]);
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int CH = CN / 8;  // 16-byte chunks per row
+#pragma unroll 4
+  for (int i = 0; i < RM * CH / 256; ++i) {
+    const int id = i * 256 + threadIdx.x;
+    const int row = id / CH, ch = id % CH;
+    if (row < nrows && ch * 8 < ncols) {
+      const af3_u32x4 v = *(const af3_u32x4*)(lds + row * RB + ((ch ^ (((row >> 2) & 1) << 2)) << 4));
+      *(af3_u32x4*)(p.c + (int64_t)(row_lo + row) * p.ldc + n0 + ch * 8) = v;
+    }
+  }
+}
 
-  int mt, nt;
-  if (!g4_work_item(p, mt, nt)) return;
-  const int32_t ent = p.tile_map[mt];
-  if (ent < 0) return;
-  const int e = ent & 0xFFFF, blk = ent >> 16;
-  const int row_lo = p.offs[e] + blk * kG4Rows;
-  const int nrows = min(kG4Rows, p.offs[e + 1] - row_lo);
-  if (nrows <= 0) return;
-  const int n0 = nt * kG4Rows;
-  const int ncols = min(kG4Rows, p.N - n0);  // multiple of 64
+// One work item of gemm5 dgrad.  NARROW = false: 256 rows x 256 columns, wave
+// w owns all rows and columns 64 w .. 64 w + 63 (8 x 2 MFMA sub-tiles).
+// NARROW = true (m-tiles of <= 128 rows): 128 rows x 512 columns (two n-tiles),
+// wave w owns columns 128 w .. 128 w + 127 (4 x 4 sub-tiles, two pair groups),
+// so a short expert tile still gives every wave 16 MFMAs per sub-step.  Both
+// copy 12 instructions per wave per k-step (A / B / S = 8 / 2 / 2 or 4 / 4 / 4).
+template <bool NARROW, int BXK>
+__device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, int row_lo, int nrows, int n0, int ncols) {
+  constexpr int RM = NARROW ? 128 : 256;  // tile rows
+  constexpr int CN = NARROW ? 512 : 256;  // tile columns
+  constexpr int TM = RM / 32;
+  constexpr int PG = CN / 256;            // pair groups (64 columns each) per wave
+  constexpr int TN = 2 * PG;
+  constexpr int WC = CN / 4;              // columns per wave
+  constexpr int BRB = CN / 2;             // packed bytes per weight row
+  constexpr int NCH = BRB / 16;           // 16-byte chunks per weight row
+  constexpr int NBLK = CN / 32;           // scale blocks
+  constexpr int AI = RM / 32, BI = BRB / 64, SI = NBLK / 4;  // copies per wave per k-step
+  static_assert(AI + BI + SI == 12, "12 copies per wave per k-step");
+  constexpr int AOFF = 0, BOFF = NARROW ? 16384 : 32768, SOFF = NARROW ? 32768 : 40960;
+  static_assert(SOFF + NBLK * 256 <= kD5Stage, "stage layout");
+  // slot of chunk c in weight row k (keeps the transposing reads conflict-free)
+  auto bswz = [](int k) { return NARROW ? ((k & 7) << 1) : (k & 7); };
+
   const int nk = p.K / kBK;
-
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lr = lane & 31, lh = lane >> 5;
-  const int wn0 = wave * 64;
-  const int tm_live = min(8, (nrows + 31) >> 5);
-  const bool wave_live = wn0 < ncols;
-  const bool full = tm_live == 8 && wave_live;
+  const int wn0 = wave * WC;
+  const int tm_live = min(TM, (nrows + 31) >> 5);
+  const int pg_live = min(PG, max(0, (ncols - wn0) >> 6));  // ncols is a multiple of 64
+  const bool wave_live = pg_live > 0;
 
-  // ---- global -> LDS copy sources (12 instructions per wave per k-step) ----
-  const uint16_t* arow[8];  // A: rows (8 w + i) * 8 + lane / 8, chunk lane % 8 (swizzled)
+  // ---- global -> LDS copy sources ----
+  const uint16_t* arow[AI];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = (wave * 8 + i) * 8 + (lane >> 3);
+  for (int i = 0; i < AI; ++i) {
+    const int row = (wave * AI + i) * 8 + (lane >> 3);
     int64_t src = row_lo + (row < nrows ? row : 0);
     if (p.a.gather) src = p.a.gather[src] / p.a.gdiv;
     arow[i] = (const uint16_t*)p.a.ptr + src * p.a.ld + (((lane & 7) ^ swz(row)) << 3);
   }
-  const uint8_t* bsrc[2];  // B: rows 8 q .. 8 q + 7 (q = 2 w + j), LDS slot lane % 8 holds chunk slot ^ (k & 7)
+  const uint8_t* bsrc[BI];  // 1 KB of weight rows per copy: 1024 / BRB rows, LDS slot lane % NCH
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int kr = (wave * 2 + j) * 8 + (lane >> 3);
-    int c = (lane & 7) ^ (kr & 7);
+  for (int j = 0; j < BI; ++j) {
+    const int kr = (wave * BI + j) * (1024 / BRB) + lane / NCH;
+    int c = (lane % NCH) ^ bswz(kr);
     if (c * 32 >= ncols) c = 0;  // columns past the tile: any valid bytes (never read)
     bsrc[j] = (const uint8_t*)p.b.ptr + e * p.b.estride + (int64_t)kr * p.b.ld + (n0 >> 1) + c * 16;
   }
-  const uint8_t* ssrc[2];  // S: block q = 2 w + j, k row = lane
+  const uint8_t* ssrc[SI];  // block q = SI w + j, k row = lane
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    int q = wave * 2 + j;
+  for (int j = 0; j < SI; ++j) {
+    int q = wave * SI + j;
     if (q * 32 >= ncols) q = 0;
     ssrc[j] = p.b.scales + e * p.b.sestride + (int64_t)lane * p.b.sld + (n0 >> 5) + q;
   }
   const int64_t bstep = (int64_t)kBK * p.b.ld, sstep = (int64_t)kBK * p.b.sld;
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
-  // copy j (0..11) of k-step kc: 0..7 A, 8..9 B, 10..11 S
+  // copy j (0..11) of k-step kc: A, then B, then S
   auto issue_one = [&](int kc, int j) {
     const uint32_t st = lds0 + (uint32_t)((kc % kD5Stages) * kD5Stage);
-    if (j < 8) {
-      g4_dma16(arow[j] + kc * kBK, st + (uint32_t)(kD5AOff + (wave * 8 + j) * 1024));
-    } else if (j < 10) {
-      g4_dma16(bsrc[j - 8] + kc * bstep, st + (uint32_t)(kD5BOff + (wave * 2 + j - 8) * 1024));
+    if (j < AI) {
+      g4_dma16(arow[j] + kc * kBK, st + (uint32_t)(AOFF + (wave * AI + j) * 1024));
+    } else if (j < AI + BI) {
+      g4_dma16(bsrc[j - AI] + kc * bstep, st + (uint32_t)(BOFF + (wave * BI + j - AI) * 1024));
     } else {
-      asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_ubyte %0, off" ::"v"(ssrc[j - 10] + kc * sstep),
-                   "s"(st + (uint32_t)(kD5SOff + (wave * 2 + j - 10) * 256))
+      asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_ubyte %0, off" ::"v"(ssrc[j - AI - BI] + kc * sstep),
+                   "s"(st + (uint32_t)(SOFF + (wave * SI + j - AI - BI) * 256))
                    : "memory", "m0");
     }
   };
@@ -1777,19 +1846,26 @@ __global__ __launch_bounds__(256) void gemm5_dgrad_kernel(Params p) {
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) aoff[t][s] = kD5AOff + lr * 128 + ((((lh * 4 + s) ^ ax) ^ (t << 2)) << 4);
-  // B transposed read: group g = lane / 16 (k half g / 2, column-pair half g % 2), i = lane % 16
+    for (int s = 0; s < 4; ++s) aoff[t][s] = AOFF + lr * 128 + ((((lh * 4 + s) ^ ax) ^ (t << 2)) << 4);
+  // B transposed read of pair group pg: lane group g = lane / 16 (k half g / 2,
+  // chunk (2 pg + g % 2) of the wave's columns), i = lane % 16
   const int gi = lane & 15, gg = lane >> 4;
-  const int boff = kD5BOff + (32 * (gg >> 1) + (gi >> 1)) * 128 + (((2 * wave + (gg & 1)) ^ (gi >> 1)) << 4) +
-                   (gi & 1) * 8;  // + 1024 s
-  const int soff = kD5SOff + ((2 * wave + (gg & 1)) * 64 + 32 * (gg >> 1)) * 4;  // + 32 s
-  const int coff = kD5SOff + (2 * wave * 64 + 2 * lane) * 4;  // the wave's 128 scale dwords, 2 per lane
+  int boff[PG], soff[PG];
+#pragma unroll
+  for (int pg = 0; pg < PG; ++pg) {
+    const int chunk = wn0 / 32 + 2 * pg + (gg & 1);
+    const int kr = 32 * (gg >> 1) + (gi >> 1);
+    boff[pg] = BOFF + kr * BRB + ((chunk ^ bswz(kr)) << 4) + (gi & 1) * 8;  // + 8 BRB s
+    soff[pg] = SOFF + (chunk * 64 + 32 * (gg >> 1)) * 4;                   // + 32 s
+  }
+  constexpr int CW = WC / 32;  // scale dwords per lane for the wave's check (its blocks x 64 k / 64 lanes)
+  const int coff = SOFF + (wn0 / 32 * 64 + CW * lane) * 4;
 
-  af3_f32x16 acc[8][2];
+  af3_f32x16 acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
@@ -1798,7 +1874,7 @@ __global__ __launch_bounds__(256) void gemm5_dgrad_kernel(Params p) {
 
   auto kloop = [&](auto full_c) {
     constexpr bool FULL = decltype(full_c)::value;
-    af3_bf16x8 af[2][8], bf[2][2];
+    af3_bf16x8 af[2][TM], bf[2][TN];
     // one k-step: iterations s = -1 (the carried sub-step of the previous
     // k-step, skipped at kt = 0) and 0..2; iteration s runs the MFMAs of
     // sub-step s while reading and converting the fragments of s + 1
@@ -1810,81 +1886,114 @@ __global__ __launch_bounds__(256) void gemm5_dgrad_kernel(Params p) {
       for (int s = -1; s < 3; ++s) {
         const int c = s < 0 ? 1 : (s & 1);   // fragments of sub-step s
         const int nx = s < 0 ? 0 : (c ^ 1);  // fragments of sub-step s + 1
-        __builtin_amdgcn_sched_barrier(0);
-        uint32_t w0 = 0, w1 = 0;
-        uint32_t sc[8];
-        uint32_t chk0 = 2, chk1 = 2;
-        if (FULL || wave_live) {
-          const af3_i32x2 wv =
-              __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) af3_i32x2*)(stg + boff + 1024 * (s + 1)));
-          w0 = (uint32_t)wv[0];
-          w1 = (uint32_t)wv[1];
-          const af3_u32x4 s0 = *(const af3_u32x4*)(stg + soff + 32 * (s + 1));
-          const af3_u32x4 s1 = *(const af3_u32x4*)(stg + soff + 32 * (s + 1) + 16);
+        const int o = s + 1;                 // sub-step whose operands are read
+        uint32_t w[PG][2];
+        uint32_t sc[PG][8];
+        uint32_t chk[CW];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            sc[q] = s0[q];
-            sc[4 + q] = s1[q];
-          }
-          if (s < 0) {
-            const uint2 cv = *(const uint2*)(stg + coff);
-            chk0 = cv.x;
-            chk1 = cv.y;
-          }
-#pragma unroll
-          for (int tm = 0; tm < 8; ++tm)
-            if (FULL || tm < tm_live) af[nx][tm] = *(const af3_bf16x8*)(stg + aoff[tm & 1][s + 1] + 4096 * tm);
-        }
+        for (int q = 0; q < CW; ++q) chk[q] = 2;
+        uint32_t dw[PG][8];
+        // 16 MFMAs of sub-step s, one LDS read or a slice of the B conversion
+        // of sub-step s + 1 after each (a burst of reads would hold the wave at
+        // issue while its MFMA pipe idles).  Slots (read order B, scales,
+        // check, A; conversions once their operands have had time to land):
+        //   PG 1: 0 B, 1-2 S, 3 check, 4-11 A, 6-13 convert, 14-15 fragments
+        //   PG 2: 0-1 B, 2-5 S, 6 check, 7-10 A, 5-12 / 7-14 convert, 13 / 15
+        // the copies of k-step kt + 2 after slots 2, 7, 12
+        constexpr int SB = PG;             // first scale read slot
+        constexpr int SC = SB + 2 * PG;    // check slot
+        constexpr int SA = SC + 1;         // first A read slot
         __builtin_amdgcn_sched_barrier(0);
-        // 16 MFMAs of sub-step s; the copies of k-step kt + 2 (12 per wave
-        // per k-step, 3 per iteration) go after MFMAs 1, 6, 11; the B
-        // conversion of sub-step s + 1 after MFMAs 7..15
-        uint32_t dw[8];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int tm = i >> 1, tn = i & 1;
-          if (!(s < 0 && first) && (FULL || (wave_live && tm < tm_live)))
+          const int tm = i / TN, tn = i % TN;
+          if (!(s < 0 && first) && (FULL || (tm < tm_live && (tn >> 1) < pg_live)))
             acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[c][tm], bf[c][tn], acc[tm][tn], 0, 0, 0);
-          if (pf && (i == 1 || i == 6 || i == 11)) issue_one(nxt_copy, (s + 1) * 3 + (i == 1 ? 0 : i == 6 ? 1 : 2));
-          if ((FULL || wave_live) && i >= 7 && i < 15) {
-            const int q = i - 7;
-            const uint32_t src = q < 4 ? w0 : w1;
-            const float scf = __uint_as_float(sc[q] << 23);
-            switch (q & 3) {
-              case 0: dw[q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, scf, 0)); break;
-              case 1: dw[q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, scf, 1)); break;
-              case 2: dw[q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, scf, 2)); break;
-              default: dw[q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, scf, 3)); break;
-            }
-          }
-          if ((FULL || wave_live) && i == 15) {
-            af3_u32x4 e4, o4;
+          if (FULL || wave_live) {
+            if (i < SB) {
+              const int pg = i;
+              const af3_i32x2 wv = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                  (__attribute__((address_space(3))) af3_i32x2*)(stg + boff[pg] + 8 * BRB * o));
+              w[pg][0] = (uint32_t)wv[0];
+              w[pg][1] = (uint32_t)wv[1];
+            } else if (i < SC) {
+              const int pg = (i - SB) >> 1, h = (i - SB) & 1;
+              const af3_u32x4 sv = *(const af3_u32x4*)(stg + soff[pg] + 32 * o + 16 * h);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              e4[j] = perm_lo(dw[2 * j], dw[2 * j + 1]);
-              o4[j] = perm_hi(dw[2 * j], dw[2 * j + 1]);
+              for (int q = 0; q < 4; ++q) sc[pg][4 * h + q] = sv[q];
+            } else if (i == SC) {
+              if (s < 0) {
+                if constexpr (CW == 2) {
+                  const uint2 cv = *(const uint2*)(stg + coff);
+                  chk[0] = cv.x;
+                  chk[1] = cv.y;
+                } else {
+                  const af3_u32x4 cv = *(const af3_u32x4*)(stg + coff);
+#pragma unroll
+                  for (int q = 0; q < CW; ++q) chk[q] = cv[q];
+                }
+              }
+            } else if (i < SA + TM) {
+              const int t = i - SA;
+              if (FULL || t < tm_live) af[nx][t] = *(const af3_bf16x8*)(stg + aoff[t & 1][o] + 4096 * t);
             }
-            // materialise the fast conversion here, ahead of the rare exact
-            // rebuild below (otherwise it is sunk past that branch)
-            asm volatile("" : "+v"(e4), "+v"(o4));
-            bf[nx][0] = __builtin_bit_cast(af3_bf16x8, e4);
-            bf[nx][1] = __builtin_bit_cast(af3_bf16x8, o4);
+#pragma unroll
+            for (int pg = 0; pg < PG; ++pg) {
+              const int c0 = PG == 1 ? 6 : (pg ? 7 : 5);  // first conversion slot of this pair group
+              if (i >= c0 && i < c0 + 8 && (FULL || pg < pg_live)) {
+                const int q = i - c0;
+                const uint32_t src = w[pg][q >> 2];
+                const float scf = __uint_as_float(sc[pg][q] << 23);
+                switch (q & 3) {
+                  case 0: dw[pg][q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, scf, 0)); break;
+                  case 1: dw[pg][q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, scf, 1)); break;
+                  case 2: dw[pg][q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, scf, 2)); break;
+                  default: dw[pg][q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, scf, 3)); break;
+                }
+                asm volatile("" : "+v"(dw[pg][q]));  // keep the conversion in its slot
+              }
+              const int pe = PG == 1 ? 14 : (pg ? 15 : 13);  // even fragment slot (odd: next slot for PG 1)
+              if ((i == pe) && (FULL || pg < pg_live)) {
+                af3_u32x4 e4;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) e4[j] = perm_lo(dw[pg][2 * j], dw[pg][2 * j + 1]);
+                // materialise the fast conversion here, ahead of the rare exact
+                // rebuild below (otherwise it is sunk past that branch)
+                asm volatile("" : "+v"(e4));
+                bf[nx][2 * pg] = __builtin_bit_cast(af3_bf16x8, e4);
+              }
+              if ((i == (PG == 1 ? 15 : pe)) && (FULL || pg < pg_live)) {
+                af3_u32x4 o4;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) o4[j] = perm_hi(dw[pg][2 * j], dw[pg][2 * j + 1]);
+                asm volatile("" : "+v"(o4));
+                bf[nx][2 * pg + 1] = __builtin_bit_cast(af3_bf16x8, o4);
+              }
+            }
           }
+          if (pf && (i == 2 || i == 7 || i == 12)) issue_one(nxt_copy, o * 3 + (i == 2 ? 0 : i == 7 ? 1 : 2));
           __builtin_amdgcn_sched_barrier(0);
         }
         if (FULL || wave_live) {
           if (s < 0) {  // does this wave's part of k-step kt hold a scale byte outside [2, 252]?
-            const bool lane_odd = (chk0 - 2u > 250u) || (chk1 - 2u > 250u);
+            bool lane_odd = false;
+#pragma unroll
+            for (int q = 0; q < CW; ++q) lane_odd |= chk[q] - 2u > 250u;
             odd = __builtin_amdgcn_ballot_w64(lane_odd) != 0;
           }
-          if (odd) d5_cvt_exact(w0, w1, sc, bf[nx][0], bf[nx][1]);
+          if (odd) {
+#pragma unroll
+            for (int pg = 0; pg < PG; ++pg)
+              if (FULL || pg < pg_live) d5_cvt_exact(w[pg][0], w[pg][1], sc[pg], bf[nx][2 * pg], bf[nx][2 * pg + 1]);
+          }
         }
       }
     };
     const af3_bf16x8 zf = __builtin_bit_cast(af3_bf16x8, zero4());
 #pragma unroll
-    for (int tm = 0; tm < 8; ++tm) af[1][tm] = zf;
-    bf[1][0] = bf[1][1] = zf;
+    for (int tm = 0; tm < TM; ++tm) af[1][tm] = zf;
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) bf[1][tn] = zf;
     if (nk > 1)
       AF3_ASM_WAIT_VM(12);
     else
@@ -1903,21 +2012,23 @@ __global__ __launch_bounds__(256) void gemm5_dgrad_kernel(Params p) {
     // the last k-step's sub-step 3
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int tm = i >> 1, tn = i & 1;
-      if (FULL || (wave_live && tm < tm_live))
+      const int tm = i / TN, tn = i % TN;
+      if (FULL || (tm < tm_live && (tn >> 1) < pg_live))
         acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[1][tm], bf[1][tn], acc[tm][tn], 0, 0, 0);
     }
   };
-  if (full)
-    kloop(std::true_type{});
-  else
-    kloop(std::false_type{});
+  // every tile runs all of its MFMAs: rows and columns past the tile read
+  // valid addresses and are never stored (the k-step is not MFMA-bound, and a
+  // variant that skips dead sub-tiles needs more scalar registers than a wave
+  // has)
+  kloop(std::true_type{});
 
   if constexpr (BXK != NONE) {
     if (p.kx > 0) {  // expert-LoRA segment: + L[r] . Bx[e][:, n] (Bx [r][N], n contiguous)
       uint16_t* const As = (uint16_t*)lds;
-      Loader<kG4Rows, ROWS_BF16, 256> la;
-      Loader<kG4Rows, COLS_BF16, 256> lb;
+      uint16_t* const Bs = As + RM * kBK;
+      Loader<RM, ROWS_BF16, 256> la;
+      Loader<CN, COLS_BF16, 256> lb;
       la.init(p.ax, 0, row_lo, nrows, p.kx);
       lb.init(p.bx, e, n0, ncols, 0, p.kx);
       for (int k0 = 0; k0 < p.kx; k0 += kBK) {
@@ -1925,26 +2036,47 @@ __global__ __launch_bounds__(256) void gemm5_dgrad_kernel(Params p) {
         lb.load(k0);
         __syncthreads();
         la.store(As);
-        lb.store(As + kG4AStage);
+        lb.store(Bs);
         __syncthreads();
 #pragma unroll
         for (int ks = 0; ks < kBK / 16; ++ks) {
-          af3_bf16x8 af[8], bf[2];
+          af3_bf16x8 af[TM], bf[TN];
 #pragma unroll
-          for (int tm = 0; tm < 8; ++tm) af[tm] = *(const af3_bf16x8*)(As + lds_off(tm * 32 + lr, ks * 2 + lh));
+          for (int tm = 0; tm < TM; ++tm) af[tm] = *(const af3_bf16x8*)(As + lds_off(tm * 32 + lr, ks * 2 + lh));
 #pragma unroll
-          for (int tn = 0; tn < 2; ++tn)
-            bf[tn] = *(const af3_bf16x8*)(As + kG4AStage + lds_off(wn0 + 2 * lr + tn, ks * 2 + lh));
+          for (int tn = 0; tn < TN; ++tn)
+            bf[tn] = *(const af3_bf16x8*)(Bs + lds_off(wn0 + 64 * (tn >> 1) + 2 * lr + (tn & 1), ks * 2 + lh));
 #pragma unroll
-          for (int tm = 0; tm < 8; ++tm)
+          for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-            for (int tn = 0; tn < 2; ++tn)
+            for (int tn = 0; tn < TN; ++tn)
               acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[tm], bf[tn], acc[tm][tn], 0, 0, 0);
         }
       }
     }
   }
-  g4_epilogue<true, 8, 2>(p, lds, acc, e, row_lo, nrows, n0, ncols, 0, wn0);
+  d5_epilogue<RM, CN>(p, lds, acc, e, row_lo, nrows, n0, ncols, wn0);
+}
+
+template <int BXK>
+__global__ __launch_bounds__(256) void gemm5_dgrad_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kD5LdsBytes];
+  int mt, nt;
+  if (!g4_work_item(p, mt, nt)) return;
+  const int32_t ent = p.tile_map[mt];
+  if (ent < 0) return;
+  const int e = ent & 0xFFFF, blk = ent >> 16;
+  const int row_lo = p.offs[e] + blk * kG4Rows;
+  const int nrows = min(kG4Rows, p.offs[e + 1] - row_lo);
+  if (nrows <= 0) return;
+  const int n0 = nt * kG4Rows;
+  if (nrows <= 128) {
+    // short tile: even n-tiles take the next n-tile too, odd ones have no work
+    if (nt & 1) return;
+    d5_tile<true, BXK>(p, lds, e, row_lo, nrows, n0, min(2 * kG4Rows, p.N - n0));
+  } else {
+    d5_tile<false, BXK>(p, lds, e, row_lo, nrows, n0, min(kG4Rows, p.N - n0));
+  }
 }
 
 // ---------------------------------------------------------------------------
