@@ -36,6 +36,9 @@ _SIGNATURES = {
     "af3_tile_order": (_i32, [_p, _i32, _i32, _p, _i32, _p, _p]),
     "af3_moe_gemm": (_i32, [_p, _i64, _p, _i32, _p, _p, _i32, _p, _p, _i32, _p, _i64, _p, _i32,
                             _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p]),
+    "af3_moe_gemm_swiglu": (_i32, [_p, _i64, _p, _i32, _p, _p, _i32, _p, _p, _i32, _p, _i64, _p, _i32,
+                                   _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _p, _i64,
+                                   _f32, _f32, _p]),
     "af3_moe_combine": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _p, _i64, _p]),
     "af3_lora_rows": (_i32, [_p, _i64, _p, _i32, _p, _i32, _f32, _p, _p, _i32, _i32, _i32, _i32,
                              _p, _i64, _p]),
@@ -84,6 +87,24 @@ def call(name: str, *args) -> None:
         msg = lib.af3_last_error().decode(errors="replace")
         kind = "argument error" if rc < 0 else f"HIP error {rc}"
         raise RuntimeError(f"{name}: {kind}: {msg}")
+
+
+EUNSUPPORTED = -2
+
+
+def try_call(name: str, *args) -> bool:
+    """Call an entry point that may decline a configuration: False when it
+    returns AF3_EUNSUPPORTED (nothing was launched), True on success; raise
+    RuntimeError on any other error."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc == EUNSUPPORTED:
+        return False
+    if rc != 0:
+        msg = lib.af3_last_error().decode(errors="replace")
+        kind = "argument error" if rc < 0 else f"HIP error {rc}"
+        raise RuntimeError(f"{name}: {kind}: {msg}")
+    return True
 
 
 def workspace_bytes(n_tokens: int, n_expts_tot: int, n_expts_act: int) -> int:

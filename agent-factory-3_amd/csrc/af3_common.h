@@ -115,3 +115,32 @@ __device__ __forceinline__ void af3_dequant_u32_int(uint32_t v, uint32_t scale, 
 }
 
 __host__ __device__ __forceinline__ int64_t af3_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// gpt-oss clamped SwiGLU per element (kernels.py:431-441 forward, 533-545
+// backward): g = min(G, limit), u = clamp(U, -limit, limit),
+// s = 1 / (1 + 2^(-alpha g log2 e)); out = g s (u + 1);
+// dg = dO (u + 1) s (1 + alpha g (1 - s)) where g < limit, else 0;
+// du = dO g s where -limit < u < limit, else 0.  exp2 is v_exp_f32 and the
+// reciprocal v_rcp_f32.  Shared by the standalone SwiGLU kernels and the
+// grouped-GEMM epilogues that fuse it, so both round identically.
+__device__ __forceinline__ float af3_sigmoid_alpha(float g, float alpha) {
+  const float e = __builtin_amdgcn_exp2f(-alpha * g * 1.4426950408889634f);
+  return __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+__device__ __forceinline__ void af3_swiglu_fwd_elem(float graw, float uraw, float alpha, float limit, float& out,
+                                                    float& g, float& u) {
+  g = fminf(graw, limit);
+  u = fminf(fmaxf(uraw, -limit), limit);
+  const float s = af3_sigmoid_alpha(g, alpha);
+  out = g * s * (u + 1.0f);
+}
+
+__device__ __forceinline__ void af3_swiglu_bwd_elem(float dout, float g, float u, float alpha, float limit, float& dg,
+                                                    float& du) {
+  const float s = af3_sigmoid_alpha(g, alpha);
+  dg = dout * (u + 1.0f) * s * (1.0f + alpha * g * (1.0f - s));
+  dg = (g < limit) ? dg : 0.0f;
+  du = dout * g * s;
+  du = (u > -limit && u < limit) ? du : 0.0f;
+}

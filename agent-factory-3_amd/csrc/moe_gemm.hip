@@ -72,6 +72,15 @@ struct Params {
   float* partials;          // wgrad fp32 partials [chunk][M][N]
   int M, N;                 // output extents (M used by wgrad; rows come from offs in row tiles)
   int group_m;              // work-item grouping (m-tiles per group), gemm4
+  // fused SwiGLU epilogue (gemm4 forward / gemm5 dgrad): 0 none;
+  // 1 backward: c receives dGU [rows][2N] from the bf16 product dI and the
+  //   saved interleaved pre-activation glu [rows][2N];
+  // 2 forward: besides the bf16 product (the interleaved pre-activation), glu
+  //   receives its SwiGLU output [rows][N / 2]
+  int epi;
+  void* glu;
+  int64_t ld_glu;
+  float alpha, limit;
 };
 
 __device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
@@ -979,6 +988,19 @@ __device__ __forceinline__ void g4_epilogue(const Params& p, uint8_t* lds, af3_f
     if (row < nrows && ch * 8 < ncols) {
       const af3_u32x4 v = *(const af3_u32x4*)(lds + row * 512 + ((ch ^ (((row >> 2) & 1) << 2)) << 4));
       *(af3_u32x4*)(p.c + (int64_t)(row_lo + row) * p.ldc + n0 + ch * 8) = v;
+      if (p.epi == 2) {  // SwiGLU of the chunk's 4 (gate, up) pairs, from the bf16 values just stored
+        uint32_t o[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          float r0, r1, g, u;
+          af3_swiglu_fwd_elem(af3_bf16_to_f32(v[2 * h] & 0xFFFFu), af3_bf16_to_f32(v[2 * h] >> 16), p.alpha,
+                              p.limit, r0, g, u);
+          af3_swiglu_fwd_elem(af3_bf16_to_f32(v[2 * h + 1] & 0xFFFFu), af3_bf16_to_f32(v[2 * h + 1] >> 16),
+                              p.alpha, p.limit, r1, g, u);
+          o[h] = af3_pack_bf16x2(r0, r1);
+        }
+        *(uint2*)((uint16_t*)p.glu + (int64_t)(row_lo + row) * p.ld_glu + ((n0 + ch * 8) >> 1)) = uint2{o[0], o[1]};
+      }
     }
   }
 }
@@ -1758,7 +1780,28 @@ __device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f
     const int row = id / CH, ch = id % CH;
     if (row < nrows && ch * 8 < ncols) {
       const af3_u32x4 v = *(const af3_u32x4*)(lds + row * RB + ((ch ^ (((row >> 2) & 1) << 2)) << 4));
-      *(af3_u32x4*)(p.c + (int64_t)(row_lo + row) * p.ldc + n0 + ch * 8) = v;
+      const int64_t grow = row_lo + row;
+      if (p.epi == 1) {  // SwiGLU backward: dI (the bf16 values v) and the saved pre-activation -> dGU
+        const int64_t col2 = 2 * (int64_t)(n0 + ch * 8);
+        const uint16_t* gu = (const uint16_t*)p.glu + grow * p.ld_glu + col2;
+        const af3_u32x4 x0 = *(const af3_u32x4*)gu, x1 = *(const af3_u32x4*)(gu + 8);
+        const uint32_t xw[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        uint32_t o[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const float d = af3_bf16_to_f32(q & 1 ? v[q >> 1] >> 16 : v[q >> 1] & 0xFFFFu);
+          const float g = fminf(af3_bf16_to_f32(xw[q] & 0xFFFFu), p.limit);
+          const float u = fminf(fmaxf(af3_bf16_to_f32(xw[q] >> 16), -p.limit), p.limit);
+          float dg, du;
+          af3_swiglu_bwd_elem(d, g, u, p.alpha, p.limit, dg, du);
+          o[q] = af3_pack_bf16x2(dg, du);
+        }
+        af3_u32x4* dst = (af3_u32x4*)(p.c + grow * p.ldc + col2);
+        dst[0] = af3_u32x4{o[0], o[1], o[2], o[3]};
+        dst[1] = af3_u32x4{o[4], o[5], o[6], o[7]};
+      } else {
+        *(af3_u32x4*)(p.c + grow * p.ldc + n0 + ch * 8) = v;
+      }
     }
   }
 }
@@ -2330,12 +2373,13 @@ static void launch_gemm2(bool trans, int max_tiles, int N, hipStream_t stream, P
 // e owns rows [token_offs[e], token_offs[e+1]); block_pid_map is the map of
 // af3_expt_data for BM = block_m; grid.x = max_tiles.  tile_cfg selects the
 // block tile (0 = default for block_m; see the table below).
-extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
-                            const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
-                            const void* gammas, int gammas_f32, const uint16_t* lora_l, int64_t ld_l,
-                            const uint16_t* lora_b, int lora_r, const int32_t* token_offs, const int32_t* block_pid_map,
-                            const int32_t* tile_offs, int max_tiles, int block_m, int tile_cfg, int n_expts, int N,
-                            int K, uint16_t* y, int64_t ldy, void* stream_) {
+static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
+                         const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
+                         const void* gammas, int gammas_f32, const uint16_t* lora_l, int64_t ld_l,
+                         const uint16_t* lora_b, int lora_r, const int32_t* token_offs, const int32_t* block_pid_map,
+                         const int32_t* tile_offs, int max_tiles, int block_m, int tile_cfg, int n_expts, int N,
+                         int K, uint16_t* y, int64_t ldy, int epi, void* glu, int64_t ld_glu, float alpha,
+                         float limit, void* stream_) {
   hipStream_t stream = (hipStream_t)stream_;
   AF3_REQUIRE(N > 0 && K > 0 && n_expts > 0 && max_tiles >= 0, "moe_gemm: bad sizes N=%d K=%d E=%d", N, K, n_expts);
   if (max_tiles == 0) return 0;
@@ -2384,6 +2428,11 @@ extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gathe
   p.c = y;
   p.ldc = ldy;
   p.N = N;
+  p.epi = epi;
+  p.glu = glu;
+  p.ld_glu = ld_glu;
+  p.alpha = alpha;
+  p.limit = limit;
   const bool trans = trans_w != 0;
   // tile configurations: (BM, BN, waves)
   //   1: 128x128, 2x2    2: 128x256, 2x2    3: 256x128, 2x2
@@ -2416,6 +2465,17 @@ extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gathe
           : block_m == 128;
   AF3_REQUIRE(bm_ok, "moe_gemm: tile_cfg %d does not match block_m %d", cfg, block_m);
   if (K % kBK != 0) cfg = 9;  // direct A loads need whole 64-deep k-steps
+  if (epi != 0) {
+    AF3_REQUIRE(glu && (epi == 1 || epi == 2), "moe_gemm: bad SwiGLU epilogue %d", epi);
+    const bool ok = epi == 1 ? (trans && cfg == 23 && ld_glu % 8 == 0 && al16(glu) && ldy >= 2LL * N)
+                             : (!trans && (cfg == 20 || cfg == 22) && N % 2 == 0 && ld_glu % 4 == 0 &&
+                                ((uintptr_t)glu & 7) == 0);
+    if (!ok) {
+      af3::set_error("moe_gemm: the fused SwiGLU epilogue %d is not available for tile_cfg %d / these operands", epi,
+                     cfg);
+      return AF3_EUNSUPPORTED;
+    }
+  }
   if (cfg == 9 && block_m != 128) {
     af3::set_error("moe_gemm: K %% 64 != 0 needs block_m 128");
     return AF3_EINVAL;
@@ -2471,6 +2531,35 @@ extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gathe
       return AF3_EINVAL;
   }
   return af3::check_launch("moe_gemm");
+}
+
+extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
+                            const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
+                            const void* gammas, int gammas_f32, const uint16_t* lora_l, int64_t ld_l,
+                            const uint16_t* lora_b, int lora_r, const int32_t* token_offs, const int32_t* block_pid_map,
+                            const int32_t* tile_offs, int max_tiles, int block_m, int tile_cfg, int n_expts, int N,
+                            int K, uint16_t* y, int64_t ldy, void* stream) {
+  return moe_gemm_impl(x, ldx, gather_indx, gather_div, w_blocks, w_scales, trans_w, bias, gammas, gammas_f32, lora_l,
+                       ld_l, lora_b, lora_r, token_offs, block_pid_map, tile_offs, max_tiles, block_m, tile_cfg,
+                       n_expts, N, K, y, ldy, 0, nullptr, 0, 0.f, 0.f, stream);
+}
+
+// af3_moe_gemm with the gpt-oss clamped SwiGLU fused into the epilogue
+// (epi 1: trans_w 1, y <- dGU [rows][2N] from dI and the saved pre-activation
+// glu [rows][2N]; epi 2: trans_w 0, y <- the pre-activation [rows][N] and glu
+// <- its SwiGLU [rows][N / 2]).  AF3_EUNSUPPORTED when the selected tile
+// configuration has no fused epilogue.
+extern "C" int af3_moe_gemm_swiglu(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
+                                   const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
+                                   const void* gammas, int gammas_f32, const uint16_t* lora_l, int64_t ld_l,
+                                   const uint16_t* lora_b, int lora_r, const int32_t* token_offs,
+                                   const int32_t* block_pid_map, const int32_t* tile_offs, int max_tiles, int block_m,
+                                   int tile_cfg, int n_expts, int N, int K, uint16_t* y, int64_t ldy, int epi,
+                                   void* glu, int64_t ld_glu, float alpha, float limit, void* stream) {
+  AF3_REQUIRE(epi == 1 || epi == 2, "moe_gemm_swiglu: epi must be 1 or 2 (got %d)", epi);
+  return moe_gemm_impl(x, ldx, gather_indx, gather_div, w_blocks, w_scales, trans_w, bias, gammas, gammas_f32, lora_l,
+                       ld_l, lora_b, lora_r, token_offs, block_pid_map, tile_offs, max_tiles, block_m, tile_cfg,
+                       n_expts, N, K, y, ldy, epi, glu, ld_glu, alpha, limit, stream);
 }
 
 // Skinny per-expert row product for the LoRA terms (BM = 128 map):

@@ -25,28 +25,14 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr float kLog2e = 1.4426950408889634f;
-
-__device__ __forceinline__ float sigmoid_alpha(float g, float alpha) {
-  float e = __builtin_amdgcn_exp2f(-alpha * g * kLog2e);
-  return __builtin_amdgcn_rcpf(1.0f + e);
-}
-
 __device__ __forceinline__ void swiglu_fwd_elem(float graw, float uraw, float alpha, float limit, float& out,
                                                 float& g, float& u) {
-  g = fminf(graw, limit);
-  u = fminf(fmaxf(uraw, -limit), limit);
-  float s = sigmoid_alpha(g, alpha);
-  out = g * s * (u + 1.0f);
+  af3_swiglu_fwd_elem(graw, uraw, alpha, limit, out, g, u);
 }
 
 __device__ __forceinline__ void swiglu_bwd_elem(float dout, float g, float u, float alpha, float limit, float& dg,
                                                 float& du) {
-  float s = sigmoid_alpha(g, alpha);
-  dg = dout * (u + 1.0f) * s * (1.0f + alpha * g * (1.0f - s));
-  dg = (g < limit) ? dg : 0.0f;
-  du = dout * g * s;
-  du = (u > -limit && u < limit) ? du : 0.0f;
+  af3_swiglu_bwd_elem(dout, g, u, alpha, limit, dg, du);
 }
 
 // ---- forward ---------------------------------------------------------------

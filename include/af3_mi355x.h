@@ -116,6 +116,25 @@ int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int
                  int max_tiles, int block_m, int tile_cfg, int n_expts, int N, int K, uint16_t* y, int64_t ldy,
                  void* stream);
 
+/* af3_moe_gemm with the gpt-oss clamped SwiGLU (kernels.py:394-582 math)
+ * fused into the epilogue, so the activation never makes a separate pass
+ * through HBM.  Replaces the SwiGLUFunction.backward that follows the
+ * down-projection dX product (quantization.py:409-418, 442-444: epi 1,
+ * trans_w 1, y <- dGU [rows][2N] from the bf16 product dI and the saved
+ * interleaved pre-activation glu [rows][2N], ld_glu) and the
+ * SwiGLUFunction.forward that follows the gate_up product (quantization.py:
+ * 516-525, 432-439: epi 2, trans_w 0, y <- the bf16 pre-activation [rows][N]
+ * and glu <- its SwiGLU [rows][N/2]).  Results equal the unfused sequence bit
+ * for bit.  Returns AF3_EUNSUPPORTED (-2) when the selected tile configuration
+ * has no fused epilogue; the caller then runs the unfused pair. */
+int af3_moe_gemm_swiglu(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
+                        const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
+                        const void* gammas, int gammas_f32, const uint16_t* lora_l, int64_t ld_l,
+                        const uint16_t* lora_b, int lora_r, const int32_t* token_offs, const int32_t* block_pid_map,
+                        const int32_t* tile_offs, int max_tiles, int block_m, int tile_cfg, int n_expts, int N, int K,
+                        uint16_t* y, int64_t ldy, int epi, void* glu, int64_t ld_glu, float alpha, float limit,
+                        void* stream);
+
 /* Scatter-sum over each token's K expert rows (the k-reduction matmul_ogs
  * performs for scatter_indx, quantization.py:532-541 and 409-418):
  * out[t] = bf16(sum_j rows[src_indx[t*K+j]]) in fp32; -1 entries skipped. */

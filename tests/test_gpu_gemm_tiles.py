@@ -19,20 +19,31 @@ from oracle import routing as O
 
 pytestmark = pytest.mark.gpu
 RTOL, ATOL = 2e-2, 1e-2
-KRED, NOUT, T, E, TOPK = 640, 576, 700, 6, 4
+KRED, NOUT, T, E, TOPK = 640, 576, 700, 7, 4
+
+
+# rows per expert: two full 256-row tiles + a tail of 188 / 178 / 138 rows
+# (full-width tail tiles), 256 + 44 and 256 + 104 rows and 100 rows (tiles of
+# <= 128 rows, which the input-gradient kernel runs two n-tiles at a time), and
+# an idle expert
+COUNTS = [700, 300, 690, 650, 100, 360, 0]
 
 
 def _routing(dev, seed):
+    """Replay routing with exactly COUNTS rows per expert (distinct experts per token)."""
     g = torch.Generator().manual_seed(seed)
-    logits = torch.randn(T, E, generator=g)
-    logits[:, 0] += 3.0      # popular: > 512 rows
-    logits[:, 4] -= 2.0      # rare: a short tail tile only
-    logits[:, 5] -= 50.0     # idle
-    logits = logits.to(torch.bfloat16)
-    ref = O.routing_topk(logits, TOPK)
-    rd, gi, si = R.routing(logits.to(dev), TOPK)
-    hist = ref["hist"]
-    assert int(hist[0]) > 512 and 0 < int(hist[4]) < 256 and int(hist[5]) == 0
+    E_ = len(COUNTS)
+    assert sum(COUNTS) == T * TOPK and max(COUNTS) <= T
+    order = sorted(range(E_), key=lambda e: -COUNTS[e])
+    multiset = [e for e in order for _ in range(COUNTS[e])]
+    ids = torch.empty(T, TOPK, dtype=torch.int32)
+    for j, e in enumerate(multiset):
+        ids[j % T, j // T] = e
+    ids = ids[torch.randperm(T, generator=g)].sort(dim=1).values
+    logits = torch.randn(T, E_, generator=g).to(torch.bfloat16)
+    ref = O.routing_replay(logits, ids, TOPK)
+    rd, gi, si = R.routing_replay(logits.to(dev), ids.to(dev), TOPK)
+    assert ref["hist"].tolist() == COUNTS
     return g, ref, rd, gi
 
 
@@ -120,3 +131,38 @@ def test_dgrad_tiles(dev, cfg, gather, lora, odd):
     assert torch.isfinite(a).all()
     bad = (a - yr.double()).abs() > ATOL + RTOL * yr.double().abs()
     assert not bad.any(), float(bad.float().mean())
+
+
+@pytest.mark.parametrize("lora", [False, True])
+def test_fused_swiglu_epilogues_bit_equal(dev, lora):
+    """af3_moe_gemm_swiglu: the forward epilogue's SwiGLU and the input-gradient
+    epilogue's SwiGLU backward equal the separate kernels bit for bit, on full,
+    partial and short (two n-tiles per work item) tiles."""
+    from agent_factory_3_amd import kernels
+    g, ref, rd, gi = _routing(dev, 13)
+    alpha, limit = 1.702, 7.0
+    Rr, r, I_ = T * TOPK, 32, 320          # 2I = 640: n-tiles 256, 256, 128; I = 320: 256 + 64
+    # gate_up: W [E, 2I, H], H = KRED
+    gu_blocks, gu_scales = _weights(g, 2 * I_, KRED, False)
+    x = torch.randn(T, KRED, generator=g).to(torch.bfloat16).to(dev)
+    bias = (torch.randn(E, 2 * I_, generator=g) * 0.5).float().to(dev)
+    L = (torch.randn(Rr, r, generator=g) * 0.3).to(torch.bfloat16).to(dev) if lora else None
+    Bx = (torch.randn(E, 2 * I_, r, generator=g) * 0.3).to(torch.bfloat16).to(dev) if lora else None
+    wb, ws = gu_blocks.to(dev), gu_scales.to(dev)
+    res = Q.moe_rows(x, wb, ws, bias, rd, gi, None, False, L, Bx, swiglu=("fwd", alpha, limit))
+    assert res is not None
+    gu, act = res
+    gu_plain = Q.moe_rows(x, wb, ws, bias, rd, gi, None, False, L, Bx)
+    assert torch.equal(gu, gu_plain)
+    assert torch.equal(act, kernels.swiglu_forward(gu_plain, alpha, limit))
+    # down dX: W [E, H, I] read transposed (output I), reduction H = KRED
+    dn_blocks, dn_scales = _weights(g, KRED, I_, False)
+    dy = torch.randn(T, KRED, generator=g).to(torch.bfloat16).to(dev)
+    u = (torch.randn(Rr, r, generator=g) * 0.3).to(torch.bfloat16).to(dev) if lora else None
+    Ax = (torch.randn(E, r, I_, generator=g) * 0.3).to(torch.bfloat16).to(dev) if lora else None
+    gam = rd.gate_scal
+    db, ds = dn_blocks.to(dev), dn_scales.to(dev)
+    dgu = Q.moe_rows(dy, db, ds, None, rd, gi, gam, True, u, Ax, swiglu=("bwd", gu, alpha, limit))
+    d_act = Q.moe_rows(dy, db, ds, None, rd, gi, gam, True, u, Ax)
+    assert dgu is not None and dgu.shape == (Rr, 2 * I_)
+    assert torch.equal(dgu, kernels.swiglu_backward_raw(d_act, gu, alpha, limit))

@@ -167,3 +167,26 @@ def test_dequant_matmul_function_without_module(dev):
     with pytest.raises(NotImplementedError):
         Q.DequantMoEMatmul.apply(x, inp.gu_blocks.to(dev), inp.gu_scales.to(dev), None, rd, gi, None, None, None,
                                  si, None, "fp8", 4, None, None)
+
+
+@pytest.mark.parametrize("lora", [False, True])
+def test_fused_swiglu_module_matches_unfused_chain(dev, lora):
+    """The expert module's fused composition (SwiGLU inside the gate_up and dX
+    epilogues) gives the same output and gradients, bit for bit, as the
+    DequantMoEMatmul -> SwiGLUFunction -> DequantMoEMatmul chain."""
+    inp = workloads.layer(4, T=1024, E=16, H=256, I=192, lora_r=16 if lora else 0, zipf=False)
+    outs = []
+    for fused, fused_bwd in ((True, True), (True, False), (False, False)):
+        Q.FUSED_SWIGLU, Q.FUSED_SWIGLU_BWD = fused, fused_bwd
+        try:
+            m, x, y = _run_module(inp, dev, lora)
+        finally:
+            Q.FUSED_SWIGLU, Q.FUSED_SWIGLU_BWD = True, False
+        grads = [x.grad] + ([getattr(m, n).grad for n in ("gate_up_proj_lora_A", "gate_up_proj_lora_B",
+                                                        "down_proj_lora_A", "down_proj_lora_B")] if lora else [])
+        outs.append((y.detach(), grads))
+    y0, g0 = outs[-1]
+    for y1, g1 in outs[:-1]:
+        assert torch.equal(y1, y0)
+        for a, b in zip(g1, g0):
+            assert torch.equal(a, b)
