@@ -164,13 +164,19 @@ __global__ __launch_bounds__(256) void lrows_kernel(LrParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// wgrad partials: P[chunk] = sum_{r in chunk} Big[b(r)][c0 + (0..255)]^T (x) (rs(r) Small[r][0..r))
+// wgrad partials: P[chunk] = sum_{r in chunk} Big[b(r)][c0 + (0..255)]^T (x) Small[r][0..r)
+// with the entry point's row scale rs(r) folded into operand A of the entry
+// point (the Small side in MODE 1, the Big side in MODE 0) as bf16(rs(r) * A).
 // Block = (chunk of chunk_rows expert-sorted rows, 256 Big columns); 4 waves of
-// 64 columns x 32.  Per 64-row step: Big rows [64][256] (512 B rows, 16-byte
+// 64 columns x 32.  Per 32-row step: Big rows [32][256] (512 B rows, 16-byte
 // chunks XOR-swizzled by 2 (row & 3) so the transposing reads of 4 rows hit
-// distinct banks) and Small rows [64][SR bytes] go global->LDS (2 stages);
-// then each Small row is multiplied by rs(r) (0 past the chunk's rows) in place.
-// MODE 0 writes P as [W][r] (dB), MODE 1 as [r][W] (dA).
+// distinct banks) and Small rows [32][SR bytes] go global->LDS through a
+// 4-stage ring, three steps ahead.  The gather indices and the per-row scales
+// of the chunk are staged in LDS once, so no copy waits on an index load.
+// The row scales are applied in registers to the MFMA operands (each lane
+// holds 8 consecutive rows of one column of either operand); rows past the
+// chunk get scale 0 on the Small side.  MODE 0 writes P as [W][r] (dB),
+// MODE 1 as [r][W] (dA; transposed through LDS so the stores are row runs).
 // ---------------------------------------------------------------------------
 struct LwParams {
   const uint16_t* big;
@@ -186,17 +192,34 @@ struct LwParams {
   float* partials;
 };
 
-constexpr int kLwBig = 64 * 512;
-constexpr int kLwSmall = 64 * 64;
+constexpr int kLwRows = 32;               // rows per pipeline step
+constexpr int kLwStages = 4;
+constexpr int kLwBig = kLwRows * 512;     // Big bytes per step
+constexpr int kLwSmall = kLwRows * 64;    // Small bytes per step (<= 32 columns)
 constexpr int kLwStage = kLwBig + kLwSmall;
+constexpr int kLwMaxChunk = 512;          // rows per chunk (gather indices and scales staged in LDS)
+constexpr int kLwTPad = 260;              // floats per row of the MODE 1 output transpose
 
 __device__ __forceinline__ int lw_big_off(int row, int col) {  // byte offset of Big[row][col] (col % 4 == 0)
   return row * 512 + ((((col >> 3) ^ ((row & 3) << 1))) << 4) + ((col & 7) << 1);
 }
 
+// bf16(rs[i] * v[i]) for the 8 values of an MFMA operand
+__device__ __forceinline__ af3_bf16x8 lw_scale8(af3_bf16x8 v, const float4 r0, const float4 r1) {
+  af3_u32x4 w = __builtin_bit_cast(af3_u32x4, v);
+  const float rs[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+  for (int h = 0; h < 4; ++h)
+    w[h] = af3_pack_bf16x2(af3_bf16_to_f32(w[h] & 0xFFFFu) * rs[2 * h], af3_bf16_to_f32(w[h] >> 16) * rs[2 * h + 1]);
+  return __builtin_bit_cast(af3_bf16x8, w);
+}
+
 template <int SR, int MODE>
-__global__ __launch_bounds__(256) void lwg_kernel(LwParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kLwStage];
+__global__ __launch_bounds__(256, 2) void lwg_kernel(LwParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kLwStages * kLwStage];
+  __shared__ int32_t gsrc[kLwMaxChunk];                             // source row of each chunk row
+  __shared__ __attribute__((aligned(16))) float rs_small[kLwMaxChunk];  // 0 past the chunk's rows
+  __shared__ __attribute__((aligned(16))) float rs_big[kLwMaxChunk];    // MODE 0 row scale
   const int chunk = blockIdx.x / p.nbb, bb = blockIdx.x % p.nbb;
   const int32_t ent = p.chunk_map[chunk];
   if (ent < 0) return;
@@ -204,40 +227,47 @@ __global__ __launch_bounds__(256) void lwg_kernel(LwParams p) {
   const int kb = p.offs[e] + cb * p.chunk_rows;
   const int kend = min(p.chunk_rows, p.offs[e + 1] - kb);
   if (kend <= 0) return;
+  const int nsteps = (kend + kLwRows - 1) / kLwRows;
+  const bool big_rs = MODE == 0 && p.rowscale != nullptr;
+  const bool small_rs = MODE == 1 && p.rowscale != nullptr;
+  for (int i = threadIdx.x; i < nsteps * kLwRows; i += 256) {
+    const bool valid = i < kend;
+    const int64_t src = kb + (valid ? i : 0);  // rows past the chunk read its first row
+    gsrc[i] = p.big_gather ? p.big_gather[src] / p.big_div : (int32_t)src;
+    const float rs = p.rowscale ? af3_bf16_to_f32(p.rowscale[src]) : 1.f;
+    rs_small[i] = valid ? (small_rs ? rs : 1.f) : 0.f;
+    rs_big[i] = rs;
+  }
+  __syncthreads();
   const int c0 = bb * 256;
   const int ncols = min(256, p.W - c0);
-  const int nsteps = (kend + 63) / 64;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  constexpr int NS = (64 * SR) / 1024;  // Small copies per step (block)
+  constexpr int NS = (kLwRows * SR) / 1024;  // Small copies per step (block)
+  constexpr int NB = kLwBig / 1024 / 4;      // Big copies per step and wave
   const bool has_s = wave < NS;
 
-  // Big: 8 copies per wave, copy i covers rows 2 i, 2 i + 1
-  const uint16_t* brow[8];
+  // Big: NB copies per wave, copy c = NB wave + i covers rows 2 c, 2 c + 1
+  const uint16_t* bcol[NB];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int rr = (wave * 8 + i) * 2 + (lane >> 5);
+  for (int i = 0; i < NB; ++i) {
+    const int rr = (wave * NB + i) * 2 + (lane >> 5);
     const int lc = (lane & 31) ^ ((rr & 3) << 1);
-    const int col = lc * 8 < ncols ? c0 + lc * 8 : c0;
-    brow[i] = p.big + col;  // row part added per step (the gather differs per row)
-    (void)rr;
+    bcol[i] = p.big + (lc * 8 < ncols ? c0 + lc * 8 : c0);  // row part added per step (rows are gathered)
   }
   const uint8_t* ssrc = (const uint8_t*)p.small;
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(l_lds_addr(lds));
   auto issue = [&](int st_i) {
-    const uint32_t st = lds0 + (uint32_t)((st_i & 1) * kLwStage);
+    const uint32_t st = lds0 + (uint32_t)((st_i % kLwStages) * kLwStage);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int rr = (wave * 8 + i) * 2 + (lane >> 5);
-      const int rl = st_i * 64 + rr;
-      int64_t src = kb + (rl < kend ? rl : 0);
-      if (p.big_gather) src = p.big_gather[src] / p.big_div;
-      l_dma16(brow[i] + src * p.ld_big, st + (uint32_t)((wave * 8 + i) * 1024));
+    for (int i = 0; i < NB; ++i) {
+      const int rr = (wave * NB + i) * 2 + (lane >> 5);
+      const int64_t src = gsrc[st_i * kLwRows + rr];
+      l_dma16(bcol[i] + src * p.ld_big, st + (uint32_t)((wave * NB + i) * 1024));
     }
     if (has_s) {
       const int off = wave * 1024 + lane * 16;  // byte offset inside the step's Small rows
-      const int rr = off / SR;
-      const int rl = st_i * 64 + rr;
+      const int rl = st_i * kLwRows + off / SR;
       const int64_t srow = kb + (rl < kend ? rl : 0);
       l_dma16(ssrc + srow * SR + (off % SR), st + (uint32_t)(kLwBig + wave * 1024));
     }
@@ -249,77 +279,84 @@ __global__ __launch_bounds__(256) void lwg_kernel(LwParams p) {
     for (int q = 0; q < 16; ++q) acc[t][q] = 0.f;
 
   issue(0);
+  if (nsteps > 1) issue(1);
+  if (nsteps > 2) issue(2);
+  const int gi = lane >> 4, q = lane & 15;
+  const int lrow = 8 * (lane >> 5);  // first of the lane's 8 operand rows inside a 16-row slice
   for (int st_i = 0; st_i < nsteps; ++st_i) {
-    if (st_i + 1 < nsteps) issue(st_i + 1);
-    if (st_i + 1 < nsteps) {
-      if (has_s)
-        L_WAIT_VM(9);
+    // this step's copies are in once at most the (up to two) later issued steps are outstanding
+    const int ahead = min(2, nsteps - 1 - st_i);
+    if (has_s) {
+      if (ahead == 2)
+        L_WAIT_VM(10);
+      else if (ahead == 1)
+        L_WAIT_VM(5);
       else
-        L_WAIT_VM(8);
+        L_WAIT_VM(0);
     } else {
-      L_WAIT_VM(0);
+      if (ahead == 2)
+        L_WAIT_VM(8);
+      else if (ahead == 1)
+        L_WAIT_VM(4);
+      else
+        L_WAIT_VM(0);
     }
     L_BARRIER();
-    uint8_t* bs = lds + (st_i & 1) * kLwStage;
-    uint8_t* ss = bs + kLwBig;
-    // row scale rs(r) -> bf16(rs(r) * operand A of the entry point) (the
-    // Small side in MODE 1, the Big side in MODE 0); rows past the chunk get 0
-    // on the Small side
-    {
-      constexpr int TPR = 256 / 64;  // threads per row
-      const int rr = threadIdx.x / TPR, part = threadIdx.x % TPR;
-      const int rl = st_i * 64 + rr;
-      const bool valid = rl < kend;
-      const float rs = (valid && p.rowscale) ? af3_bf16_to_f32(p.rowscale[kb + rl]) : 1.f;
-      constexpr int VPT = SR / 2 / TPR;  // Small values per thread (4 or 8)
-      const float ssc = valid ? (MODE == 1 ? rs : 1.f) : 0.f;
-      uint16_t* v = (uint16_t*)(ss + rr * SR) + part * VPT;
+    // the slot of step st_i + 3 was last read in step st_i - 1 (all waves are past it)
+    if (st_i + 3 < nsteps) issue(st_i + 3);
+    const uint8_t* bs = lds + (st_i % kLwStages) * kLwStage;
+    const uint8_t* ss = bs + kLwBig;
+    const bool scale_s = small_rs || (st_i + 1) * kLwRows > kend;
 #pragma unroll
-      for (int q = 0; q < VPT; ++q) v[q] = (uint16_t)af3_f32_to_bf16(af3_bf16_to_f32(v[q]) * ssc);
-      if (MODE == 0 && p.rowscale) {  // this thread's 64 Big values of row rr (order inside the row is irrelevant)
-        af3_u32x4* bv = (af3_u32x4*)(bs + rr * 512 + part * 128);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          af3_u32x4 w = bv[c];
-#pragma unroll
-          for (int h = 0; h < 4; ++h)
-            w[h] = af3_pack_bf16x2(af3_bf16_to_f32(w[h] & 0xFFFFu) * rs, af3_bf16_to_f32(w[h] >> 16) * rs);
-          bv[c] = w;
-        }
-      }
-    }
-    L_BARRIER();
-    const int gi = lane >> 4, q = lane & 15;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < kLwRows / 16; ++s) {
       const int kr = s * 16 + (gi >> 1) * 8 + (q >> 2);
       const int scol = (gi & 1) * 16 + 4 * (q & 3);
-      const af3_bf16x8 b = l_tr8(ss + kr * SR + scol * 2, ss + (kr + 4) * SR + scol * 2);
+      const int r0 = st_i * kLwRows + s * 16 + lrow;
+      af3_bf16x8 b = l_tr8(ss + kr * SR + scol * 2, ss + (kr + 4) * SR + scol * 2);
+      if (scale_s) b = lw_scale8(b, *(const float4*)&rs_small[r0], *(const float4*)&rs_small[r0 + 4]);
+      float4 g0, g1;
+      if (big_rs) {
+        g0 = *(const float4*)&rs_big[r0];
+        g1 = *(const float4*)&rs_big[r0 + 4];
+      }
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const int bcol = wave * 64 + t * 32 + (gi & 1) * 16 + 4 * (q & 3);
-        const af3_bf16x8 a = l_tr8(bs + lw_big_off(kr, bcol), bs + lw_big_off(kr + 4, bcol));
+        const int bc = wave * 64 + t * 32 + (gi & 1) * 16 + 4 * (q & 3);
+        af3_bf16x8 a = l_tr8(bs + lw_big_off(kr, bc), bs + lw_big_off(kr + 4, bc));
+        if (big_rs) a = lw_scale8(a, g0, g1);
         acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[t], 0, 0, 0);
       }
     }
-    L_BARRIER();  // the stage is refilled by the next step's copies
   }
-  // acc[t][q]: Big column c0 + 64 wave + 32 t + i (i = 8 (q / 4) + 4 lh + q % 4), Small column j = lane % 32
+  // acc[t][qq]: Big column c0 + 64 wave + 32 t + 8 (qq / 4) + 4 lh + qq % 4, Small column j = lane % 32
   const int lr = lane & 31, lh = lane >> 5;
   const int j = lr;
-  if (j >= p.r) return;
   float* P = p.partials + (int64_t)chunk * p.W * p.r;
+  if (MODE == 0) {
+    if (j >= p.r) return;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < 2; ++t) {
 #pragma unroll
-    for (int qq = 0; qq < 16; ++qq) {
-      const int col = c0 + wave * 64 + t * 32 + (qq >> 2) * 8 + lh * 4 + (qq & 3);
-      if (col < c0 + ncols) {
-        if (MODE == 0)
-          P[(int64_t)col * p.r + j] = acc[t][qq];
-        else
-          P[(int64_t)j * p.W + col] = acc[t][qq];
+      for (int qq = 0; qq < 16; ++qq) {
+        const int col = wave * 64 + t * 32 + (qq >> 2) * 8 + lh * 4 + (qq & 3);
+        if (col < ncols) P[(int64_t)(c0 + col) * p.r + j] = acc[t][qq];
       }
+    }
+  } else {
+    // [r][256] through LDS (rows padded to kLwTPad floats), then row runs of ncols floats
+    float* T = (float*)lds;
+    L_BARRIER();  // every wave is done with the ring
+    if (j < p.r) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int qq = 0; qq < 16; ++qq)
+          T[j * kLwTPad + wave * 64 + t * 32 + (qq >> 2) * 8 + lh * 4 + (qq & 3)] = acc[t][qq];
+    }
+    L_BARRIER();
+    for (int i = threadIdx.x; i < p.r * 64; i += 256) {
+      const int jj = i >> 6, c = (i & 63) * 4;
+      if (c < ncols) *(float4*)(P + (int64_t)jj * p.W + c0 + c) = *(const float4*)(T + jj * kLwTPad + c);
     }
   }
 }
@@ -384,7 +421,7 @@ int lora_wgrad_fast(const uint16_t* big, int64_t ld_big, const int32_t* big_gath
                     float scale, const int32_t* token_offs, const int32_t* chunk_map, const int32_t* chunk_offs,
                     int max_chunks, int chunk_rows, int n_expts, float* partials, uint16_t* g, hipStream_t stream) {
   if (!(r == 16 || r == 32) || ld_small != r || W % 8 != 0 || ld_big % 8 != 0 || !l_al16(big) || !l_al16(small) ||
-      !l_al16(partials) || !l_al16(g))
+      !l_al16(partials) || !l_al16(g) || chunk_rows > kLwMaxChunk || chunk_rows % kLwRows != 0)
     return AF3_EUNSUPPORTED;
   LwParams p{};
   p.big = big;
