@@ -14,7 +14,7 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kWordsPerThread = 4;
+constexpr int kWordsPerThread = 8;
 
 __global__ __launch_bounds__(kThreads) void mxfp4_to_bf16_kernel(const uint32_t* __restrict__ blocks,
                                                                  const uint8_t* __restrict__ scales,

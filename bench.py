@@ -69,21 +69,33 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def _batched_us(torch, fn, sets, reps):
-    """Average per-launch time of ``reps`` rounds over rotating buffer sets,
-    one event pair around the whole batch (per-launch event pairs would add
-    their own overhead to microsecond kernels)."""
-    for args in sets:
-        fn(*args)
+def _graph_us(torch, fn, sets, reps):
+    """Average device time per launch: one call per buffer set is captured into a
+    HIP graph, which is replayed ``reps`` times between one event pair (Python's
+    launch cost would otherwise exceed these microsecond kernels).  The last
+    replay's outputs are checked bit for bit against an eager call."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        eager = [fn(*args) for args in sets]
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = [fn(*args) for args in sets]
+    g.replay()
     torch.cuda.synchronize()
     s = torch.cuda.Event(enable_timing=True)
     e = torch.cuda.Event(enable_timing=True)
     s.record()
     for _ in range(reps):
-        for args in sets:
-            fn(*args)
+        g.replay()
     e.record()
     torch.cuda.synchronize()
+    same = all(torch.equal(a, b) for a, b in zip(eager, outs))
+    if not same:
+        raise RuntimeError("graph replay output differs from the eager call")
+    del g, outs, eager
     return s.elapsed_time(e) * 1e3 / (reps * len(sets))
 
 
@@ -98,16 +110,24 @@ def bandwidth_extras(torch, dev, kernels, workloads, reps=50):
     blocks, scales = workloads.cfg0()
     # 8 x 42 MB > 256 MB MALL: each launch reads cold data
     sets = [(blocks.to(dev), scales.to(dev)) for _ in range(8)]
-    rec("dequant_cfg0", _batched_us(torch, kernels.mxfp4_to_bf16_hip, sets, reps), 8294400 + 518400 + 33177600)
+    rec("dequant_cfg0", _graph_us(torch, kernels.mxfp4_to_bf16_hip, sets, reps), 8294400 + 518400 + 33177600)
     del sets
+    # the same kernel over a whole 120b gate_up stack (128 experts of cfg0's shape, 5.4 GB
+    # moved), where the launch and drain latency of a 42 MB launch no longer dominate
+    bl, sc = blocks.to(dev), scales.to(dev)
+    big = [(bl.expand(128, *bl.shape).contiguous(), sc.expand(128, *sc.shape).contiguous())]
+    del bl, sc
+    rec("dequant_120b_gate_up", _graph_us(torch, kernels.mxfp4_to_bf16_hip, big, 5),
+        128 * (8294400 + 518400 + 33177600))
+    del big
     gu, dout = workloads.cfg1()
     M, N2 = gu.shape
     N = N2 // 2
     sets = [(gu.to(dev), dout.to(dev)) for _ in range(2)]
-    rec("swiglu_fwd_cfg1", _batched_us(torch, lambda g, d: kernels.swiglu_forward(g, 1.702, 7.0), sets, reps),
+    rec("swiglu_fwd_cfg1", _graph_us(torch, lambda g, d: kernels.swiglu_forward(g, 1.702, 7.0), sets, reps),
         M * N2 * 2 + M * N * 2)
     rec("swiglu_bwd_cfg1",
-        _batched_us(torch, lambda g, d: kernels.swiglu_backward_raw(d, g, 1.702, 7.0), sets, reps),
+        _graph_us(torch, lambda g, d: kernels.swiglu_backward_raw(d, g, 1.702, 7.0), sets, reps),
         M * N * 2 + M * N2 * 2 + M * N2 * 2)
     return res
 
@@ -116,7 +136,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cfg", type=int, default=4, choices=(2, 3, 4))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", action="store_true",
@@ -212,7 +232,9 @@ def main():
     traffic = None
     from agent_factory_3_amd.profiling import read_traffic
     tj = read_traffic(args.traffic_profile)
-    kname = {"moe_gemm_dgrad": "gemm4_dgrad_kernel", "moe_gemm_fwd": "gemm4_fwd_kernel"}.get(dom_tag)
+    # kernels of the default tile configurations (input gradient: the transposing-read
+    # kernel, tile_cfg 23; forward: tile_cfg 22)
+    kname = {"moe_gemm_dgrad": "gemm5_dgrad_kernel", "moe_gemm_fwd": "gemm4_fwd_kernel"}.get(dom_tag)
     if tj and kname:
         vals = [v["bytes"] for k, v in tj["kernels"].items() if kname in k.split("|")[0]]
         if vals:
