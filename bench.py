@@ -230,11 +230,9 @@ def main():
     # HBM bytes per launch of the dominant kernel from the committed rocprofv3
     # FETCH_SIZE / WRITE_SIZE summary (same kernel, same workload)
     traffic = None
-    from agent_factory_3_amd.profiling import read_traffic
+    from agent_factory_3_amd.profiling import GEMM_KERNELS, read_traffic
     tj = read_traffic(args.traffic_profile)
-    # kernels of the default tile configurations (input gradient: the transposing-read
-    # kernel, tile_cfg 23; forward: tile_cfg 22)
-    kname = {"moe_gemm_dgrad": "gemm5_dgrad_kernel", "moe_gemm_fwd": "gemm4_fwd_kernel"}.get(dom_tag)
+    kname = GEMM_KERNELS.get(dom_tag)
     if tj and kname:
         vals = [v["bytes"] for k, v in tj["kernels"].items() if kname in k.split("|")[0]]
         if vals:
