@@ -921,15 +921,16 @@ static inline unsigned g4_grid(int max_tiles, int NN, int GM) {
   return (unsigned)(8 * ((groups + 7) / 8) * GM * NN);
 }
 
-// Epilogue of a 256x256 tile computed by 4 waves (2x2) of 4x4 32x32 MFMA
+// Epilogue of a 256x256 (or CN = 512: 128x512) tile computed by waves of 32x32 MFMA
 // sub-tiles: v = (acc + bias[n]) * gamma[row] -> bf16, staged through LDS as
 // a [256][256] bf16 tile (16-byte chunks XOR-swizzled so the two row groups
 // of an MFMA output store hit disjoint banks), then written out with one
 // 16-byte store per chunk (a wave writes two whole 512-byte rows at a time).
 // `lds` must hold >= 129 KB; every wave must have finished reading its
 // operands from it.
+template <int CN = 256>
 __device__ __forceinline__ int g4_c_off(int row, int col) {  // byte offset of C[row][col] in the LDS tile
-  return row * 512 + ((((col >> 3) ^ (((row >> 2) & 1) << 2))) << 4) + ((col & 7) << 1);
+  return row * (CN * 2) + ((((col >> 3) ^ (((row >> 2) & 1) << 2))) << 4) + ((col & 7) << 1);
 }
 
 // Column of MFMA sub-tile tn, lane column lr inside a wave's 128 columns:
@@ -940,9 +941,10 @@ __device__ __forceinline__ int g4_col(int tn, int lr) {
   return PAIRED ? 64 * (tn >> 1) + 2 * lr + (tn & 1) : tn * 32 + lr;
 }
 
-template <bool PAIRED = false, int TM = 4, int TN = 4, int NT = 256>
+template <bool PAIRED = false, int TM = 4, int TN = 4, int NT = 256, int CN = 256>
 __device__ __forceinline__ void g4_epilogue(const Params& p, uint8_t* lds, af3_f32x16 acc[TM][TN], int e, int row_lo,
                                             int nrows, int n0, int ncols, int wm0, int wn0) {
+  constexpr int CH = CN / 8;  // 16-byte chunks per tile row
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
   float* const gl = (float*)(lds + 256 * 512);  // per-row gammas
@@ -975,7 +977,7 @@ __device__ __forceinline__ void g4_epilogue(const Params& p, uint8_t* lds, af3_f
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const float v = (acc[tm][tn][j * 4 + q] + bv[tn]) * gq[q];
-          *(uint16_t*)(lds + g4_c_off(row0 + q, col)) = (uint16_t)af3_f32_to_bf16(v);
+          *(uint16_t*)(lds + g4_c_off<CN>(row0 + q, col)) = (uint16_t)af3_f32_to_bf16(v);
         }
       }
     }
@@ -984,9 +986,9 @@ __device__ __forceinline__ void g4_epilogue(const Params& p, uint8_t* lds, af3_f
 #pragma unroll 4
   for (int i = 0; i < 32 * 256 / NT; ++i) {
     const int id = i * NT + threadIdx.x;
-    const int row = id >> 5, ch = id & 31;
+    const int row = id / CH, ch = id % CH;
     if (row < nrows && ch * 8 < ncols) {
-      const af3_u32x4 v = *(const af3_u32x4*)(lds + row * 512 + ((ch ^ (((row >> 2) & 1) << 2)) << 4));
+      const af3_u32x4 v = *(const af3_u32x4*)(lds + row * (CN * 2) + ((ch ^ (((row >> 2) & 1) << 2)) << 4));
       *(af3_u32x4*)(p.c + (int64_t)(row_lo + row) * p.ldc + n0 + ch * 8) = v;
       if (p.epi == 2) {  // SwiGLU of the chunk's 4 (gate, up) pairs, from the bf16 values just stored
         uint32_t o[2];
@@ -1121,33 +1123,32 @@ __device__ __forceinline__ void g4_kstep(const uint16_t* as, const uint8_t* bs, 
   }
 }
 
-template <int WM, int WN, int BXK>
-__global__ __launch_bounds__(WM * WN * 64) void gemm4_fwd_kernel(Params p) {
+// One work item of the forward kernel: a RM x CN output tile (256 x 256, or
+// NARROW 128 x 512 for the partial tiles of short experts, so a tail tile of
+// <= 128 rows converts each weight byte once per 128 rows instead of per 256).
+// The 8 waves are WM x WN (NARROW: 1 x 8) of the same 128 x 64 wave tile.
+template <int WM, int WN, int BXK, bool NARROW>
+__device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, int row_lo, int nrows, int n0,
+                                         int ncols) {
   constexpr int NW = WM * WN, NT = NW * 64;
-  constexpr int TM = 256 / WM / 32, TN = 256 / WN / 32;
-  constexpr int API = 32 / NW, BPI = 8 / NW, DPW = API + BPI;  // copies per wave per k-step
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kG4LdsBytes];
-  uint16_t* const As = (uint16_t*)lds;                          // 3 x 32 KB
-  uint8_t* const Bs = lds + kG4Stages * kG4AStage * 2;          // 3 x 8 KB
-  uint8_t* const Ss = Bs + kG4Stages * kG4BStage;               // <= 32 KB
-
-  int mt, nt;
-  if (!g4_work_item(p, mt, nt)) return;
-  const int32_t ent = p.tile_map[mt];
-  if (ent < 0) return;
-  const int e = ent & 0xFFFF, blk = ent >> 16;
-  const int row_lo = p.offs[e] + blk * kG4Rows;
-  const int nrows = min(kG4Rows, p.offs[e + 1] - row_lo);
-  if (nrows <= 0) return;
-  const int n0 = nt * kG4Rows;
-  const int ncols = min(kG4Rows, p.N - n0);
+  constexpr int RM = NARROW ? 128 : kG4Rows, CN = NARROW ? 512 : kG4Rows;
+  constexpr int WMX = NARROW ? 1 : WM, WNX = NARROW ? NW : WN;
+  constexpr int TM = RM / WMX / 32, TN = CN / WNX / 32;
+  constexpr int ASTAGE = RM * kBK;  // bf16 elements per A stage
+  constexpr int BSTAGE = CN * 32;   // bytes per packed-B stage
+  constexpr int API = RM / 8 / NW, BPI = CN / 32 / NW, DPW = API + BPI;  // copies per wave per k-step
+  static_assert(API >= 1 && BPI >= 1 && (DPW == 10 || DPW == 8 || DPW == 5 || DPW == 4), "copy schedule");
+  static_assert(kG4Stages * (ASTAGE * 2 + BSTAGE) <= kG4Stages * (kG4AStage * 2 + kG4BStage), "LDS ring");
+  uint16_t* const As = (uint16_t*)lds;                    // 3 x RM x 64 bf16
+  uint8_t* const Bs = lds + kG4Stages * ASTAGE * 2;       // 3 x CN x 32 bytes
+  uint8_t* const Ss = Bs + kG4Stages * BSTAGE;            // CN x G scale bytes
   const int G = p.K >> 5;
   const int nk = p.K / kBK;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar)
   const int lr = lane & 31, lh = lane >> 5;
-  const int wm0 = (wave / WN) * (32 * TM), wn0 = (wave % WN) * (32 * TN);
+  const int wm0 = (wave / WNX) * (32 * TM), wn0 = (wave % WNX) * (32 * TN);
   const int tm_live = min(TM, max(0, (nrows - wm0 + 31) >> 5));
   const int tn_live = min(TN, max(0, (ncols - wn0 + 31) >> 5));
   const bool full = tm_live == TM && tn_live == TN;
@@ -1182,19 +1183,33 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm4_fwd_kernel(Params p) {
       g4_dma16(sbase + src, __builtin_amdgcn_readfirstlane(lds_addr(Ss)) + (uint32_t)(i * 1024));
     }
   }
-  // copy j (0..9) of k-step kt: 8 A instructions (8 rows each), 2 packed-B
+  // copy j (0..DPW-1) of k-step kt: API A instructions (8 rows each), then BPI packed-B
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));  // LDS byte address of the block's area
   auto issue_one = [&](int kt, int j) {
     const int st = kt % kG4Stages;
     if (j < API)
-      g4_dma16(arow[j] + kt * kBK, lds0 + (uint32_t)(st * kG4AStage * 2 + (wave * API + j) * 8 * kBK * 2));
+      g4_dma16(arow[j] + kt * kBK, lds0 + (uint32_t)(st * ASTAGE * 2 + (wave * API + j) * 8 * kBK * 2));
     else
       g4_dma16(bsrc[j - API] + kt * 32,
-               lds0 + (uint32_t)(kG4Stages * kG4AStage * 2 + st * kG4BStage + (wave * BPI + j - API) * 1024));
+               lds0 + (uint32_t)(kG4Stages * ASTAGE * 2 + st * BSTAGE + (wave * BPI + j - API) * 1024));
   };
   auto issue = [&](int kt) {
 #pragma unroll
     for (int j = 0; j < DPW; ++j) issue_one(kt, j);
+  };
+  // k-step kt's stage is complete once this wave's copies for it have landed
+  // (at most DPW newer ones outstanding, none for the last k-step)
+  auto wait_stage = [&](bool last) {
+    if (last)
+      AF3_ASM_WAIT_VM(0);
+    else if constexpr (DPW == 10)
+      AF3_ASM_WAIT_VM(10);
+    else if constexpr (DPW == 8)
+      AF3_ASM_WAIT_VM(8);
+    else if constexpr (DPW == 5)
+      AF3_ASM_WAIT_VM(5);
+    else
+      AF3_ASM_WAIT_VM(4);
   };
 
   af3_f32x16 acc[TM][TN];
@@ -1232,21 +1247,14 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm4_fwd_kernel(Params p) {
     for (int tm = 0; tm < TM; ++tm) af[1][tm] = zf;
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) bf[1][tn] = zf;
-    // k-step kt: its stage is complete once this wave's copies for it have
-    // landed (at most DPW newer ones outstanding) and every wave passed the
-    // barrier, which also orders the carried fragment reads of stage kt - 1
-    // before the copies into that stage (issued for kt + 2 during kt)
+    // the barrier after the wait also orders the carried fragment reads of
+    // stage kt - 1 before the copies into that stage (issued for kt + 2 during kt)
     auto step = [&](int kt, bool last, auto&& dma) {
-      if (last)
-        AF3_ASM_WAIT_VM(0);
-      else if constexpr (DPW == 10)
-        AF3_ASM_WAIT_VM(10);
-      else
-        AF3_ASM_WAIT_VM(5);
+      wait_stage(last);
       AF3_ASM_LDS_BARRIER();
       const int st = kt % kG4Stages;
-      g4_kstep<TM, TN, DPW, FULL, EXACT>(As + st * kG4AStage, Bs + st * kG4BStage, Ss, G, kt, wm0, wn0, tm_live,
-                                         tn_live, acc, af, bf, dma);
+      g4_kstep<TM, TN, DPW, FULL, EXACT>(As + st * ASTAGE, Bs + st * BSTAGE, Ss, G, kt, wm0, wn0, tm_live, tn_live,
+                                         acc, af, bf, dma);
     };
     int kt = 0;
     for (; kt + 2 < nk; ++kt) step(kt, false, [&](int j) { issue_one(kt + 2, j); });
@@ -1270,12 +1278,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm4_fwd_kernel(Params p) {
     // partial tile) only keeps the copy / barrier protocol of the k-loop, so
     // the live wave sharing its SIMD runs alone
     for (int kt = 0; kt < nk; ++kt) {
-      if (kt + 1 == nk)
-        AF3_ASM_WAIT_VM(0);
-      else if constexpr (DPW == 10)
-        AF3_ASM_WAIT_VM(10);
-      else
-        AF3_ASM_WAIT_VM(5);
+      wait_stage(kt + 1 == nk);
       AF3_ASM_LDS_BARRIER();
       if (kt + 2 < nk) issue(kt + 2);
     }
@@ -1283,7 +1286,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm4_fwd_kernel(Params p) {
 
   if constexpr (BXK != NONE) {
     if (p.kx > 0) {  // expert-LoRA segment: + L[r] . Bx[e][n]^T, both bf16 through LDS
-      Loader<kG4Rows, ROWS_BF16, NT> la, lb;
+      Loader<RM, ROWS_BF16, NT> la;
+      Loader<CN, ROWS_BF16, NT> lb;
       la.init(p.ax, 0, row_lo, nrows, p.kx);
       lb.init(p.bx, e, n0, ncols, p.kx);
       for (int k0 = 0; k0 < p.kx; k0 += kBK) {
@@ -1291,14 +1295,40 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm4_fwd_kernel(Params p) {
         lb.load(k0);
         __syncthreads();
         la.store(As);
-        lb.store(As + kG4AStage);
+        lb.store(As + RM * kBK);
         __syncthreads();
-        mma_kstep<TM, TN>(As, As + kG4AStage, wm0, wn0, acc);
+        mma_kstep<TM, TN>(As, As + RM * kBK, wm0, wn0, acc);
       }
     }
   }
 
-  g4_epilogue<false, TM, TN, NT>(p, lds, acc, e, row_lo, nrows, n0, ncols, wm0, wn0);
+  g4_epilogue<false, TM, TN, NT, CN>(p, lds, acc, e, row_lo, nrows, n0, ncols, wm0, wn0);
+}
+
+// scale bytes of a NARROW work item (512 weight rows x G) fit behind its rings
+constexpr int kG4NarrowMaxG = (kG4LdsBytes - kG4Stages * (128 * kBK * 2 + 512 * 32)) / 512;
+
+template <int WM, int WN, int BXK>
+__global__ __launch_bounds__(WM * WN * 64) void gemm4_fwd_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kG4LdsBytes];
+  int mt, nt;
+  if (!g4_work_item(p, mt, nt)) return;
+  const int32_t ent = p.tile_map[mt];
+  if (ent < 0) return;
+  const int e = ent & 0xFFFF, blk = ent >> 16;
+  const int row_lo = p.offs[e] + blk * kG4Rows;
+  const int nrows = min(kG4Rows, p.offs[e + 1] - row_lo);
+  if (nrows <= 0) return;
+  const int n0 = nt * kG4Rows;
+  if constexpr (WM * WN == 8) {  // (the 4-wave variant keeps 256 x 256 items: its registers are full)
+    if (nrows <= 128 && (p.K >> 5) <= kG4NarrowMaxG) {
+      // tiles of <= 128 rows take n-tiles nt and nt + 1 as one 128 x 512 item
+      if (nt & 1) return;
+      g4f_tile<WM, WN, BXK, true>(p, lds, e, row_lo, nrows, n0, min(512, p.N - n0));
+      return;
+    }
+  }
+  g4f_tile<WM, WN, BXK, false>(p, lds, e, row_lo, nrows, n0, min(kG4Rows, p.N - n0));
 }
 
 // ---------------------------------------------------------------------------

@@ -24,8 +24,8 @@ KRED, NOUT, T, E, TOPK = 640, 576, 700, 7, 4
 
 # rows per expert: two full 256-row tiles + a tail of 188 / 178 / 138 rows
 # (full-width tail tiles), 256 + 44 and 256 + 104 rows and 100 rows (tiles of
-# <= 128 rows, which the input-gradient kernel runs two n-tiles at a time), and
-# an idle expert
+# <= 128 rows, which the default kernels of both directions run two n-tiles at
+# a time, with N = 576 leaving a lone third n-tile), and an idle expert
 COUNTS = [700, 300, 690, 650, 100, 360, 0]
 
 
