@@ -349,7 +349,11 @@ def _lora_rows(x, gather, k_act, wl, trans_b, scale, ed, n_out, K):
     dev = x.device
     R = gather.shape[0] if gather is not None else x.shape[0]
     out = torch.empty(R, n_out, dtype=torch.bfloat16, device=dev)
-    pid_map = ed.block_pid_map[GEMM_BLOCK_M]
+    # full tiles first: the tiles past one round of resident blocks are then the
+    # partial ones, whose clamped rows are cache hits
+    pid_map = getattr(ed, "gemm_order", {}).get(GEMM_BLOCK_M)
+    if pid_map is None:
+        pid_map = ed.block_pid_map[GEMM_BLOCK_M]
     if R and pid_map.numel():
         E = wl.shape[0]
         _capi.call("af3_lora_rows", x.data_ptr(), x.stride(0) if x.shape[0] > 1 else K, _capi.ptr(gather),

@@ -26,7 +26,7 @@ from . import _capi
 # block sizes for which tile maps are built: 128- and 256-row GEMM tiles and
 # the 512-row chunks of the LoRA weight-gradient reduction
 BLOCK_MS = (128, 256, 512)
-GEMM_ORDER_BMS = (256,)
+GEMM_ORDER_BMS = (128, 256)  # tile sizes with a full-first work order (LoRA row tiles, GEMM tiles)
 
 
 @dataclass
