@@ -12,6 +12,9 @@ this module                              reference (kernels.py)
 ``swiglu_forward``                       ``_swiglu_forward_triton`` 451-490
 ``swiglu_backward``                      ``_swiglu_backward`` 556-582
 ``swiglu_backward_raw``                  (new: backward from the raw input)
+``mxfp4_to_fp8_e5m2``                    ``mxfp4_to_fp8_e5m2_triton`` 20-108
+``mxfp4_to_fp8_e5m2_colmajor``           ``mxfp4_to_fp8_e5m2_colmajor`` 238-312
+``dynamic_quantize_per_token``           ``dynamic_quantize_per_token`` 319-388
 =======================================  =====================================
 
 The reference's names are provided as aliases so code that imports them keeps
@@ -132,7 +135,69 @@ def swiglu_backward_raw(grad_output: torch.Tensor, gate_up_raw: torch.Tensor, al
     return out
 
 
+def mxfp4_to_fp8_e5m2(blocks: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """MXFP4 -> fp8 E5M2 bits, row-major [..., G*32] (kernels.py:20-108 rule
+    and uint16 packing, bit for bit)."""
+    _need_cuda(blocks, "blocks")
+    if blocks.dtype != torch.uint8 or scales.dtype != torch.uint8:
+        raise TypeError("blocks and scales must be uint8")
+    if blocks.shape[-1] != 16 or tuple(blocks.shape[:-1]) != tuple(scales.shape):
+        raise ValueError(f"shape mismatch: blocks {tuple(blocks.shape)} scales {tuple(scales.shape)}")
+    prefix, G = blocks.shape[:-2], blocks.shape[-2]
+    n_groups = blocks.numel() // 16
+    bf = blocks.reshape(n_groups, 16).contiguous()
+    sf = scales.reshape(n_groups).contiguous()
+    out = torch.empty(n_groups, 32, dtype=torch.uint8, device=blocks.device)
+    _capi.call("af3_mxfp4_to_fp8_e5m2", bf.data_ptr(), sf.data_ptr(), out.data_ptr(), n_groups,
+               _capi.stream_of(blocks.device))
+    return out.reshape(*prefix, G * 32).view(torch.float8_e5m2)
+
+
+def mxfp4_to_fp8_e5m2_colmajor(blocks: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """MXFP4 [E, N, G, 16] -> fp8 E5M2 [E, K, N] (N contiguous), K = 32 G
+    (kernels.py:238-312, values truncated to a byte as its stores do)."""
+    _need_cuda(blocks, "blocks")
+    if blocks.dim() != 4 or blocks.shape[-1] != 16:
+        raise ValueError(f"blocks must be [E, N, G, 16], got {tuple(blocks.shape)}")
+    E, N, G, _ = blocks.shape
+    if tuple(scales.shape) != (E, N, G):
+        raise ValueError(f"scales must be [{E}, {N}, {G}], got {tuple(scales.shape)}")
+    out = torch.empty(E, G * 32, N, dtype=torch.uint8, device=blocks.device)
+    _capi.call("af3_mxfp4_to_fp8_e5m2_colmajor", blocks.contiguous().data_ptr(), scales.contiguous().data_ptr(),
+               out.data_ptr(), E, N, G, _capi.stream_of(blocks.device))
+    return out.view(torch.float8_e5m2)
+
+
+def quantize_per_token_e4m3(x: torch.Tensor, with_bf16: bool = False):
+    """Per-row fp8 E4M3FN codes of ``x`` [M, K] bf16 and fp32 scales [M]:
+    scale = max(amax, 1e-12) / 448, codes = E4M3(x / scale) (round to nearest
+    even, saturating).  ``with_bf16`` also returns the codes' values as bf16."""
+    _need_cuda(x, "x")
+    if x.dtype != torch.bfloat16 or x.dim() != 2:
+        raise TypeError("x must be a 2-D bfloat16 tensor")
+    M, K = x.shape
+    Kp = (K + 7) // 8 * 8
+    if not (x.stride(-1) == 1 and (x.stride(0) % 8 == 0 or M == 1) and x.data_ptr() % 16 == 0):
+        xp = torch.empty(M, Kp, dtype=x.dtype, device=x.device)   # rows 16-byte aligned
+        xp[:, :K] = x
+        x = xp[:, :K]
+    codes = torch.empty(M, Kp, dtype=torch.uint8, device=x.device)[:, :K]
+    scale = torch.empty(M, dtype=torch.float32, device=x.device)
+    vals = torch.empty(M, Kp, dtype=torch.bfloat16, device=x.device)[:, :K] if with_bf16 else None
+    _capi.call("af3_quantize_per_token_e4m3", x.data_ptr(), x.stride(0) if M > 1 else Kp, M, K, codes.data_ptr(),
+               Kp, scale.data_ptr(), _capi.ptr(vals), Kp, _capi.stream_of(x.device))
+    codes = codes.view(torch.float8_e4m3fn)
+    return (codes, scale, vals) if with_bf16 else (codes, scale)
+
+
+def dynamic_quantize_per_token(x: torch.Tensor):
+    """BF16 -> (fp8 E4M3FN [M, K], fp32 per-row scale [M]) (kernels.py:375-388)."""
+    codes, scale = quantize_per_token_e4m3(x)
+    return codes.contiguous() if codes.stride(0) != codes.shape[1] else codes, scale
+
+
 # the reference's names (kernels.py), for code that imports them directly
 mxfp4_to_bf16_triton = mxfp4_to_bf16_hip
+mxfp4_to_fp8_e5m2_triton = mxfp4_to_fp8_e5m2
 _swiglu_forward_triton = swiglu_forward
 _swiglu_backward = swiglu_backward

@@ -1,7 +1,7 @@
 """gpt-oss MoE experts with frozen MXFP4 weights on MI355X (drop-in module).
 
 Same public API as the reference's ``src/agent_factory_3/models/gpt_oss/
-quantization.py`` for the ``dequant_dtype="bf16"`` path:
+quantization.py``, for both ``dequant_dtype`` modes:
 
 ================================  ===========================================
 reference (quantization.py)       here
@@ -31,9 +31,15 @@ LoRA on both projections (``enable_expert_lora``), with the PEFT convention
 ``W_eff = W + (lora_alpha / r) * B @ A`` (model_trainer.py:665,711) and bf16
 adapters; its autograd function returns gradients for ``x``, ``A`` and ``B``.
 
+``dequant_dtype="fp8"`` (quantization.py:332-357, 382-408) quantizes the
+activation (forward) or the incoming gradient (backward) per token to fp8
+E4M3FN and runs the same grouped GEMM on the codes' values (exact in bf16)
+with the per-token scale applied to the fp32 accumulator; the reference's
+E5M2 weights hold exactly the MXFP4 values, so the products are the same.
+Expert LoRA is bf16-mode only.
+
 Every compute call goes to ``libaf3_mi355x.so``; there is no CPU or eager
-fallback.  Only ``dequant_dtype="bf16"`` is implemented (the fp8 mode of the
-reference is unused by its recipes).
+fallback.
 """
 from __future__ import annotations
 
@@ -43,7 +49,7 @@ from contextlib import contextmanager
 import torch
 from torch import nn
 
-from . import _capi
+from . import _capi, kernels
 from .kernels import mxfp4_to_bf16_hip, swiglu_backward_raw, swiglu_forward
 from .routing import (  # noqa: F401  (re-exported names of the routing layer)
     ExptData, GatherIndx, RoutingData, ScatterIndx, compute_expt_data, compute_expt_data_torch,
@@ -163,7 +169,7 @@ def _weight_dims(blocks, trans_w):
 
 
 def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=None, trans_w=False,
-             lora_l=None, lora_b=None, swiglu=None):
+             lora_l=None, lora_b=None, swiglu=None, a_row_scale=None):
     """Expert-sorted output rows of the grouped GEMM (no scatter).
 
     ``trans_w=False``: ``Y[r] = X[a(r)] @ W[e]^T`` with W = dequant(blocks) [E, N, K]
@@ -238,7 +244,17 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
             y.shape[1])
     stream = _capi.stream_of(dev)
 
+    if a_row_scale is not None:  # fp8 mode: (acc * a_row_scale[a(r)] + bias) * gammas
+        if epi or lr:
+            raise ValueError("a row scale cannot be combined with the LoRA segment or a fused SwiGLU")
+        a_row_scale = a_row_scale.to(torch.float32).contiguous()
+
     def launch():
+        if a_row_scale is not None:
+            rargs = args[:10] + args[14:]   # without the LoRA operands
+            if not _capi.try_call("af3_moe_gemm_rowscale", *rargs, a_row_scale.data_ptr(), stream):
+                raise RuntimeError("moe_gemm: the A row scale needs the default tile configurations (20-23)")
+            return True
         if epi == 0:
             _capi.call("af3_moe_gemm", *args, stream)
             return True
@@ -268,10 +284,13 @@ def moe_combine(rows, scatter_indx, n_expts_act):
 
 
 def matmul_ogs(x, w_blocks_scales, bias, routing_data=None, gather_indx=None, scatter_indx=None, gammas=None,
-               trans_w=False):
-    """matmul_ogs semantics over MXFP4 weights: rows, then the scatter-sum if any."""
+               trans_w=False, a_row_scale=None):
+    """matmul_ogs semantics over MXFP4 weights: rows, then the scatter-sum if any.
+    ``a_row_scale`` (fp32, one per row of ``x``): the per-token scale of fp8
+    activations (PrecisionConfig lhs ``scale_mode="per_token"``), applied to
+    the accumulator before bias and gammas."""
     blocks, scales = w_blocks_scales
-    y = moe_rows(x, blocks, scales, bias, routing_data, gather_indx, gammas, trans_w)
+    y = moe_rows(x, blocks, scales, bias, routing_data, gather_indx, gammas, trans_w, a_row_scale=a_row_scale)
     if scatter_indx is None:
         return y
     k = routing_data.n_expts_act if routing_data is not None else 1
@@ -293,11 +312,18 @@ class DequantMoEMatmul(torch.autograd.Function):
     def forward(ctx, x, blocks, scales, bias, routing_data, fwd_gather_indx, fwd_scatter_indx, fwd_gammas,
                 bwd_gather_indx, bwd_scatter_indx, bwd_gammas, dequant_dtype="bf16", n_expts_act=1,
                 experts_module=None, proj_name=None):
-        if dequant_dtype != "bf16":
-            raise NotImplementedError(f"dequant_dtype={dequant_dtype!r}: only 'bf16' is implemented")
+        if dequant_dtype not in ("bf16", "fp8"):
+            raise NotImplementedError(f"dequant_dtype={dequant_dtype!r}: 'bf16' or 'fp8'")
         with on_device(x.device):
-            out = matmul_ogs(x, (blocks, scales), bias, routing_data, fwd_gather_indx, fwd_scatter_indx,
-                             fwd_gammas, trans_w=False)
+            if dequant_dtype == "fp8":
+                # quantization.py:332-357: per-token E4M3 activations x MXFP4 weights (their E5M2
+                # form has the same values), fp32 accumulation scaled per row, bf16 out
+                _, xs, xq = kernels.quantize_per_token_e4m3(x.to(torch.bfloat16), with_bf16=True)
+                out = matmul_ogs(xq, (blocks, scales), bias, routing_data, fwd_gather_indx, fwd_scatter_indx,
+                                 fwd_gammas, trans_w=False, a_row_scale=xs)
+            else:
+                out = matmul_ogs(x, (blocks, scales), bias, routing_data, fwd_gather_indx, fwd_scatter_indx,
+                                 fwd_gammas, trans_w=False)
         ctx.experts_module = experts_module
         ctx.proj_name = proj_name
         if experts_module is None:  # no module to re-derive from: keep the (view) tensors
@@ -317,9 +343,14 @@ class DequantMoEMatmul(torch.autograd.Function):
         else:
             blocks, scales = ctx.weights
         with on_device(grad_output.device):
-            grad_x = matmul_ogs(grad_output.to(torch.bfloat16).contiguous(), (blocks, scales), None,
-                                ctx.routing_data, ctx.bwd_gather_indx, ctx.bwd_scatter_indx, ctx.bwd_gammas,
-                                trans_w=True)
+            g = grad_output.to(torch.bfloat16).contiguous()
+            if ctx.dequant_dtype == "fp8":  # quantization.py:382-408
+                _, gs, gq = kernels.quantize_per_token_e4m3(g, with_bf16=True)
+                grad_x = matmul_ogs(gq, (blocks, scales), None, ctx.routing_data, ctx.bwd_gather_indx,
+                                    ctx.bwd_scatter_indx, ctx.bwd_gammas, trans_w=True, a_row_scale=gs)
+            else:
+                grad_x = matmul_ogs(g, (blocks, scales), None, ctx.routing_data, ctx.bwd_gather_indx,
+                                    ctx.bwd_scatter_indx, ctx.bwd_gammas, trans_w=True)
         return grad_x, None, None, None, None, None, None, None, None, None, None, None, None, None, None
 
 
@@ -659,6 +690,8 @@ class Mxfp4Bf16DequantGptOssExperts(nn.Module):
 
     def _proj(self, x, proj, bias, routing_data, fg, fs, fgam, bg, bs, bgam):
         blocks, scales = self._get_uint8_weights(proj)
+        if self.expert_lora_r and self.dequant_dtype != "bf16":
+            raise NotImplementedError("expert LoRA is implemented for dequant_dtype='bf16' only")
         if self.expert_lora_r:
             return LoraDequantMoEMatmul.apply(
                 x, getattr(self, f"{proj}_lora_A"), getattr(self, f"{proj}_lora_B"), self.expert_lora_scaling,

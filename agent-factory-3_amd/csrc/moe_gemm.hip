@@ -81,7 +81,18 @@ struct Params {
   void* glu;
   int64_t ld_glu;
   float alpha, limit;
+  // per-row scale of the A operand (fp8 mode: per-token activation scale),
+  // indexed like the A rows (gather[r] / gdiv, or r); the default epilogues
+  // then store (acc * ascale + bias) * gammas
+  const float* ascale;
 };
+
+// scale of A row a(r) for output row r (1 without a row scale)
+__device__ __forceinline__ float g4_ascale(const Params& p, int64_t r) {
+  if (!p.ascale) return 1.f;
+  const int64_t ar = p.a.gather ? p.a.gather[r] / p.a.gdiv : r;
+  return p.ascale[ar];
+}
 
 __device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
 
@@ -888,7 +899,7 @@ constexpr int kG4AStage = kG4Rows * kBK;   // bf16 elements per A stage (32 KB)
 constexpr int kG4BStage = kG4Rows * 32;    // bytes per packed-B stage (8 KB)
 constexpr int kG4MaxG = 128;               // scale bytes per weight row (K <= 4096)
 constexpr int kG4LdsBytes = kG4Stages * (kG4AStage * 2 + kG4BStage) + kG4Rows * kG4MaxG;  // 152 KB
-static_assert(kG4LdsBytes >= 256 * 512 + 1024, "the epilogue reuses the LDS for the bf16 tile + row gammas");
+static_assert(kG4LdsBytes >= 256 * 512 + 2048, "the epilogue reuses the LDS for the bf16 tile + row gammas / scales");
 static_assert(kG4LdsBytes <= 160 * 1024, "gfx950 LDS per workgroup");
 
 // Work item (m-tile, n-tile) of workgroup b.  Work goes in groups of GM
@@ -948,6 +959,7 @@ __device__ __forceinline__ void g4_epilogue(const Params& p, uint8_t* lds, af3_f
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
   float* const gl = (float*)(lds + 256 * 512);  // per-row gammas
+  float* const al = gl + 256;                    // per-row A scales
   __syncthreads();
   for (int t = threadIdx.x; t < 256; t += NT) {
     float gv = 1.f;
@@ -956,6 +968,7 @@ __device__ __forceinline__ void g4_epilogue(const Params& p, uint8_t* lds, af3_f
       gv = p.gammas_f32 ? ((const float*)p.gammas)[gr] : af3_bf16_to_f32(((const uint16_t*)p.gammas)[gr]);
     }
     gl[t] = gv;
+    al[t] = t < nrows ? g4_ascale(p, row_lo + t) : 1.f;
   }
   float bv[TN];
 #pragma unroll
@@ -971,12 +984,15 @@ __device__ __forceinline__ void g4_epilogue(const Params& p, uint8_t* lds, af3_f
       const int row0 = wm0 + tm * 32 + j * 8 + lh * 4;
       const float4 g = *(const float4*)(gl + row0);
       const float gq[4] = {g.x, g.y, g.z, g.w};
+      const float4 a = *(const float4*)(al + row0);
+      const float aq[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn) {
         const int col = wn0 + g4_col<PAIRED>(tn, lr);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const float v = (acc[tm][tn][j * 4 + q] + bv[tn]) * gq[q];
+          const float x = acc[tm][tn][j * 4 + q];
+          const float v = p.ascale ? (x * aq[q] + bv[tn]) * gq[q] : (x + bv[tn]) * gq[q];
           *(uint16_t*)(lds + g4_c_off<CN>(row0 + q, col)) = (uint16_t)af3_f32_to_bf16(v);
         }
       }
@@ -1705,7 +1721,7 @@ constexpr int kD5AOff = 0;
 constexpr int kD5BOff = 256 * 64 * 2;           // 32 KB of A
 constexpr int kD5SOff = kD5BOff + 64 * 128;     // + 8 KB of packed B
 constexpr int kD5Stage = kD5SOff + 8 * 64 * 4;  // + 2 KB of scale dwords = 42 KB
-constexpr int kD5LdsBytes = kD5Stages * kD5Stage > 256 * 512 + 1024 ? kD5Stages * kD5Stage : 256 * 512 + 1024;
+constexpr int kD5LdsBytes = kD5Stages * kD5Stage > 256 * 512 + 2048 ? kD5Stages * kD5Stage : 256 * 512 + 2048;
 static_assert(kD5LdsBytes <= 160 * 1024, "gemm5 dgrad LDS budget");
 
 typedef __attribute__((ext_vector_type(2))) int af3_i32x2;
@@ -1768,6 +1784,7 @@ __device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
   float* const gl = (float*)(lds + RM * RB);
+  float* const al = gl + 256;  // per-row A scales
   auto coff = [&](int row, int col) { return row * RB + ((((col >> 3) ^ (((row >> 2) & 1) << 2))) << 4) + ((col & 7) << 1); };
   __syncthreads();
   for (int t = threadIdx.x; t < RM; t += 256) {
@@ -1777,6 +1794,7 @@ __device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f
       gv = p.gammas_f32 ? ((const float*)p.gammas)[gr] : af3_bf16_to_f32(((const uint16_t*)p.gammas)[gr]);
     }
     gl[t] = gv;
+    al[t] = t < nrows ? g4_ascale(p, row_lo + t) : 1.f;
   }
   float bv[TN];
 #pragma unroll
@@ -1792,13 +1810,17 @@ __device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f
       const int row0 = tm * 32 + j * 8 + lh * 4;
       const float4 g = *(const float4*)(gl + row0);
       const float gq[4] = {g.x, g.y, g.z, g.w};
+      const float4 a = *(const float4*)(al + row0);
+      const float aq[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn) {
         const int col = wn0 + 64 * (tn >> 1) + 2 * lr + (tn & 1);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          *(uint16_t*)(lds + coff(row0 + q, col)) =
-              (uint16_t)af3_f32_to_bf16((acc[tm][tn][j * 4 + q] + bv[tn]) * gq[q]);
+        for (int q = 0; q < 4; ++q) {
+          const float x = acc[tm][tn][j * 4 + q];
+          const float v = p.ascale ? (x * aq[q] + bv[tn]) * gq[q] : (x + bv[tn]) * gq[q];
+          *(uint16_t*)(lds + coff(row0 + q, col)) = (uint16_t)af3_f32_to_bf16(v);
+        }
       }
     }
   }
@@ -2409,7 +2431,7 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
                          const uint16_t* lora_b, int lora_r, const int32_t* token_offs, const int32_t* block_pid_map,
                          const int32_t* tile_offs, int max_tiles, int block_m, int tile_cfg, int n_expts, int N,
                          int K, uint16_t* y, int64_t ldy, int epi, void* glu, int64_t ld_glu, float alpha,
-                         float limit, void* stream_) {
+                         float limit, const float* a_row_scale, void* stream_) {
   hipStream_t stream = (hipStream_t)stream_;
   AF3_REQUIRE(N > 0 && K > 0 && n_expts > 0 && max_tiles >= 0, "moe_gemm: bad sizes N=%d K=%d E=%d", N, K, n_expts);
   if (max_tiles == 0) return 0;
@@ -2460,6 +2482,7 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
   p.N = N;
   p.epi = epi;
   p.glu = glu;
+  p.ascale = a_row_scale;
   p.ld_glu = ld_glu;
   p.alpha = alpha;
   p.limit = limit;
@@ -2503,6 +2526,13 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
     if (!ok) {
       af3::set_error("moe_gemm: the fused SwiGLU epilogue %d is not available for tile_cfg %d / these operands", epi,
                      cfg);
+      return AF3_EUNSUPPORTED;
+    }
+  }
+  if (a_row_scale) {
+    AF3_REQUIRE(lora_r == 0, "moe_gemm: a row scale cannot be combined with the LoRA extension segment");
+    if (!(cfg == 20 || cfg == 21 || cfg == 22 || cfg == 23)) {
+      af3::set_error("moe_gemm: the A row scale needs tile_cfg 20-23 (got %d)", cfg);
       return AF3_EUNSUPPORTED;
     }
   }
@@ -2571,7 +2601,23 @@ extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gathe
                             int K, uint16_t* y, int64_t ldy, void* stream) {
   return moe_gemm_impl(x, ldx, gather_indx, gather_div, w_blocks, w_scales, trans_w, bias, gammas, gammas_f32, lora_l,
                        ld_l, lora_b, lora_r, token_offs, block_pid_map, tile_offs, max_tiles, block_m, tile_cfg,
-                       n_expts, N, K, y, ldy, 0, nullptr, 0, 0.f, 0.f, stream);
+                       n_expts, N, K, y, ldy, 0, nullptr, 0, 0.f, 0.f, nullptr, stream);
+}
+
+// af3_moe_gemm with a per-row scale of the A operand applied to the
+// accumulator: y = bf16((acc * a_row_scale[a(r)] + bias) * gammas), a(r) the
+// A row of output row r.  The fp8 mode's per-token activation scale.
+// AF3_EUNSUPPORTED when the selected tile configuration has no such epilogue.
+extern "C" int af3_moe_gemm_rowscale(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
+                                     const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
+                                     const void* gammas, int gammas_f32, const int32_t* token_offs,
+                                     const int32_t* block_pid_map, const int32_t* tile_offs, int max_tiles,
+                                     int block_m, int tile_cfg, int n_expts, int N, int K, uint16_t* y, int64_t ldy,
+                                     const float* a_row_scale, void* stream) {
+  AF3_REQUIRE(a_row_scale, "moe_gemm_rowscale: null row scale");
+  return moe_gemm_impl(x, ldx, gather_indx, gather_div, w_blocks, w_scales, trans_w, bias, gammas, gammas_f32, nullptr,
+                       0, nullptr, 0, token_offs, block_pid_map, tile_offs, max_tiles, block_m, tile_cfg, n_expts, N,
+                       K, y, ldy, 0, nullptr, 0, 0.f, 0.f, a_row_scale, stream);
 }
 
 // af3_moe_gemm with the gpt-oss clamped SwiGLU fused into the epilogue
@@ -2589,7 +2635,7 @@ extern "C" int af3_moe_gemm_swiglu(const uint16_t* x, int64_t ldx, const int32_t
   AF3_REQUIRE(epi == 1 || epi == 2, "moe_gemm_swiglu: epi must be 1 or 2 (got %d)", epi);
   return moe_gemm_impl(x, ldx, gather_indx, gather_div, w_blocks, w_scales, trans_w, bias, gammas, gammas_f32, lora_l,
                        ld_l, lora_b, lora_r, token_offs, block_pid_map, tile_offs, max_tiles, block_m, tile_cfg,
-                       n_expts, N, K, y, ldy, epi, glu, ld_glu, alpha, limit, stream);
+                       n_expts, N, K, y, ldy, epi, glu, ld_glu, alpha, limit, nullptr, stream);
 }
 
 // Skinny per-expert row product for the LoRA terms (BM = 128 map):

@@ -135,6 +135,41 @@ int af3_moe_gemm_swiglu(const uint16_t* x, int64_t ldx, const int32_t* gather_in
                         uint16_t* y, int64_t ldy, int epi, void* glu, int64_t ld_glu, float alpha, float limit,
                         void* stream);
 
+/* af3_moe_gemm (no LoRA segment) with a per-row scale of the A operand on
+ * the accumulator: y = bf16((acc * a_row_scale[a(r)] + bias[e][n]) * gammas[r]),
+ * a(r) the A row of output row r (a_row_scale has one fp32 per row of x).
+ * Replaces matmul_ogs with PrecisionConfig(lhs InFlexData(scale,
+ * scale_mode="per_token")) in the fp8 mode, quantization.py:338-356 (forward)
+ * and 382-408 (dX), fed with the E4M3 codes' values as bf16.  Returns
+ * AF3_EUNSUPPORTED (-2) when the selected tile configuration has no scaled
+ * epilogue (only the default kernels, tile_cfg 20-23, have one). */
+int af3_moe_gemm_rowscale(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
+                          const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
+                          const void* gammas, int gammas_f32, const int32_t* token_offs, const int32_t* block_pid_map,
+                          const int32_t* tile_offs, int max_tiles, int block_m, int tile_cfg, int n_expts, int N,
+                          int K, uint16_t* y, int64_t ldy, const float* a_row_scale, void* stream);
+
+/* MXFP4 -> fp8 E5M2, row-major.  Replaces kernels.py:20-108
+ * (mxfp4_to_fp8_e5m2_triton): blocks [n_groups][16], scales [n_groups] ->
+ * out [n_groups][32] bytes, bit-exact with the reference's int32 rule and its
+ * uint16 (lo | hi << 8) stores, also for scale bytes outside the format. */
+int af3_mxfp4_to_fp8_e5m2(const uint8_t* blocks, const uint8_t* scales, uint8_t* out, int64_t n_groups,
+                          void* stream);
+
+/* MXFP4 [E][N][G][16] -> fp8 E5M2 [E][G*32][N] (N contiguous).  Replaces
+ * kernels.py:238-312 (mxfp4_to_fp8_e5m2_colmajor), each value truncated to a
+ * byte as its stores do. */
+int af3_mxfp4_to_fp8_e5m2_colmajor(const uint8_t* blocks, const uint8_t* scales, uint8_t* out, int E, int N, int G,
+                                   void* stream);
+
+/* Per-token dynamic quantization to fp8 E4M3FN.  Replaces kernels.py:319-388
+ * (dynamic_quantize_per_token): x [M][ldx] bf16 -> out [M][ld_out] codes and
+ * scale [M] fp32 = max(row amax, 1e-12) / 448; codes = E4M3(x * (1 / scale)),
+ * round to nearest even, saturating at 448 (IEEE division for both quotients).
+ * out_bf16 (optional, [M][ld_bf16]) receives the codes' values as bf16. */
+int af3_quantize_per_token_e4m3(const uint16_t* x, int64_t ldx, int64_t M, int K, uint8_t* out, int64_t ld_out,
+                                float* scale, uint16_t* out_bf16, int64_t ld_bf16, void* stream);
+
 /* Scatter-sum over each token's K expert rows (the k-reduction matmul_ogs
  * performs for scatter_indx, quantization.py:532-541 and 409-418):
  * out[t] = bf16(sum_j rows[src_indx[t*K+j]]) in fp32; -1 entries skipped. */

@@ -166,7 +166,7 @@ def test_dequant_matmul_function_without_module(dev):
     assert _rel(x.grad, moe.combine(dxr, rt["gate_indx"], 4)) < 1e-2
     with pytest.raises(NotImplementedError):
         Q.DequantMoEMatmul.apply(x, inp.gu_blocks.to(dev), inp.gu_scales.to(dev), None, rd, gi, None, None, None,
-                                 si, None, "fp8", 4, None, None)
+                                 si, None, "fp4", 4, None, None)
 
 
 @pytest.mark.parametrize("lora", [False, True])
