@@ -283,6 +283,55 @@ def moe_combine(rows, scatter_indx, n_expts_act):
     return out
 
 
+def moe_rows_f8(codes, a_row_scale, blocks, scales, bias, routing_data, gather_indx=None, gammas=None):
+    """Forward rows of the fp8 mode on the block-scaled MFMA: per-token E4M3
+    ``codes`` [Tx, K] (float8_e4m3fn, rows 16-byte aligned) times the MXFP4
+    weights, ``(acc * a_row_scale[a(r)] + bias[e]) * gammas`` in bf16.  None
+    when the kernel's requirements do not hold (the caller then runs the
+    bf16-operand form of the same arithmetic)."""
+    dev = codes.device
+    E, N, K = _weight_dims(blocks, False)
+    if codes.shape[-1] != K:
+        raise ValueError(f"codes have {codes.shape[-1]} columns, weight reduction dim is {K}")
+    g = _gather_ptr(gather_indx)
+    R = g.shape[0] if g is not None else codes.shape[0]
+    routing_data, k_act = _expt_data(routing_data, R, dev)
+    ed = routing_data.expt_data
+    bm = 256
+    pid_map = getattr(ed, "gemm_order", {}).get(bm) if GEMM_TILE.get("order", True) else None
+    if pid_map is None:
+        pid_map = ed.block_pid_map[bm]
+    y = torch.empty(R, N, dtype=torch.bfloat16, device=dev)
+    if R == 0 or pid_map.numel() == 0:
+        return y
+    ld = codes.stride(0) if codes.shape[0] > 1 else K
+    if codes.stride(-1) != 1 or ld % 16 or codes.data_ptr() % 16 or K % 64 or GEMM_TILE["tile_cfg"] not in (0, 22):
+        return None
+    blocks = blocks if blocks.data_ptr() % 16 == 0 else blocks.clone()
+    b = bias.to(torch.float32).contiguous() if bias is not None else None
+    gm, gm_f32 = None, 0
+    if gammas is not None:
+        gm, gm_f32 = (gammas.contiguous(), 1) if gammas.dtype == torch.float32 else (
+            gammas.to(torch.bfloat16).contiguous(), 0)
+    s = a_row_scale.to(torch.float32).contiguous()
+
+    def launch():
+        return _capi.try_call("af3_moe_gemm_f8", codes.data_ptr(), ld, _capi.ptr(g),
+                              k_act if g is not None else 1, blocks.data_ptr(), scales.data_ptr(), _capi.ptr(b),
+                              _capi.ptr(gm), gm_f32, ed.token_offs_raw.data_ptr(), pid_map.data_ptr(),
+                              ed.token_offs_pad[bm].data_ptr(), pid_map.numel(), bm, 0, E, N, K, y.data_ptr(), N,
+                              s.data_ptr(), _capi.stream_of(dev))
+    if KERNEL_TIMER is None:
+        ok = launch()
+    else:
+        with KERNEL_TIMER("moe_gemm_fwd_f8", 2 * R * N * K):
+            ok = launch()
+    return y if ok else None
+
+
+FP8_BLOCK_SCALED = True  # fp8-mode forward on the block-scaled MFMA (else: E4M3 values as bf16 operands)
+
+
 def matmul_ogs(x, w_blocks_scales, bias, routing_data=None, gather_indx=None, scatter_indx=None, gammas=None,
                trans_w=False, a_row_scale=None):
     """matmul_ogs semantics over MXFP4 weights: rows, then the scatter-sum if any.
@@ -318,9 +367,16 @@ class DequantMoEMatmul(torch.autograd.Function):
             if dequant_dtype == "fp8":
                 # quantization.py:332-357: per-token E4M3 activations x MXFP4 weights (their E5M2
                 # form has the same values), fp32 accumulation scaled per row, bf16 out
-                _, xs, xq = kernels.quantize_per_token_e4m3(x.to(torch.bfloat16), with_bf16=True)
-                out = matmul_ogs(xq, (blocks, scales), bias, routing_data, fwd_gather_indx, fwd_scatter_indx,
-                                 fwd_gammas, trans_w=False, a_row_scale=xs)
+                y = None
+                if FP8_BLOCK_SCALED:
+                    xc, xs = kernels.quantize_per_token_e4m3(x.to(torch.bfloat16))
+                    y = moe_rows_f8(xc, xs, blocks, scales, bias, routing_data, fwd_gather_indx, fwd_gammas)
+                if y is None:
+                    _, xs, xq = kernels.quantize_per_token_e4m3(x.to(torch.bfloat16), with_bf16=True)
+                    y = moe_rows(xq, blocks, scales, bias, routing_data, fwd_gather_indx, fwd_gammas, False,
+                                 a_row_scale=xs)
+                k = routing_data.n_expts_act if routing_data is not None else 1
+                out = y if fwd_scatter_indx is None else moe_combine(y, fwd_scatter_indx, k)
             else:
                 out = matmul_ogs(x, (blocks, scales), bias, routing_data, fwd_gather_indx, fwd_scatter_indx,
                                  fwd_gammas, trans_w=False)

@@ -1348,6 +1348,162 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm4_fwd_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------
+// fp8-mode forward: A = per-token E4M3 codes [rows][K] bytes, B = the packed
+// MXFP4 weights fed to the block-scaled MFMA v_mfma_scale_f32_32x32x64_f8f6f4
+// (A format E4M3 with block scale 2^0, B format E2M1 with the group's e8m0
+// byte), so the weights are never converted: one 16-byte MXFP4 group is the B
+// operand of a lane (lanes 32 h + n hold weight row n, k block h of the
+// 64-deep step).  The A operand of lane 32 h + r holds row r's k 16 h .. 16 h
+// + 15 in bytes 0-15 and k 32 + 16 h .. in bytes 16-31 (measured on gfx950).
+// The per-token scale multiplies the fp32 accumulator in the epilogue.
+// Same work items, ring and epilogue as g4f_tile (8 waves of 128 x 64).
+// ---------------------------------------------------------------------------
+typedef __attribute__((ext_vector_type(8))) int af3_i32x8;
+
+__device__ __forceinline__ int f8_chunk(int row, int c) { return c ^ ((row >> 2) & 3); }  // physical 16-B chunk
+
+template <bool NARROW>
+__device__ __forceinline__ void g4f8_tile(const Params& p, uint8_t* lds, int e, int row_lo, int nrows, int n0,
+                                          int ncols) {
+  constexpr int WM = 2, WN = 4, NW = 8, NT = 512;
+  constexpr int RM = NARROW ? 128 : kG4Rows, CN = NARROW ? 512 : kG4Rows;
+  constexpr int WMX = NARROW ? 1 : WM, WNX = NARROW ? NW : WN;
+  constexpr int TM = RM / WMX / 32, TN = CN / WNX / 32;
+  constexpr int ASTAGE = RM * kBK;  // bytes per A stage (1 byte per code)
+  constexpr int BSTAGE = CN * 32;   // bytes per packed-B stage
+  constexpr int API = RM / 16 / NW, BPI = CN / 32 / NW, DPW = API + BPI;  // copies per wave per k-step
+  static_assert(API >= 1 && BPI >= 1 && (DPW == 3), "copy schedule");
+  uint8_t* const As = lds;
+  uint8_t* const Bs = lds + kG4Stages * ASTAGE;
+  uint8_t* const Ss = Bs + kG4Stages * BSTAGE;  // [ncols][G] scale bytes
+  const int G = p.K >> 5;
+  const int nk = p.K / kBK;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = lane & 31, lh = lane >> 5;
+  const int wm0 = (wave / WNX) * (32 * TM), wn0 = (wave % WNX) * (32 * TN);
+  const int tm_live = min(TM, max(0, (nrows - wm0 + 31) >> 5));
+  const int tn_live = min(TN, max(0, (ncols - wn0 + 31) >> 5));
+
+  // A copies: 16 rows x 64 bytes each
+  const uint8_t* arow[API];
+#pragma unroll
+  for (int i = 0; i < API; ++i) {
+    const int row = (wave * API + i) * 16 + (lane >> 2);
+    int64_t src = row_lo + (row < nrows ? row : 0);
+    if (p.a.gather) src = p.a.gather[src] / p.a.gdiv;
+    arow[i] = (const uint8_t*)p.a.ptr + src * p.a.ld + (f8_chunk(row, lane & 3) << 4);
+  }
+  const uint8_t* bsrc[BPI];
+#pragma unroll
+  for (int j = 0; j < BPI; ++j) {
+    const int row4 = (wave * BPI + j) * 8 + (lane >> 3);
+    const int lc = (lane & 7) ^ (((row4 >> 1) & 1) << 2);
+    int nn = row4 * 4 + (lc & 3);
+    if (nn >= ncols) nn = 0;
+    bsrc[j] = (const uint8_t*)p.b.ptr + e * p.b.estride + (int64_t)(n0 + nn) * p.b.ld + (lc >> 2) * 16;
+  }
+  {
+    const uint8_t* sbase = p.b.scales + e * p.b.sestride + (int64_t)n0 * G;
+    const int nbytes = ncols * G;
+    const int ninstr = (nbytes + 1023) >> 10;
+    for (int i = wave; i < ninstr; i += NW) {
+      const int off = i * 1024 + lane * 16;
+      g4_dma16(sbase + (off < nbytes ? off : 0), __builtin_amdgcn_readfirstlane(lds_addr(Ss)) + (uint32_t)(i * 1024));
+    }
+  }
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+  auto issue_one = [&](int kt, int j) {
+    const int st = kt % kG4Stages;
+    if (j < API)
+      g4_dma16(arow[j] + kt * kBK, lds0 + (uint32_t)(st * ASTAGE + (wave * API + j) * 1024));
+    else
+      g4_dma16(bsrc[j - API] + kt * 32,
+               lds0 + (uint32_t)(kG4Stages * ASTAGE + st * BSTAGE + (wave * BPI + j - API) * 1024));
+  };
+  af3_f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+#pragma unroll
+  for (int j = 0; j < DPW; ++j) issue_one(0, j);
+  if (nk > 1) {
+#pragma unroll
+    for (int j = 0; j < DPW; ++j) issue_one(1, j);
+  }
+  AF3_ASM_WAIT_VM(0);
+  AF3_ASM_BARRIER();
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt > 0) {
+      if (kt + 1 < nk)
+        AF3_ASM_WAIT_VM(3);
+      else
+        AF3_ASM_WAIT_VM(0);
+      AF3_ASM_LDS_BARRIER();
+    }
+    const int st = kt % kG4Stages;
+    const uint8_t* as = As + st * ASTAGE;
+    const uint8_t* bs = Bs + st * BSTAGE;
+    af3_i32x8 af[TM], bfr[TN];
+    int sc[TN];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int n = wn0 + tn * 32 + lr;
+      const af3_u32x4 b4 = (tn < tn_live) ? *(const af3_u32x4*)(bs + g4_b_off(n, lh)) : zero4();
+      bfr[tn] = af3_i32x8{(int)b4[0], (int)b4[1], (int)b4[2], (int)b4[3], 0, 0, 0, 0};
+      sc[tn] = (tn < tn_live) ? (int)Ss[n * G + 2 * kt + lh] : 127;
+    }
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+      if (tm < tm_live) {
+        const int row = wm0 + tm * 32 + lr;
+        const af3_u32x4 lo = *(const af3_u32x4*)(as + row * 64 + (f8_chunk(row, lh) << 4));
+        const af3_u32x4 hi = *(const af3_u32x4*)(as + row * 64 + (f8_chunk(row, 2 + lh) << 4));
+        af[tm] = af3_i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2],
+                           (int)hi[3]};
+      } else {
+        af[tm] = af3_i32x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    }
+    if (kt + 2 < nk) {
+#pragma unroll
+      for (int j = 0; j < DPW; ++j) issue_one(kt + 2, j);
+    }
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+        if (tm < tm_live && tn < tn_live)
+          acc[tm][tn] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[tm], bfr[tn], acc[tm][tn], 0, 4, 0, 127, 0,
+                                                                         sc[tn]);
+  }
+  g4_epilogue<false, TM, TN, NT, CN>(p, lds, acc, e, row_lo, nrows, n0, ncols, wm0, wn0);
+}
+
+template <int BXK>
+__global__ __launch_bounds__(512) void gemm4_fwd_f8_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kG4LdsBytes];
+  int mt, nt;
+  if (!g4_work_item(p, mt, nt)) return;
+  const int32_t ent = p.tile_map[mt];
+  if (ent < 0) return;
+  const int e = ent & 0xFFFF, blk = ent >> 16;
+  const int row_lo = p.offs[e] + blk * kG4Rows;
+  const int nrows = min(kG4Rows, p.offs[e + 1] - row_lo);
+  if (nrows <= 0) return;
+  const int n0 = nt * kG4Rows;
+  if (nrows <= 128 && (p.K >> 5) <= kG4NarrowMaxG) {
+    if (nt & 1) return;
+    g4f8_tile<true>(p, lds, e, row_lo, nrows, n0, min(512, p.N - n0));
+    return;
+  }
+  g4f8_tile<false>(p, lds, e, row_lo, nrows, n0, min(kG4Rows, p.N - n0));
+}
+
+// ---------------------------------------------------------------------------
 // gemm4 dgrad: grouped GEMM through MXFP4 weights packed along the OUTPUT
 // axis, W[e][k][n/32][16] with scales [e][k][n/32] (the input-gradient
 // products dX = dY . W of quantization.py:409-418).  Same block / wave tiling,
@@ -2431,7 +2587,7 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
                          const uint16_t* lora_b, int lora_r, const int32_t* token_offs, const int32_t* block_pid_map,
                          const int32_t* tile_offs, int max_tiles, int block_m, int tile_cfg, int n_expts, int N,
                          int K, uint16_t* y, int64_t ldy, int epi, void* glu, int64_t ld_glu, float alpha,
-                         float limit, const float* a_row_scale, void* stream_) {
+                         float limit, const float* a_row_scale, void* stream_, int a_fp8 = 0) {
   hipStream_t stream = (hipStream_t)stream_;
   AF3_REQUIRE(N > 0 && K > 0 && n_expts > 0 && max_tiles >= 0, "moe_gemm: bad sizes N=%d K=%d E=%d", N, K, n_expts);
   if (max_tiles == 0) return 0;
@@ -2517,6 +2673,18 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
           ? block_m == 256
           : block_m == 128;
   AF3_REQUIRE(bm_ok, "moe_gemm: tile_cfg %d does not match block_m %d", cfg, block_m);
+  if (a_fp8) {  // E4M3 activations x MXFP4 weights on the block-scaled MFMA (forward, 256-row map)
+    if (trans || block_m != 256 || K % kBK != 0 || K / 32 > kG4MaxG || !al16(w_scales) || !al16(y) || ldy % 8 != 0 ||
+        ldx % 16 != 0 || !al16(x) || !a_row_scale || lora_r != 0 || epi != 0 || !(cfg == 22 || cfg == 0)) {
+      af3::set_error("moe_gemm_f8: needs trans_w 0, block_m 256, K %% 64 == 0, 16-byte aligned rows, a row scale");
+      return AF3_EUNSUPPORTED;
+    }
+    p.group_m = group_m;
+    p.n_nblk = (N + kG4Rows - 1) / kG4Rows;
+    dim3 grid(g4_grid(max_tiles, p.n_nblk, p.group_m));
+    hipLaunchKernelGGL((gemm4_fwd_f8_kernel<NONE>), grid, dim3(512), 0, stream, p);
+    return af3::check_launch("moe_gemm_f8");
+  }
   if (K % kBK != 0) cfg = 9;  // direct A loads need whole 64-deep k-steps
   if (epi != 0) {
     AF3_REQUIRE(glu && (epi == 1 || epi == 2), "moe_gemm: bad SwiGLU epilogue %d", epi);
@@ -2602,6 +2770,21 @@ extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gathe
   return moe_gemm_impl(x, ldx, gather_indx, gather_div, w_blocks, w_scales, trans_w, bias, gammas, gammas_f32, lora_l,
                        ld_l, lora_b, lora_r, token_offs, block_pid_map, tile_offs, max_tiles, block_m, tile_cfg,
                        n_expts, N, K, y, ldy, 0, nullptr, 0, 0.f, 0.f, nullptr, stream);
+}
+
+// fp8-mode forward: A = per-token E4M3 codes [rows][ldx bytes] (ldx % 16 == 0),
+// y = bf16((acc * a_row_scale[a(r)] + bias) * gammas) with acc the fp32 sum of
+// E4M3 codes x MXFP4 weights on the block-scaled MFMA.  trans_w 0, block_m
+// 256, no LoRA; AF3_EUNSUPPORTED when a requirement fails.
+extern "C" int af3_moe_gemm_f8(const uint8_t* x_e4m3, int64_t ldx, const int32_t* gather_indx, int gather_div,
+                               const uint8_t* w_blocks, const uint8_t* w_scales, const float* bias, const void* gammas,
+                               int gammas_f32, const int32_t* token_offs, const int32_t* block_pid_map,
+                               const int32_t* tile_offs, int max_tiles, int block_m, int tile_cfg, int n_expts, int N,
+                               int K, uint16_t* y, int64_t ldy, const float* a_row_scale, void* stream) {
+  AF3_REQUIRE(a_row_scale, "moe_gemm_f8: null row scale");
+  return moe_gemm_impl((const uint16_t*)x_e4m3, ldx, gather_indx, gather_div, w_blocks, w_scales, 0, bias, gammas,
+                       gammas_f32, nullptr, 0, nullptr, 0, token_offs, block_pid_map, tile_offs, max_tiles, block_m,
+                       tile_cfg, n_expts, N, K, y, ldy, 0, nullptr, 0, 0.f, 0.f, a_row_scale, stream, 1);
 }
 
 // af3_moe_gemm with a per-row scale of the A operand applied to the

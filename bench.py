@@ -92,7 +92,9 @@ def _graph_us(torch, fn, sets, reps):
         g.replay()
     e.record()
     torch.cuda.synchronize()
-    same = all(torch.equal(a, b) for a, b in zip(eager, outs))
+    def bits(t):
+        return t.view(torch.uint8) if t.dtype in (torch.float8_e4m3fn, torch.float8_e5m2) else t
+    same = all(torch.equal(bits(a), bits(b)) for a, b in zip(eager, outs))
     if not same:
         raise RuntimeError("graph replay output differs from the eager call")
     del g, outs, eager
@@ -129,6 +131,54 @@ def bandwidth_extras(torch, dev, kernels, workloads, reps=50):
     rec("swiglu_bwd_cfg1",
         _graph_us(torch, lambda g, d: kernels.swiglu_backward_raw(d, g, 1.702, 7.0), sets, reps),
         M * N * 2 + M * N2 * 2 + M * N2 * 2)
+    return res
+
+
+def fp8_extras(torch, dev, kernels, workloads, inp_cpu, k, steps=10, reps=20):
+    """fp8 dequant mode (the reference's dequant_dtype="fp8"): standalone E5M2
+    dequant and per-token E4M3 quantization bandwidths, and the cfg layer
+    without expert LoRA (bf16-only) timed in fp8 and in bf16 mode."""
+    import dataclasses
+    from agent_factory_3_amd import routing
+    res = {}
+    blocks, scales = workloads.cfg0()
+    sets = [(blocks.to(dev), scales.to(dev)) for _ in range(8)]
+    byts = 8294400 + 518400 + 16588800
+    us = _graph_us(torch, kernels.mxfp4_to_fp8_e5m2, sets, reps)
+    res["e5m2_dequant_cfg0"] = {"us": us, "GBps": byts / (us * 1e-6) / 1e9,
+                                "frac_hbm_peak": byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+    del sets
+    x = inp_cpu.x.to(dev)
+    M, K = x.shape
+    sets = [(x,), (x.clone(),)]
+    byts = M * K * 2 + M * K + M * 4
+    us = _graph_us(torch, lambda t: kernels.quantize_per_token_e4m3(t)[0], sets, reps)
+    res["quant_e4m3_per_token"] = {"shape": [M, K], "us": us, "GBps": byts / (us * 1e-6) / 1e9,
+                                   "frac_hbm_peak": byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+    del sets
+    inp_nl = dataclasses.replace(inp_cpu, lora=None)
+    inp = inp_nl.to(dev)
+    for mode in ("fp8", "bf16"):
+        m = workloads.make_experts(inp_nl, dev)
+        m.dequant_dtype = mode
+
+        def step():
+            rd, gi, si = routing.routing_replay(inp.logits, inp.expt_indx, k)
+            xx = inp.x.detach().requires_grad_(True)
+            m(xx, rd, gi, si).backward(inp.dy)
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            step()
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / steps
+        res[f"layer_no_lora_{mode}"] = {"ms_per_step": ms, "tokens_per_s": M / (ms * 1e-3)}
+        del m
     return res
 
 
@@ -247,6 +297,8 @@ def main():
     if not args.no_extras:
         log("standalone dequant / SwiGLU bandwidth")
         extra.update(bandwidth_extras(torch, dev, kernels, workloads))
+        log("fp8 mode")
+        extra["fp8_mode"] = fp8_extras(torch, dev, kernels, workloads, inp_cpu, k)
 
     cpu = None
     if not args.no_cpu_baseline and int(os.environ.get("RANK", "0")) == 0:

@@ -78,7 +78,17 @@ def _fp8_rows(x, W, offs, gather, k, trans, bias=None, gammas=None):
     return y.to(torch.bfloat16)
 
 
-def test_dequant_moe_matmul_fp8(dev):
+@pytest.mark.parametrize("block_scaled", [True, False])
+def test_dequant_moe_matmul_fp8(dev, block_scaled):
+    old = Q.FP8_BLOCK_SCALED
+    Q.FP8_BLOCK_SCALED = block_scaled
+    try:
+        _dequant_moe_matmul_fp8(dev)
+    finally:
+        Q.FP8_BLOCK_SCALED = old
+
+
+def _dequant_moe_matmul_fp8(dev):
     g = torch.Generator().manual_seed(5)
     T, E, H, N, k = 300, 6, 256, 320, 4
     x = torch.randn(T, H, generator=g).to(torch.bfloat16)
@@ -107,3 +117,33 @@ def test_dequant_moe_matmul_fp8(dev):
     y16 = Q.DequantMoEMatmul.apply(x.to(dev), blocks.to(dev), scales.to(dev), bias.float().to(dev), rd, gi, None,
                                    None, None, si, None, "bf16", k, None, None)
     assert not torch.equal(y16, y)
+
+
+@pytest.mark.parametrize("gather,odd", [(True, False), (False, False), (True, True)])
+def test_block_scaled_forward_tiles(dev, gather, odd):
+    """The block-scaled fp8 forward kernel on full, partial, <= 128-row (two
+    n-tiles per work item) and idle-expert tiles, ten k-steps, N = 576; with
+    ``odd`` also e8m0 bytes 0, 1, 254, 255 (the MFMA applies them as powers of
+    two where the reference's E5M2 bytes flush or wrap: checked for finiteness
+    and against the oracle outside those blocks)."""
+    from test_gpu_gemm_tiles import KRED, NOUT, T, TOPK, _routing, _weights
+    g, ref, rd, gi = _routing(dev, 21)
+    blocks, scales = _weights(g, NOUT, KRED, odd)
+    Rr = T * TOPK
+    x = torch.randn(T if gather else Rr, KRED, generator=g).to(torch.bfloat16)
+    bias = (torch.randn(blocks.shape[0], NOUT, generator=g) * 0.1).to(torch.bfloat16)
+    codes, s = kernels.quantize_per_token_e4m3(x.to(dev))
+    y = Q.moe_rows_f8(codes, s, blocks.to(dev), scales.to(dev), bias.float().to(dev), rd, gi if gather else None)
+    assert y is not None and y.shape == (Rr, NOUT)
+    W = mxfp4.dequant_f32(blocks, scales)
+    yr = _fp8_rows(x, W, ref["offs"], ref["topk_indx"] if gather else None, TOPK, False, bias=bias)
+    a, b = y.float().cpu().double(), yr.double()
+    skip = torch.zeros(a.shape, dtype=torch.bool)
+    if odd:   # output columns whose weight row holds a scale byte outside [2, 252] (see the docstring)
+        bad_rows = ((scales < 2) | (scales > 252)).any(dim=2)          # [E, N]
+        e_of = torch.repeat_interleave(torch.arange(len(ref["offs"]) - 1), (ref["offs"][1:] - ref["offs"][:-1]).long())
+        skip = bad_rows[e_of]
+        assert skip.any() and not skip.all()
+    assert torch.isfinite(a[~skip]).all()
+    ok = ((a - b).abs() <= 1e-2 + 2e-2 * b.abs()) | skip
+    assert ok.all(), float((~ok).float().mean())
