@@ -1428,27 +1428,11 @@ __device__ __forceinline__ void g4f8_tile(const Params& p, uint8_t* lds, int e, 
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-#pragma unroll
-  for (int j = 0; j < DPW; ++j) issue_one(0, j);
-  if (nk > 1) {
-#pragma unroll
-    for (int j = 0; j < DPW; ++j) issue_one(1, j);
-  }
-  AF3_ASM_WAIT_VM(0);
-  AF3_ASM_BARRIER();
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt > 0) {
-      if (kt + 1 < nk)
-        AF3_ASM_WAIT_VM(3);
-      else
-        AF3_ASM_WAIT_VM(0);
-      AF3_ASM_LDS_BARRIER();
-    }
+  // fragments of k-step kt from its stage (A: two 16-byte chunks per row, B: one MXFP4 group)
+  auto read_frags = [&](int kt, af3_i32x8 (&af)[TM], af3_i32x8 (&bfr)[TN], int (&sc)[TN]) {
     const int st = kt % kG4Stages;
     const uint8_t* as = As + st * ASTAGE;
     const uint8_t* bs = Bs + st * BSTAGE;
-    af3_i32x8 af[TM], bfr[TN];
-    int sc[TN];
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) {
       const int n = wn0 + tn * 32 + lr;
@@ -1468,10 +1452,8 @@ __device__ __forceinline__ void g4f8_tile(const Params& p, uint8_t* lds, int e, 
         af[tm] = af3_i32x8{0, 0, 0, 0, 0, 0, 0, 0};
       }
     }
-    if (kt + 2 < nk) {
-#pragma unroll
-      for (int j = 0; j < DPW; ++j) issue_one(kt + 2, j);
-    }
+  };
+  auto mfmas = [&](const af3_i32x8 (&af)[TM], const af3_i32x8 (&bfr)[TN], const int (&sc)[TN]) {
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
@@ -1479,7 +1461,57 @@ __device__ __forceinline__ void g4f8_tile(const Params& p, uint8_t* lds, int e, 
         if (tm < tm_live && tn < tn_live)
           acc[tm][tn] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[tm], bfr[tn], acc[tm][tn], 0, 4, 0, 127, 0,
                                                                          sc[tn]);
+  };
+  // three stages in flight: k-steps 0, 1, 2; the fragments of a k-step are read
+  // one k-step early (right after its stage is published) and its slot is
+  // refilled (k-step + 3) as soon as they are read
+#pragma unroll
+  for (int j = 0; j < DPW; ++j) issue_one(0, j);
+  if (nk > 1) {
+#pragma unroll
+    for (int j = 0; j < DPW; ++j) issue_one(1, j);
   }
+  if (nk > 2) {
+#pragma unroll
+    for (int j = 0; j < DPW; ++j) issue_one(2, j);
+  }
+  // stage 0 in: every wave waits for its own copies of k-step 0 (<= two later k-steps outstanding)
+  if (nk > 2)
+    AF3_ASM_WAIT_VM(6);
+  else if (nk > 1)
+    AF3_ASM_WAIT_VM(3);
+  else
+    AF3_ASM_WAIT_VM(0);
+  AF3_ASM_LDS_BARRIER();
+  af3_i32x8 afA[TM], bfA[TN], afB[TM], bfB[TN];
+  int scA[TN], scB[TN];
+  read_frags(0, afA, bfA, scA);
+  // k-step kt: fragments of kt in (af, bf); publish stage kt + 1, read its fragments
+  // into the other buffer, refill slot kt % 3 with k-step kt + 3, then kt's MFMAs
+  auto step = [&](int kt, af3_i32x8 (&af)[TM], af3_i32x8 (&bfr)[TN], int (&sc)[TN], af3_i32x8 (&afn)[TM],
+                  af3_i32x8 (&bfn)[TN], int (&scn)[TN]) {
+    if (kt + 1 < nk) {
+      // copies outstanding after k-step kt + 1's: those of kt + 2 (if issued)
+      if (kt + 2 < nk)
+        AF3_ASM_WAIT_VM(3);
+      else
+        AF3_ASM_WAIT_VM(0);
+      AF3_ASM_LDS_BARRIER();  // also: every wave has its k-step kt fragments (slot kt % 3 is free)
+      read_frags(kt + 1, afn, bfn, scn);
+      if (kt + 3 < nk) {
+#pragma unroll
+        for (int j = 0; j < DPW; ++j) issue_one(kt + 3, j);
+      }
+    }
+    mfmas(af, bfr, sc);
+  };
+  int kt = 0;
+#pragma nounroll
+  for (; kt + 1 < nk; kt += 2) {
+    step(kt, afA, bfA, scA, afB, bfB, scB);
+    step(kt + 1, afB, bfB, scB, afA, bfA, scA);
+  }
+  if (kt < nk) step(kt, afA, bfA, scA, afB, bfB, scB);
   g4_epilogue<false, TM, TN, NT, CN>(p, lds, acc, e, row_lo, nrows, n0, ncols, wm0, wn0);
 }
 
