@@ -15,6 +15,8 @@ this module                              reference (kernels.py)
 ``mxfp4_to_fp8_e5m2``                    ``mxfp4_to_fp8_e5m2_triton`` 20-108
 ``mxfp4_to_fp8_e5m2_colmajor``           ``mxfp4_to_fp8_e5m2_colmajor`` 238-312
 ``dynamic_quantize_per_token``           ``dynamic_quantize_per_token`` 319-388
+``mxfp4_lora_merge``                     (new: expert-LoRA merge for weight sync,
+                                         arithmetic of model_trainer.py:710-712)
 =======================================  =====================================
 
 The reference's names are provided as aliases so code that imports them keeps
@@ -166,6 +168,39 @@ def mxfp4_to_fp8_e5m2_colmajor(blocks: torch.Tensor, scales: torch.Tensor) -> to
     _capi.call("af3_mxfp4_to_fp8_e5m2_colmajor", blocks.contiguous().data_ptr(), scales.contiguous().data_ptr(),
                out.data_ptr(), E, N, G, _capi.stream_of(blocks.device))
     return out.view(torch.float8_e5m2)
+
+
+def mxfp4_lora_merge(blocks: torch.Tensor, scales: torch.Tensor, lora_A: torch.Tensor, lora_B: torch.Tensor,
+                     scaling: float, layout: str = "hf") -> torch.Tensor:
+    """bf16 expert weights with the LoRA delta folded in:
+    ``W'[e] = bf16(float(deq(W[e])) + scaling * (B[e] @ A[e]))`` in fp32.
+
+    blocks [E, N, G, 16] u8, scales [E, N, G] u8, lora_A [E, r, 32 G] bf16,
+    lora_B [E, N, r] bf16.  ``layout="hf"`` returns [E, K, N] (transformers'
+    GptOssExperts parameter layout), ``"rows"`` [E, N, K].
+    """
+    _need_cuda(blocks, "blocks")
+    if blocks.dim() != 4 or blocks.shape[-1] != 16:
+        raise ValueError(f"blocks must be [E, N, G, 16], got {tuple(blocks.shape)}")
+    E, N, G, _ = blocks.shape
+    K = 32 * G
+    r = lora_A.shape[1] if lora_A.dim() == 3 else -1
+    if tuple(scales.shape) != (E, N, G):
+        raise ValueError(f"scales must be [{E}, {N}, {G}], got {tuple(scales.shape)}")
+    if tuple(lora_A.shape) != (E, r, K) or tuple(lora_B.shape) != (E, N, r):
+        raise ValueError(f"lora_A must be [E, r, {K}] and lora_B [E, {N}, r], got "
+                         f"{tuple(lora_A.shape)} / {tuple(lora_B.shape)}")
+    if lora_A.dtype != torch.bfloat16 or lora_B.dtype != torch.bfloat16:
+        raise TypeError("LoRA factors must be bfloat16")
+    if layout not in ("hf", "rows"):
+        raise ValueError("layout must be 'hf' ([E, K, N]) or 'rows' ([E, N, K])")
+    shape = (E, K, N) if layout == "hf" else (E, N, K)
+    out = torch.empty(shape, dtype=torch.bfloat16, device=blocks.device)
+    a, b = lora_A.contiguous(), lora_B.contiguous()
+    _capi.call("af3_mxfp4_lora_merge", blocks.contiguous().data_ptr(), scales.contiguous().data_ptr(),
+               a.data_ptr(), b.data_ptr(), float(scaling), out.data_ptr(), E, N, K, r,
+               1 if layout == "hf" else 0, _capi.stream_of(blocks.device))
+    return out
 
 
 def quantize_per_token_e4m3(x: torch.Tensor, with_bf16: bool = False):

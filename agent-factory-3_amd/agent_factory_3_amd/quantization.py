@@ -814,6 +814,55 @@ def enable_expert_lora(experts: Mxfp4Bf16DequantGptOssExperts, r: int = 16, lora
     return experts
 
 
+def _full(t):
+    """The whole tensor of a (possibly FSDP2-sharded) parameter: DTensor.full_tensor() is a collective."""
+    return t.full_tensor() if hasattr(t, "full_tensor") else t
+
+
+def merge_expert_lora(experts: Mxfp4Bf16DequantGptOssExperts, proj: str, layout: str = "hf") -> torch.Tensor:
+    """bf16 weight of ``proj`` with the expert LoRA folded in, for weight sync.
+
+    ``W'[e] = bf16(float(deq(W[e])) + s * (B[e] @ A[e]))`` with fp32 base and
+    delta — the arithmetic of the reference's LoRA merge
+    (model_trainer.py:710-712) — in one HIP kernel over the packed weight.
+    ``layout="hf"``: [E, K, N] as transformers' GptOssExperts holds
+    ``gate_up_proj`` / ``down_proj``; ``"rows"``: [E, N, K].
+    """
+    if not experts.expert_lora_r:
+        raise ValueError("the experts module has no expert LoRA (enable_expert_lora)")
+    shapes = getattr(experts, f"_{proj}_shapes", None)
+    blocks_p, scales_p = _full(getattr(experts, f"{proj}_blocks")), _full(getattr(experts, f"{proj}_scales"))
+    if shapes is not None:
+        blocks, scales = _unpack_bf16_as_uint8(blocks_p, shapes[0]), _unpack_bf16_as_uint8(scales_p, shapes[1])
+    else:
+        blocks, scales = blocks_p, scales_p
+    A = _full(getattr(experts, f"{proj}_lora_A")).detach()
+    B = _full(getattr(experts, f"{proj}_lora_B")).detach()
+    with torch.no_grad():
+        return kernels.mxfp4_lora_merge(blocks, scales, A, B, experts.expert_lora_scaling, layout)
+
+
+def build_merged_expert_state_dict(model, to_cpu: bool = True) -> dict:
+    """Merged expert weights of every experts module carrying expert LoRA.
+
+    The expert-side counterpart of the reference's ``_build_merged_state_dict``
+    (model_trainer.py:653-719) for sglang's ``update_weights_from_disk``: keys
+    are the module path plus ``.gate_up_proj`` / ``.down_proj`` with PEFT's
+    ``base_model.model.`` prefix removed (the names of a bf16 gpt-oss
+    checkpoint), values [E, K, N] bf16.  Only the tensors the adapters change
+    are included; biases stay as they are.
+    """
+    merged = {}
+    for name, mod in model.named_modules():
+        if not isinstance(mod, Mxfp4Bf16DequantGptOssExperts) or not mod.expert_lora_r:
+            continue
+        prefix = name.removeprefix("base_model.model.")
+        for proj in ("gate_up_proj", "down_proj"):
+            w = merge_expert_lora(mod, proj, "hf")
+            merged[f"{prefix}.{proj}"] = w.cpu() if to_cpu else w
+    return merged
+
+
 # ---------------------------------------------------------------------------
 # Routing entry points and the MLP forward
 # ---------------------------------------------------------------------------

@@ -102,7 +102,7 @@ def _graph_us(torch, fn, sets, reps):
 
 
 def bandwidth_extras(torch, dev, kernels, workloads, reps=50):
-    """cfg 0 dequant and cfg 1 SwiGLU fwd/bwd: algorithmic GB/s per launch."""
+    """cfg 0 dequant, the expert-LoRA merge and cfg 1 SwiGLU fwd/bwd: algorithmic GB/s per launch."""
     res = {}
 
     def rec(name, us, byts):
@@ -122,6 +122,21 @@ def bandwidth_extras(torch, dev, kernels, workloads, reps=50):
     rec("dequant_120b_gate_up", _graph_us(torch, kernels.mxfp4_to_bf16_hip, big, 5),
         128 * (8294400 + 518400 + 33177600))
     del big
+    # expert-LoRA merge for weight sync over 16 experts of the 120b gate_up shape, r = 32:
+    # the packed weight and the adapters read, the merged bf16 weight written once
+    E, r = 16, 32
+    g = torch.Generator().manual_seed(7)
+    bl, sc = blocks.to(dev), scales.to(dev)
+    mset = [(bl.expand(E, *bl.shape).contiguous(), sc.expand(E, *sc.shape).contiguous(),
+             (torch.randn(E, r, 2880, generator=g) * 0.01).to(torch.bfloat16).to(dev),
+             (torch.randn(E, 5760, r, generator=g) * 0.01).to(torch.bfloat16).to(dev))]
+    del bl, sc
+    mbytes = E * (8294400 + 518400 + 33177600 + r * (2880 + 5760) * 2)
+    for layout in ("hf", "rows"):
+        rec(f"lora_merge_{layout}_16x_gate_up",
+            _graph_us(torch, lambda b, s_, a, bb: kernels.mxfp4_lora_merge(b, s_, a, bb, 1.0, layout), mset, 5),
+            mbytes)
+    del mset
     gu, dout = workloads.cfg1()
     M, N2 = gu.shape
     N = N2 // 2

@@ -210,6 +210,18 @@ int af3_lora_wgrad(const uint16_t* a, int64_t lda, const int32_t* a_gather, int 
                    const int32_t* chunk_offs, int max_chunks, int chunk_rows, float* partials, size_t partial_bytes,
                    uint16_t* g, void* stream);
 
+/* Expert-LoRA merge for weight sync.  The reference merges attention LoRA
+ * into bf16 weights for sglang (model_trainer.py:653-719: fp32 base + fp32
+ * (B @ A) * scaling, one cast to bf16); this is the same merge for the expert
+ * adapters over the MXFP4 weight:
+ *   W'[e][n][k] = bf16(float(deq(W[e])[n][k]) + scaling * sum_j B[e][n][j] A[e][j][k])
+ * blocks [E][N][K/32][16], scales [E][N][K/32], lora_a [E][r][K], lora_b [E][N][r]
+ * (bf16, r % 8 == 0); deq = the rule of af3_mxfp4_to_bf16.  layout 0: out
+ * [E][N][K]; layout 1: out [E][K][N] (transformers' GptOssExperts parameter
+ * layout, modeling_gpt_oss.py:75-77). */
+int af3_mxfp4_lora_merge(const uint8_t* blocks, const uint8_t* scales, const uint16_t* lora_a, const uint16_t* lora_b,
+                         float scaling, uint16_t* out, int E, int N, int K, int r, int layout, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

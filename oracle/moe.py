@@ -9,6 +9,8 @@ backward with ``w``): for each expert e, over its expert-sorted rows,
 (quantization.py:507-544) and the backward of its autograd functions
 (quantization.py:376-421, 442-444), with the expert-LoRA terms of the build
 (scaling s = lora_alpha / r, PEFT convention model_trainer.py:665,711).
+``lora_merge`` folds the expert adapters into bf16 weights the way the
+reference merges its attention adapters for weight sync (model_trainer.py:710-712).
 """
 from __future__ import annotations
 
@@ -184,3 +186,17 @@ def dense_reference(x, p, expt_ids, scal, alpha=_sw.ALPHA, limit=_sw.LIMIT, lora
         A, B = lora["Adn"].to(dtype)[ids], lora["Bdn"].to(dtype)[ids]
         y = y + s * torch.einsum("tkhr,tkr->tkh", B, torch.einsum("tkri,tki->tkr", A, act))
     return (y * scal.to(dtype)[..., None]).sum(1)
+
+
+def lora_merge(blocks, scales, A, B, s, layout="hf"):
+    """Expert weight with the LoRA delta folded in, as the reference merges
+    adapters for weight sync (model_trainer.py:710-712):
+    ``(base.float() + (B.float() @ A.float()) * s).to(bf16)`` per expert, with
+    base = the MXFP4 -> bf16 dequant (oracle.mxfp4) and the r-term sum taken
+    exactly (float64) and rounded once to float32.  blocks [E, N, G, 16],
+    A [E, r, K], B [E, N, r] -> bf16 [E, K, N] ("hf") or [E, N, K] ("rows")."""
+    from . import mxfp4 as _mx
+    base = _mx.dequant_f32(blocks, scales)                                   # [E, N, K] f32
+    delta = torch.matmul(B.to(torch.float64), A.to(torch.float64)).to(F32)   # exact sum, one rounding
+    w = (base + delta * torch.tensor(s, dtype=F32)).to(BF16)
+    return w.transpose(1, 2).contiguous() if layout == "hf" else w

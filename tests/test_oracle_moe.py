@@ -102,3 +102,56 @@ def test_combine_skips_dropped_slots():
     gi = torch.tensor([5, -1, 0, 2, 1, 3], dtype=torch.int32)
     out = moe.combine(rows, gi, 2)
     assert out.float().tolist() == [[10.0, 11.0], [4.0, 6.0], [8.0, 10.0]]
+
+
+def _merge_inputs(E=2, N=40, G=3, r=16, seed=5):
+    g = torch.Generator().manual_seed(seed)
+    blocks = torch.randint(0, 256, (E, N, G, 16), generator=g, dtype=torch.uint8)
+    scales = torch.randint(118, 131, (E, N, G), generator=g, dtype=torch.uint8)
+    A = (torch.randn(E, r, 32 * G, generator=g) * 0.1).to(torch.bfloat16)
+    B = (torch.randn(E, N, r, generator=g) * 0.03).to(torch.bfloat16)
+    return blocks, scales, A, B
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16).numpy().astype(np.int64)
+
+
+def test_lora_merge_with_zero_b_is_the_dequant():
+    blocks, scales, A, B = _merge_inputs()
+    w = moe.lora_merge(blocks, scales, A, torch.zeros_like(B), 2.0, layout="rows")
+    ref = mxfp4.dequant_bits(blocks.numpy(), scales.numpy()).astype(np.int64)
+    ref[ref == 0x8000] = 0          # -0.0 + 0.0 = +0.0 in the fp32 add, as in the reference's merge
+    got = _bits(w) & 0xFFFF
+    assert (got == ref).all()
+
+
+def test_lora_merge_exact_delta_and_layouts():
+    # entries on a 2^-4 / 2^-3 grid: every product and every sum over r is exact in fp32,
+    # so the merged value is the exact base + s * (B @ A), rounded once to bf16
+    blocks, scales, _, _ = _merge_inputs()
+    g = torch.Generator().manual_seed(9)
+    E, N, G, _ = blocks.shape
+    r = 16
+    A = (torch.randint(-8, 9, (E, r, 32 * G), generator=g).double() / 16).to(torch.bfloat16)
+    B = (torch.randint(-8, 9, (E, N, r), generator=g).double() / 8).to(torch.bfloat16)
+    s = 0.5
+    exact = mxfp4.dequant_f32(blocks, scales).double()
+    for e in range(E):
+        exact[e] += s * (B[e].double() @ A[e].double())
+    rows = moe.lora_merge(blocks, scales, A, B, s, layout="rows")
+    assert (_bits(rows) == _bits(exact.to(torch.float32).to(torch.bfloat16))).all()
+    hf = moe.lora_merge(blocks, scales, A, B, s, layout="hf")
+    assert hf.shape == (E, 32 * G, N) and (_bits(hf) == _bits(rows.transpose(1, 2))).all()
+
+
+def test_lora_merge_matches_the_reference_expression():
+    # the reference's literal fp32 expression (model_trainer.py:710-712) differs only where
+    # its fp32 matmul rounds the r-term sum differently: at most one bf16 step, rarely
+    blocks, scales, A, B = _merge_inputs(E=3, N=64, G=4, r=32)
+    s = 1.0
+    ours = moe.lora_merge(blocks, scales, A, B, s, layout="rows")
+    base = mxfp4.dequant_f32(blocks, scales)
+    ref = torch.stack([(base[e] + (B[e].float() @ A[e].float()) * s).to(torch.bfloat16) for e in range(3)])
+    d = np.abs(_bits(ours) - _bits(ref))
+    assert d.max() <= 1 and (d > 0).mean() < 1e-3
