@@ -196,90 +196,125 @@ __global__ __launch_bounds__(256, 6) void lora_merge_generic_kernel(const uint8_
   }
 }
 
-// The same merge for r <= 64 with the whole next tile prefetched into registers
-// while the current one is computed: its packed dwords, its A slice (two 16-byte
-// chunks per thread) and this lane's B fragments (one 16-byte chunk per 16 j), so
-// that no global round trip is left between a tile's barriers.
-__global__ __launch_bounds__(256, 5) void lora_merge_kernel(const uint8_t* __restrict__ blocks,
+// The merge for r <= 64.  A block owns one (expert, 64-column k-tile, run of up to
+// kMgRun n-tiles) unit: A's k-slice is staged once, transposed (At[k][j], so a lane's
+// MFMA fragment is one 16-byte read), then the block walks down its n-tiles.  For
+// each tile the next tile's packed dwords and B fragments are loaded into registers
+// while the current tile is computed; every pointer is a per-tile uniform base plus a
+// per-thread 32-bit offset that does not change along the walk.  Units are dealt to
+// the XCDs in contiguous runs (k-tile fastest), so the blocks sharing the lines of a
+// packed row run on one L2.
+constexpr int kMgRun = 16;
+constexpr int kMgAtP = 72;  // u16 pitch of At (16-byte rows)
+
+__global__ __launch_bounds__(256, 4) void lora_merge_kernel(const uint8_t* __restrict__ blocks,
                                                             const uint8_t* __restrict__ scales,
                                                             const uint16_t* __restrict__ la,
                                                             const uint16_t* __restrict__ lb, float s,
                                                             uint16_t* __restrict__ out, int N, int K, int r,
-                                                            int layout, int n_tiles_n, int n_tiles_k,
-                                                            int64_t n_tiles, int64_t per_xcd, int blocks_per_xcd) {
+                                                            int layout, int n_tiles_n, int n_tiles_k, int n_runs,
+                                                            int n_units, int per_xcd) {
+  __shared__ __attribute__((aligned(16))) uint16_t At[kMgK * kMgAtP];
   __shared__ __attribute__((aligned(16))) float D[kMgN * kMgDP];
-  __shared__ __attribute__((aligned(16))) uint16_t LM[kMgN * kMgLP];
-  uint16_t* const La = LM;
-  uint16_t* const Mt = LM;
+  __shared__ __attribute__((aligned(16))) uint16_t Mt[kMgN * kMgMP];
+  const int unit = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+  if (unit >= n_units || unit >= ((int)(blockIdx.x & 7) + 1) * per_xcd) return;
+  const int kt_i = unit % n_tiles_k;
+  const int rest = unit / n_tiles_k;
+  const int run = rest % n_runs;
+  const int e = rest / n_runs;
+  const int k0 = kt_i * kMgK;
+  const int t_first = run * kMgRun;
+  const int t_last = min(n_tiles_n, t_first + kMgRun);
+  const int G = K >> 5;
   const int tid = threadIdx.x;
   const int w = tid >> 6;
   const int lane = tid & 63;
-  const int xcd = blockIdx.x & 7;
-  const int64_t t_end = min(n_tiles, (int64_t)(xcd + 1) * per_xcd);
-  int64_t tile = (int64_t)xcd * per_xcd + (blockIdx.x >> 3);
-  const int kcl = (w & 1) * 32 + (lane & 31);
-  const int nsub = (w >> 1) * 32 + (lane & 31);
 
-  uint32_t v[2], sc[2];
-  af3_u32x4 av[2], bv[4];
-  auto fetch = [&](int64_t ti, uint32_t v_[2], uint32_t sc_[2], af3_u32x4 av_[2], af3_u32x4 bv_[4]) {
-    const MergeTile t = merge_tile(ti, n_tiles_n, n_tiles_k);
-    merge_load_packed(blocks, scales, t, N, K, tid, v_, sc_);
-    const int kk = t.k0 + (tid & 7) * 8;
+  // ---- At[k][j] = A[e][j][k0 + k]
+  {
+    const uint16_t* a_e = la + (int64_t)e * r * K + k0;
+    const int c = tid & 7;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int j = h * 32 + (tid >> 3);
-      av_[h] = (af3_u32x4){0u, 0u, 0u, 0u};
-      if (j < r && kk < K) av_[h] = *(const af3_u32x4*)(la + ((int64_t)t.e * r + j) * K + kk);
+      if (j < r) {
+        af3_u32x4 val = {0u, 0u, 0u, 0u};
+        if (k0 + c * 8 < K) val = *(const af3_u32x4*)(a_e + j * K + c * 8);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          At[(c * 8 + 2 * i) * kMgAtP + j] = (uint16_t)(val[i] & 0xFFFFu);
+          At[(c * 8 + 2 * i + 1) * kMgAtP + j] = (uint16_t)(val[i] >> 16);
+        }
+      }
     }
-    const int nr = t.n0 + nsub;
+  }
+
+  // per-thread offsets, fixed along the walk
+  const int kl = (tid & 7) * 8;            // 8 consecutive k of rows p*32 + tid/8
+  const bool k_live = k0 + kl < K;
+  const int kcl = (w & 1) * 32 + (lane & 31);
+  const int nsub = (w >> 1) * 32 + (lane & 31);
+  const int jh = (lane >> 5) * 8;
+  uint32_t off_b[2], off_s[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int nl = p * 32 + (tid >> 3);
+    off_b[p] = (uint32_t)(nl * G * 16 + (kl >> 1));
+    off_s[p] = (uint32_t)(nl * G + (kl >> 5));
+  }
+  const uint32_t off_lb = (uint32_t)(nsub * r + jh);
+
+  uint32_t v[2], sc[2];
+  af3_u32x4 bv[4];
+  auto fetch = [&](int ti, uint32_t v_[2], uint32_t sc_[2], af3_u32x4 bv_[4]) {
+    const int n0 = ti * kMgN;
+    const int64_t row0 = (int64_t)e * N + n0;
+    const uint8_t* bt = blocks + (row0 * G + (k0 >> 5)) * 16;
+    const uint8_t* st = scales + row0 * G + (k0 >> 5);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      v_[p] = 0u;
+      sc_[p] = 0u;
+      if (n0 + p * 32 + (tid >> 3) < N && k_live) {
+        v_[p] = __builtin_nontemporal_load((const uint32_t*)(bt + off_b[p]));
+        sc_[p] = st[off_s[p]];
+      }
+    }
+    const uint16_t* lt = lb + row0 * r;
+    const bool n_ok = n0 + nsub < N;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int jl = q * 16 + (lane >> 5) * 8;
       bv_[q] = (af3_u32x4){0u, 0u, 0u, 0u};
-      if (jl < r && nr < N) bv_[q] = *(const af3_u32x4*)(lb + ((int64_t)t.e * N + nr) * r + jl);
+      if (q * 16 + jh < r && n_ok) bv_[q] = *(const af3_u32x4*)(lt + off_lb + q * 16);
     }
   };
-  if (tile < t_end) fetch(tile, v, sc, av, bv);
+  fetch(t_first, v, sc, bv);
 
-  for (; tile < t_end; tile += blocks_per_xcd) {
-    const MergeTile t = merge_tile(tile, n_tiles_n, n_tiles_k);
-    const int e = t.e, n0 = t.n0, k0 = t.k0;
-    // Consume every register the previous prefetch filled before the next one is
-    // issued (the packed dwords dequantised, the A slice stored to LDS, the B
-    // fragments pinned): the wait-count pass then has no reason to wait for the new
-    // loads before the end of this tile.
+  for (int ti = t_first; ti < t_last; ++ti) {
+    const int n0 = ti * kMgN;
+    // consume the registers the previous fetch filled before the next fetch is issued,
+    // so that no wait for the new loads is needed before the end of this tile
     uint32_t qd[2][4];
 #pragma unroll
     for (int p = 0; p < 2; ++p) af3_dequant_u32(v[p], sc[p], qd[p]);
-    __syncthreads();  // the previous tile's reads of the merged tile (same buffer) are done
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int j = h * 32 + (tid >> 3);
-      if (j < r) *(af3_u32x4*)(La + j * kMgLP + (tid & 7) * 8) = av[h];
-    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) asm volatile("" : "+v"(bv[q]));
     uint32_t vn[2] = {0u, 0u}, scn[2] = {0u, 0u};
-    af3_u32x4 avn[2] = {}, bvn[4] = {};
-    if (tile + blocks_per_xcd < t_end) fetch(tile + blocks_per_xcd, vn, scn, avn, bvn);
-    __syncthreads();
+    af3_u32x4 bvn[4] = {};
+    if (ti + 1 < t_last) fetch(ti + 1, vn, scn, bvn);
+    __syncthreads();  // At staged (first tile); the previous tile's reads of D and Mt are done
+
     af3_f32x16 acc;
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = 0.f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       if (q * 16 >= r) break;
-      const int jl = q * 16 + (lane >> 5) * 8;
-      uint32_t bw[4] = {0u, 0u, 0u, 0u};
-      if (jl < r) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          bw[c] = (uint32_t)La[(jl + 2 * c) * kMgLP + kcl] | ((uint32_t)La[(jl + 2 * c + 1) * kMgLP + kcl] << 16);
-      }
+      af3_u32x4 bw = {0u, 0u, 0u, 0u};
+      if (q * 16 + jh < r) bw = *(const af3_u32x4*)(At + kcl * kMgAtP + q * 16 + jh);
       acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(af3_bf16x8, bv[q]),
-                                                    __builtin_bit_cast(af3_bf16x8, (af3_u32x4){bw[0], bw[1], bw[2], bw[3]}),
-                                                    acc, 0, 0, 0);
+                                                    __builtin_bit_cast(af3_bf16x8, bw), acc, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -288,20 +323,17 @@ __global__ __launch_bounds__(256, 5) void lora_merge_kernel(const uint8_t* __res
     }
     __syncthreads();
 
-    const int kl = (tid & 7) * 8;
-    const int k = k0 + kl;
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       const int nl = p * 32 + (tid >> 3);
-      const bool live = n0 + nl < N && k < K;
+      const bool live = n0 + nl < N && k_live;
       uint32_t m[4] = {0u, 0u, 0u, 0u};
       if (live) {
-        const uint32_t* q4 = qd[p];
         const float4* d4 = (const float4*)(D + nl * kMgDP + kl);
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
           const float4 d = d4[c];
-          const uint32_t lo = q4[2 * c], hi = q4[2 * c + 1];
+          const uint32_t lo = qd[p][2 * c], hi = qd[p][2 * c + 1];
           m[2 * c] = af3_pack_bf16x2(af3_bf16_to_f32(lo & 0xFFFFu) + d.x, af3_bf16_to_f32(lo >> 16) + d.y);
           m[2 * c + 1] = af3_pack_bf16x2(af3_bf16_to_f32(hi & 0xFFFFu) + d.z, af3_bf16_to_f32(hi >> 16) + d.w);
         }
@@ -309,7 +341,7 @@ __global__ __launch_bounds__(256, 5) void lora_merge_kernel(const uint8_t* __res
       if (layout == 0) {
         if (live)
           __builtin_nontemporal_store((af3_u32x4){m[0], m[1], m[2], m[3]},
-                                      (af3_u32x4*)(out + ((int64_t)e * N + n0 + nl) * K + k));
+                                      (af3_u32x4*)(out + ((int64_t)e * N + n0) * K + k0 + (uint32_t)(nl * K + kl)));
       } else {
         uint32_t* mrow = (uint32_t*)(Mt + nl * kMgMP + kl);
 #pragma unroll
@@ -319,16 +351,16 @@ __global__ __launch_bounds__(256, 5) void lora_merge_kernel(const uint8_t* __res
     if (layout != 0) {
       __syncthreads();
       const int nt = (tid & 7) * 8;
+      uint16_t* ot = out + ((int64_t)e * K + k0) * N + n0;
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         const int kt = p * 32 + (tid >> 3);
-        const int kk = k0 + kt;
-        if (kk >= K) break;
+        if (k0 + kt >= K) break;
         uint32_t t4[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c)
           t4[c] = (uint32_t)Mt[(nt + 2 * c) * kMgMP + kt] | ((uint32_t)Mt[(nt + 2 * c + 1) * kMgMP + kt] << 16);
-        uint16_t* o = out + ((int64_t)e * K + kk) * N + n0 + nt;
+        uint16_t* o = ot + (uint32_t)(kt * N + nt);
         if ((N & 7) == 0 && n0 + nt + 8 <= N) {
           __builtin_nontemporal_store((af3_u32x4){t4[0], t4[1], t4[2], t4[3]}, (af3_u32x4*)o);
         } else {
@@ -340,7 +372,6 @@ __global__ __launch_bounds__(256, 5) void lora_merge_kernel(const uint8_t* __res
     for (int p = 0; p < 2; ++p) {
       v[p] = vn[p];
       sc[p] = scn[p];
-      av[p] = avn[p];
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) bv[q] = bvn[q];
@@ -367,10 +398,13 @@ extern "C" int af3_mxfp4_lora_merge(const uint8_t* blocks, const uint8_t* scales
   const int64_t per_xcd = af3_cdiv(tiles, 8);
   // resident blocks per XCD: 32 CUs x 6 blocks of 26 KB LDS
   if (r <= 64) {
-    // resident blocks per XCD: 32 CUs x 5 blocks (register-limited)
-    const int bpx = (int)(per_xcd < 32 * 5 ? per_xcd : 32 * 5);
-    hipLaunchKernelGGL(lora_merge_kernel, dim3((unsigned)(8 * bpx)), dim3(256), 0, stream, blocks, scales, lora_a,
-                       lora_b, scaling, out, N, K, r, layout, ntn, ntk, tiles, per_xcd, bpx);
+    const int runs = (int)af3_cdiv(ntn, kMgRun);
+    const int64_t units = (int64_t)E * runs * ntk;
+    AF3_REQUIRE(units <= 0x7ffffff0LL && (int64_t)kMgN * N <= 0x7fffffffLL && (int64_t)kMgK * N <= 0x7fffffffLL,
+                "mxfp4_lora_merge: tensor too large");
+    const int upx = (int)af3_cdiv(units, 8);
+    hipLaunchKernelGGL(lora_merge_kernel, dim3((unsigned)(8 * upx)), dim3(256), 0, stream, blocks, scales, lora_a,
+                       lora_b, scaling, out, N, K, r, layout, ntn, ntk, runs, (int)units, upx);
   } else {
     const int bpx = (int)(per_xcd < kMgBlocksPerXcd ? per_xcd : kMgBlocksPerXcd);
     hipLaunchKernelGGL(lora_merge_generic_kernel, dim3((unsigned)(8 * bpx)), dim3(256), 0, stream, blocks, scales,
