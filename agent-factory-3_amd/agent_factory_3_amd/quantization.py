@@ -350,6 +350,26 @@ def matmul_ogs(x, w_blocks_scales, bias, routing_data=None, gather_indx=None, sc
 # Autograd functions
 # ---------------------------------------------------------------------------
 
+def _gamma_grad(d_act, act, dY, gather, k_act, bias, routing_data, gammas):
+    """d gamma[r] = <dY[t(r)], y[r]> for the down projection's expert rows, from its
+    gamma-scaled input gradient ``d_act`` (= gamma * dY W), its input ``act`` and the
+    bias (``af3_gamma_grad``); returned in ``gammas``' dtype."""
+    R, N = act.shape
+    ed = routing_data.expt_data
+    out = torch.empty(R, dtype=torch.float32, device=act.device)
+    gam = _bf16c(gammas)
+    b = bias.float().contiguous() if bias is not None else None
+    dyc = dY.contiguous()
+    gp = _gather_ptr(gather)
+    _capi.call("af3_gamma_grad", d_act.data_ptr(), d_act.stride(0), act.data_ptr(), act.stride(0), N,
+               dyc.data_ptr(), dyc.stride(0), gp.data_ptr() if gp is not None else None,
+               k_act if gather is not None else 1,
+               b.data_ptr() if b is not None else None, b.shape[1] if b is not None else 0,
+               ed.token_offs_raw.data_ptr(), routing_data.n_expts_tot, gam.data_ptr(), R, out.data_ptr(),
+               _capi.stream_of(act.device))
+    return out.to(gammas.dtype)
+
+
 class DequantMoEMatmul(torch.autograd.Function):
     """MXFP4 grouped GEMM (quantization.py:294-421), dequant fused into the GEMM.
 
@@ -384,6 +404,11 @@ class DequantMoEMatmul(torch.autograd.Function):
         ctx.proj_name = proj_name
         if experts_module is None:  # no module to re-derive from: keep the (view) tensors
             ctx.weights = (blocks, scales)
+        if ctx.needs_input_grad[7]:  # routing-weight gradient (routing.GAMMA_GRAD)
+            if fwd_gather_indx is not None or fwd_scatter_indx is None:
+                raise NotImplementedError("routing-weight gradients are implemented for the down projection")
+            ctx.save_for_backward(x, fwd_gammas)
+            ctx.gamma_bias = bias
         ctx.routing_data = routing_data
         ctx.bwd_gather_indx = bwd_gather_indx
         ctx.bwd_scatter_indx = bwd_scatter_indx
@@ -407,7 +432,12 @@ class DequantMoEMatmul(torch.autograd.Function):
             else:
                 grad_x = matmul_ogs(g, (blocks, scales), None, ctx.routing_data, ctx.bwd_gather_indx,
                                     ctx.bwd_scatter_indx, ctx.bwd_gammas, trans_w=True)
-        return grad_x, None, None, None, None, None, None, None, None, None, None, None, None, None, None
+            d_gam = None
+            if ctx.needs_input_grad[7]:
+                x, gam = ctx.saved_tensors
+                d_gam = _gamma_grad(grad_x, _bf16c(x), g, ctx.bwd_gather_indx, ctx.n_expts_act, ctx.gamma_bias,
+                                    ctx.routing_data, gam)
+        return grad_x, None, None, None, None, None, None, d_gam, None, None, None, None, None, None, None
 
 
 class SwiGLUFunction(torch.autograd.Function):
@@ -487,6 +517,9 @@ class LoraDequantMoEMatmul(torch.autograd.Function):
     def forward(ctx, x, lora_A, lora_B, scaling, blocks, scales, bias, routing_data, fwd_gather_indx,
                 fwd_scatter_indx, fwd_gammas, bwd_gather_indx, bwd_scatter_indx, bwd_gammas, experts_module=None,
                 proj_name=None):
+        if ctx.needs_input_grad[10]:
+            raise NotImplementedError("routing-weight gradients with expert LoRA need the fused SwiGLU path "
+                                      "(quantization.FUSED_SWIGLU)")
         dev = x.device
         E, N, K = _weight_dims(blocks, False)
         xg = x if x.stride(-1) == 1 and x.data_ptr() % 16 == 0 and x.stride(0) % 8 == 0 else x.contiguous()
@@ -671,6 +704,7 @@ class _SwiGLUDown(torch.autograd.Function):
         ctx.routing_data = routing_data
         ctx.k_act = k_act
         ctx.gammas = gammas
+        ctx.gamma_bias = bias if ctx.needs_input_grad[10] else None
         ctx.bwd_gather_indx = bwd_gather_indx
         ctx.alpha, ctx.limit = float(alpha), float(limit)
         ctx.lora_dtypes = (lora_A.dtype, lora_B.dtype) if lora_A is not None else None
@@ -690,19 +724,23 @@ class _SwiGLUDown(torch.autograd.Function):
         with on_device(dY.device):
             if A is not None:
                 u = _lora_rows(dY, bg, k_act, B, 1, ctx.scaling, ed, A.shape[1], N)
-            dgu = None
-            if FUSED_SWIGLU_BWD:
+            dgu = d_gam = None
+            want_gam = ctx.needs_input_grad[10]  # routing-weight gradient (routing.GAMMA_GRAD)
+            if FUSED_SWIGLU_BWD and not want_gam:
                 dgu = moe_rows(dY, blocks, scales, None, ctx.routing_data, ctx.bwd_gather_indx, gam, True, u, A,
                                swiglu=("bwd", gate_up, ctx.alpha, ctx.limit))
             if dgu is None:
                 d_act = moe_rows(dY, blocks, scales, None, ctx.routing_data, ctx.bwd_gather_indx, gam, True, u, A)
+                if want_gam:
+                    d_gam = _gamma_grad(d_act, act, dY, ctx.bwd_gather_indx, k_act, ctx.gamma_bias,
+                                        ctx.routing_data, ctx.gammas)
                 dgu = swiglu_backward_raw(d_act, gate_up, ctx.alpha, ctx.limit)
             if A is not None:
                 r = A.shape[1]
                 dA = _lora_wgrad(u, None, 1, gam, act, None, 1, ed, E, r, K).to(ctx.lora_dtypes[0])
                 dB = _lora_wgrad(dY, bg, k_act if bg is not None else 1, gam, L, None, 1, ed, E, N,
                                  r).to(ctx.lora_dtypes[1])
-        return (dgu, None, dA, dB) + (None,) * 12
+        return (dgu, None, dA, dB) + (None,) * 6 + (d_gam,) + (None,) * 5
 
 
 # ---------------------------------------------------------------------------

@@ -124,6 +124,45 @@ def _bf16_logits(logits: torch.Tensor) -> torch.Tensor:
     return logits
 
 
+# Routing-weight (gamma) gradients.  The reference's expert layer returns no gradient
+# for the routing weights (quantization.py:421), so its router only learns through
+# other paths; with GAMMA_GRAD set, gate_scal stays attached to the router logits
+# (softmax over each token's K selected logits) and the down projection returns
+# d gamma, so a trainable router receives the gradient of the routing weights.
+GAMMA_GRAD = False
+
+
+class _GateScal(torch.autograd.Function):
+    """gate_scal (sorted rows) as a differentiable function of the router logits:
+    forward passes the routing kernel's softmax weights through; backward is the
+    softmax backward over each token's K slots, scattered to the selected logits."""
+
+    @staticmethod
+    def forward(ctx, logits, gate_scal, topk_indx, hist, K):
+        ctx.save_for_backward(gate_scal, topk_indx, hist)
+        ctx.K, ctx.shape, ctx.dtype = int(K), tuple(logits.shape), logits.dtype
+        return gate_scal.view_as(gate_scal)
+
+    @staticmethod
+    def backward(ctx, grad):
+        gs, topk, hist = ctx.saved_tensors
+        T, E = ctx.shape
+        K = ctx.K
+        R = T * K
+        dev = gs.device
+        tk = topk.long()
+        gam = torch.empty(R, dtype=torch.float32, device=dev)
+        gam[tk] = gs.float()
+        d = torch.empty(R, dtype=torch.float32, device=dev)
+        d[tk] = grad.float()
+        ids = torch.empty(R, dtype=torch.long, device=dev)
+        ids[tk] = torch.repeat_interleave(torch.arange(E, device=dev), hist.long(), output_size=R)
+        gam, d, ids = gam.view(T, K), d.view(T, K), ids.view(T, K)
+        dl = gam * (d - (gam * d).sum(-1, keepdim=True))
+        dlogits = torch.zeros(T, E, dtype=torch.float32, device=dev).scatter_add_(1, ids, dl)
+        return dlogits.to(ctx.dtype), None, None, None, None
+
+
 def _run_routing(logits: torch.Tensor, n_expts_act: int, expt_indx: torch.Tensor | None):
     out_dtype = logits.dtype
     lg = _bf16_logits(logits)
@@ -153,6 +192,8 @@ def _run_routing(logits: torch.Tensor, n_expts_act: int, expt_indx: torch.Tensor
     expt_data = compute_expt_data(hist, E, R, token_offs_raw=offs)
     if out_dtype != torch.bfloat16 and out_dtype.is_floating_point:
         gate_scal = gate_scal.to(out_dtype)
+    if GAMMA_GRAD and torch.is_grad_enabled() and logits.requires_grad:
+        gate_scal = _GateScal.apply(logits, gate_scal, topk_indx, hist, K)
     return (
         RoutingData(gate_scal, hist, E, K, expt_data),
         GatherIndx(src_indx=topk_indx, dst_indx=gate_indx),

@@ -11,7 +11,8 @@ Inputs are seeded synthetic tensors already resident in HBM.
 Prints ONE JSON line.  ``roofline`` is for the dominant kernel (the grouped
 GEMM instantiation with the largest total time), timed with HIP events on the
 launch stream inside the timed region; ``extra`` holds the standalone dequant
-(cfg 0) and SwiGLU (cfg 1) bandwidths; ``cpu_baseline`` is the PyTorch-eager
+(cfg 0), LoRA-merge and SwiGLU (cfg 1) bandwidths, the fp8 mode and the cost of
+routing-weight gradients; ``cpu_baseline`` is the PyTorch-eager
 CPU path on a bounded sample (rank 0 only).
 """
 from __future__ import annotations
@@ -197,6 +198,44 @@ def fp8_extras(torch, dev, kernels, workloads, inp_cpu, k, steps=10, reps=20):
     return res
 
 
+def gamma_extras(torch, dev, workloads, inp_cpu, k, steps=10):
+    """The cfg layer (with its expert LoRA) with routing-weight gradients on
+    (routing.GAMMA_GRAD, router logits requiring grad) and off: the cost of the
+    extra af3_gamma_grad pass and the softmax backward."""
+    from agent_factory_3_amd import routing
+    inp = inp_cpu.to(dev)
+    M = inp.x.shape[0]
+    res = {}
+    prev = routing.GAMMA_GRAD
+    try:
+        for on in (True, False):
+            routing.GAMMA_GRAD = on
+            m = workloads.make_experts(inp_cpu, dev)
+
+            def step():
+                lg = inp.logits.detach().requires_grad_(True)
+                rd, gi, si = routing.routing_replay(lg, inp.expt_indx, k)
+                xx = inp.x.detach().requires_grad_(True)
+                m(xx, rd, gi, si).backward(inp.dy)
+            for _ in range(3):
+                step()
+            torch.cuda.synchronize()
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for _ in range(steps):
+                step()
+            t1.record()
+            torch.cuda.synchronize()
+            ms = t0.elapsed_time(t1) / steps
+            res["layer_gamma_grad" if on else "layer_no_gamma_grad"] = {"ms_per_step": ms,
+                                                                        "tokens_per_s": M / (ms * 1e-3)}
+            del m
+    finally:
+        routing.GAMMA_GRAD = prev
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -314,6 +353,8 @@ def main():
         extra.update(bandwidth_extras(torch, dev, kernels, workloads))
         log("fp8 mode")
         extra["fp8_mode"] = fp8_extras(torch, dev, kernels, workloads, inp_cpu, k)
+        log("routing-weight gradients")
+        extra["gamma_grad"] = gamma_extras(torch, dev, workloads, inp_cpu, k)
 
     cpu = None
     if not args.no_cpu_baseline and int(os.environ.get("RANK", "0")) == 0:

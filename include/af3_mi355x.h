@@ -222,6 +222,18 @@ int af3_lora_wgrad(const uint16_t* a, int64_t lda, const int32_t* a_gather, int 
 int af3_mxfp4_lora_merge(const uint8_t* blocks, const uint8_t* scales, const uint16_t* lora_a, const uint16_t* lora_b,
                          float scaling, uint16_t* out, int E, int N, int K, int r, int layout, void* stream);
 
+/* Routing-weight gradient of the down projection.  The reference returns no
+ * gradient for gamma (quantization.py:421; forward quantization.py:532-541
+ * scales row r by gamma[r]); this computes it for trainable routers:
+ *   out[r] = <d_act[r], act[r]> / gammas[r] + <dy[gather[r] / gdiv], bias[e(r)]>
+ * d_act = the down projection's input gradient (gamma-scaled) [R][ld_d], act =
+ * its input [R][ld_a] (N columns, bf16), dy [.][ld_dy] and bias [E][H] fp32
+ * optional (bias == NULL drops the second term), e(r) from token_offs [E+1]
+ * (expert-sorted rows), fp32 sums, deterministic. */
+int af3_gamma_grad(const uint16_t* d_act, int64_t ld_d, const uint16_t* act, int64_t ld_a, int N, const uint16_t* dy,
+                   int64_t ld_dy, const int32_t* gather, int gdiv, const float* bias, int H, const int32_t* token_offs,
+                   int n_expts, const uint16_t* gammas, int64_t R, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -155,3 +155,51 @@ def test_lora_merge_matches_the_reference_expression():
     ref = torch.stack([(base[e] + (B[e].float() @ A[e].float()) * s).to(torch.bfloat16) for e in range(3)])
     d = np.abs(_bits(ours) - _bits(ref))
     assert d.max() <= 1 and (d > 0).mean() < 1e-3
+
+
+def test_gamma_grad_identity_used_by_the_kernel():
+    # d gamma[r] = <dY[t(r)], y[r]> (autograd of the weighted scatter-sum) equals
+    # <dI[r], I[r]> / gamma[r] + <dY[t(r)], b[e(r)]>, dI = gamma * (dY W (+ s (dY B) A)):
+    # the form af3_gamma_grad evaluates from the down projection's input gradient
+    g = torch.Generator().manual_seed(4)
+    T, k, E, H, I, r, s = 7, 3, 4, 24, 16, 4, 1.5
+    R = T * k
+    t_of = torch.arange(R) // k
+    e_of = torch.randint(0, E, (R,), generator=g)
+    act = torch.randn(R, I, generator=g, dtype=torch.float64)
+    W = torch.randn(E, H, I, generator=g, dtype=torch.float64)
+    b = torch.randn(E, H, generator=g, dtype=torch.float64)
+    A = torch.randn(E, r, I, generator=g, dtype=torch.float64)
+    B = torch.randn(E, H, r, generator=g, dtype=torch.float64)
+    dY = torch.randn(T, H, generator=g, dtype=torch.float64)
+    gam = torch.rand(R, generator=g, dtype=torch.float64).add(0.05).requires_grad_(True)
+    y = torch.einsum("ri,rhi->rh", act, W[e_of]) + b[e_of]
+    y = y + s * torch.einsum("rq,rhq->rh", torch.einsum("ri,rqi->rq", act, A[e_of]), B[e_of])
+    Y = torch.zeros(T, H, dtype=torch.float64).index_add(0, t_of, gam[:, None] * y)
+    (dY * Y).sum().backward()
+    dyr = dY[t_of]
+    dI = gam.detach()[:, None] * (torch.einsum("rh,rhi->ri", dyr, W[e_of])
+                                  + s * torch.einsum("rq,rqi->ri", torch.einsum("rh,rhq->rq", dyr, B[e_of]), A[e_of]))
+    ident = (dI * act).sum(1) / gam.detach() + (dyr * b[e_of]).sum(1)
+    assert torch.allclose(gam.grad, ident, rtol=1e-12, atol=1e-10)
+
+
+def test_gate_scal_backward_is_the_softmax_backward():
+    # routing._GateScal.backward (torch ops only) against autograd of the reference's
+    # routing_replay expression: softmax over the K gathered logits, sorted by expert
+    from agent_factory_3_amd import routing as R
+    g = torch.Generator().manual_seed(8)
+    T, E, K = 9, 5, 3
+    logits = torch.randn(T, E, generator=g, dtype=torch.float64)
+    ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+    rt = routing.routing_replay(logits.to(torch.bfloat16), ids, K)
+    topk = rt["topk_indx"].long()
+    hist = torch.bincount(ids.reshape(-1), minlength=E).to(torch.int32)
+    lg = logits.clone().requires_grad_(True)
+    gs_ref = torch.softmax(torch.take_along_dim(lg, ids, dim=-1), -1).reshape(-1)[topk]
+    w = torch.randn(T * K, generator=g, dtype=torch.float64)
+    (gs_ref * w).sum().backward()
+    lg2 = logits.clone().requires_grad_(True)
+    gs = R._GateScal.apply(lg2, gs_ref.detach().float(), topk.to(torch.int32), hist, K)
+    (gs.double() * w).sum().backward()
+    assert torch.allclose(lg2.grad, lg.grad, rtol=1e-5, atol=1e-6)
