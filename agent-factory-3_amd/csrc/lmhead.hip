@@ -1,0 +1,314 @@
+// LM-head log-probabilities and entropy without materialised logits.
+//
+// Restates the fused linear cross entropy of the reference's trainer
+// (trainer/losses/kernels.py:157-385 forward, 704-880 backward logits,
+// wrapper trainer/losses/linear_cross_entropy.py): with z = hidden @ W^T / T
+// (hidden [M][H], W [V][H] bf16, fp32 accumulation),
+//
+//   logprob[m] = z[m][label[m]] - lse[m],   lse = max + log(sum exp(z - max))
+//   entropy[m] = lse[m] - E_p[z][m],        E_p[z] = sum exp(z - max) z / sum exp(z - max)
+//
+// and, for the backward, the logits gradient
+//
+//   dz[m][v] = ( dlp[m] (onehot - p) - dent[m] p (z - E_p[z]) ) / T
+//
+// which two plain GEMMs turn into d_hidden = dz W and d_weight = dz^T hidden.
+//
+// lmh_gemm_kernel<MODE>: one 256 (rows) x 256 (vocabulary) tile per block of
+// 8 waves (2 x 4, 128 x 64 each), v_mfma_f32_32x32x16_bf16, 32-deep k-steps
+// double-buffered through LDS (16-byte chunks XOR-swizzled by row / 4 so the
+// fragment reads of 16 lanes hit distinct banks).  Blocks are ordered
+// vocabulary-tile-major and dealt to the XCDs in contiguous runs, so the row
+// tiles that reuse one W tile run together on one L2.
+//   MODE 0: per row and tile, (max, sum exp, sum exp * z) over the tile's 256
+//   columns (wave-wide shuffle reductions, then the four column waves through
+//   LDS) -> partials [n_vtiles][M] float4; the row's label logit is stored by
+//   the one lane that holds it.
+//   MODE 1: dz for the tile from the row statistics of the forward, bf16.
+// lmh_reduce_kernel combines the partials of a row (running max rescaling).
+#include "af3_common.h"
+
+namespace {
+
+constexpr int kLmBM = 256, kLmBN = 256, kLmBK = 32;
+constexpr int kLmStage = (kLmBM + kLmBN) * kLmBK * 2;  // bytes per stage (A then B)
+
+__device__ __forceinline__ int lm_swz(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
+
+__device__ __forceinline__ float wave32_max(float v) {
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 32));
+  return v;
+}
+
+__device__ __forceinline__ float wave32_sum(float v) {
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 32);
+  return v;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
+    const uint16_t* __restrict__ hidden, int64_t ldh, const uint16_t* __restrict__ weight, int64_t ldw, int M, int V,
+    int H, float rcp_t, const int64_t* __restrict__ labels, int n_mtiles, int n_vtiles, int per_xcd,
+    // MODE 0
+    float4* __restrict__ partials, float* __restrict__ zlab,
+    // MODE 1
+    const float* __restrict__ lse, const float* __restrict__ ez, const float* __restrict__ dlp, int64_t dlp_stride,
+    float dlp_scale, const float* __restrict__ dent, uint16_t* __restrict__ dz, int64_t lddz) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int xcd = blockIdx.x & 7;
+  const int tile = xcd * per_xcd + (int)(blockIdx.x >> 3);
+  if (tile >= n_mtiles * n_vtiles || tile >= (xcd + 1) * per_xcd) return;
+  const int vt = tile / n_mtiles;
+  const int mt = tile % n_mtiles;
+  const int m0 = mt * kLmBM, v0 = vt * kLmBN;
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, lane = tid & 63;
+  const int wm0 = (w >> 2) * 128, wn0 = (w & 3) * 64;
+
+  // global -> register copies: thread = (row t/4 (+128), 16-byte chunk t%4) of A and of B
+  const int crow = tid >> 2, cch = tid & 3;
+  const uint16_t* ga[2];
+  const uint16_t* gb[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int ra = min(m0 + crow + 128 * h, M - 1);  // clamped rows: valid data, results never stored
+    const int rb = min(v0 + crow + 128 * h, V - 1);
+    ga[h] = hidden + (int64_t)ra * ldh + cch * 8;
+    gb[h] = weight + (int64_t)rb * ldw + cch * 8;
+  }
+  af3_u32x4 ra_[2], rb_[2];
+  auto gload = [&](int kt) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      ra_[h] = *(const af3_u32x4*)(ga[h] + kt * kLmBK);
+      rb_[h] = *(const af3_u32x4*)(gb[h] + kt * kLmBK);
+    }
+  };
+  auto lstore = [&](int st) {
+    uint8_t* base = lds + st * kLmStage;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int row = crow + 128 * h;
+      *(af3_u32x4*)(base + row * 64 + 16 * lm_swz(row, cch)) = ra_[h];
+      *(af3_u32x4*)(base + kLmBM * 64 + row * 64 + 16 * lm_swz(row, cch)) = rb_[h];
+    }
+  };
+
+  af3_f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.f;
+
+  const int nk = H / kLmBK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) gload(kt + 1);
+    const uint8_t* As = lds + cur * kLmStage;
+    const uint8_t* Bs = As + kLmBM * 64;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int ch = ks * 2 + (lane >> 5);
+      af3_u32x4 af[4], bf[2];
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm) {
+        const int row = wm0 + tm * 32 + (lane & 31);
+        af[tm] = *(const af3_u32x4*)(As + row * 64 + 16 * lm_swz(row, ch));
+      }
+#pragma unroll
+      for (int tn = 0; tn < 2; ++tn) {
+        const int row = wn0 + tn * 32 + (lane & 31);
+        bf[tn] = *(const af3_u32x4*)(Bs + row * 64 + 16 * lm_swz(row, ch));
+      }
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn)
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(af3_bf16x8, af[tm]),
+                                                                __builtin_bit_cast(af3_bf16x8, bf[tn]),
+                                                                acc[tm][tn], 0, 0, 0);
+    }
+    if (kt + 1 < nk) lstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  const int c0 = v0 + wn0 + (lane & 31);  // this lane's columns c0 and c0 + 32
+  if constexpr (MODE == 0) {
+    float* part = (float*)lds;  // [256 rows][4 column waves][3]
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int rl = wm0 + tm * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+        const int row = m0 + rl;
+        const float z0 = acc[tm][0][i] * rcp_t, z1 = acc[tm][1][i] * rcp_t;
+        const bool ok0 = c0 < V, ok1 = c0 + 32 < V;
+        const float mx = wave32_max(fmaxf(ok0 ? z0 : -INFINITY, ok1 ? z1 : -INFINITY));
+        const float e0 = ok0 ? __expf(z0 - mx) : 0.f, e1 = ok1 ? __expf(z1 - mx) : 0.f;
+        const float s = wave32_sum(e0 + e1);
+        const float t = wave32_sum((ok0 ? e0 * z0 : 0.f) + (ok1 ? e1 * z1 : 0.f));
+        if ((lane & 31) == 0) {
+          float* pp = part + (rl * 4 + (w & 3)) * 3;
+          pp[0] = mx;
+          pp[1] = s;
+          pp[2] = t;
+        }
+        if (row < M) {
+          const int64_t lab = labels[row];
+          if (ok0 && lab == c0) zlab[row] = z0;
+          if (ok1 && lab == c0 + 32) zlab[row] = z1;
+        }
+      }
+    }
+    __syncthreads();
+    if (tid < kLmBM && m0 + tid < M) {
+      const float* pp = part + tid * 12;
+      float mx = fmaxf(fmaxf(pp[0], pp[3]), fmaxf(pp[6], pp[9]));
+      float s = 0.f, t = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float f = pp[3 * q] == -INFINITY ? 0.f : __expf(pp[3 * q] - mx);
+        s += pp[3 * q + 1] * f;
+        t += pp[3 * q + 2] * f;
+      }
+      partials[(int64_t)vt * M + m0 + tid] = make_float4(mx, s, t, 0.f);
+    }
+  } else {
+    float* rs = (float*)lds;  // per row: lse, E_p[z], dlp, dent, label (as float bits)
+    if (tid < kLmBM) {
+      const int row = min(m0 + tid, M - 1);
+      rs[tid * 5 + 0] = lse[row];
+      rs[tid * 5 + 1] = ez[row];
+      rs[tid * 5 + 2] = dlp[(int64_t)row * dlp_stride] * dlp_scale;
+      rs[tid * 5 + 3] = dent[row];
+      const int64_t lab = labels[row];
+      rs[tid * 5 + 4] = __int_as_float(lab >= 0 && lab < V ? (int)lab : -1);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int rl = wm0 + tm * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+        const int row = m0 + rl;
+        if (row >= M) continue;
+        const float* r = rs + rl * 5;
+        const float l_ = r[0], e_ = r[1], g_ = r[2], h_ = r[3];
+        const int lab = __float_as_int(r[4]);
+        uint16_t* drow = dz + (int64_t)row * lddz;
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn) {
+          const int c = c0 + tn * 32;
+          if (c >= V) continue;
+          const float z = acc[tm][tn][i] * rcp_t;
+          const float p = __expf(z - l_);
+          const float d = (g_ * ((c == lab ? 1.f : 0.f) - p) - h_ * p * (z - e_)) * rcp_t;
+          drow[c] = (uint16_t)af3_f32_to_bf16(d);
+        }
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void lmh_reduce_kernel(const float4* __restrict__ partials, int M, int n_vtiles,
+                                                         const float* __restrict__ zlab,
+                                                         const int64_t* __restrict__ labels, int V,
+                                                         float* __restrict__ logprobs, float* __restrict__ entropy,
+                                                         float* __restrict__ lse, float* __restrict__ ez) {
+  const int row = blockIdx.x * 256 + threadIdx.x;
+  if (row >= M) return;
+  float mx = -INFINITY, s = 0.f, t = 0.f;
+  for (int j = 0; j < n_vtiles; ++j) {
+    const float4 p = partials[(int64_t)j * M + row];
+    if (p.x == -INFINITY) continue;
+    if (p.x > mx) {
+      const float f = __expf(mx - p.x);  // 0 on the first tile (mx = -inf)
+      s = s * f + p.y;
+      t = t * f + p.z;
+      mx = p.x;
+    } else {
+      const float f = __expf(p.x - mx);
+      s += p.y * f;
+      t += p.z * f;
+    }
+  }
+  const float l = mx + __logf(s);
+  const float e = t / s;
+  const int64_t lab = labels[row];
+  const float zl = (lab >= 0 && lab < V) ? zlab[row] : 0.f;
+  logprobs[row] = zl - l;
+  entropy[row] = l - e;
+  lse[row] = l;
+  ez[row] = e;
+}
+
+int lmh_grid(int M, int V, int& n_mtiles, int& n_vtiles, int& per_xcd) {
+  n_mtiles = (int)af3_cdiv(M, kLmBM);
+  n_vtiles = (int)af3_cdiv(V, kLmBN);
+  const int64_t tiles = (int64_t)n_mtiles * n_vtiles;
+  per_xcd = (int)af3_cdiv(tiles, 8);
+  return 8 * per_xcd;
+}
+
+}  // namespace
+
+extern "C" size_t af3_lm_head_workspace_bytes(int M, int V) {
+  return (size_t)af3_cdiv(V, kLmBN) * (size_t)(M > 0 ? M : 0) * sizeof(float4) + (size_t)(M > 0 ? M : 0) * 4;
+}
+
+extern "C" int af3_lm_head_logprobs(const uint16_t* hidden, int64_t ldh, const uint16_t* weight, int64_t ldw, int M,
+                                    int V, int H, const int64_t* labels, float temperature, float* logprobs,
+                                    float* entropy, float* lse, float* ez, void* workspace, size_t ws_bytes,
+                                    void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  AF3_REQUIRE(M >= 0 && V > 0 && H > 0 && H % kLmBK == 0, "lm_head_logprobs: H must be a positive multiple of 32");
+  if (M == 0) return 0;
+  AF3_REQUIRE(hidden && weight && labels && logprobs && entropy && lse && ez && workspace,
+              "lm_head_logprobs: null pointer");
+  AF3_REQUIRE(temperature > 0.f, "lm_head_logprobs: temperature must be positive");
+  AF3_REQUIRE(ldh % 8 == 0 && ldw % 8 == 0 && ((uintptr_t)hidden & 15) == 0 && ((uintptr_t)weight & 15) == 0,
+              "lm_head_logprobs: rows must be 16-byte aligned");
+  AF3_REQUIRE(ws_bytes >= af3_lm_head_workspace_bytes(M, V) && ((uintptr_t)workspace & 15) == 0,
+              "lm_head_logprobs: workspace too small or misaligned");
+  int nm, nv, px;
+  const int grid = lmh_grid(M, V, nm, nv, px);
+  float4* partials = (float4*)workspace;
+  float* zlab = (float*)((uint8_t*)workspace + (size_t)nv * M * sizeof(float4));
+  const size_t lds_bytes = 2 * kLmStage;
+  hipLaunchKernelGGL(lmh_gemm_kernel<0>, dim3(grid), dim3(512), lds_bytes, stream, hidden, ldh, weight, ldw, M, V, H,
+                     1.f / temperature, labels, nm, nv, px, partials, zlab, nullptr, nullptr, nullptr, 0, 0.f,
+                     nullptr, nullptr, 0);
+  int rc = af3::check_launch("lm_head_logprobs (gemm)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(lmh_reduce_kernel, dim3((unsigned)af3_cdiv(M, 256)), dim3(256), 0, stream, partials, M, nv, zlab,
+                     labels, V, logprobs, entropy, lse, ez);
+  return af3::check_launch("lm_head_logprobs (reduce)");
+}
+
+extern "C" int af3_lm_head_dlogits(const uint16_t* hidden, int64_t ldh, const uint16_t* weight, int64_t ldw, int M,
+                                   int V, int H, const int64_t* labels, float temperature, const float* lse,
+                                   const float* ez, const float* dlogprobs, int64_t dlp_stride, float dlp_scale,
+                                   const float* dentropy, uint16_t* dz, int64_t lddz, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  AF3_REQUIRE(M >= 0 && V > 0 && H > 0 && H % kLmBK == 0, "lm_head_dlogits: H must be a positive multiple of 32");
+  if (M == 0) return 0;
+  AF3_REQUIRE(hidden && weight && labels && lse && ez && dlogprobs && dentropy && dz, "lm_head_dlogits: null pointer");
+  AF3_REQUIRE(temperature > 0.f, "lm_head_dlogits: temperature must be positive");
+  AF3_REQUIRE(ldh % 8 == 0 && ldw % 8 == 0 && ((uintptr_t)hidden & 15) == 0 && ((uintptr_t)weight & 15) == 0 &&
+                  lddz >= V,
+              "lm_head_dlogits: rows must be 16-byte aligned");
+  int nm, nv, px;
+  const int grid = lmh_grid(M, V, nm, nv, px);
+  const size_t lds_bytes = 2 * kLmStage;
+  hipLaunchKernelGGL(lmh_gemm_kernel<1>, dim3(grid), dim3(512), lds_bytes, stream, hidden, ldh, weight, ldw, M, V, H,
+                     1.f / temperature, labels, nm, nv, px, nullptr, nullptr, lse, ez, dlogprobs, dlp_stride,
+                     dlp_scale, dentropy, dz, lddz);
+  return af3::check_launch("lm_head_dlogits");
+}

@@ -234,6 +234,28 @@ int af3_gamma_grad(const uint16_t* d_act, int64_t ld_d, const uint16_t* act, int
                    int64_t ld_dy, const int32_t* gather, int gdiv, const float* bias, int H, const int32_t* token_offs,
                    int n_expts, const uint16_t* gammas, int64_t R, float* out, void* stream);
 
+/* LM-head log-probabilities and entropy without materialised logits.  Replaces
+ * the reference's efficient_entropy_forward (trainer/losses/kernels.py:511-700,
+ * mainloop 157-292, epilogue 296-385) for reduction "none", one rank:
+ * z = hidden [M][ldh] @ weight [V][ldw]^T / temperature (bf16, fp32 accumulation),
+ * logprobs = z[label] - lse, entropy = lse - E_p[z]; lse and ez = E_p[z] are kept
+ * for the backward.  A label outside [0, V) contributes z = 0.  Workspace:
+ * af3_lm_head_workspace_bytes(M, V) bytes (per-tile partials + label logits). */
+size_t af3_lm_head_workspace_bytes(int M, int V);
+int af3_lm_head_logprobs(const uint16_t* hidden, int64_t ldh, const uint16_t* weight, int64_t ldw, int M, int V, int H,
+                         const int64_t* labels, float temperature, float* logprobs, float* entropy, float* lse,
+                         float* ez, void* workspace, size_t ws_bytes, void* stream);
+
+/* Logits gradient of the above (the d_logits of trainer/losses/kernels.py:829-839):
+ * dz[m][v] = (g[m] (onehot - p) - dentropy[m] p (z - ez[m])) / temperature in bf16,
+ * g[m] = dlogprobs[m * dlp_stride] * dlp_scale (stride 0 for a scalar "sum"/"mean"
+ * gradient, dlp_scale = 1/M for "mean").  d_hidden = dz @ weight and
+ * d_weight = dz^T @ hidden are plain GEMMs left to the caller. */
+int af3_lm_head_dlogits(const uint16_t* hidden, int64_t ldh, const uint16_t* weight, int64_t ldw, int M, int V, int H,
+                        const int64_t* labels, float temperature, const float* lse, const float* ez,
+                        const float* dlogprobs, int64_t dlp_stride, float dlp_scale, const float* dentropy,
+                        uint16_t* dz, int64_t lddz, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
