@@ -15,9 +15,9 @@
 // which two plain GEMMs turn into d_hidden = dz W and d_weight = dz^T hidden.
 //
 // lmh_gemm_kernel<MODE>: one 256 (rows) x 256 (vocabulary) tile per block of
-// 8 waves (2 x 4, 128 x 64 each), v_mfma_f32_32x32x16_bf16, 32-deep k-steps
-// double-buffered through LDS (16-byte chunks XOR-swizzled by row / 4 so the
-// fragment reads of 16 lanes hit distinct banks).  Blocks are ordered
+// 8 waves (2 x 4, 128 x 64 each), v_mfma_f32_32x32x16_bf16, 64-deep k-steps
+// double-buffered through registers and LDS (16-byte chunks XOR-swizzled by
+// row / 2 so the fragment reads of 16 lanes hit distinct banks).  Blocks are ordered
 // vocabulary-tile-major and dealt to the XCDs in contiguous runs, so the row
 // tiles that reuse one W tile run together on one L2.
 //   MODE 0: per row and tile, (max, sum exp, sum exp * z) over the tile's 256
@@ -30,10 +30,16 @@
 
 namespace {
 
-constexpr int kLmBM = 256, kLmBN = 256, kLmBK = 32;
+constexpr int kLmBM = 256, kLmBN = 256, kLmBK = 64;
+constexpr int kLmRowB = kLmBK * 2;   // bytes per tile row and k-step
+constexpr int kLmCh = kLmRowB / 16;   // 16-byte chunks per row
 constexpr int kLmStage = (kLmBM + kLmBN) * kLmBK * 2;  // bytes per stage (A then B)
+static_assert(2 * kLmStage <= 160 * 1024, "gfx950 LDS per workgroup");
 
-__device__ __forceinline__ int lm_swz(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
+// 16-byte chunk position of (row, chunk) in a 128-byte LDS row: rows of one parity
+// spread their chunks over 8 positions, so 16 lanes reading one chunk of 16 rows hit
+// distinct banks
+__device__ __forceinline__ int lm_swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
 __device__ __forceinline__ float wave32_max(float v) {
 #pragma unroll
@@ -56,7 +62,7 @@ __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
     // MODE 1
     const float* __restrict__ lse, const float* __restrict__ ez, const float* __restrict__ dlp, int64_t dlp_stride,
     float dlp_scale, const float* __restrict__ dent, uint16_t* __restrict__ dz, int64_t lddz) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kLmStage];
   const int xcd = blockIdx.x & 7;
   const int tile = xcd * per_xcd + (int)(blockIdx.x >> 3);
   if (tile >= n_mtiles * n_vtiles || tile >= (xcd + 1) * per_xcd) return;
@@ -67,32 +73,35 @@ __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
   const int w = tid >> 6, lane = tid & 63;
   const int wm0 = (w >> 2) * 128, wn0 = (w & 3) * 64;
 
-  // global -> register copies: thread = (row t/4 (+128), 16-byte chunk t%4) of A and of B
-  const int crow = tid >> 2, cch = tid & 3;
-  const uint16_t* ga[2];
-  const uint16_t* gb[2];
+  // global -> register copies: thread = (row t/8 + 64 h, 16-byte chunk t%8) of A and of B
+  constexpr int kRowsPerPass = 512 / kLmCh;
+  constexpr int kPasses = kLmBM / kRowsPerPass;
+  const int crow = tid / kLmCh, cch = tid % kLmCh;
+  const uint16_t* ga[kPasses];
+  const uint16_t* gb[kPasses];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int ra = min(m0 + crow + 128 * h, M - 1);  // clamped rows: valid data, results never stored
-    const int rb = min(v0 + crow + 128 * h, V - 1);
+  for (int h = 0; h < kPasses; ++h) {
+    const int ra = min(m0 + crow + kRowsPerPass * h, M - 1);  // clamped rows: valid data, results never stored
+    const int rb = min(v0 + crow + kRowsPerPass * h, V - 1);
     ga[h] = hidden + (int64_t)ra * ldh + cch * 8;
     gb[h] = weight + (int64_t)rb * ldw + cch * 8;
   }
-  af3_u32x4 ra_[2], rb_[2];
+  af3_u32x4 ra_[kPasses], rb_[kPasses];
   auto gload = [&](int kt) {
+    const bool kin = kt * kLmBK + cch * 8 < H;  // H % 64 == 32: the last k-step is half zeros
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      ra_[h] = *(const af3_u32x4*)(ga[h] + kt * kLmBK);
-      rb_[h] = *(const af3_u32x4*)(gb[h] + kt * kLmBK);
+    for (int h = 0; h < kPasses; ++h) {
+      ra_[h] = kin ? *(const af3_u32x4*)(ga[h] + kt * kLmBK) : (af3_u32x4){0u, 0u, 0u, 0u};
+      rb_[h] = kin ? *(const af3_u32x4*)(gb[h] + kt * kLmBK) : (af3_u32x4){0u, 0u, 0u, 0u};
     }
   };
   auto lstore = [&](int st) {
     uint8_t* base = lds + st * kLmStage;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int row = crow + 128 * h;
-      *(af3_u32x4*)(base + row * 64 + 16 * lm_swz(row, cch)) = ra_[h];
-      *(af3_u32x4*)(base + kLmBM * 64 + row * 64 + 16 * lm_swz(row, cch)) = rb_[h];
+    for (int h = 0; h < kPasses; ++h) {
+      const int row = crow + kRowsPerPass * h;
+      *(af3_u32x4*)(base + row * kLmRowB + 16 * lm_swz(row, cch)) = ra_[h];
+      *(af3_u32x4*)(base + kLmBM * kLmRowB + row * kLmRowB + 16 * lm_swz(row, cch)) = rb_[h];
     }
   };
 
@@ -104,7 +113,7 @@ __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
 #pragma unroll
       for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.f;
 
-  const int nk = H / kLmBK;
+  const int nk = (H + kLmBK - 1) / kLmBK;
   gload(0);
   lstore(0);
   __syncthreads();
@@ -112,20 +121,20 @@ __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
     const int cur = kt & 1;
     if (kt + 1 < nk) gload(kt + 1);
     const uint8_t* As = lds + cur * kLmStage;
-    const uint8_t* Bs = As + kLmBM * 64;
+    const uint8_t* Bs = As + kLmBM * kLmRowB;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < kLmBK / 16; ++ks) {
       const int ch = ks * 2 + (lane >> 5);
       af3_u32x4 af[4], bf[2];
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm) {
         const int row = wm0 + tm * 32 + (lane & 31);
-        af[tm] = *(const af3_u32x4*)(As + row * 64 + 16 * lm_swz(row, ch));
+        af[tm] = *(const af3_u32x4*)(As + row * kLmRowB + 16 * lm_swz(row, ch));
       }
 #pragma unroll
       for (int tn = 0; tn < 2; ++tn) {
         const int row = wn0 + tn * 32 + (lane & 31);
-        bf[tn] = *(const af3_u32x4*)(Bs + row * 64 + 16 * lm_swz(row, ch));
+        bf[tn] = *(const af3_u32x4*)(Bs + row * kLmRowB + 16 * lm_swz(row, ch));
       }
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm)
@@ -268,7 +277,7 @@ extern "C" int af3_lm_head_logprobs(const uint16_t* hidden, int64_t ldh, const u
                                     float* entropy, float* lse, float* ez, void* workspace, size_t ws_bytes,
                                     void* stream_) {
   hipStream_t stream = (hipStream_t)stream_;
-  AF3_REQUIRE(M >= 0 && V > 0 && H > 0 && H % kLmBK == 0, "lm_head_logprobs: H must be a positive multiple of 32");
+  AF3_REQUIRE(M >= 0 && V > 0 && H > 0 && H % 32 == 0, "lm_head_logprobs: H must be a positive multiple of 32");
   if (M == 0) return 0;
   AF3_REQUIRE(hidden && weight && labels && logprobs && entropy && lse && ez && workspace,
               "lm_head_logprobs: null pointer");
@@ -281,8 +290,7 @@ extern "C" int af3_lm_head_logprobs(const uint16_t* hidden, int64_t ldh, const u
   const int grid = lmh_grid(M, V, nm, nv, px);
   float4* partials = (float4*)workspace;
   float* zlab = (float*)((uint8_t*)workspace + (size_t)nv * M * sizeof(float4));
-  const size_t lds_bytes = 2 * kLmStage;
-  hipLaunchKernelGGL(lmh_gemm_kernel<0>, dim3(grid), dim3(512), lds_bytes, stream, hidden, ldh, weight, ldw, M, V, H,
+  hipLaunchKernelGGL(lmh_gemm_kernel<0>, dim3(grid), dim3(512), 0, stream, hidden, ldh, weight, ldw, M, V, H,
                      1.f / temperature, labels, nm, nv, px, partials, zlab, nullptr, nullptr, nullptr, 0, 0.f,
                      nullptr, nullptr, 0);
   int rc = af3::check_launch("lm_head_logprobs (gemm)");
@@ -297,7 +305,7 @@ extern "C" int af3_lm_head_dlogits(const uint16_t* hidden, int64_t ldh, const ui
                                    const float* ez, const float* dlogprobs, int64_t dlp_stride, float dlp_scale,
                                    const float* dentropy, uint16_t* dz, int64_t lddz, void* stream_) {
   hipStream_t stream = (hipStream_t)stream_;
-  AF3_REQUIRE(M >= 0 && V > 0 && H > 0 && H % kLmBK == 0, "lm_head_dlogits: H must be a positive multiple of 32");
+  AF3_REQUIRE(M >= 0 && V > 0 && H > 0 && H % 32 == 0, "lm_head_dlogits: H must be a positive multiple of 32");
   if (M == 0) return 0;
   AF3_REQUIRE(hidden && weight && labels && lse && ez && dlogprobs && dentropy && dz, "lm_head_dlogits: null pointer");
   AF3_REQUIRE(temperature > 0.f, "lm_head_dlogits: temperature must be positive");
@@ -306,8 +314,7 @@ extern "C" int af3_lm_head_dlogits(const uint16_t* hidden, int64_t ldh, const ui
               "lm_head_dlogits: rows must be 16-byte aligned");
   int nm, nv, px;
   const int grid = lmh_grid(M, V, nm, nv, px);
-  const size_t lds_bytes = 2 * kLmStage;
-  hipLaunchKernelGGL(lmh_gemm_kernel<1>, dim3(grid), dim3(512), lds_bytes, stream, hidden, ldh, weight, ldw, M, V, H,
+  hipLaunchKernelGGL(lmh_gemm_kernel<1>, dim3(grid), dim3(512), 0, stream, hidden, ldh, weight, ldw, M, V, H,
                      1.f / temperature, labels, nm, nv, px, nullptr, nullptr, lse, ez, dlogprobs, dlp_stride,
                      dlp_scale, dentropy, dz, lddz);
   return af3::check_launch("lm_head_dlogits");

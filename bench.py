@@ -11,8 +11,8 @@ Inputs are seeded synthetic tensors already resident in HBM.
 Prints ONE JSON line.  ``roofline`` is for the dominant kernel (the grouped
 GEMM instantiation with the largest total time), timed with HIP events on the
 launch stream inside the timed region; ``extra`` holds the standalone dequant
-(cfg 0), LoRA-merge and SwiGLU (cfg 1) bandwidths, the fp8 mode and the cost of
-routing-weight gradients; ``cpu_baseline`` is the PyTorch-eager
+(cfg 0), LoRA-merge and SwiGLU (cfg 1) bandwidths, the fp8 mode, the cost of
+routing-weight gradients and the fused LM head; ``cpu_baseline`` is the PyTorch-eager
 CPU path on a bounded sample (rank 0 only).
 """
 from __future__ import annotations
@@ -236,6 +236,51 @@ def gamma_extras(torch, dev, workloads, inp_cpu, k, steps=10):
     return res
 
 
+def lm_head_extras(torch, dev, M=8192, H=2880, V=201088, reps=3):
+    """The fused LM-head log-probabilities / entropy at the gpt-oss vocabulary:
+    forward kernel (GEMM + softmax statistics, no logits written), the
+    logits-gradient kernel, the whole forward + backward, and a plain hipBLASLt
+    bf16 GEMM of the same shape (logits written) for comparison."""
+    from agent_factory_3_amd import linear_cross_entropy as lce
+    g = torch.Generator().manual_seed(3)
+    h = torch.randn(M, H, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(V, H, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    lab = torch.randint(0, V, (M,), generator=g).to(dev)
+    flops = 2.0 * M * V * H
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / reps
+
+    res = {"shape": {"tokens": M, "hidden": H, "vocab": V}}
+    ms = timed(lambda: lce.lm_head_forward(h, w, lab, 1.0))
+    res["forward"] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12}
+    _, _, lse, ez = lce.lm_head_forward(h, w, lab, 1.0)
+    dlp = torch.randn(M, device=dev)
+    dent = torch.randn(M, device=dev)
+    ms = timed(lambda: lce.lm_head_dlogits(h, w, lab, 1.0, lse, ez, dlp, dent))
+    res["dlogits"] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12}
+    hh = h.detach().requires_grad_(True)
+    ww = w.detach().requires_grad_(True)
+
+    def fwd_bwd():
+        lp, ent = lce.linear_cross_entropy(hh, ww, lab, 1.0, "none")
+        torch.autograd.backward([lp, ent], [dlp, dent])
+    ms = timed(fwd_bwd)
+    res["fwd_bwd"] = {"ms": ms, "tflops": 4 * flops / (ms * 1e-3) / 1e12}
+    ms = timed(lambda: torch.mm(h, w.t()))
+    res["hipblaslt_logits_gemm"] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -355,6 +400,8 @@ def main():
         extra["fp8_mode"] = fp8_extras(torch, dev, kernels, workloads, inp_cpu, k)
         log("routing-weight gradients")
         extra["gamma_grad"] = gamma_extras(torch, dev, workloads, inp_cpu, k)
+        log("LM head")
+        extra["lm_head"] = lm_head_extras(torch, dev)
 
     cpu = None
     if not args.no_cpu_baseline and int(os.environ.get("RANK", "0")) == 0:
