@@ -10,10 +10,9 @@ reference's ``quantizer_config.py:49-226``:
 * checkpoint ``*_blocks`` / ``*_scales`` are stored as-is (bf16 containers),
   or, with ``dequantize=True``, expanded to bf16 weights by the HIP dequant.
 
-Differences: only ``dequant_dtype="bf16"`` is accepted (the fp8 mode is not
-implemented), the environment check asks for a ROCm GPU with the built HIP
+Differences: the environment check asks for a ROCm GPU with the built HIP
 library instead of Triton / the kernels hub, and nothing is fetched from the
-network.  Importing this module registers the config (once per process).
+network.  ``dequant_dtype`` "bf16" and "fp8" are both served by the HIP path.  Importing this module registers the config (once per process).
 """
 from __future__ import annotations
 
@@ -53,8 +52,8 @@ class Mxfp4Bf16DequantQuantizer(HfQuantizer):
     def validate_environment(self, *args, **kwargs):
         if getattr(self.quantization_config, "dequantize", False):
             return
-        if getattr(self.quantization_config, "dequant_dtype", "bf16") != "bf16":
-            raise ValueError("mxfp4_bf16_dequant on MI355X implements dequant_dtype='bf16' only")
+        if getattr(self.quantization_config, "dequant_dtype", "bf16") not in ("bf16", "fp8"):
+            raise ValueError("dequant_dtype must be 'bf16' or 'fp8'")
         if not torch.cuda.is_available():
             raise RuntimeError("MXFP4 dequant requires a GPU")
         from . import _capi
