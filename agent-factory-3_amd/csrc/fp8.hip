@@ -105,6 +105,61 @@ __device__ __forceinline__ uint32_t f8_e4m3_to_bf16(uint32_t c) {
 // One row per block: amax over the row (fp32), scale = max(amax, 1e-12) / 448,
 // codes = E4M3(x * (1 / scale)).  Optionally also the codes' values as bf16
 // (the activation operand of the MXFP4 grouped GEMM in fp8 mode).
+// One wave per row, the whole row held in registers (up to CPL 8-element chunks
+// per lane, K <= 512 * CPL): a single HBM pass, the row maximum by a wave
+// shuffle reduction, then the codes from the registers.  Four rows per block.
+template <int CPL>
+__global__ __launch_bounds__(256) void quant_e4m3_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M,
+                                                              int K, uint8_t* __restrict__ out, int64_t ld_out,
+                                                              float* __restrict__ scale,
+                                                              uint16_t* __restrict__ out_bf16, int64_t ld_bf16) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;  // wave-uniform
+  const int lane = threadIdx.x & 63;
+  const int nch = K >> 3;
+  const uint16_t* xr = x + row * ldx;
+  af3_u32x4 v[CPL];
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + 64 * j;
+    v[j] = c < nch ? __builtin_nontemporal_load((const af3_u32x4*)(xr + c * 8)) : (af3_u32x4){0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int j = 0; j < CPL; ++j)
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+      amax = fmaxf(amax, fmaxf(fabsf(af3_bf16_to_f32(v[j][h] & 0xFFFFu)), fabsf(af3_bf16_to_f32(v[j][h] >> 16))));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  const float sc = __fdiv_rn(fmaxf(amax, 1e-12f), 448.0f);
+  const float inv = __fdiv_rn(1.0f, sc);
+  if (lane == 0) scale[row] = sc;
+  uint8_t* orow = out + row * ld_out;
+  uint16_t* brow = out_bf16 ? out_bf16 + row * ld_bf16 : nullptr;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + 64 * j;
+    if (c >= nch) break;
+    uint32_t q[8];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      q[2 * h] = f8_e4m3_rne_sat(af3_bf16_to_f32(v[j][h] & 0xFFFFu) * inv);
+      q[2 * h + 1] = f8_e4m3_rne_sat(af3_bf16_to_f32(v[j][h] >> 16) * inv);
+    }
+    typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+    __builtin_nontemporal_store((u32x2){q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24),
+                                        q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24)},
+                                (u32x2*)(orow + c * 8));
+    if (brow)
+      __builtin_nontemporal_store(af3_u32x4{f8_e4m3_to_bf16(q[0]) | (f8_e4m3_to_bf16(q[1]) << 16),
+                                            f8_e4m3_to_bf16(q[2]) | (f8_e4m3_to_bf16(q[3]) << 16),
+                                            f8_e4m3_to_bf16(q[4]) | (f8_e4m3_to_bf16(q[5]) << 16),
+                                            f8_e4m3_to_bf16(q[6]) | (f8_e4m3_to_bf16(q[7]) << 16)},
+                                  (af3_u32x4*)(brow + c * 8));
+  }
+}
+
 __global__ __launch_bounds__(256) void quant_e4m3_kernel(const uint16_t* __restrict__ x, int64_t ldx, int K,
                                                         uint8_t* __restrict__ out, int64_t ld_out,
                                                         float* __restrict__ scale, uint16_t* __restrict__ out_bf16,
@@ -195,7 +250,17 @@ extern "C" int af3_quantize_per_token_e4m3(const uint16_t* x, int64_t ldx, int64
                   (!out_bf16 || (ld_bf16 % 8 == 0 && ((uintptr_t)out_bf16 & 15) == 0)),
               "quantize_per_token_e4m3: rows must be 16-byte aligned (bf16) / 8-byte aligned (fp8)");
   AF3_REQUIRE(M <= 0x7fffffffLL, "quantize_per_token_e4m3: too many rows");
-  hipLaunchKernelGGL(quant_e4m3_kernel, dim3((unsigned)M), dim3(256), 0, stream, x, ldx, K, out, ld_out, scale,
-                     out_bf16, ld_bf16);
+  if (K % 8 == 0 && K <= 512 * 12) {
+    const unsigned grid = (unsigned)af3_cdiv(M, 4);
+    if (K <= 512 * 6)
+      hipLaunchKernelGGL(quant_e4m3_rows_kernel<6>, dim3(grid), dim3(256), 0, stream, x, ldx, M, K, out, ld_out,
+                         scale, out_bf16, ld_bf16);
+    else
+      hipLaunchKernelGGL(quant_e4m3_rows_kernel<12>, dim3(grid), dim3(256), 0, stream, x, ldx, M, K, out, ld_out,
+                         scale, out_bf16, ld_bf16);
+  } else {
+    hipLaunchKernelGGL(quant_e4m3_kernel, dim3((unsigned)M), dim3(256), 0, stream, x, ldx, K, out, ld_out, scale,
+                       out_bf16, ld_bf16);
+  }
   return af3::check_launch("quantize_per_token_e4m3");
 }

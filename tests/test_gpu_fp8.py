@@ -46,7 +46,7 @@ def test_e5m2_colmajor(dev):
     assert np.array_equal(_u8(out), fp8.e5m2_colmajor(blocks, scales))
 
 
-@pytest.mark.parametrize("M,K", [(257, 2880), (33, 100), (1, 8)])
+@pytest.mark.parametrize("M,K", [(257, 2880), (129, 5760), (66, 6144), (5, 6152), (33, 100), (1, 8)])
 def test_quantize_per_token(dev, M, K):
     g = torch.Generator().manual_seed(M + K)
     x = (torch.randn(M, K, generator=g) * torch.logspace(-4, 4, M)[:, None]).to(torch.bfloat16)
