@@ -15,9 +15,10 @@
 // which two plain GEMMs turn into d_hidden = dz W and d_weight = dz^T hidden.
 //
 // lmh_gemm_kernel<MODE>: one 256 (rows) x 256 (vocabulary) tile per block of
-// 8 waves (2 x 4, 128 x 64 each), v_mfma_f32_32x32x16_bf16, 64-deep k-steps
-// double-buffered through registers and LDS (16-byte chunks XOR-swizzled by
-// row / 2 so the fragment reads of 16 lanes hit distinct banks).  Blocks are ordered
+// 8 waves (2 x 4, 128 x 64 each), v_mfma_f32_32x32x16_bf16, 32-deep k-steps in a
+// 4-stage global->LDS ring (global_load_lds_dwordx4, three k-steps ahead, one
+// barrier per k-step; 16-byte chunks XOR-swizzled by row / 4 so the fragment
+// reads of 16 lanes hit distinct banks).  Blocks are ordered
 // vocabulary-tile-major and dealt to the XCDs in contiguous runs, so the row
 // tiles that reuse one W tile run together on one L2.
 //   MODE 0: per row and tile, (max, sum exp, sum exp * z) over the tile's 256
@@ -30,16 +31,32 @@
 
 namespace {
 
-constexpr int kLmBM = 256, kLmBN = 256, kLmBK = 64;
+constexpr int kLmBM = 256, kLmBN = 256, kLmBK = 32;
+constexpr int kLmStages = 4;
 constexpr int kLmRowB = kLmBK * 2;   // bytes per tile row and k-step
 constexpr int kLmCh = kLmRowB / 16;   // 16-byte chunks per row
-constexpr int kLmStage = (kLmBM + kLmBN) * kLmBK * 2;  // bytes per stage (A then B)
-static_assert(2 * kLmStage <= 160 * 1024, "gfx950 LDS per workgroup");
+constexpr int kLmStage = (kLmBM + kLmBN) * kLmRowB;  // bytes per stage (A then B)
+constexpr int kLmCopies = kLmBM * kLmRowB / 1024 / 8;  // 1 KB copy instructions per wave and operand
+static_assert(kLmBM == kLmBN && kLmCopies * 8 * 1024 == kLmBM * kLmRowB, "copy plan covers each operand once");
+static_assert(kLmStages * kLmStage <= 160 * 1024, "gfx950 LDS per workgroup");
 
-// 16-byte chunk position of (row, chunk) in a 128-byte LDS row: rows of one parity
-// spread their chunks over 8 positions, so 16 lanes reading one chunk of 16 rows hit
+// 16-byte chunk position of (row, chunk) in a 64-byte LDS row: rows 4 apart (same
+// banks) take different positions, so 16 lanes reading one chunk of 16 rows hit
 // distinct banks
-__device__ __forceinline__ int lm_swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+__device__ __forceinline__ int lm_swz(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
+
+// global -> LDS copy of 16 bytes per lane (lane i lands at m0 + 16 i); issued by
+// inline assembly with explicit vmcnt waits, so the compiler's wait-count pass
+// places no wait for the whole ring before the first LDS read of a stage
+__device__ __forceinline__ void lm_dma16(const void* gptr, uint32_t lds_byte_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_byte_addr)
+               : "memory", "m0");
+}
+#define LM_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
+#define LM_BARRIER() asm volatile("s_barrier" ::: "memory")
+__device__ __forceinline__ uint32_t lm_lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
 
 __device__ __forceinline__ float wave32_max(float v) {
 #pragma unroll
@@ -62,7 +79,7 @@ __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
     // MODE 1
     const float* __restrict__ lse, const float* __restrict__ ez, const float* __restrict__ dlp, int64_t dlp_stride,
     float dlp_scale, const float* __restrict__ dent, uint16_t* __restrict__ dz, int64_t lddz) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kLmStage];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kLmStages * kLmStage];
   const int xcd = blockIdx.x & 7;
   const int tile = xcd * per_xcd + (int)(blockIdx.x >> 3);
   if (tile >= n_mtiles * n_vtiles || tile >= (xcd + 1) * per_xcd) return;
@@ -73,36 +90,27 @@ __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
   const int w = tid >> 6, lane = tid & 63;
   const int wm0 = (w >> 2) * 128, wn0 = (w & 3) * 64;
 
-  // global -> register copies: thread = (row t/8 + 64 h, 16-byte chunk t%8) of A and of B
-  constexpr int kRowsPerPass = 512 / kLmCh;
-  constexpr int kPasses = kLmBM / kRowsPerPass;
-  const int crow = tid / kLmCh, cch = tid % kLmCh;
-  const uint16_t* ga[kPasses];
-  const uint16_t* gb[kPasses];
+  // global -> LDS copies: stage slot q (16 bytes) of the A (B) half holds row q / 4,
+  // chunk (q % 4) ^ swizzle(row); wave w copies slots (w * kLmCopies + j) * 64 + lane
+  const uint16_t* src[2 * kLmCopies];
+  uint32_t dst_off[2 * kLmCopies];
 #pragma unroll
-  for (int h = 0; h < kPasses; ++h) {
-    const int ra = min(m0 + crow + kRowsPerPass * h, M - 1);  // clamped rows: valid data, results never stored
-    const int rb = min(v0 + crow + kRowsPerPass * h, V - 1);
-    ga[h] = hidden + (int64_t)ra * ldh + cch * 8;
-    gb[h] = weight + (int64_t)rb * ldw + cch * 8;
+  for (int j = 0; j < kLmCopies; ++j) {
+    const int q = (w * kLmCopies + j) * 64 + lane;
+    const int row = q / kLmCh;
+    const int ch = (q % kLmCh) ^ ((row >> 2) & 3);
+    src[j] = hidden + (int64_t)min(m0 + row, M - 1) * ldh + ch * 8;             // clamped rows: results never stored
+    src[kLmCopies + j] = weight + (int64_t)min(v0 + row, V - 1) * ldw + ch * 8;
+    dst_off[j] = (uint32_t)((w * kLmCopies + j) * 1024);
+    dst_off[kLmCopies + j] = (uint32_t)(kLmBM * kLmRowB + (w * kLmCopies + j) * 1024);
   }
-  af3_u32x4 ra_[kPasses], rb_[kPasses];
-  auto gload = [&](int kt) {
-    const bool kin = kt * kLmBK + cch * 8 < H;  // H % 64 == 32: the last k-step is half zeros
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lm_lds_addr(lds));
+  const int nk = (H + kLmBK - 1) / kLmBK;  // H % 32 == 0
+  auto issue = [&](int kt) {
+    const uint32_t base = lds0 + (uint32_t)((kt % kLmStages) * kLmStage);
 #pragma unroll
-    for (int h = 0; h < kPasses; ++h) {
-      ra_[h] = kin ? *(const af3_u32x4*)(ga[h] + kt * kLmBK) : (af3_u32x4){0u, 0u, 0u, 0u};
-      rb_[h] = kin ? *(const af3_u32x4*)(gb[h] + kt * kLmBK) : (af3_u32x4){0u, 0u, 0u, 0u};
-    }
-  };
-  auto lstore = [&](int st) {
-    uint8_t* base = lds + st * kLmStage;
-#pragma unroll
-    for (int h = 0; h < kPasses; ++h) {
-      const int row = crow + kRowsPerPass * h;
-      *(af3_u32x4*)(base + row * kLmRowB + 16 * lm_swz(row, cch)) = ra_[h];
-      *(af3_u32x4*)(base + kLmBM * kLmRowB + row * kLmRowB + 16 * lm_swz(row, cch)) = rb_[h];
-    }
+    for (int j = 0; j < 2 * kLmCopies; ++j)
+      lm_dma16(src[j] + kt * kLmBK, __builtin_amdgcn_readfirstlane(base + dst_off[j]));  // wave-uniform
   };
 
   af3_f32x16 acc[4][2];
@@ -113,14 +121,20 @@ __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
 #pragma unroll
       for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.f;
 
-  const int nk = (H + kLmBK - 1) / kLmBK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
+#pragma unroll
+  for (int kt = 0; kt < kLmStages - 1; ++kt)
+    if (kt < nk) issue(kt);
   for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) gload(kt + 1);
-    const uint8_t* As = lds + cur * kLmStage;
+    // this wave's copies of k-step kt have landed once at most those of kt+1 and kt+2 are in flight
+    if (kt + 2 < nk)
+      LM_WAIT_VM(8);
+    else if (kt + 1 < nk)
+      LM_WAIT_VM(4);
+    else
+      LM_WAIT_VM(0);
+    LM_BARRIER();  // every wave's copies of kt visible; every wave done with kt-1's stage
+    if (kt + kLmStages - 1 < nk) issue(kt + kLmStages - 1);
+    const uint8_t* As = lds + (kt % kLmStages) * kLmStage;
     const uint8_t* Bs = As + kLmBM * kLmRowB;
 #pragma unroll
     for (int ks = 0; ks < kLmBK / 16; ++ks) {
@@ -144,9 +158,8 @@ __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
                                                                 __builtin_bit_cast(af3_bf16x8, bf[tn]),
                                                                 acc[tm][tn], 0, 0, 0);
     }
-    if (kt + 1 < nk) lstore(cur ^ 1);
-    __syncthreads();
   }
+  __syncthreads();  // all fragment reads done before the epilogue reuses the LDS
 
   const int c0 = v0 + wn0 + (lane & 31);  // this lane's columns c0 and c0 + 32
   if constexpr (MODE == 0) {
