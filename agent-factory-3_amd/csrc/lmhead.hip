@@ -15,10 +15,10 @@
 // which two plain GEMMs turn into d_hidden = dz W and d_weight = dz^T hidden.
 //
 // lmh_gemm_kernel<MODE>: one 256 (rows) x 256 (vocabulary) tile per block of
-// 8 waves (2 x 4, 128 x 64 each), v_mfma_f32_32x32x16_bf16, 32-deep k-steps in a
-// 4-stage global->LDS ring (global_load_lds_dwordx4, three k-steps ahead, one
-// barrier per k-step; 16-byte chunks XOR-swizzled by row / 4 so the fragment
-// reads of 16 lanes hit distinct banks).  Blocks are ordered
+// 8 waves (2 x 4, 128 x 64 each), v_mfma_f32_32x32x16_bf16, a 128 KB global->LDS
+// ring (global_load_lds_dwordx4): 64-deep k-steps in 2 stages when H % 64 == 0,
+// else 32-deep in 4 stages; one barrier per k-step; 16-byte chunks XOR-swizzled
+// so the fragment reads of 16 lanes hit distinct banks.  Blocks are ordered
 // vocabulary-tile-major and dealt to the XCDs in contiguous runs, so the row
 // tiles that reuse one W tile run together on one L2.
 //   MODE 0: per row and tile, (max, sum exp, sum exp * z) over the tile's 256
@@ -31,19 +31,27 @@
 
 namespace {
 
-constexpr int kLmBM = 256, kLmBN = 256, kLmBK = 32;
-constexpr int kLmStages = 4;
-constexpr int kLmRowB = kLmBK * 2;   // bytes per tile row and k-step
-constexpr int kLmCh = kLmRowB / 16;   // 16-byte chunks per row
-constexpr int kLmStage = (kLmBM + kLmBN) * kLmRowB;  // bytes per stage (A then B)
-constexpr int kLmCopies = kLmBM * kLmRowB / 1024 / 8;  // 1 KB copy instructions per wave and operand
-static_assert(kLmBM == kLmBN && kLmCopies * 8 * 1024 == kLmBM * kLmRowB, "copy plan covers each operand once");
-static_assert(kLmStages * kLmStage <= 160 * 1024, "gfx950 LDS per workgroup");
+constexpr int kLmBM = 256, kLmBN = 256;
+constexpr int kLmLds = 128 * 1024;
 
-// 16-byte chunk position of (row, chunk) in a 64-byte LDS row: rows 4 apart (same
-// banks) take different positions, so 16 lanes reading one chunk of 16 rows hit
-// distinct banks
-__device__ __forceinline__ int lm_swz(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
+// Ring geometry per k-step depth: 64 (H % 64 == 0; 2 stages, one k-step ahead)
+// or 32 (4 stages, three ahead), 128 KB either way.
+template <int BK>
+struct LmRing {
+  static constexpr int kRowB = BK * 2;                      // bytes per tile row and k-step
+  static constexpr int kCh = kRowB / 16;                    // 16-byte chunks per row
+  static constexpr int kStage = (kLmBM + kLmBN) * kRowB;    // bytes per stage (A then B)
+  static constexpr int kStages = kLmLds / kStage;
+  static constexpr int kCopies = kLmBM * kRowB / 1024 / 8;  // 1 KB copy instructions per wave and operand
+  static_assert(kLmBM == kLmBN && kCopies * 8 * 1024 == kLmBM * kRowB, "copy plan covers each operand once");
+  static_assert(kStages >= 2 && kStages <= 4, "ring depth");
+  // 16-byte chunk position of (row, chunk) in an LDS row: rows that share banks
+  // (4 apart for 64-byte rows, 2 apart for 128-byte rows) take different positions,
+  // so 16 lanes reading one chunk of 16 rows hit distinct banks; an involution
+  static __device__ __forceinline__ int swz(int row, int chunk) {
+    return kCh == 4 ? chunk ^ ((row >> 2) & 3) : chunk ^ ((row >> 1) & 7);
+  }
+};
 
 // global -> LDS copy of 16 bytes per lane (lane i lands at m0 + 16 i); issued by
 // inline assembly with explicit vmcnt waits, so the compiler's wait-count pass
@@ -52,7 +60,10 @@ __device__ __forceinline__ void lm_dma16(const void* gptr, uint32_t lds_byte_add
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_byte_addr)
                : "memory", "m0");
 }
-#define LM_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
+template <int N>
+__device__ __forceinline__ void lm_wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 #define LM_BARRIER() asm volatile("s_barrier" ::: "memory")
 __device__ __forceinline__ uint32_t lm_lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
@@ -70,7 +81,7 @@ __device__ __forceinline__ float wave32_sum(float v) {
   return v;
 }
 
-template <int MODE>
+template <int MODE, int BK>
 __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
     const uint16_t* __restrict__ hidden, int64_t ldh, const uint16_t* __restrict__ weight, int64_t ldw, int M, int V,
     int H, float rcp_t, const int64_t* __restrict__ labels, int n_mtiles, int n_vtiles, int per_xcd,
@@ -79,7 +90,10 @@ __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
     // MODE 1
     const float* __restrict__ lse, const float* __restrict__ ez, const float* __restrict__ dlp, int64_t dlp_stride,
     float dlp_scale, const float* __restrict__ dent, uint16_t* __restrict__ dz, int64_t lddz) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kLmStages * kLmStage];
+  using Ring = LmRing<BK>;
+  constexpr int kLmBK = BK, kLmRowB = Ring::kRowB, kLmCh = Ring::kCh, kLmStage = Ring::kStage;
+  constexpr int kLmStages = Ring::kStages, kLmCopies = Ring::kCopies;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kLmLds];
   const int xcd = blockIdx.x & 7;
   const int tile = xcd * per_xcd + (int)(blockIdx.x >> 3);
   if (tile >= n_mtiles * n_vtiles || tile >= (xcd + 1) * per_xcd) return;
@@ -98,14 +112,14 @@ __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
   for (int j = 0; j < kLmCopies; ++j) {
     const int q = (w * kLmCopies + j) * 64 + lane;
     const int row = q / kLmCh;
-    const int ch = (q % kLmCh) ^ ((row >> 2) & 3);
+    const int ch = Ring::swz(row, q % kLmCh);  // the swizzle is an involution
     src[j] = hidden + (int64_t)min(m0 + row, M - 1) * ldh + ch * 8;             // clamped rows: results never stored
     src[kLmCopies + j] = weight + (int64_t)min(v0 + row, V - 1) * ldw + ch * 8;
     dst_off[j] = (uint32_t)((w * kLmCopies + j) * 1024);
     dst_off[kLmCopies + j] = (uint32_t)(kLmBM * kLmRowB + (w * kLmCopies + j) * 1024);
   }
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lm_lds_addr(lds));
-  const int nk = (H + kLmBK - 1) / kLmBK;  // H % 32 == 0
+  const int nk = H / kLmBK;  // H % BK == 0 (the host picks BK)
   auto issue = [&](int kt) {
     const uint32_t base = lds0 + (uint32_t)((kt % kLmStages) * kLmStage);
 #pragma unroll
@@ -125,13 +139,16 @@ __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
   for (int kt = 0; kt < kLmStages - 1; ++kt)
     if (kt < nk) issue(kt);
   for (int kt = 0; kt < nk; ++kt) {
-    // this wave's copies of k-step kt have landed once at most those of kt+1 and kt+2 are in flight
-    if (kt + 2 < nk)
-      LM_WAIT_VM(8);
-    else if (kt + 1 < nk)
-      LM_WAIT_VM(4);
+    // this wave's copies of k-step kt have landed once at most those of the (up to
+    // kLmStages - 2) later k-steps already issued are in flight
+    constexpr int kCpw = 2 * kLmCopies;
+    const int newer = min(kLmStages - 2, nk - 1 - kt);
+    if (newer >= 2)
+      lm_wait_vm<2 * kCpw>();
+    else if (newer == 1)
+      lm_wait_vm<kCpw>();
     else
-      LM_WAIT_VM(0);
+      lm_wait_vm<0>();
     LM_BARRIER();  // every wave's copies of kt visible; every wave done with kt-1's stage
     if (kt + kLmStages - 1 < nk) issue(kt + kLmStages - 1);
     const uint8_t* As = lds + (kt % kLmStages) * kLmStage;
@@ -143,12 +160,12 @@ __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm) {
         const int row = wm0 + tm * 32 + (lane & 31);
-        af[tm] = *(const af3_u32x4*)(As + row * kLmRowB + 16 * lm_swz(row, ch));
+        af[tm] = *(const af3_u32x4*)(As + row * kLmRowB + 16 * Ring::swz(row, ch));
       }
 #pragma unroll
       for (int tn = 0; tn < 2; ++tn) {
         const int row = wn0 + tn * 32 + (lane & 31);
-        bf[tn] = *(const af3_u32x4*)(Bs + row * kLmRowB + 16 * lm_swz(row, ch));
+        bf[tn] = *(const af3_u32x4*)(Bs + row * kLmRowB + 16 * Ring::swz(row, ch));
       }
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm)
@@ -303,9 +320,14 @@ extern "C" int af3_lm_head_logprobs(const uint16_t* hidden, int64_t ldh, const u
   const int grid = lmh_grid(M, V, nm, nv, px);
   float4* partials = (float4*)workspace;
   float* zlab = (float*)((uint8_t*)workspace + (size_t)nv * M * sizeof(float4));
-  hipLaunchKernelGGL(lmh_gemm_kernel<0>, dim3(grid), dim3(512), 0, stream, hidden, ldh, weight, ldw, M, V, H,
-                     1.f / temperature, labels, nm, nv, px, partials, zlab, nullptr, nullptr, nullptr, 0, 0.f,
-                     nullptr, nullptr, 0);
+  if (H % 64 == 0)
+    hipLaunchKernelGGL((lmh_gemm_kernel<0, 64>), dim3(grid), dim3(512), 0, stream, hidden, ldh, weight, ldw, M, V, H,
+                       1.f / temperature, labels, nm, nv, px, partials, zlab, nullptr, nullptr, nullptr, 0, 0.f,
+                       nullptr, nullptr, 0);
+  else
+    hipLaunchKernelGGL((lmh_gemm_kernel<0, 32>), dim3(grid), dim3(512), 0, stream, hidden, ldh, weight, ldw, M, V, H,
+                       1.f / temperature, labels, nm, nv, px, partials, zlab, nullptr, nullptr, nullptr, 0, 0.f,
+                       nullptr, nullptr, 0);
   int rc = af3::check_launch("lm_head_logprobs (gemm)");
   if (rc) return rc;
   hipLaunchKernelGGL(lmh_reduce_kernel, dim3((unsigned)af3_cdiv(M, 256)), dim3(256), 0, stream, partials, M, nv, zlab,
@@ -327,8 +349,13 @@ extern "C" int af3_lm_head_dlogits(const uint16_t* hidden, int64_t ldh, const ui
               "lm_head_dlogits: rows must be 16-byte aligned");
   int nm, nv, px;
   const int grid = lmh_grid(M, V, nm, nv, px);
-  hipLaunchKernelGGL(lmh_gemm_kernel<1>, dim3(grid), dim3(512), 0, stream, hidden, ldh, weight, ldw, M, V, H,
-                     1.f / temperature, labels, nm, nv, px, nullptr, nullptr, lse, ez, dlogprobs, dlp_stride,
-                     dlp_scale, dentropy, dz, lddz);
+  if (H % 64 == 0)
+    hipLaunchKernelGGL((lmh_gemm_kernel<1, 64>), dim3(grid), dim3(512), 0, stream, hidden, ldh, weight, ldw, M, V, H,
+                       1.f / temperature, labels, nm, nv, px, nullptr, nullptr, lse, ez, dlogprobs, dlp_stride,
+                       dlp_scale, dentropy, dz, lddz);
+  else
+    hipLaunchKernelGGL((lmh_gemm_kernel<1, 32>), dim3(grid), dim3(512), 0, stream, hidden, ldh, weight, ldw, M, V, H,
+                       1.f / temperature, labels, nm, nv, px, nullptr, nullptr, lse, ez, dlogprobs, dlp_stride,
+                       dlp_scale, dentropy, dz, lddz);
   return af3::check_launch("lm_head_dlogits");
 }
