@@ -69,16 +69,31 @@ __device__ __forceinline__ uint32_t lm_lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
+// Reductions over each 32-lane half of a wave, every lane receiving the result:
+// DPP quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror (partners
+// within 4, 8 and 16 lanes), then ds_swizzle xor 16 (bit mode, and 0x1f).
+template <int CTRL>
+__device__ __forceinline__ float lm_dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lm_xor16(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+
 __device__ __forceinline__ float wave32_max(float v) {
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 32));
-  return v;
+  v = fmaxf(v, lm_dpp<0xB1>(v));
+  v = fmaxf(v, lm_dpp<0x4E>(v));
+  v = fmaxf(v, lm_dpp<0x141>(v));
+  v = fmaxf(v, lm_dpp<0x140>(v));
+  return fmaxf(v, lm_xor16(v));
 }
 
 __device__ __forceinline__ float wave32_sum(float v) {
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 32);
-  return v;
+  v += lm_dpp<0xB1>(v);
+  v += lm_dpp<0x4E>(v);
+  v += lm_dpp<0x141>(v);
+  v += lm_dpp<0x140>(v);
+  return v + lm_xor16(v);
 }
 
 template <int MODE, int BK>
