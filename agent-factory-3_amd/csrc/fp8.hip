@@ -28,21 +28,56 @@ __device__ __forceinline__ uint32_t f8_e5m2_bits(uint32_t nib, int scale_adj) {
 
 // row-major: group g, byte j -> out[g][2j] (lo nibble), out[g][2j+1] (hi), as
 // the uint16 (lo | hi << 8) the reference stores (kernels.py:80-84).  A lane
-// converts 4 packed bytes into one 8-byte store.
-__global__ __launch_bounds__(256) void e5m2_rows_kernel(const uint32_t* __restrict__ blocks,
-                                                       const uint8_t* __restrict__ scales, uint2* __restrict__ out,
-                                                       int64_t n_words) {
-  const int64_t w = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (w >= n_words) return;
-  const uint32_t v = blocks[w];
-  const int adj = (int)scales[w >> 2] - 113;
+// converts 4 packed bytes into one 8-byte store, four words per lane; scale
+// bytes 114..141 take a byte-table path, the others the integer rule above.
+__device__ __forceinline__ void e5m2_word(uint32_t v, uint32_t S, uint32_t& o0, uint32_t& o1) {
+  if (S - 114u <= 27u) {
+    // every nonzero code lands inside E5M2 (exponent 1..31): the magnitude byte is a
+    // table of the 3-bit code, (S - 113) * 4 + {0, 0, 4, 6, 8, 10, 12, 14} (0 for
+    // code 0), looked up for four nibbles at once with v_perm_b32; the sign bit is
+    // the nibble's bit 3 moved to bit 7
+    const uint32_t a = (S - 113u) << 2;
+    const uint32_t tlo = a * 0x01010100u + 0x06040000u, thi = a * 0x01010101u + 0x0E0C0A08u;
+    const uint32_t lo = __builtin_amdgcn_perm(thi, tlo, v & 0x07070707u) | ((v & 0x08080808u) << 4);
+    const uint32_t hi = __builtin_amdgcn_perm(thi, tlo, (v >> 4) & 0x07070707u) | (v & 0x80808080u);
+    o0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+    o1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+    return;
+  }
+  const int adj = (int)S - 113;
   uint32_t h[4];
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     const uint32_t byte = (v >> (8 * b)) & 0xFFu;
     h[b] = (f8_e5m2_bits(byte & 0xFu, adj) | (f8_e5m2_bits(byte >> 4, adj) << 8)) & 0xFFFFu;
   }
-  out[w] = uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+  o0 = h[0] | (h[1] << 16);
+  o1 = h[2] | (h[3] << 16);
+}
+
+constexpr int kE5Words = 4;
+
+__global__ __launch_bounds__(256) void e5m2_rows_kernel(const uint32_t* __restrict__ blocks,
+                                                       const uint8_t* __restrict__ scales, uint2* __restrict__ out,
+                                                       int64_t n_words) {
+  typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+  const int64_t base = (int64_t)blockIdx.x * (256 * kE5Words) + threadIdx.x;
+  uint32_t v[kE5Words], S[kE5Words];
+#pragma unroll
+  for (int i = 0; i < kE5Words; ++i) {
+    const int64_t w = base + (int64_t)i * 256;
+    const bool ok = w < n_words;
+    v[i] = ok ? __builtin_nontemporal_load(blocks + w) : 0u;
+    S[i] = ok ? (uint32_t)scales[w >> 2] : 127u;
+  }
+#pragma unroll
+  for (int i = 0; i < kE5Words; ++i) {
+    const int64_t w = base + (int64_t)i * 256;
+    if (w >= n_words) break;
+    uint32_t o0, o1;
+    e5m2_word(v[i], S[i], o0, o1);
+    __builtin_nontemporal_store((u32x2){o0, o1}, (u32x2*)(out + w));
+  }
 }
 
 // column-major: out[e][k][n] (n contiguous), each value truncated to a byte
@@ -220,7 +255,7 @@ extern "C" int af3_mxfp4_to_fp8_e5m2(const uint8_t* blocks, const uint8_t* scale
   AF3_REQUIRE(((uintptr_t)blocks & 3) == 0 && ((uintptr_t)out & 7) == 0,
               "mxfp4_to_fp8_e5m2: blocks must be 4-byte and out 8-byte aligned");
   const int64_t n_words = n_groups * 4;
-  const int64_t grid = af3_cdiv(n_words, 256);
+  const int64_t grid = af3_cdiv(n_words, 256 * kE5Words);
   AF3_REQUIRE(grid <= 0x7fffffffLL, "mxfp4_to_fp8_e5m2: tensor too large");
   hipLaunchKernelGGL(e5m2_rows_kernel, dim3((unsigned)grid), dim3(256), 0, stream, (const uint32_t*)blocks, scales,
                      (uint2*)out, n_words);
