@@ -33,6 +33,10 @@ namespace {
 
 constexpr int kLmBM = 256, kLmBN = 256;
 constexpr int kLmLds = 128 * 1024;
+// waves: 2 along the rows (128 each) x kLmWN along the vocabulary columns
+constexpr int kLmWN = 4;
+constexpr int kLmWaves = 2 * kLmWN, kLmThreads = 64 * kLmWaves;
+constexpr int kLmTN = kLmBN / kLmWN / 32;  // 32-column sub-tiles per wave
 
 // Ring geometry per k-step depth: 64 (H % 64 == 0; 2 stages, one k-step ahead)
 // or 32 (4 stages, three ahead), 128 KB either way.
@@ -42,8 +46,8 @@ struct LmRing {
   static constexpr int kCh = kRowB / 16;                    // 16-byte chunks per row
   static constexpr int kStage = (kLmBM + kLmBN) * kRowB;    // bytes per stage (A then B)
   static constexpr int kStages = kLmLds / kStage;
-  static constexpr int kCopies = kLmBM * kRowB / 1024 / 8;  // 1 KB copy instructions per wave and operand
-  static_assert(kLmBM == kLmBN && kCopies * 8 * 1024 == kLmBM * kRowB, "copy plan covers each operand once");
+  static constexpr int kCopies = kLmBM * kRowB / 1024 / kLmWaves;  // 1 KB copies per wave and operand
+  static_assert(kLmBM == kLmBN && kCopies * kLmWaves * 1024 == kLmBM * kRowB, "copy plan covers each operand once");
   static_assert(kStages >= 2 && kStages <= 4, "ring depth");
   // 16-byte chunk position of (row, chunk) in an LDS row: rows that share banks
   // (4 apart for 64-byte rows, 2 apart for 128-byte rows) take different positions,
@@ -97,7 +101,7 @@ __device__ __forceinline__ float wave32_sum(float v) {
 }
 
 template <int MODE, int BK>
-__global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
+__global__ __launch_bounds__(kLmThreads, 1) void lmh_gemm_kernel(
     const uint16_t* __restrict__ hidden, int64_t ldh, const uint16_t* __restrict__ weight, int64_t ldw, int M, int V,
     int H, float rcp_t, const int64_t* __restrict__ labels, int n_mtiles, int n_vtiles, int per_xcd,
     // MODE 0
@@ -117,7 +121,7 @@ __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
   const int m0 = mt * kLmBM, v0 = vt * kLmBN;
   const int tid = threadIdx.x;
   const int w = tid >> 6, lane = tid & 63;
-  const int wm0 = (w >> 2) * 128, wn0 = (w & 3) * 64;
+  const int wm0 = (w / kLmWN) * 128, wn0 = (w % kLmWN) * (kLmBN / kLmWN);
 
   // global -> LDS copies: stage slot q (16 bytes) of the A (B) half holds row q / 4,
   // chunk (q % 4) ^ swizzle(row); wave w copies slots (w * kLmCopies + j) * 64 + lane
@@ -142,11 +146,11 @@ __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
       lm_dma16(src[j] + kt * kLmBK, __builtin_amdgcn_readfirstlane(base + dst_off[j]));  // wave-uniform
   };
 
-  af3_f32x16 acc[4][2];
+  af3_f32x16 acc[4][kLmTN];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < kLmTN; ++j)
 #pragma unroll
       for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.f;
 
@@ -171,21 +175,21 @@ __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
 #pragma unroll
     for (int ks = 0; ks < kLmBK / 16; ++ks) {
       const int ch = ks * 2 + (lane >> 5);
-      af3_u32x4 af[4], bf[2];
+      af3_u32x4 af[4], bf[kLmTN];
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm) {
         const int row = wm0 + tm * 32 + (lane & 31);
         af[tm] = *(const af3_u32x4*)(As + row * kLmRowB + 16 * Ring::swz(row, ch));
       }
 #pragma unroll
-      for (int tn = 0; tn < 2; ++tn) {
+      for (int tn = 0; tn < kLmTN; ++tn) {
         const int row = wn0 + tn * 32 + (lane & 31);
         bf[tn] = *(const af3_u32x4*)(Bs + row * kLmRowB + 16 * Ring::swz(row, ch));
       }
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm)
 #pragma unroll
-        for (int tn = 0; tn < 2; ++tn)
+        for (int tn = 0; tn < kLmTN; ++tn)
           acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(af3_bf16x8, af[tm]),
                                                                 __builtin_bit_cast(af3_bf16x8, bf[tn]),
                                                                 acc[tm][tn], 0, 0, 0);
@@ -193,41 +197,57 @@ __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
   }
   __syncthreads();  // all fragment reads done before the epilogue reuses the LDS
 
-  const int c0 = v0 + wn0 + (lane & 31);  // this lane's columns c0 and c0 + 32
+  const int c0 = v0 + wn0 + (lane & 31);  // this lane's columns c0 + 32 tn
   if constexpr (MODE == 0) {
-    float* part = (float*)lds;  // [256 rows][4 column waves][3]
+    float* part = (float*)lds;  // [256 rows][kLmWN column waves][3]
 #pragma unroll
     for (int tm = 0; tm < 4; ++tm) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int rl = wm0 + tm * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
         const int row = m0 + rl;
-        const float z0 = acc[tm][0][i] * rcp_t, z1 = acc[tm][1][i] * rcp_t;
-        const bool ok0 = c0 < V, ok1 = c0 + 32 < V;
-        const float mx = wave32_max(fmaxf(ok0 ? z0 : -INFINITY, ok1 ? z1 : -INFINITY));
-        const float e0 = ok0 ? __expf(z0 - mx) : 0.f, e1 = ok1 ? __expf(z1 - mx) : 0.f;
-        const float s = wave32_sum(e0 + e1);
-        const float t = wave32_sum((ok0 ? e0 * z0 : 0.f) + (ok1 ? e1 * z1 : 0.f));
+        float z[kLmTN];
+        bool ok[kLmTN];
+        float lm = -INFINITY;
+#pragma unroll
+        for (int tn = 0; tn < kLmTN; ++tn) {
+          z[tn] = acc[tm][tn][i] * rcp_t;
+          ok[tn] = c0 + 32 * tn < V;
+          lm = fmaxf(lm, ok[tn] ? z[tn] : -INFINITY);
+        }
+        const float mx = wave32_max(lm);
+        float se = 0.f, te = 0.f;
+#pragma unroll
+        for (int tn = 0; tn < kLmTN; ++tn) {
+          const float e = ok[tn] ? __expf(z[tn] - mx) : 0.f;
+          se += e;
+          te += ok[tn] ? e * z[tn] : 0.f;
+        }
+        const float s = wave32_sum(se);
+        const float t = wave32_sum(te);
         if ((lane & 31) == 0) {
-          float* pp = part + (rl * 4 + (w & 3)) * 3;
+          float* pp = part + (rl * kLmWN + (w % kLmWN)) * 3;
           pp[0] = mx;
           pp[1] = s;
           pp[2] = t;
         }
         if (row < M) {
           const int64_t lab = labels[row];
-          if (ok0 && lab == c0) zlab[row] = z0;
-          if (ok1 && lab == c0 + 32) zlab[row] = z1;
+#pragma unroll
+          for (int tn = 0; tn < kLmTN; ++tn)
+            if (ok[tn] && lab == c0 + 32 * tn) zlab[row] = z[tn];
         }
       }
     }
     __syncthreads();
     if (tid < kLmBM && m0 + tid < M) {
-      const float* pp = part + tid * 12;
-      float mx = fmaxf(fmaxf(pp[0], pp[3]), fmaxf(pp[6], pp[9]));
+      const float* pp = part + tid * 3 * kLmWN;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < kLmWN; ++q) mx = fmaxf(mx, pp[3 * q]);
       float s = 0.f, t = 0.f;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < kLmWN; ++q) {
         const float f = pp[3 * q] == -INFINITY ? 0.f : __expf(pp[3 * q] - mx);
         s += pp[3 * q + 1] * f;
         t += pp[3 * q + 2] * f;
@@ -258,7 +278,7 @@ __global__ __launch_bounds__(512, 1) void lmh_gemm_kernel(
         const int lab = __float_as_int(r[4]);
         uint16_t* drow = dz + (int64_t)row * lddz;
 #pragma unroll
-        for (int tn = 0; tn < 2; ++tn) {
+        for (int tn = 0; tn < kLmTN; ++tn) {
           const int c = c0 + tn * 32;
           if (c >= V) continue;
           const float z = acc[tm][tn][i] * rcp_t;
@@ -336,11 +356,11 @@ extern "C" int af3_lm_head_logprobs(const uint16_t* hidden, int64_t ldh, const u
   float4* partials = (float4*)workspace;
   float* zlab = (float*)((uint8_t*)workspace + (size_t)nv * M * sizeof(float4));
   if (H % 64 == 0)
-    hipLaunchKernelGGL((lmh_gemm_kernel<0, 64>), dim3(grid), dim3(512), 0, stream, hidden, ldh, weight, ldw, M, V, H,
+    hipLaunchKernelGGL((lmh_gemm_kernel<0, 64>), dim3(grid), dim3(kLmThreads), 0, stream, hidden, ldh, weight, ldw, M, V, H,
                        1.f / temperature, labels, nm, nv, px, partials, zlab, nullptr, nullptr, nullptr, 0, 0.f,
                        nullptr, nullptr, 0);
   else
-    hipLaunchKernelGGL((lmh_gemm_kernel<0, 32>), dim3(grid), dim3(512), 0, stream, hidden, ldh, weight, ldw, M, V, H,
+    hipLaunchKernelGGL((lmh_gemm_kernel<0, 32>), dim3(grid), dim3(kLmThreads), 0, stream, hidden, ldh, weight, ldw, M, V, H,
                        1.f / temperature, labels, nm, nv, px, partials, zlab, nullptr, nullptr, nullptr, 0, 0.f,
                        nullptr, nullptr, 0);
   int rc = af3::check_launch("lm_head_logprobs (gemm)");
@@ -365,11 +385,11 @@ extern "C" int af3_lm_head_dlogits(const uint16_t* hidden, int64_t ldh, const ui
   int nm, nv, px;
   const int grid = lmh_grid(M, V, nm, nv, px);
   if (H % 64 == 0)
-    hipLaunchKernelGGL((lmh_gemm_kernel<1, 64>), dim3(grid), dim3(512), 0, stream, hidden, ldh, weight, ldw, M, V, H,
+    hipLaunchKernelGGL((lmh_gemm_kernel<1, 64>), dim3(grid), dim3(kLmThreads), 0, stream, hidden, ldh, weight, ldw, M, V, H,
                        1.f / temperature, labels, nm, nv, px, nullptr, nullptr, lse, ez, dlogprobs, dlp_stride,
                        dlp_scale, dentropy, dz, lddz);
   else
-    hipLaunchKernelGGL((lmh_gemm_kernel<1, 32>), dim3(grid), dim3(512), 0, stream, hidden, ldh, weight, ldw, M, V, H,
+    hipLaunchKernelGGL((lmh_gemm_kernel<1, 32>), dim3(grid), dim3(kLmThreads), 0, stream, hidden, ldh, weight, ldw, M, V, H,
                        1.f / temperature, labels, nm, nv, px, nullptr, nullptr, lse, ez, dlogprobs, dlp_stride,
                        dlp_scale, dentropy, dz, lddz);
   return af3::check_launch("lm_head_dlogits");
