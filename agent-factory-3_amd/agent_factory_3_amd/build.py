@@ -33,6 +33,9 @@ HIPCC_FLAGS = [
     # packed fp32 VALU forms are kept out of the generated code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
+    # inline assembly must not clobber registers the compiler reserves (m0 is
+    # passed to the LDS-DMA statements as an input operand instead)
+    "-Werror=inline-asm",
     "-Wno-unused-function",
     "-Wno-unused-variable",
 ]

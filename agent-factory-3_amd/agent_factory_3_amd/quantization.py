@@ -637,7 +637,9 @@ class _GateUpSwiGLU(torch.autograd.Function):
                 gu, act = res
         ctx.mark_non_differentiable(act)
         ctx.set_materialize_grads(False)
-        ctx.save_for_backward(xg, A, B, L)
+        # the input is needed only for the LoRA weight gradient dA (the
+        # reference's DequantMoEMatmul saves nothing, quantization.py:364-373)
+        ctx.save_for_backward(xg if A is not None else None, A, B, L)
         ctx.scaling = float(scaling)
         ctx.experts_module = experts_module
         ctx.proj_name = proj_name
@@ -695,7 +697,11 @@ class _SwiGLUDown(torch.autograd.Function):
             y = moe_rows(act, blocks, scales, bias, routing_data, None, gammas, False, L, B)
             if scatter_indx is not None:
                 y = moe_combine(y, scatter_indx, k_act)
-        ctx.save_for_backward(gate_up, act, A, B, L)
+        # gate_up (the SwiGLU's input, the same bytes as the reference's saved
+        # clamped gate / up pair, quantization.py:434-436) is always needed;
+        # act only for the LoRA weight gradient dA and the routing-weight gradient
+        keep_act = A is not None or ctx.needs_input_grad[10]
+        ctx.save_for_backward(gate_up, act if keep_act else None, A, B, L)
         ctx.scaling = float(scaling)
         ctx.experts_module = experts_module
         ctx.proj_name = proj_name

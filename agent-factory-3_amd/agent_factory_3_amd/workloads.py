@@ -31,8 +31,8 @@ def gen(cfg: int) -> torch.Generator:
 def mxfp4_weight(g: torch.Generator, shape_rows: tuple, k: int, scale_lo: int = 118, scale_hi: int = 130):
     """Packed codes uniform over all 16 nibbles, e8m0 scales uniform in [lo, hi]."""
     G = k // 32
-    blocks = torch.randint(0, 256, (*shape_rows, G, 16), generator=g, dtype=torch.int32).to(torch.uint8)
-    scales = torch.randint(scale_lo, scale_hi + 1, (*shape_rows, G), generator=g, dtype=torch.int32).to(torch.uint8)
+    blocks = torch.randint(0, 256, (*shape_rows, G, 16), generator=g, dtype=torch.uint8)
+    scales = torch.randint(scale_lo, scale_hi + 1, (*shape_rows, G), generator=g, dtype=torch.uint8)
     return blocks, scales
 
 

@@ -61,8 +61,7 @@ struct LmRing {
 // inline assembly with explicit vmcnt waits, so the compiler's wait-count pass
 // places no wait for the whole ring before the first LDS read of a stage
 __device__ __forceinline__ void lm_dma16(const void* gptr, uint32_t lds_byte_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_byte_addr)
-               : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(lds_byte_addr) : "memory");
 }
 template <int N>
 __device__ __forceinline__ void lm_wait_vm() {

@@ -1036,8 +1036,7 @@ __device__ __forceinline__ int g4_b_off(int n, int h) {
 // alone; the loop waits for them explicitly (vmcnt) and publishes a stage with
 // a bare s_barrier.  All three are compiler memory barriers.
 __device__ __forceinline__ void g4_dma16(const void* gptr, uint32_t lds_byte_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_byte_addr)
-               : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(lds_byte_addr) : "memory");
 }
 #define AF3_ASM_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
 #define AF3_ASM_BARRIER() asm volatile("s_barrier" ::: "memory")
@@ -1682,8 +1681,7 @@ __global__ __launch_bounds__(256) void gemm4_dgrad_kernel(Params p) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) g4_dma16(bsrc[j] + kb * bstep, bb + j * 1024);
     const uint32_t sb = lds0 + (uint32_t)(kD4OffS + slot * kD4SStage + wave * 256);
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_ushort %0, off" ::"v"(ssrc + kb * sstep), "s"(sb)
-                 : "memory", "m0");
+    asm volatile("s_nop 0\n\tglobal_load_lds_ushort %0, off" ::"v"(ssrc + kb * sstep), "{m0}"(sb) : "memory");
   };
   auto issue_a = [&](int ka, int j) {  // A instruction j (0..7) of k-step ka
     g4_dma16(arow[j] + ka * kBK,
@@ -2113,9 +2111,7 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
     } else if (j < AI + BI) {
       g4_dma16(bsrc[j - AI] + kc * bstep, st + (uint32_t)(BOFF + (wave * BI + j - AI) * 1024));
     } else {
-      asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_ubyte %0, off" ::"v"(ssrc[j - AI - BI] + kc * sstep),
-                   "s"(st + (uint32_t)(SOFF + (wave * SI + j - AI - BI) * 256))
-                   : "memory", "m0");
+      asm volatile("s_nop 0\n\tglobal_load_lds_ubyte %0, off" ::"v"(ssrc[j - AI - BI] + kc * sstep), "{m0}"(st + (uint32_t)(SOFF + (wave * SI + j - AI - BI) * 256)) : "memory");
     }
   };
   auto issue = [&](int kc) {

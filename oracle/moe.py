@@ -44,18 +44,59 @@ def rows(x, W, offs, gather=None, k=1, bias=None, gammas=None, trans=False, lora
         if hi <= lo:
             continue
         idx = (gather[lo:hi].long() // k) if gather is not None else torch.arange(lo, hi)
-        We = W[e].to(acc)
-        out = xf[idx] @ (We if trans else We.T)
-        if lora_l is not None:
-            Le = lora_l[lo:hi].to(acc)
-            Be = lora_b[e].to(acc)
-            out = out + (Le @ Be if trans else Le @ Be.T)
-        if bias is not None:
-            out = out + bias[e].to(acc)
-        if gammas is not None:
-            out = out * gammas[lo:hi, None].to(acc)
-        y[lo:hi] = out
+        y[lo:hi] = _expert_acc(xf[idx], W[e], trans, None if lora_l is None else lora_l[lo:hi],
+                               None if lora_b is None else lora_b[e], None if bias is None else bias[e],
+                               None if gammas is None else gammas[lo:hi], acc)
     return y.to(rd)
+
+
+def _expert_acc(xe, We, trans, Le, Be, be, ge, acc, mag=False):
+    """One expert's rows in ``acc``: xe @ We^T (trans: xe @ We) [+ Le @ Be^T (Le @ Be)]
+    [+ be] [* ge].  ``mag``: the same products over absolute values instead
+    (the sum of |term| per output, scaled by |ge|; bias not included)."""
+    f = (lambda t: t.to(acc).abs()) if mag else (lambda t: t.to(acc))  # noqa: E731
+    W = f(We)
+    out = f(xe) @ (W if trans else W.T)
+    if Le is not None:
+        B = f(Be)
+        out = out + f(Le) @ (B if trans else B.T)
+    if be is not None and not mag:
+        out = out + be.to(acc)
+    if ge is not None:
+        out = out * f(ge)[:, None]
+    return out
+
+
+def expert_rows(x, We, idx, trans=False, lora_l=None, lora_b=None, bias=None, gammas=None):
+    """Rows of one expert as ``rows`` computes them (fp32 sums, one bf16
+    rounding) and, for tolerances, the fp32 sum of the magnitudes of their
+    terms: (bf16 [n, N], float32 [n, N]).  ``idx``: the source rows of x;
+    ``We`` [N, K] float32; lora_l / gammas: the expert's rows; lora_b, bias:
+    the expert's slices."""
+    xe = x[idx]
+    out = _expert_acc(xe, We, trans, lora_l, lora_b, bias, gammas, F32)
+    mag = _expert_acc(xe, We, trans, lora_l, lora_b, None, gammas, F32, mag=True)
+    return out.to(BF16), mag
+
+
+def expert_lora_rows(x, Wl, idx, scale, trans=False):
+    """One expert of ``lora_rows``: s * x[idx] @ Wl^T (trans: @ Wl) and its term magnitudes."""
+    xe = x[idx].to(F32)
+    W = Wl.to(F32)
+    out = scale * (xe @ (W if trans else W.T))
+    mag = abs(scale) * (xe.abs() @ (W.abs() if trans else W.abs().T))
+    return out.to(BF16), mag
+
+
+def expert_wgrad(a_e, b_e, rowscale=None):
+    """One expert of ``wgrad``: bf16(rs * a_e)^T @ b_e (fp32 sum, one bf16
+    rounding) and the magnitudes of its terms.  a_e, b_e: the expert's rows
+    (already gathered), rowscale its row scales."""
+    ae = a_e.to(F32)
+    if rowscale is not None:
+        ae = (ae * rowscale.to(F32)[:, None]).to(BF16).to(F32)
+    bf = b_e.to(F32)
+    return (ae.T @ bf).to(BF16), ae.abs().T @ bf.abs()
 
 
 def combine(r, gate_indx, k, rd=BF16):

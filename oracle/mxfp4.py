@@ -86,3 +86,21 @@ def dequant_f32(blocks, scales) -> torch.Tensor:
     b = blocks.numpy() if isinstance(blocks, torch.Tensor) else blocks
     s = scales.numpy() if isinstance(scales, torch.Tensor) else scales
     return torch.from_numpy(bits_to_f32(dequant_bits(b, s)).copy())
+
+
+_TABLE_F32 = None
+
+
+def dequant_f32_table(blocks, scales) -> torch.Tensor:
+    """float32 weight [..., G*32]: the values of ``dequant_f32`` looked up in the
+    exhaustive [256 scales x 16 nibbles] table of ``nibble_to_bf16_bits``
+    (same rule and layout, fast enough for whole experts at gpt-oss size)."""
+    global _TABLE_F32
+    if _TABLE_F32 is None:
+        _TABLE_F32 = torch.from_numpy(bits_to_f32(exhaustive_table()).reshape(-1).copy())
+    b = torch.as_tensor(blocks).to(torch.int64)
+    s = torch.as_tensor(scales).to(torch.int64).unsqueeze(-1) * 16
+    out = torch.empty(*b.shape, 2, dtype=torch.float32)
+    out[..., 0] = _TABLE_F32[s + (b & 15)]
+    out[..., 1] = _TABLE_F32[s + (b >> 4)]
+    return out.reshape(*b.shape[:-2], b.shape[-2] * 32)

@@ -125,7 +125,7 @@ def test_dgrad_tiles(dev, cfg, gather, lora, odd):
         Q.GEMM_TILE.update(old)
     W = mxfp4.dequant_f32(blocks, scales)
     yr = moe.rows(x, W, ref["offs"], ref["topk_indx"] if gather else None, TOPK,
-                  gammas=ref["gate_scal"] if gather else None, trans=True, lora_l=L, lora_b=Ax)
+                  gammas=gam.cpu() if gather else None, trans=True, lora_l=L, lora_b=Ax)
     assert y.shape == (Rr, NOUT)
     a = y.float().cpu().double()
     assert torch.isfinite(a).all()
