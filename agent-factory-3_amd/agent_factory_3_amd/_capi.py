@@ -32,6 +32,8 @@ _SIGNATURES = {
     "af3_routing_workspace_bytes": (_sz, [_i64, _i32, _i32]),
     "af3_routing_replay": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _sz, _p]),
     "af3_routing_topk": (_i32, [_p, _i64, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _sz, _p]),
+    "af3_routing_scratch_bytes": (_sz, []),
+    "af3_routing_replay_noalloc": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p]),
     "af3_expt_data": (_i32, [_p, _i32, _p, _i32, _i32, _p, _p, _p]),
     "af3_tile_order": (_i32, [_p, _i32, _i32, _p, _i32, _p, _p]),
     "af3_moe_gemm": (_i32, [_p, _i64, _p, _i32, _p, _p, _i32, _p, _p, _i32, _p, _i64, _p, _i32,

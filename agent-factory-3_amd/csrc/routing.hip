@@ -21,6 +21,8 @@
 // earlier in its chunk keeps the order of the flat index.  Entries whose
 // expert id is outside [0, E) are dropped (gate_indx = -1), the same shape the
 // reference gives expert-parallel-masked entries.
+#include <mutex>
+
 #include "af3_common.h"
 
 namespace {
@@ -394,6 +396,59 @@ extern "C" int af3_routing_replay(const uint16_t* logits, int64_t ld_logits, con
   AF3_REQUIRE(expt_indx || n_tokens == 0, "routing_replay: null expt_indx");
   return routing_common(false, logits, ld_logits, expt_indx, n_tokens, n_expts_tot, n_expts_act, gate_scal, hist,
                         topk_indx, gate_indx, token_offs_raw, workspace, ws_bytes, (hipStream_t)stream);
+}
+
+// ---- allocation-free routing replay --------------------------------------
+// The workspace of af3_routing_replay (ids, softmax weights, per-chunk counts;
+// every byte is written before it is read, so nothing needs clearing) lives in
+// this file-scope device array.  Each device holds its own copy; host code
+// never passes the array's name to a kernel (on the host it only names the
+// symbol), it passes the device address taken once per device with
+// hipGetSymbolAddress.
+constexpr size_t kRoutingScratchBytes = size_t(4) << 20;
+static __device__ __align__(256) unsigned char scratch[kRoutingScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+extern "C" size_t af3_routing_scratch_bytes(void) { return kRoutingScratchBytes; }
+
+extern "C" int af3_routing_replay_noalloc(const uint16_t* logits, int64_t ld_logits, const int32_t* expt_indx,
+                                          int64_t n_tokens, int n_expts_tot, int n_expts_act, uint16_t* gate_scal,
+                                          int32_t* hist, int32_t* topk_indx, int32_t* gate_indx,
+                                          int32_t* token_offs_raw, void* stream) {
+  AF3_REQUIRE(expt_indx || n_tokens == 0, "routing_replay_noalloc: null expt_indx");
+  AF3_REQUIRE(n_tokens >= 0 && n_expts_tot > 0 && n_expts_act > 0, "routing_replay_noalloc: bad sizes");
+  const size_t need = af3_routing_workspace_bytes(n_tokens, n_expts_tot, n_expts_act);
+  AF3_REQUIRE(need <= kRoutingScratchBytes,
+              "routing_replay_noalloc: T=%lld E=%d K=%d needs %zu scratch bytes, the built-in buffer holds %zu "
+              "(use af3_routing_replay with a workspace)",
+              (long long)n_tokens, n_expts_tot, n_expts_act, need, kRoutingScratchBytes);
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    af3::set_error("routing_replay_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  AF3_REQUIRE(dev >= 0 && dev < kMaxDevices, "routing_replay_noalloc: device %d out of range", dev);
+  void* ws = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {  // first call on this device: its copy of the array
+      e = hipGetSymbolAddress(&g_scratch_ptr[dev], HIP_SYMBOL(scratch));
+      if (e != hipSuccess) {
+        g_scratch_ptr[dev] = nullptr;
+        af3::set_error("routing_replay_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+        return (int)e;
+      }
+    }
+    ws = g_scratch_ptr[dev];
+  }
+  return routing_common(false, logits, ld_logits, expt_indx, n_tokens, n_expts_tot, n_expts_act, gate_scal, hist,
+                        topk_indx, gate_indx, token_offs_raw, ws, kRoutingScratchBytes, (hipStream_t)stream);
 }
 
 extern "C" int af3_routing_topk(const uint16_t* logits, int64_t ld_logits, int64_t n_tokens, int n_expts_tot,

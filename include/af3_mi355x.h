@@ -72,6 +72,21 @@ int af3_routing_replay(const uint16_t* logits, int64_t ld_logits, const int32_t*
                        int32_t* gate_indx, int32_t* token_offs_raw, void* workspace, size_t ws_bytes,
                        void* stream);
 
+/* Allocation-free variant of af3_routing_replay (no counterpart in the
+ * reference): same arguments and outputs without the workspace, which comes
+ * from a built-in per-device scratch array of af3_routing_scratch_bytes()
+ * (4 MiB: T*K up to ~500k rows at E = 128).  For callers that cannot
+ * allocate device memory (HIP graph capture, tight serving loops).  Makes no
+ * allocation; a shape needing more than the array returns AF3_EINVAL with a
+ * message.  Calls that overlap on one device share its array and race: issue
+ * them on one stream.  The first call on a device takes the array's address
+ * (hipGetSymbolAddress). */
+size_t af3_routing_scratch_bytes(void);
+int af3_routing_replay_noalloc(const uint16_t* logits, int64_t ld_logits, const int32_t* expt_indx,
+                               int64_t n_tokens, int n_expts_tot, int n_expts_act, uint16_t* gate_scal,
+                               int32_t* hist, int32_t* topk_indx, int32_t* gate_indx, int32_t* token_offs_raw,
+                               void* stream);
+
 /* Top-K routing.  Replaces triton_kernels.routing.routing as called at
  * quantization.py:651,664 (torch restatement: routing_torch_dist,
  * quantization.py:551-590 at world size 1).  Same outputs as above. */

@@ -44,6 +44,19 @@ def test_library_loads_and_reports_abi():
     assert _capi.workspace_bytes(16, 4, 2) > 0
 
 
+def test_noalloc_routing_rejects_shapes_beyond_its_scratch():
+    """af3_routing_replay_noalloc checks the shape against its built-in scratch
+    array before touching the device (no GPU needed for the error path)."""
+    from agent_factory_3_amd import _capi
+    if not _capi.lib_path().exists():
+        pytest.skip("library not built")
+    lib = _capi.load()
+    T, E, K = 1 << 20, 128, 4
+    assert _capi.workspace_bytes(T, E, K) > int(lib.af3_routing_scratch_bytes()) == 4 << 20
+    with pytest.raises(RuntimeError, match="scratch"):
+        _capi.call("af3_routing_replay_noalloc", 1, E, 1, T, E, K, 1, 1, 1, 1, 1, None)
+
+
 def test_product_path_has_no_oracle_dependency():
     pkg = ROOT / "agent-factory-3_amd" / "agent_factory_3_amd"
     for f in pkg.glob("*.py"):
