@@ -412,13 +412,16 @@ def main():
             sample = (f"rows of experts {r['sample_experts']} ({r['sample_rows']} rows) fwd+bwd with LoRA, plus "
                       f"their MXFP4 dequant; scaled to {E} experts dequantized twice and {T * k} rows "
                       f"(sample wall {r['sample_wall_s']:.1f} s)")
+            r.update(cpu_baseline.host_info())
         else:
-            r = cpu_baseline.run_layer(inp_cpu)
-            sample = (f"the whole layer once: all {E} experts' MXFP4 weights dequantized (LUT + ldexp) for the "
-                      f"forward and again for the backward, then the per-expert bf16 loop over all {T * k} routed "
-                      f"rows, fwd+bwd with LoRA (wall {r['t_layer_s']:.1f} s)")
+            r = cpu_baseline.run_layer(inp_cpu, warmup=1, runs=1)
+            sample = (f"the whole layer (after one untimed warm-up pass): all {E} experts' MXFP4 weights dequantized "
+                      f"(LUT + ldexp) for the forward and again for the backward ({r['dequant_s']:.1f} s), then the "
+                      f"per-expert bf16 loop over all {T * k} routed rows, fwd+bwd with LoRA ({r['loop_s']:.1f} s); "
+                      f"wall {r['t_layer_s']:.1f} s")
         cpu = {"value": r["tokens_per_s"], "unit": "tokens/s", "cores": r["threads"], "kind": "port",
-               "sample": sample, "dequant_s_per_expert": r["dequant_s_per_expert"],
+               "sample": sample, "cpu_model": r["cpu_model"], "affinity_cores": r["affinity_cores"],
+               "omp_num_threads": r["omp_num_threads"], "dequant_s_per_expert": r["dequant_s_per_expert"],
                "loop_s_per_row": r["loop_s_per_row"]}
         log(f"cpu baseline {r['tokens_per_s']:.1f} tokens/s")
 

@@ -37,9 +37,27 @@ def _swiglu(gu):
 
 
 def threads() -> int:
+    """Every core this process may run on (its affinity mask), limited only by
+    OMP_NUM_THREADS where the environment sets it (the GPU box sets it to the
+    one-GPU share of the host)."""
     n = len(os.sched_getaffinity(0))
-    cap = int(os.environ.get("OMP_NUM_THREADS", n))
-    return max(1, min(n, cap, 16))
+    cap = os.environ.get("OMP_NUM_THREADS")
+    return max(1, min(n, int(cap))) if cap and cap.isdigit() and int(cap) > 0 else n
+
+
+def host_info() -> dict:
+    """CPU model, affinity core count and the OMP_NUM_THREADS setting of this host."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "affinity_cores": len(os.sched_getaffinity(0)),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"), "threads": threads()}
 
 
 def _expert_step(inp, e, W, ids, gam, s):
@@ -64,9 +82,18 @@ def _expert_step(inp, e, W, ids, gam, s):
     return tok.numel()
 
 
-def run_layer(inp) -> dict:
-    """The whole layer once on the CPU (inp: workloads.LayerInputs on the CPU)."""
+def run_layer(inp, warmup: int = 1, runs: int = 1) -> dict:
+    """The whole layer on the CPU (inp: workloads.LayerInputs on the CPU):
+    ``warmup`` untimed passes, then the median of ``runs`` timed passes."""
     torch.set_num_threads(threads())
+    res = [_layer_once(inp) for _ in range(warmup + runs)][warmup:]
+    res.sort(key=lambda r: r["t_layer_s"])
+    out = dict(res[len(res) // 2])
+    out.update(host_info(), warmup=warmup, runs=runs)
+    return out
+
+
+def _layer_once(inp) -> dict:
     E = inp.gu_blocks.shape[0]
     ids = inp.expt_indx.long()
     T = inp.x.shape[0]
@@ -88,8 +115,9 @@ def run_layer(inp) -> dict:
     del W
     t_layer = t3 - t0
     t_deq = (t1 - t0) + (t3 - t2)
-    return dict(tokens_per_s=T / t_layer, t_layer_s=t_layer, dequant_s_per_expert=t_deq / (2 * E),
-                loop_s_per_row=(t2 - t1) / max(1, rows), rows=rows, threads=torch.get_num_threads())
+    return dict(tokens_per_s=T / t_layer, t_layer_s=t_layer, dequant_s=t_deq, dequant_s_per_expert=t_deq / (2 * E),
+                loop_s=t2 - t1, loop_s_per_row=(t2 - t1) / max(1, rows), rows=rows,
+                threads_used=torch.get_num_threads())
 
 
 def run_sample(inp, ranks=(0, 10, 60, 110)) -> dict:
