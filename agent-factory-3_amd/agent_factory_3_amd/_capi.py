@@ -35,6 +35,7 @@ _SIGNATURES = {
     "af3_routing_scratch_bytes": (_sz, []),
     "af3_routing_replay_noalloc": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p]),
     "af3_expt_data": (_i32, [_p, _i32, _p, _i32, _i32, _p, _p, _p]),
+    "af3_router_logits": (_i32, [_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _p, _i64, _p]),
     "af3_tile_order": (_i32, [_p, _i32, _i32, _p, _i32, _p, _p]),
     "af3_moe_gemm": (_i32, [_p, _i64, _p, _i32, _p, _p, _i32, _p, _p, _i32, _p, _i64, _p, _i32,
                             _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p]),

@@ -53,7 +53,7 @@ from . import _capi, kernels
 from .kernels import mxfp4_to_bf16_hip, swiglu_backward_raw, swiglu_forward
 from .routing import (  # noqa: F401  (re-exported names of the routing layer)
     ExptData, GatherIndx, RoutingData, ScatterIndx, compute_expt_data, compute_expt_data_torch,
-    dense_routing, routing, routing_replay,
+    dense_routing, router_linear, routing, routing_replay,
 )
 
 GEMM_BLOCK_M = 128
@@ -935,8 +935,9 @@ def mlp_forward(self, hidden_states, router_indices=None):
         router_indices = current_router_indices(self)
     batch_size = hidden_states.shape[0]
     hidden_states = hidden_states.reshape(-1, self.router.hidden_dim)
-    router_logits = nn.functional.linear(hidden_states, self.router.weight, self.router.bias)
-    with on_device(router_logits.device):
+    with on_device(hidden_states.device):
+        # router GEMM on the HIP kernel (the reference's nn.functional.linear, quantization.py:654)
+        router_logits = router_linear(hidden_states, self.router.weight, self.router.bias)
         if router_indices is not None:
             expt_indx = router_indices.reshape(-1, self.router.top_k).to(device=router_logits.device,
                                                                          dtype=torch.int32)

@@ -235,3 +235,56 @@ def dense_routing(n_rows: int, device) -> RoutingData:
     """Single-expert routing (matmul_ogs with routing_data=None)."""
     hist = torch.tensor([n_rows], dtype=torch.int32, device=device)
     return RoutingData(None, hist, 1, 1, compute_expt_data(hist, 1, n_rows))
+
+
+# ---------------------------------------------------------------------------
+# router logits (quantization.py:653-654: nn.functional.linear(hidden, router.weight, router.bias))
+# ---------------------------------------------------------------------------
+
+def router_logits_hip(hidden: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+    """logits [T, E] bf16 = bf16(hidden @ weight^T + bias) with fp32 sums (af3_router_logits).
+    hidden [T, H] bf16, weight [E, H] bf16, bias [E] bf16 or None; H % 64 == 0, E <= 256."""
+    if not hidden.is_cuda:
+        raise RuntimeError("router_logits: hidden must be a GPU tensor (no CPU implementation)")
+    for name, t in (("hidden", hidden), ("weight", weight)) + ((("bias", bias),) if bias is not None else ()):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"router_logits: {name} must be bfloat16 (got {t.dtype})")
+    x = hidden if hidden.stride(-1) == 1 and hidden.data_ptr() % 16 == 0 and hidden.stride(0) % 8 == 0 \
+        else hidden.contiguous()
+    w = weight.contiguous()
+    T, H = x.shape
+    E = w.shape[0]
+    if w.shape[1] != H:
+        raise ValueError(f"router_logits: weight is {tuple(w.shape)}, hidden has {H} columns")
+    b = bias.contiguous() if bias is not None else None
+    out = torch.empty(T, E, dtype=torch.bfloat16, device=x.device)
+    if T:
+        _capi.call("af3_router_logits", x.data_ptr(), x.stride(0) if T > 1 else H, w.data_ptr(), w.stride(0),
+                   _capi.ptr(b), T, H, E, out.data_ptr(), E, _capi.stream_of(x.device))
+    return out
+
+
+class RouterLinear(torch.autograd.Function):
+    """Router logits with the HIP kernel in the forward; the backward (needed
+    only when a loss reads the logits, e.g. routing-weight gradients or an
+    auxiliary loss) is two plain GEMMs and a column sum, as F.linear's."""
+
+    @staticmethod
+    def forward(ctx, hidden, weight, bias):
+        ctx.save_for_backward(hidden, weight)
+        ctx.has_bias = bias is not None
+        return router_logits_hip(hidden, weight, bias)
+
+    @staticmethod
+    def backward(ctx, g):
+        hidden, weight = ctx.saved_tensors
+        g = g.to(torch.bfloat16)
+        dh = g @ weight if ctx.needs_input_grad[0] else None
+        dw = g.t() @ hidden if ctx.needs_input_grad[1] else None
+        db = g.float().sum(0).to(torch.bfloat16) if ctx.has_bias and ctx.needs_input_grad[2] else None
+        return dh, dw, db
+
+
+def router_linear(hidden: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+    """The router's nn.functional.linear on the HIP kernel (autograd-aware)."""
+    return RouterLinear.apply(hidden, weight, bias)

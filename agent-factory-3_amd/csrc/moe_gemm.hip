@@ -1077,38 +1077,39 @@ __device__ __forceinline__ af3_bf16x8 g4_bfrag(uint32_t v, uint32_t sc, float sc
 // sub-step (zeros before the first k-step), whose MFMAs run first and cover
 // the LDS reads and B conversions of this k-step's sub-step 0; this k-step's
 // sub-step 3 leaves in af[1] / bf[1].  FULL: every sub-tile live.
+// sc[] enters holding this k-step's e8m0 bytes and leaves holding the next
+// k-step's (the scales stay in LDS for the whole work item, so they are read
+// a k-step ahead and the k-step starts without waiting for them).
 // Instruction order is fixed by scheduling barriers: the conversions of the
-// next sub-step's B fragments and the k-step's DPW global->LDS copies are
-// spread between the MFMAs, and the A-fragment LDS reads of sub-step s + 1
-// are issued ahead of the MFMAs of sub-step s.
+// next sub-step's B fragments take the last TN MFMA slots of a sub-step (so
+// the packed B bytes read after the k-step's barrier have the sub-step's
+// first MFMAs to land), the k-step's DPW global->LDS copies are spread
+// between the MFMAs, and the A-fragment LDS reads of sub-step s + 1 are
+// issued ahead of the MFMAs of sub-step s.
 template <int TM, int TN, int DPW, bool FULL, bool EXACT, class Dma>
 __device__ __forceinline__ void g4_kstep(const uint16_t* as, const uint8_t* bs, const uint8_t* ss, int G, int kt,
-                                         int wm0, int wn0, int tm_live, int tn_live, af3_f32x16 acc[TM][TN],
-                                         af3_bf16x8 af[2][TM], af3_bf16x8 bf[2][TN], Dma&& dma) {
+                                         bool more, int wm0, int wn0, int tm_live, int tn_live,
+                                         af3_f32x16 acc[TM][TN], af3_bf16x8 af[2][TM], af3_bf16x8 bf[2][TN],
+                                         uint32_t sc[TN], Dma&& dma) {
   constexpr int NM = TM * TN * 4;      // MFMAs per k-step
   constexpr int GAP = NM / (DPW + 1);  // MFMAs between copies
+  constexpr int NS = TM * TN;          // MFMAs per sub-step
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
   af3_u32x4 bp[TN];
-  uint32_t sc[TN];
   float scf[TN];
+  uint32_t sc_next[TN];
   // (partial tiles: no LDS reads or conversions for dead sub-tiles)
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) {
     const int n = wn0 + tn * 32 + lr;
-    if (FULL || tn < tn_live) {
-      bp[tn] = *(const af3_u32x4*)(bs + g4_b_off(n, lh));
-      sc[tn] = ss[n * G + 2 * kt + lh];
-    } else {
-      bp[tn] = zero4();
-      sc[tn] = 127u;
-    }
+    bp[tn] = (FULL || tn < tn_live) ? *(const af3_u32x4*)(bs + g4_b_off(n, lh)) : zero4();
+    scf[tn] = __uint_as_float(sc[tn] << 23);
+    sc_next[tn] = 127u;
   }
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm)
     if (FULL || tm < tm_live) af[0][tm] = *(const af3_bf16x8*)(as + lds_off(wm0 + tm * 32 + lr, lh * 4));
-#pragma unroll
-  for (int tn = 0; tn < TN; ++tn) scf[tn] = __uint_as_float(sc[tn] << 23);
   // sub-step -1 (the carried one) and sub-steps 0..2; the k-step's copies
   // are spread over all of their MFMAs
 #pragma unroll
@@ -1121,21 +1122,28 @@ __device__ __forceinline__ void g4_kstep(const uint16_t* as, const uint8_t* bs, 
       for (int tm = 0; tm < TM; ++tm)
         if (FULL || tm < tm_live) af[nx][tm] = *(const af3_bf16x8*)(as + lds_off(wm0 + tm * 32 + lr, lh * 4 + s + 1));
     }
+    if (s == 0 && more) {  // the next k-step's scale bytes
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+        if (FULL || tn < tn_live) sc_next[tn] = ss[(wn0 + tn * 32 + lr) * G + 2 * (kt + 1) + lh];
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < TM * TN; ++i) {
+    for (int i = 0; i < NS; ++i) {
       const int tm = i / TN, tn = i % TN;
       if (FULL || (tm < tm_live && tn < tn_live))
         acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[c][tm], bf[c][tn], acc[tm][tn], 0, 0, 0);
-      if ((i % TM) == TM - 1) {  // one B fragment of sub-step s + 1 per TM MFMAs
-        const int t = i / TM;
+      if (i >= NS - TN) {  // B fragment t of sub-step s + 1 in each of the last TN slots
+        const int t = i - (NS - TN);
         if (FULL || t < tn_live) bf[nx][t] = g4_bfrag<EXACT>(bp[t][s + 1], sc[t], scf[t]);
       }
-      const int q = (s + 1) * TM * TN + i;
+      const int q = (s + 1) * NS + i;
       if (q % GAP == GAP / 2 && q / GAP < DPW) dma(q / GAP);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) sc[tn] = sc_next[tn];
 }
 
 // One work item of the forward kernel: a RM x CN output tile (256 x 256, or
@@ -1264,12 +1272,16 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
     for (int tn = 0; tn < TN; ++tn) bf[1][tn] = zf;
     // the barrier after the wait also orders the carried fragment reads of
     // stage kt - 1 before the copies into that stage (issued for kt + 2 during kt)
+    uint32_t sc[TN];  // the e8m0 bytes of the lane's B rows for the current k-step
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+      sc[tn] = (FULL || tn < tn_live) ? Ss[(wn0 + tn * 32 + lr) * G + lh] : 127u;
     auto step = [&](int kt, bool last, auto&& dma) {
       wait_stage(last);
       AF3_ASM_LDS_BARRIER();
       const int st = kt % kG4Stages;
-      g4_kstep<TM, TN, DPW, FULL, EXACT>(As + st * ASTAGE, Bs + st * BSTAGE, Ss, G, kt, wm0, wn0, tm_live, tn_live,
-                                         acc, af, bf, dma);
+      g4_kstep<TM, TN, DPW, FULL, EXACT>(As + st * ASTAGE, Bs + st * BSTAGE, Ss, G, kt, !last, wm0, wn0, tm_live,
+                                         tn_live, acc, af, bf, sc, dma);
     };
     int kt = 0;
     for (; kt + 2 < nk; ++kt) step(kt, false, [&](int j) { issue_one(kt + 2, j); });
@@ -2687,6 +2699,8 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
   //   23: gemm5 dgrad (packed weight rows read with transposing LDS loads, one
   //       three-stage ring for A, B and scales; 4 waves of 256x64); default
   //       for trans_w 1 when the requirements hold
+  //   25: gemm4 forward with 8 waves of 64x128 (half the A-fragment LDS reads
+  //       of 22 per MFMA, twice the B conversions per wave)
   //   tile_cfg / 100 = m-tiles per group of the 20/21/22 work order (default 4)
   int cfg = tile_cfg % 100;
   const int group_m = tile_cfg / 100 > 0 ? tile_cfg / 100 : 4;
@@ -2697,7 +2711,8 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
     cfg = g4_fwd ? 22 : g4_dgrad ? 23 : (block_m == 256 ? 4 : 2);
   }
   const bool bm_ok =
-      (cfg == 3 || cfg == 4 || cfg == 6 || cfg == 7 || cfg == 12 || cfg == 20 || cfg == 21 || cfg == 22 || cfg == 23)
+      (cfg == 3 || cfg == 4 || cfg == 6 || cfg == 7 || cfg == 12 || cfg == 20 || cfg == 21 || cfg == 22 || cfg == 23 ||
+       cfg == 25)
           ? block_m == 256
           : block_m == 128;
   AF3_REQUIRE(bm_ok, "moe_gemm: tile_cfg %d does not match block_m %d", cfg, block_m);
@@ -2717,7 +2732,7 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
   if (epi != 0) {
     AF3_REQUIRE(glu && (epi == 1 || epi == 2), "moe_gemm: bad SwiGLU epilogue %d", epi);
     const bool ok = epi == 1 ? (trans && cfg == 23 && ld_glu % 8 == 0 && al16(glu) && ldy >= 2LL * N)
-                             : (!trans && (cfg == 20 || cfg == 22) && N % 2 == 0 && ld_glu % 4 == 0 &&
+                             : (!trans && (cfg == 20 || cfg == 22 || cfg == 25) && N % 2 == 0 && ld_glu % 4 == 0 &&
                                 ((uintptr_t)glu & 7) == 0);
     if (!ok) {
       af3::set_error("moe_gemm: the fused SwiGLU epilogue %d is not available for tile_cfg %d / these operands", epi,
@@ -2727,7 +2742,7 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
   }
   if (a_row_scale) {
     AF3_REQUIRE(lora_r == 0, "moe_gemm: a row scale cannot be combined with the LoRA extension segment");
-    if (!(cfg == 20 || cfg == 21 || cfg == 22 || cfg == 23)) {
+    if (!(cfg == 20 || cfg == 21 || cfg == 22 || cfg == 23 || cfg == 25)) {
       af3::set_error("moe_gemm: the A row scale needs tile_cfg 20-23 (got %d)", cfg);
       return AF3_EUNSUPPORTED;
     }
@@ -2749,6 +2764,7 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
     case 12: launch_gemm3<256, 128, 2, 2>(trans, max_tiles, N, stream, p); break;
     case 20:
     case 22:
+    case 25:
       p.group_m = group_m;
       AF3_REQUIRE(!trans && block_m == 256 && K % kBK == 0 && K / 32 <= kG4MaxG && al16(w_scales) && al16(y) &&
                       ldy % 8 == 0,
@@ -2756,6 +2772,8 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
                   kG4MaxG * 32);
       if (cfg == 20)
         launch_gemm4_fwd<2, 2>(max_tiles, N, stream, p);
+      else if (cfg == 25)
+        launch_gemm4_fwd<4, 2>(max_tiles, N, stream, p);
       else
         launch_gemm4_fwd<2, 4>(max_tiles, N, stream, p);
       break;

@@ -94,6 +94,14 @@ int af3_routing_topk(const uint16_t* logits, int64_t ld_logits, int64_t n_tokens
                      int n_expts_act, uint16_t* gate_scal, int32_t* hist, int32_t* topk_indx, int32_t* gate_indx,
                      int32_t* token_offs_raw, void* workspace, size_t ws_bytes, void* stream);
 
+/* Router logits.  Replaces nn.functional.linear(hidden_states,
+ * router.weight, router.bias) in mlp_forward (quantization.py:653-654):
+ * logits[t][e] = bf16(sum_k x[t][k] w[e][k] + bias[e]) with fp32 sums.
+ * x [T][ldx] bf16, w [E][ldw] bf16, bias [E] bf16 or NULL, logits
+ * [T][ld_logits] bf16; hidden % 64 == 0, E <= 256, rows 16-byte aligned. */
+int af3_router_logits(const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t ldw, const uint16_t* bias,
+                      int64_t n_tokens, int hidden, int n_expts, uint16_t* logits, int64_t ld_logits, void* stream);
+
 /* Tile metadata.  Replaces triton_kernels.routing.compute_expt_data_torch
  * (quantization.py:588,627).  block_ms_dev [n_block_ms] (device) ->
  * token_offs_pad [n_block_ms][E+1], block_pid_map [n_block_ms][max_tiles]

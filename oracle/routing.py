@@ -3,6 +3,8 @@
 * ``routing_replay``  — quantization.py:593-636.
 * ``routing_topk``    — quantization.py:551-590 (routing_torch_dist) at world
   size 1: stable descending sort, softmax over the K, per-token sort by id.
+* ``router_logits``   — quantization.py:653-654 (nn.functional.linear of the
+  hidden states with the router weight and bias): fp32 sums, one bf16 rounding.
 * ``expt_data``       — triton_kernels.routing.compute_expt_data_torch as
   called at quantization.py:588,627: token_offs_raw, token_offs_pad[BM] and
   block_pid_map[BM] ((block << 16) | expert, -1 padding).
@@ -65,3 +67,12 @@ def expt_data(hist: torch.Tensor, block_m: int, max_tiles: int):
         for b in range(int(n_tiles[e])):
             pid[o + b] = (b << 16) + e
     return offs_pad, pid
+
+
+def router_logits(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None):
+    """-> (bf16 logits [T, E], float32 sum of |x_k w_k| per logit for tolerances)."""
+    xf, wf = x.to(torch.float32), weight.to(torch.float32)
+    out = xf @ wf.T
+    if bias is not None:
+        out = out + bias.to(torch.float32)
+    return out.to(torch.bfloat16), xf.abs() @ wf.abs().T

@@ -79,7 +79,7 @@ CASES = [  # (gather, lora, odd)
 ]
 
 
-@pytest.mark.parametrize("cfg", [0, 20, 22])
+@pytest.mark.parametrize("cfg", [0, 20, 22, 25])
 @pytest.mark.parametrize("gather,lora,odd", CASES)
 def test_forward_tiles(dev, cfg, gather, lora, odd):
     g, ref, rd, gi = _routing(dev, 11)

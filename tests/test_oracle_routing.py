@@ -42,3 +42,19 @@ def test_expt_data_tiles():
     assert offs_pad.tolist() == [0, 0, 2, 3, 3, 5]
     assert pid[:5].tolist() == [1, (1 << 16) | 1, 2, 4, (1 << 16) | 4]
     assert (pid[5:] == -1).all()
+
+
+def test_router_logits_oracle_against_float64():
+    """oracle.routing.router_logits: fp32 sums of bf16 inputs, one bf16 rounding
+    (quantization.py:654's F.linear), within one bf16 rounding of the exact
+    float64 value; the magnitude bound dominates the result."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(64, 2880, generator=g).to(torch.bfloat16)
+    w = (torch.randn(128, 2880, generator=g) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(128, generator=g) * 0.1).to(torch.bfloat16)
+    got, mag = routing.router_logits(x, w, b)
+    exact = x.double() @ w.double().T + b.double()
+    assert ((got.double() - exact).abs() <= 2.0 ** -8 * exact.abs() + 1e-6).all()
+    assert (mag.double() + b.double().abs() >= exact.abs() - 1e-3).all()
+    # the reference's own expression on the CPU gives the same bits
+    assert torch.equal(got, torch.nn.functional.linear(x.float(), w.float(), b.float()).to(torch.bfloat16))
