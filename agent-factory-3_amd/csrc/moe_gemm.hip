@@ -545,333 +545,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm2_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------
-// Prefetching B loaders for gemm3: every global load is unconditional (rows /
-// columns past the tile edge are clamped to valid ones; their results land in
-// output columns that are never stored), so each wave issues exactly kOps
-// vector-memory instructions per load() and the k-loop can wait for an older
-// stage with an exact vmcnt.  Addresses live in the loader; the raw data of a
-// k-step lives in a separate Data object so two k-steps can be in flight.
-// ---------------------------------------------------------------------------
-template <int TR, int NT>
-struct PfRowsFp4 {  // W[e][n][k/32][16], nibbles along k
-  static constexpr int kUnits = TR * 2;
-  static_assert(kUnits % NT == 0, "units must split evenly over the threads");
-  static constexpr int kUPT = kUnits / NT;
-  static constexpr int kOps = 2 * kUPT;  // dwordx4 + ubyte per unit
-  struct Data {
-    af3_u32x4 v[kUPT];
-    uint32_t s[kUPT];
-  };
-  const uint8_t* bp[kUPT];
-  const uint8_t* sp[kUPT];
-
-  __device__ __forceinline__ void init(const Operand& op, int e, int row0, int nvalid) {
-#pragma unroll
-    for (int i = 0; i < kUPT; ++i) {
-      const int u = threadIdx.x + i * NT;
-      const int64_t n = row0 + min(u >> 1, nvalid - 1);
-      bp[i] = (const uint8_t*)op.ptr + e * op.estride + n * op.ld + ((u & 1) << 4);
-      sp[i] = op.scales + e * op.sestride + n * op.sld + (u & 1);
-    }
-  }
-  __device__ __forceinline__ void load(Data& d, int k0) const {
-#pragma unroll
-    for (int i = 0; i < kUPT; ++i) {
-      d.v[i] = *(const af3_u32x4*)(bp[i] + (k0 >> 1));
-      d.s[i] = (uint32_t)sp[i][k0 >> 5];
-    }
-  }
-  __device__ __forceinline__ void store(const Data& d, uint16_t* lds) const {
-#pragma unroll
-    for (int i = 0; i < kUPT; ++i) {
-      const int u = threadIdx.x + i * NT;
-      const int r = u >> 1, ch0 = (u & 1) << 2;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        uint32_t o[4];
-        af3_dequant_u32(d.v[i][q], d.s[i], o);
-        *(af3_u32x4*)(lds + lds_off(r, ch0 + q)) = af3_u32x4{o[0], o[1], o[2], o[3]};
-      }
-    }
-  }
-};
-
-template <int TR, int NT>
-struct PfColsFp4 {  // W[e][k][n/32][16], nibbles along n: unit = 8 k x 8 n
-  static constexpr int kCO = TR / 8;
-  static constexpr int kUnits = 8 * kCO;
-  static_assert(kUnits % NT == 0 || NT % kUnits == 0, "units and threads must divide");
-  // with fewer units than threads the extra threads load a duplicate unit (so
-  // every wave issues the same instructions) and store nothing
-  static constexpr int kUPT = kUnits >= NT ? kUnits / NT : 1;
-  static constexpr int kOps = 16 * kUPT;  // 8 dwords + 8 scale bytes per unit
-  struct Data {
-    uint32_t w[kUPT][8];
-    uint32_t s[kUPT][8];
-  };
-  const uint8_t* bp[kUPT];
-  const uint8_t* sp[kUPT];
-  int64_t ld, sld;
-
-  __device__ __forceinline__ void init(const Operand& op, int e, int col0, int ncols) {
-    ld = op.ld;
-    sld = op.sld;
-#pragma unroll
-    for (int i = 0; i < kUPT; ++i) {
-      const int u = (threadIdx.x + i * NT) % kUnits;
-      const int ko = u / kCO, co = u % kCO;
-      const int c = col0 + min(co * 8, ncols - 8);
-      bp[i] = (const uint8_t*)op.ptr + e * op.estride + (int64_t)(ko * 8) * ld + (c >> 1);
-      sp[i] = op.scales + e * op.sestride + (int64_t)(ko * 8) * sld + (c >> 5);
-    }
-  }
-  __device__ __forceinline__ void load(Data& d, int k0) const {
-#pragma unroll
-    for (int i = 0; i < kUPT; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        d.w[i][j] = *(const uint32_t*)(bp[i] + (int64_t)(k0 + j) * ld);
-        d.s[i][j] = (uint32_t)sp[i][(int64_t)(k0 + j) * sld];
-      }
-  }
-  __device__ __forceinline__ void store(const Data& d, uint16_t* lds) const {
-#pragma unroll
-    for (int i = 0; i < kUPT; ++i) {
-      const int u = threadIdx.x + i * NT;
-      if (kUnits < NT && u >= kUnits) continue;
-      const int ko = u / kCO, co = u % kCO;
-      af3_u32x4 x[8], t[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        uint32_t o[4];
-        af3_dequant_u32(d.w[i][j], d.s[i][j], o);
-        x[j] = af3_u32x4{o[0], o[1], o[2], o[3]};
-      }
-      transpose8x8(x, t);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) *(af3_u32x4*)(lds + lds_off(co * 8 + j, ko)) = t[j];
-    }
-  }
-};
-
-template <int TR, int NT>
-struct PfRowsBf16 {  // k-contiguous bf16 rows, optionally gathered (A operand)
-  static constexpr int kUnits = TR * 8;
-  static_assert(kUnits % NT == 0, "units must split evenly over the threads");
-  static constexpr int kUPT = kUnits / NT;
-  struct Data {
-    af3_u32x4 v[kUPT];
-  };
-  const uint16_t* rp[kUPT];
-
-  // rows past nvalid read the tile's first row (results never stored)
-  __device__ __forceinline__ void init(const Operand& op, int row0, int nvalid) {
-#pragma unroll
-    for (int i = 0; i < kUPT; ++i) {
-      const int u = threadIdx.x + i * NT;
-      int64_t src = row0 + min(u >> 3, nvalid - 1);
-      if (op.gather) src = op.gather[src] / op.gdiv;
-      rp[i] = (const uint16_t*)op.ptr + src * op.ld + ((u & 7) << 3);
-    }
-  }
-  __device__ __forceinline__ void load(Data& d, int k0) const {
-#pragma unroll
-    for (int i = 0; i < kUPT; ++i) d.v[i] = *(const af3_u32x4*)(rp[i] + k0);
-  }
-  __device__ __forceinline__ void store(const Data& d, uint16_t* lds) const {
-#pragma unroll
-    for (int i = 0; i < kUPT; ++i) {
-      const int u = threadIdx.x + i * NT;
-      *(af3_u32x4*)(lds + lds_off(u >> 3, u & 7)) = d.v[i];
-    }
-  }
-};
-
-template <int KIND, int TR, int NT>
-struct PfLoader;
-template <int TR, int NT>
-struct PfLoader<ROWS_FP4, TR, NT> {
-  using type = PfRowsFp4<TR, NT>;
-};
-template <int TR, int NT>
-struct PfLoader<COLS_FP4, TR, NT> {
-  using type = PfColsFp4<TR, NT>;
-};
-
-// s_waitcnt with vmcnt(n) and lgkmcnt(0) (expcnt not waited)
-#define AF3_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4))
-
-// MFMA over one LDS k-step with the fragments of sub-step s+1 read while the
-// MFMAs of sub-step s issue.
-template <int TM, int TN>
-__device__ __forceinline__ void mma_kstep_pf(const uint16_t* As, const uint16_t* Bs, int wm0, int wn0,
-                                             af3_f32x16 acc[TM][TN]) {
-  const int lane = threadIdx.x & 63;
-  const int lr = lane & 31, lk = lane >> 5;
-  af3_bf16x8 af[2][TM], bf[2][TN];
-#pragma unroll
-  for (int tm = 0; tm < TM; ++tm) af[0][tm] = *(const af3_bf16x8*)(As + lds_off(wm0 + tm * 32 + lr, lk));
-#pragma unroll
-  for (int tn = 0; tn < TN; ++tn) bf[0][tn] = *(const af3_bf16x8*)(Bs + lds_off(wn0 + tn * 32 + lr, lk));
-#pragma unroll
-  for (int ks = 0; ks < kBK / 16; ++ks) {
-    const int cur = ks & 1, nxt = cur ^ 1;
-    if (ks + 1 < kBK / 16) {
-#pragma unroll
-      for (int tm = 0; tm < TM; ++tm)
-        af[nxt][tm] = *(const af3_bf16x8*)(As + lds_off(wm0 + tm * 32 + lr, (ks + 1) * 2 + lk));
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn)
-        bf[nxt][tn] = *(const af3_bf16x8*)(Bs + lds_off(wn0 + tn * 32 + lr, (ks + 1) * 2 + lk));
-    }
-#pragma unroll
-    for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn)
-        acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][tm], bf[cur][tn], acc[tm][tn], 0, 0, 0);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// gemm3: main grouped GEMM with a two-k-step-deep prefetch.  A (activations)
-// goes global->LDS directly into one of three LDS stages two k-steps ahead; B
-// (MXFP4) is loaded two k-steps ahead into one of two register sets and
-// dequantised into one of two LDS stages one k-step ahead.  One barrier per
-// k-step; before it each wave waits (exact vmcnt) for everything except the
-// loads it issued in the current step.
-// ---------------------------------------------------------------------------
-template <int BM, int BN, int WM, int WN, int BK_, int BXK>
-__global__ __launch_bounds__(WM * WN * 64) void gemm3_kernel(Params p) {
-  constexpr int NW = WM * WN, NT = NW * 64;
-  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
-  using LB = typename PfLoader<BK_, BN, NT>::type;
-  constexpr int kStageA = BM * kBK, kStageB = BN * kBK;
-  __shared__ __attribute__((aligned(16))) uint16_t Ab[2 * kStageA];
-  __shared__ __attribute__((aligned(16))) uint16_t Bb[2 * kStageB];
-
-  const int NN = p.n_nblk;
-  const int W = p.tile_offs[p.E] * NN;
-  const int b = blockIdx.x;
-  if (b >= W) return;
-  const int W8 = W & ~7;
-  const int w = b < W8 ? (b & 7) * (W8 >> 3) + (b >> 3) : b;
-  const int32_t ent = p.tile_map[w / NN];
-  if (ent < 0) return;
-  const int e = ent & 0xFFFF, blk = ent >> 16;
-  const int row_lo = p.offs[e] + blk * BM;
-  const int nrows = min(BM, p.offs[e + 1] - row_lo);
-  if (nrows <= 0) return;
-  const int n0 = (w % NN) * BN;
-  const int ncols = min(BN, p.N - n0);
-
-  const int wave = threadIdx.x >> 6;
-  const int wm0 = (wave / WN) * (BM / WM), wn0 = (wave % WN) * (BN / WN);
-  af3_f32x16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  {
-    using LA = PfRowsBf16<BM, NT>;
-    LA la;
-    la.init(p.a, row_lo, nrows);
-    LB lb;
-    lb.init(p.b, e, n0, ncols);
-    typename LA::Data a0, a1;
-    typename LB::Data b0, b1;
-    const int nk = p.K / kBK;
-    la.load(a0, 0);
-    lb.load(b0, 0);
-    if (nk > 1) {
-      la.load(a1, kBK);
-      lb.load(b1, kBK);
-    }
-    la.store(a0, Ab);
-    lb.store(b0, Bb);
-    __syncthreads();
-
-    // steady state: step kt computes stage kt & 1, stores k-step kt + 1 (loaded
-    // one step earlier) into the other stage and loads k-step kt + 2 into the
-    // register set it just freed; two steps per iteration keep the register
-    // sets static.
-    auto step_pf = [&](int kt, typename LA::Data& acur, typename LB::Data& bcur, const typename LA::Data& anxt,
-                       const typename LB::Data& bnxt) {
-      la.load(acur, (kt + 2) * kBK);
-      lb.load(bcur, (kt + 2) * kBK);
-      mma_kstep_pf<TM, TN>(Ab + (kt & 1) * kStageA, Bb + (kt & 1) * kStageB, wm0, wn0, acc);
-      __syncthreads();
-      la.store(anxt, Ab + ((kt + 1) & 1) * kStageA);
-      lb.store(bnxt, Bb + ((kt + 1) & 1) * kStageB);
-      __syncthreads();
-    };
-    const int n_pf = nk - 2;
-    int kt = 0;
-    for (; kt + 1 < n_pf; kt += 2) {
-      step_pf(kt, a0, b0, a1, b1);
-      step_pf(kt + 1, a1, b1, a0, b0);
-    }
-    if (kt < n_pf) {  // odd count: kt even
-      step_pf(kt, a0, b0, a1, b1);
-      ++kt;
-    }
-    for (; kt < nk; ++kt) {
-      mma_kstep_pf<TM, TN>(Ab + (kt & 1) * kStageA, Bb + (kt & 1) * kStageB, wm0, wn0, acc);
-      __syncthreads();
-      if (kt + 1 < nk) {
-        if (kt & 1) {
-          la.store(a0, Ab + ((kt + 1) & 1) * kStageA);
-          lb.store(b0, Bb + ((kt + 1) & 1) * kStageB);
-        } else {
-          la.store(a1, Ab + ((kt + 1) & 1) * kStageA);
-          lb.store(b1, Bb + ((kt + 1) & 1) * kStageB);
-        }
-      }
-      __syncthreads();
-    }
-  }
-  if constexpr (BXK != NONE) {
-    if (p.kx > 0) {
-      Loader<BM, ROWS_BF16, NT> la;
-      Loader<BN, BXK, NT> lb;
-      la.init(p.ax, 0, row_lo, nrows, p.kx);
-      if constexpr (BXK == ROWS_BF16)
-        lb.init(p.bx, e, n0, ncols, p.kx);
-      else
-        lb.init(p.bx, e, n0, ncols, 0, p.kx);
-      run_segment<Loader<BM, ROWS_BF16, NT>, Loader<BN, BXK, NT>, TM, TN>(la, lb, p.kx, Ab, Bb, wm0, wn0, acc);
-    }
-  }
-
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int tm = 0; tm < TM; ++tm) {
-#pragma unroll
-    for (int tn = 0; tn < TN; ++tn) {
-      const int col = wn0 + tn * 32 + (lane & 31);
-      if (col >= ncols) continue;
-      const int n = n0 + col;
-      const float bv = p.bias ? p.bias[e * p.bias_estride + n] : 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = wm0 + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        if (row >= nrows) continue;
-        const int64_t gr = row_lo + row;
-        float v = acc[tm][tn][r] + bv;
-        if (p.gammas)
-          v *= p.gammas_f32 ? ((const float*)p.gammas)[gr] : af3_bf16_to_f32(((const uint16_t*)p.gammas)[gr]);
-        p.c[gr * p.ldc + n] = (uint16_t)af3_f32_to_bf16(v);
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
 // gemm4: forward grouped GEMM through MXFP4 weights packed along k
-// (W[e][n][k/32][16]).  256 threads = 4 waves in a 2x2 arrangement of 128x128
-// wave tiles over a 256x256 output tile.
+// (W[e][n][k/32][16]).  512 threads = 8 waves (two per SIMD) in a 2x4
+// arrangement of 128x64 wave tiles over a 256x256 output tile (tiles of
+// <= 128 rows: 128x512, waves 1x8).
 //   * A (activation rows, optionally gathered) goes global->LDS directly
 //     (global_load_lds_dwordx4) into a 3-stage ring of [256][64] bf16 tiles
 //     (16-byte chunks XOR-swizzled by row, as lds_off);
@@ -1347,7 +1024,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm4_fwd_kernel(Params p) {
   const int nrows = min(kG4Rows, p.offs[e + 1] - row_lo);
   if (nrows <= 0) return;
   const int n0 = nt * kG4Rows;
-  if constexpr (WM * WN == 8) {  // (the 4-wave variant keeps 256 x 256 items: its registers are full)
+  if constexpr (WM * WN == 8) {
     if (nrows <= 128 && (p.K >> 5) <= kG4NarrowMaxG) {
       // tiles of <= 128 rows take n-tiles nt and nt + 1 as one 128 x 512 item
       if (nt & 1) return;
@@ -1544,343 +1221,6 @@ __global__ __launch_bounds__(512) void gemm4_fwd_f8_kernel(Params p) {
     return;
   }
   g4f8_tile<false>(p, lds, e, row_lo, nrows, n0, min(kG4Rows, p.N - n0));
-}
-
-// ---------------------------------------------------------------------------
-// gemm4 dgrad: grouped GEMM through MXFP4 weights packed along the OUTPUT
-// axis, W[e][k][n/32][16] with scales [e][k][n/32] (the input-gradient
-// products dX = dY . W of quantization.py:409-418).  Same block / wave tiling,
-// A ring, grouping and epilogue as gemm4 forward.  The packed weight bytes of a
-// k-step ([64 k][128 B] for 256 columns) and their scales are loaded
-// global->LDS four k-steps deep, then transposed in LDS to [column pair][k]
-// (one byte = the two nibbles of columns 2p, 2p+1 at one k) while the MFMAs of
-// the previous k-step run.  A lane then reads the 8 bytes of its column pair
-// for the 8 k of a sub-step plus the 8 scale bytes of those k, and one
-// v_cvt_scalef32_pk_bf16_fp4 per byte yields the (even, odd) column values:
-// the even values form the B fragment of one MFMA sub-tile and the odd values
-// that of its partner (sub-tiles 2t, 2t + 1 hold the even / odd columns of 64
-// consecutive columns), so no value is converted twice or discarded.
-// ---------------------------------------------------------------------------
-constexpr int kD4BStage = 64 * 128;  // packed-B staging per k-step [64 k][128 B]
-constexpr int kD4SStage = 64 * 16;   // scale staging per k-step [64 k][4 x (2 bytes + 2 zero bytes)]
-constexpr int kD4BRing = 4;
-constexpr int kD4TBuf = 128 * 64;    // transposed packed B [128 pairs][64 k]
-constexpr int kD4TsBuf = 8 * 64;     // transposed scales [8 blocks][64 k]
-constexpr int kD4OffB = kG4Stages * kG4AStage * 2;
-constexpr int kD4OffS = kD4OffB + kD4BRing * kD4BStage;
-constexpr int kD4OffT = kD4OffS + kD4BRing * kD4SStage;
-constexpr int kD4OffTs = kD4OffT + 2 * kD4TBuf;
-constexpr int kD4LdsBytes = kD4OffTs + 2 * kD4TsBuf + 16;  // ~149 KB
-static_assert(kD4LdsBytes >= 256 * 512 + 1024 && kD4LdsBytes <= 160 * 1024, "dgrad LDS budget");
-
-// byte offset of (column pair p, k) in a transposed buffer: 64 bytes per pair,
-// 8-byte k groups XOR-swizzled by p / 4 so 32 lanes reading one k group of 32
-// consecutive pairs hit 32 distinct 8-byte bank pairs
-__device__ __forceinline__ int d4_t_off(int p, int k) {
-  return p * 64 + ((((k >> 3) ^ ((p >> 2) & 7))) << 3) + (k & 7);
-}
-
-// scale bytes outside [2, 252] among the 4 bytes of x
-__device__ __forceinline__ bool d4_odd4(uint32_t x) {
-  const uint32_t lo = (x - 0x02020202u) & ~x & 0x80808080u;    // some byte < 2
-  const uint32_t nx = ~x;
-  const uint32_t hi = (nx - 0x03030303u) & ~nx & 0x80808080u;  // some byte > 252
-  return (lo | hi) != 0u;
-}
-
-// B fragments of the sub-tile pair (even, odd columns) for one sub-step from
-// the 8 packed bytes (w0: k 0..3, w1: k 4..7) and their 8 scale bytes.
-template <bool EXACT>
-__device__ __forceinline__ void d4_frags(uint32_t w0, uint32_t w1, uint32_t s0, uint32_t s1, af3_bf16x8& ev,
-                                         af3_bf16x8& od) {
-  uint32_t dw[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t src = i < 4 ? w0 : w1;
-    const uint32_t sb = ((i < 4 ? s0 : s1) >> (8 * (i & 3))) & 0xFFu;
-    const float sc = __uint_as_float(sb << 23);
-    switch (i & 3) {
-      case 0: dw[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, sc, 0)); break;
-      case 1: dw[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, sc, 1)); break;
-      case 2: dw[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, sc, 2)); break;
-      default: dw[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, sc, 3)); break;
-    }
-  }
-  if constexpr (EXACT) {  // k-steps with scale bytes outside [2, 252] only
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t src = i < 4 ? w0 : w1;
-      const uint32_t sb = ((i < 4 ? s0 : s1) >> (8 * (i & 3))) & 0xFFu;
-      const uint32_t byte = (src >> (8 * (i & 3))) & 0xFFu;
-      const uint32_t alt = af3_e2m1_to_bf16_bits(byte & 0xFu, sb) | (af3_e2m1_to_bf16_bits(byte >> 4, sb) << 16);
-      dw[i] = sb - 2u > 250u ? alt : dw[i];
-    }
-  }
-  af3_u32x4 e4, o4;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    e4[j] = perm_lo(dw[2 * j], dw[2 * j + 1]);
-    o4[j] = perm_hi(dw[2 * j], dw[2 * j + 1]);
-  }
-  ev = __builtin_bit_cast(af3_bf16x8, e4);
-  od = __builtin_bit_cast(af3_bf16x8, o4);
-}
-
-template <int BXK>
-__global__ __launch_bounds__(256) void gemm4_dgrad_kernel(Params p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kD4LdsBytes];
-  uint16_t* const As = (uint16_t*)lds;
-  uint8_t* const Bp = lds + kD4OffB;
-  uint8_t* const Sp = lds + kD4OffS;
-  uint8_t* const Tb = lds + kD4OffT;
-  uint8_t* const Ts = lds + kD4OffTs;
-
-  int mt, nt;
-  if (!g4_work_item(p, mt, nt)) return;
-  const int32_t ent = p.tile_map[mt];
-  if (ent < 0) return;
-  const int e = ent & 0xFFFF, blk = ent >> 16;
-  const int row_lo = p.offs[e] + blk * kG4Rows;
-  const int nrows = min(kG4Rows, p.offs[e + 1] - row_lo);
-  if (nrows <= 0) return;
-  const int n0 = nt * kG4Rows;
-  const int ncols = min(kG4Rows, p.N - n0);  // multiple of 64
-  const int nk = p.K / kBK;
-
-  // 1 x 4 waves: wave w owns all 256 rows and the 64 columns 64 w .. 64 w + 63
-  // (sub-tile pair: even / odd columns), so every weight byte is converted by
-  // exactly one wave
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lr = lane & 31, lh = lane >> 5;
-  const int wn0 = wave * 64;
-  const int tm_live = min(8, (nrows + 31) >> 5);
-  const bool wave_live = wn0 < ncols;  // ncols is a multiple of 64
-  const bool full = tm_live == 8 && wave_live;
-
-  // DMA sources.  A rows: as gemm4 forward.
-  const uint16_t* arow[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = (wave * 8 + i) * 8 + (lane >> 3);
-    int64_t src = row_lo + (row < nrows ? row : 0);
-    if (p.a.gather) src = p.a.gather[src] / p.a.gdiv;
-    arow[i] = (const uint16_t*)p.a.ptr + src * p.a.ld + (((lane & 7) ^ swz(row)) << 3);
-  }
-  // packed weight rows of a k-step: instruction q covers k rows 8q..8q+7, 128 B each
-  const uint8_t* bsrc[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int kr = (wave * 2 + j) * 8 + (lane >> 3);
-    int c16 = (lane & 7) * 16;
-    if (c16 >= (ncols >> 1)) c16 = 0;
-    bsrc[j] = (const uint8_t*)p.b.ptr + e * p.b.estride + (int64_t)kr * p.b.ld + (n0 >> 1) + c16;
-  }
-  // scales of a k-step: instruction `wave` covers k rows 16 wave .. + 15, 8 B each; a 2-byte
-  // global->LDS copy lands in a 4-byte LDS slot per lane (zero-extended)
-  const uint8_t* ssrc;
-  {
-    const int kr = wave * 16 + (lane >> 2);
-    int c2 = (lane & 3) * 2;
-    if (c2 >= (ncols >> 5)) c2 = 0;
-    ssrc = p.b.scales + e * p.b.sestride + (int64_t)kr * p.b.sld + (n0 >> 5) + c2;
-  }
-  const int64_t bstep = (int64_t)kBK * p.b.ld, sstep = (int64_t)kBK * p.b.sld;
-  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
-  auto issue_b = [&](int kb) {  // packed B + scales of k-step kb (3 instructions)
-    const int slot = kb % kD4BRing;
-    const uint32_t bb = lds0 + (uint32_t)(kD4OffB + slot * kD4BStage + wave * 2 * 1024);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) g4_dma16(bsrc[j] + kb * bstep, bb + j * 1024);
-    const uint32_t sb = lds0 + (uint32_t)(kD4OffS + slot * kD4SStage + wave * 256);
-    asm volatile("s_nop 0\n\tglobal_load_lds_ushort %0, off" ::"v"(ssrc + kb * sstep), "{m0}"(sb) : "memory");
-  };
-  auto issue_a = [&](int ka, int j) {  // A instruction j (0..7) of k-step ka
-    g4_dma16(arow[j] + ka * kBK,
-             lds0 + (uint32_t)((ka % kG4Stages) * kG4AStage * 2 + (wave * 8 + j) * 8 * kBK * 2));
-  };
-  // per-k-step flag: index of the last k-step whose scales held a byte outside
-  // [2, 252] (written by the scale transposer, read after the next barrier)
-  int* const oddk = (int*)(lds + kD4OffTs + 2 * kD4TsBuf);
-  // transposer: thread t moves packed bytes of k rows 4 rg .. 4 rg + 3, column
-  // pairs 8 hg .. 8 hg + 7 (and threads < 128 four scale bytes)
-  const int hg = threadIdx.x & 15, rg = threadIdx.x >> 4;
-  int toff[8];
-#pragma unroll
-  for (int q = 0; q < 8; ++q) toff[q] = d4_t_off(hg * 8 + q, rg * 4);
-  const int nbq = (threadIdx.x >> 4) & 7, kq = (threadIdx.x & 15) * 4;
-  const int sso = (nbq >> 1) * 4 + (nbq & 1);
-  auto transpose = [&](int kb) {
-    const int slot = kb % kD4BRing;
-    const uint8_t* st = Bp + slot * kD4BStage + rg * 4 * 128 + hg * 8;
-    uint8_t* tb = Tb + (kb & 1) * kD4TBuf;
-    uint32_t lo[4], hi[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint2 v = *(const uint2*)(st + i * 128);
-      lo[i] = v.x;
-      hi[i] = v.y;
-    }
-    auto tr4 = [&](const uint32_t x[4], uint32_t o[4]) {
-      const uint32_t a0 = __builtin_amdgcn_perm(x[1], x[0], 0x05010400u);
-      const uint32_t a1 = __builtin_amdgcn_perm(x[1], x[0], 0x07030602u);
-      const uint32_t b0 = __builtin_amdgcn_perm(x[3], x[2], 0x05010400u);
-      const uint32_t b1 = __builtin_amdgcn_perm(x[3], x[2], 0x07030602u);
-      o[0] = __builtin_amdgcn_perm(b0, a0, 0x05040100u);
-      o[1] = __builtin_amdgcn_perm(b0, a0, 0x07060302u);
-      o[2] = __builtin_amdgcn_perm(b1, a1, 0x05040100u);
-      o[3] = __builtin_amdgcn_perm(b1, a1, 0x07060302u);
-    };
-    uint32_t ol[4], oh[4];
-    tr4(lo, ol);
-    tr4(hi, oh);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      *(uint32_t*)(tb + toff[q]) = ol[q];
-      *(uint32_t*)(tb + toff[4 + q]) = oh[q];
-    }
-    if (threadIdx.x < 128) {  // scales: [64 k][8] -> [8][64 k]
-      const uint8_t* ss = Sp + slot * kD4SStage + kq * 16 + sso;
-      const uint32_t v = (uint32_t)ss[0] | ((uint32_t)ss[16] << 8) | ((uint32_t)ss[32] << 16) | ((uint32_t)ss[48] << 24);
-      *(uint32_t*)(Ts + (kb & 1) * kD4TsBuf + nbq * 64 + kq) = v;
-      if (d4_odd4(v)) oddk[kb & 1] = kb;
-    }
-  };
-
-  af3_f32x16 acc[8][2];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  // lane-fixed LDS byte offsets: A row (32 tm + lr) chunk c sits at
-  // 4096 tm + 128 lr + 16 (c ^ swz), swz = (lr ^ lr / 8 ^ 4 (tm & 1)) & 7
-  const int ax = (lr ^ (lr >> 3)) & 7;
-  const int pr = (wn0 >> 1) + lr;  // the lane's column pair
-  int foff[4], soff[4];
-#pragma unroll
-  for (int sub = 0; sub < 4; ++sub) {
-    const int c = lh * 4 + sub;
-    foff[sub] = d4_t_off(pr, c * 8);
-    soff[sub] = (pr >> 4) * 64 + c * 8;
-  }
-
-  // prologue: B(0); batch 0 = A(0) + B(1); batch 1 = A(1) + B(2)
-  auto issue_batch = [&](int j) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) issue_a(j, i);
-    issue_b(min(j + 1, nk - 1));
-  };
-  if (threadIdx.x < 2) oddk[threadIdx.x] = -1;
-  issue_b(0);
-  issue_batch(0);
-  if (nk > 1) issue_batch(1);
-  if (nk > 1)
-    AF3_ASM_WAIT_VM(22);
-  else
-    AF3_ASM_WAIT_VM(11);
-  AF3_ASM_LDS_BARRIER();
-  transpose(0);
-
-  // one k-step; EXACT k-steps (scale bytes outside [2, 252]) take a separate
-  // copy of the body so the common one carries no fix-up code
-  auto kstep = [&](auto full_c, auto exact_c, int kt) {
-    constexpr bool FULL = decltype(full_c)::value;
-    constexpr bool EXACT = decltype(exact_c)::value;
-    {
-      const bool pf = kt + 2 < nk;
-      const uint8_t* as = (const uint8_t*)As + (kt % kG4Stages) * kG4AStage * 2 + lr * 128;
-      const uint8_t* tb = Tb + (kt & 1) * kD4TBuf;
-      const uint8_t* tsb = Ts + (kt & 1) * kD4TsBuf;
-      af3_bf16x8 af[2][8], bf[2][2];
-      auto load_frags = [&](int sub, int slot) {
-        const int c = lh * 4 + sub;
-#pragma unroll
-        for (int tm = 0; tm < 8; ++tm)
-          if (FULL || tm < tm_live) af[slot][tm] = *(const af3_bf16x8*)(as + tm * 4096 + (((c ^ ax) ^ ((tm & 1) << 2)) << 4));
-        const uint2 wv = *(const uint2*)(tb + foff[sub]);
-        const uint2 sv = *(const uint2*)(tsb + soff[sub]);
-        d4_frags<EXACT>(wv.x, wv.y, sv.x, sv.y, bf[slot][0], bf[slot][1]);
-      };
-      if (FULL || wave_live) load_frags(0, 0);
-#pragma unroll
-      for (int sub = 0; sub < 4; ++sub) {
-        const int cur = sub & 1;
-        __builtin_amdgcn_sched_barrier(0);
-        if ((FULL || wave_live) && sub + 1 < 4) load_frags(sub + 1, cur ^ 1);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int tm = i >> 1, tn = i & 1;
-          if (FULL || (wave_live && tm < tm_live))
-            acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][tm], bf[cur][tn], acc[tm][tn], 0, 0, 0);
-          const int q = sub * 16 + i;
-          if (pf && q % 6 == 2 && q / 6 < 8) issue_a(kt + 2, q / 6);
-          if (pf && q == 50) issue_b(min(kt + 3, nk - 1));
-          if (q == 40 && kt + 1 < nk) transpose(kt + 1);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      }
-    }
-  };
-  // The common loop returns at the first k-step whose scales need the exact
-  // rule; the exact loop (fix-up on every k-step) finishes the tile.  The
-  // flag is block-uniform, so every wave leaves at the same k-step (and the
-  // repeated wait + barrier there is matched by all waves).
-  auto kloop = [&](auto full_c, auto exact_c, int kt) -> int {
-    for (; kt < nk; ++kt) {
-      if (kt + 1 < nk)
-        AF3_ASM_WAIT_VM(11);
-      else
-        AF3_ASM_WAIT_VM(0);
-      AF3_ASM_LDS_BARRIER();
-      if constexpr (!decltype(exact_c)::value)
-        if (__builtin_amdgcn_readfirstlane(oddk[kt & 1]) == kt) return kt;
-      kstep(full_c, exact_c, kt);
-    }
-    return nk;
-  };
-  if (full) {
-    const int kt = kloop(std::true_type{}, std::false_type{}, 0);
-    if (kt < nk) kloop(std::true_type{}, std::true_type{}, kt);
-  } else {
-    const int kt = kloop(std::false_type{}, std::false_type{}, 0);
-    if (kt < nk) kloop(std::false_type{}, std::true_type{}, kt);
-  }
-
-  if constexpr (BXK != NONE) {
-    if (p.kx > 0) {  // expert-LoRA segment: + L[r] . Bx[e][:, n] (Bx [r][N], n contiguous)
-      Loader<kG4Rows, ROWS_BF16, 256> la;
-      Loader<kG4Rows, COLS_BF16, 256> lb;
-      la.init(p.ax, 0, row_lo, nrows, p.kx);
-      lb.init(p.bx, e, n0, ncols, 0, p.kx);
-      for (int k0 = 0; k0 < p.kx; k0 += kBK) {
-        la.load(k0);
-        lb.load(k0);
-        __syncthreads();
-        la.store(As);
-        lb.store(As + kG4AStage);
-        __syncthreads();
-#pragma unroll
-        for (int ks = 0; ks < kBK / 16; ++ks) {
-          af3_bf16x8 af[8], bf[2];
-#pragma unroll
-          for (int tm = 0; tm < 8; ++tm) af[tm] = *(const af3_bf16x8*)(As + lds_off(tm * 32 + lr, ks * 2 + lh));
-#pragma unroll
-          for (int tn = 0; tn < 2; ++tn)
-            bf[tn] = *(const af3_bf16x8*)(As + kG4AStage + lds_off(wn0 + 2 * lr + tn, ks * 2 + lh));
-#pragma unroll
-          for (int tm = 0; tm < 8; ++tm)
-#pragma unroll
-            for (int tn = 0; tn < 2; ++tn)
-              acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[tm], bf[tn], acc[tm][tn], 0, 0, 0);
-        }
-      }
-    }
-  }
-  g4_epilogue<true, 8, 2>(p, lds, acc, e, row_lo, nrows, n0, ncols, 0, wn0);
 }
 
 // ---------------------------------------------------------------------------
@@ -2573,22 +1913,6 @@ inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // exported entry points
 // ---------------------------------------------------------------------------
 
-template <int BM, int BN, int WM, int WN>
-static void launch_gemm3(bool trans, int max_tiles, int N, hipStream_t stream, Params p) {
-  p.n_nblk = (N + BN - 1) / BN;
-  dim3 grid(max_tiles * p.n_nblk);
-  if (!trans)
-    hipLaunchKernelGGL((gemm3_kernel<BM, BN, WM, WN, ROWS_FP4, ROWS_BF16>), grid, dim3(WM * WN * 64), 0, stream, p);
-  else
-    hipLaunchKernelGGL((gemm3_kernel<BM, BN, WM, WN, COLS_FP4, COLS_BF16>), grid, dim3(WM * WN * 64), 0, stream, p);
-}
-
-static void launch_gemm4_dgrad(int max_tiles, int N, hipStream_t stream, Params p) {
-  p.n_nblk = (N + kG4Rows - 1) / kG4Rows;
-  dim3 grid(g4_grid(max_tiles, p.n_nblk, p.group_m));
-  hipLaunchKernelGGL((gemm4_dgrad_kernel<COLS_BF16>), grid, dim3(256), 0, stream, p);
-}
-
 static void launch_gemm5_dgrad(int max_tiles, int N, hipStream_t stream, Params p) {
   p.n_nblk = (N + kG4Rows - 1) / kG4Rows;
   dim3 grid(g4_grid(max_tiles, p.n_nblk, p.group_m));
@@ -2683,25 +2007,17 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
   p.alpha = alpha;
   p.limit = limit;
   const bool trans = trans_w != 0;
-  // tile configurations: (BM, BN, waves)
-  //   1: 128x128, 2x2    2: 128x256, 2x2    3: 256x128, 2x2
-  //   4: 256x256, 2x4    5: 128x256, 2x4    6: 256x256, 2x2
-  //   7: 256x256, 2x2 two-deep prefetch     10: 128x256, 2x2 two-deep prefetch
-  //   11: 128x128, 2x2 two-deep prefetch    12: 256x128, 2x2 two-deep prefetch
-  //   9: single-buffered 128x128 (reference kernel)
-  //   20: gemm4 forward (256x256, 4 waves of 128x128, packed MXFP4 in LDS,
-  //       three-stage global->LDS ring)
-  //   22: gemm4 forward with 8 waves of 128x64 (two waves per SIMD, so one
-  //       wave's conversions / LDS reads overlap the other's MFMAs); default
-  //       for trans_w 0 when the alignment / size requirements hold
-  //   21: gemm4 dgrad (weights packed along n, transposed in LDS; 4 waves of
-  //       256x64)
-  //   23: gemm5 dgrad (packed weight rows read with transposing LDS loads, one
-  //       three-stage ring for A, B and scales; 4 waves of 256x64); default
-  //       for trans_w 1 when the requirements hold
-  //   25: gemm4 forward with 8 waves of 64x128 (half the A-fragment LDS reads
-  //       of 22 per MFMA, twice the B conversions per wave)
-  //   tile_cfg / 100 = m-tiles per group of the 20/21/22 work order (default 4)
+  // tile configurations:
+  //   22: gemm4 forward (256x256 work items, 8 waves of 128x64, two per SIMD,
+  //       packed MXFP4 through a three-stage global->LDS ring, converted in
+  //       registers); default for trans_w 0 when its requirements hold
+  //   23: gemm5 input gradient (packed weight rows read with transposing LDS
+  //       loads, one three-stage ring for A, B and scales; 4 waves of 256x64);
+  //       default for trans_w 1 when its requirements hold
+  //   4 / 2: gemm2, 256x256 / 128x256 tiles with the weight dequantised into
+  //       LDS (general fallback for block_m 256 / 128)
+  //   9: single-buffered 128x128 row tiles (any K % 32 == 0; used when K % 64 != 0)
+  //   tile_cfg / 100 = m-tiles per group of the 22 / 23 work order (default 4)
   int cfg = tile_cfg % 100;
   const int group_m = tile_cfg / 100 > 0 ? tile_cfg / 100 : 4;
   if (cfg == 0) {
@@ -2710,11 +2026,7 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
     const bool g4_dgrad = trans && block_m == 256 && K % kBK == 0 && N % 64 == 0 && al16(y) && ldy % 8 == 0;
     cfg = g4_fwd ? 22 : g4_dgrad ? 23 : (block_m == 256 ? 4 : 2);
   }
-  const bool bm_ok =
-      (cfg == 3 || cfg == 4 || cfg == 6 || cfg == 7 || cfg == 12 || cfg == 20 || cfg == 21 || cfg == 22 || cfg == 23 ||
-       cfg == 25)
-          ? block_m == 256
-          : block_m == 128;
+  const bool bm_ok = (cfg == 4 || cfg == 22 || cfg == 23) ? block_m == 256 : block_m == 128;
   AF3_REQUIRE(bm_ok, "moe_gemm: tile_cfg %d does not match block_m %d", cfg, block_m);
   if (a_fp8) {  // E4M3 activations x MXFP4 weights on the block-scaled MFMA (forward, 256-row map)
     if (trans || block_m != 256 || K % kBK != 0 || K / 32 > kG4MaxG || !al16(w_scales) || !al16(y) || ldy % 8 != 0 ||
@@ -2732,8 +2044,7 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
   if (epi != 0) {
     AF3_REQUIRE(glu && (epi == 1 || epi == 2), "moe_gemm: bad SwiGLU epilogue %d", epi);
     const bool ok = epi == 1 ? (trans && cfg == 23 && ld_glu % 8 == 0 && al16(glu) && ldy >= 2LL * N)
-                             : (!trans && (cfg == 20 || cfg == 22 || cfg == 25) && N % 2 == 0 && ld_glu % 4 == 0 &&
-                                ((uintptr_t)glu & 7) == 0);
+                             : (!trans && cfg == 22 && N % 2 == 0 && ld_glu % 4 == 0 && ((uintptr_t)glu & 7) == 0);
     if (!ok) {
       af3::set_error("moe_gemm: the fused SwiGLU epilogue %d is not available for tile_cfg %d / these operands", epi,
                      cfg);
@@ -2742,8 +2053,8 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
   }
   if (a_row_scale) {
     AF3_REQUIRE(lora_r == 0, "moe_gemm: a row scale cannot be combined with the LoRA extension segment");
-    if (!(cfg == 20 || cfg == 21 || cfg == 22 || cfg == 23 || cfg == 25)) {
-      af3::set_error("moe_gemm: the A row scale needs tile_cfg 20-23 (got %d)", cfg);
+    if (!(cfg == 22 || cfg == 23)) {
+      af3::set_error("moe_gemm: the A row scale needs tile_cfg 22 / 23 (got %d)", cfg);
       return AF3_EUNSUPPORTED;
     }
   }
@@ -2752,43 +2063,21 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
     return AF3_EINVAL;
   }
   switch (cfg) {
-    case 1: launch_gemm2<128, 128, 2, 2>(trans, max_tiles, N, stream, p); break;
     case 2: launch_gemm2<128, 256, 2, 2>(trans, max_tiles, N, stream, p); break;
-    case 3: launch_gemm2<256, 128, 2, 2>(trans, max_tiles, N, stream, p); break;
     case 4: launch_gemm2<256, 256, 2, 4>(trans, max_tiles, N, stream, p); break;
-    case 5: launch_gemm2<128, 256, 2, 4>(trans, max_tiles, N, stream, p); break;
-    case 6: launch_gemm2<256, 256, 2, 2>(trans, max_tiles, N, stream, p); break;
-    case 7: launch_gemm3<256, 256, 2, 2>(trans, max_tiles, N, stream, p); break;
-    case 10: launch_gemm3<128, 256, 2, 2>(trans, max_tiles, N, stream, p); break;
-    case 11: launch_gemm3<128, 128, 2, 2>(trans, max_tiles, N, stream, p); break;
-    case 12: launch_gemm3<256, 128, 2, 2>(trans, max_tiles, N, stream, p); break;
-    case 20:
     case 22:
-    case 25:
       p.group_m = group_m;
       AF3_REQUIRE(!trans && block_m == 256 && K % kBK == 0 && K / 32 <= kG4MaxG && al16(w_scales) && al16(y) &&
                       ldy % 8 == 0,
-                  "moe_gemm: tile_cfg 20 needs trans_w 0, block_m 256, K %% 64 == 0, K <= %d, 16-byte aligned scales/y",
+                  "moe_gemm: tile_cfg 22 needs trans_w 0, block_m 256, K %% 64 == 0, K <= %d, 16-byte aligned scales/y",
                   kG4MaxG * 32);
-      if (cfg == 20)
-        launch_gemm4_fwd<2, 2>(max_tiles, N, stream, p);
-      else if (cfg == 25)
-        launch_gemm4_fwd<4, 2>(max_tiles, N, stream, p);
-      else
-        launch_gemm4_fwd<2, 4>(max_tiles, N, stream, p);
+      launch_gemm4_fwd<2, 4>(max_tiles, N, stream, p);
       break;
-    case 21:
     case 23:
       p.group_m = group_m;
-      AF3_REQUIRE(trans && block_m == 256 && K % kBK == 0 && N % 64 == 0 && al16(y) && ldy % 8 == 0 &&
-                      (cfg != 21 || ((uintptr_t)w_scales & 1) == 0),
-                  "moe_gemm: tile_cfg %d needs trans_w 1, block_m 256, K %% 64 == 0, N %% 64 == 0, 16-byte aligned y"
-                  " (and 2-byte aligned scales for 21)",
-                  cfg);
-      if (cfg == 21)
-        launch_gemm4_dgrad(max_tiles, N, stream, p);
-      else
-        launch_gemm5_dgrad(max_tiles, N, stream, p);
+      AF3_REQUIRE(trans && block_m == 256 && K % kBK == 0 && N % 64 == 0 && al16(y) && ldy % 8 == 0,
+                  "moe_gemm: tile_cfg 23 needs trans_w 1, block_m 256, K %% 64 == 0, N %% 64 == 0, 16-byte aligned y");
+      launch_gemm5_dgrad(max_tiles, N, stream, p);
       break;
     case 9: {
       dim3 grid(max_tiles, (N + 127) / 128);

@@ -98,17 +98,60 @@ def _graph_us(torch, fn, sets, reps):
     same = all(torch.equal(bits(a), bits(b)) for a, b in zip(eager, outs))
     if not same:
         raise RuntimeError("graph replay output differs from the eager call")
+    kern = _kernel_us(torch, g.replay, min(reps, 20))
     del g, outs, eager
-    return s.elapsed_time(e) * 1e3 / (reps * len(sets))
+    return s.elapsed_time(e) * 1e3 / (reps * len(sets)), kern
+
+
+def _short(name):
+    from agent_factory_3_amd.profiling import short_name
+    return short_name(name)
+
+
+def _device_kernels(torch, fn, reps):
+    """Device-side kernel durations (us) of ``reps`` calls of ``fn``, from the
+    profiler's kernel records (roctracer on ROCm): {kernel: [durations]}."""
+    from torch.profiler import ProfilerActivity, profile
+    torch.cuda.synchronize()
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+    out = {}
+    for ev in prof.events():
+        if ev.device_type == torch.autograd.DeviceType.CUDA:
+            t = getattr(ev, "device_time", None)
+            out.setdefault(_short(ev.name), []).append(t if t is not None else ev.cuda_time)
+    return out
+
+
+def _kernel_us(torch, fn, reps):
+    """Average device duration of the most frequent kernel of ``fn`` (None if the
+    profiler records no kernels)."""
+    try:
+        ks = _device_kernels(torch, fn, reps)
+    except Exception as ex:  # noqa: BLE001  (the profiler is optional for the bench line)
+        log(f"kernel timing unavailable: {ex}")
+        return None
+    if not ks:
+        return None
+    name = max(ks, key=lambda k: len(ks[k]))
+    return {"kernel": name, "us": sum(ks[name]) / len(ks[name]), "launches": len(ks[name])}
 
 
 def bandwidth_extras(torch, dev, kernels, workloads, reps=50):
     """cfg 0 dequant, the expert-LoRA merge and cfg 1 SwiGLU fwd/bwd: algorithmic GB/s per launch."""
     res = {}
 
-    def rec(name, us, byts):
+    def rec(name, timing, byts):
+        us, kern = timing
         gbs = byts / (us * 1e-6) / 1e9
-        res[name] = {"GBps": gbs, "us": us, "bytes": byts, "frac_hbm_peak": gbs / HBM_PEAK_GBS}
+        res[name] = {"GBps": gbs, "us": us, "bytes": byts, "frac_hbm_peak": gbs / HBM_PEAK_GBS,
+                     "timing": "HIP-graph replay, gaps between launches included"}
+        if kern:  # the kernel alone, from the profiler's device timestamps
+            kg = byts / (kern["us"] * 1e-6) / 1e9
+            res[name]["kernel"] = {"name": kern["kernel"], "us": kern["us"], "GBps": kg,
+                                   "frac_hbm_peak": kg / HBM_PEAK_GBS}
 
     blocks, scales = workloads.cfg0()
     # 8 x 42 MB > 256 MB MALL: each launch reads cold data
@@ -150,6 +193,13 @@ def bandwidth_extras(torch, dev, kernels, workloads, reps=50):
     return res
 
 
+def _kern_bw(kern, byts):
+    if not kern:
+        return None
+    gbs = byts / (kern["us"] * 1e-6) / 1e9
+    return {"name": kern["kernel"], "us": kern["us"], "GBps": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS}
+
+
 def fp8_extras(torch, dev, kernels, workloads, inp_cpu, k, steps=10, reps=20):
     """fp8 dequant mode (the reference's dequant_dtype="fp8"): standalone E5M2
     dequant and per-token E4M3 quantization bandwidths, and the cfg layer
@@ -160,17 +210,19 @@ def fp8_extras(torch, dev, kernels, workloads, inp_cpu, k, steps=10, reps=20):
     blocks, scales = workloads.cfg0()
     sets = [(blocks.to(dev), scales.to(dev)) for _ in range(8)]
     byts = 8294400 + 518400 + 16588800
-    us = _graph_us(torch, kernels.mxfp4_to_fp8_e5m2, sets, reps)
+    us, kern = _graph_us(torch, kernels.mxfp4_to_fp8_e5m2, sets, reps)
     res["e5m2_dequant_cfg0"] = {"us": us, "GBps": byts / (us * 1e-6) / 1e9,
-                                "frac_hbm_peak": byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+                                "frac_hbm_peak": byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                                "kernel": _kern_bw(kern, byts)}
     del sets
     x = inp_cpu.x.to(dev)
     M, K = x.shape
     sets = [(x,), (x.clone(),)]
     byts = M * K * 2 + M * K + M * 4
-    us = _graph_us(torch, lambda t: kernels.quantize_per_token_e4m3(t)[0], sets, reps)
+    us, kern = _graph_us(torch, lambda t: kernels.quantize_per_token_e4m3(t)[0], sets, reps)
     res["quant_e4m3_per_token"] = {"shape": [M, K], "us": us, "GBps": byts / (us * 1e-6) / 1e9,
-                                   "frac_hbm_peak": byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+                                   "frac_hbm_peak": byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                                   "kernel": _kern_bw(kern, byts)}
     del sets
     inp_nl = dataclasses.replace(inp_cpu, lora=None)
     inp = inp_nl.to(dev)
@@ -387,12 +439,27 @@ def main():
         if vals:
             traffic = sum(vals) / len(vals)
 
+    # the step's kernels from the profiler's device timestamps (outside the timed region)
+    step_k = {}
+    try:
+        ks_dev = _device_kernels(torch, step, 2)
+        step_k = {k: {"calls_per_step": len(v) / 2, "us_per_step": sum(v) / 2, "avg_us": sum(v) / len(v)}
+                  for k, v in sorted(ks_dev.items(), key=lambda kv: -sum(kv[1]))}
+    except Exception as ex:  # noqa: BLE001
+        log(f"kernel breakdown unavailable: {ex}")
+    dom_kernel_us = None
+    if kname:
+        durs = [v for k, v in step_k.items() if k.startswith(kname)]
+        if durs:
+            dom_kernel_us = sum(d["us_per_step"] for d in durs) / sum(d["calls_per_step"] for d in durs)
+
     extra = {"gemm": {t: {"launches_per_step": v["n"] / args.steps, "avg_us": v["ms"] / v["n"] * 1e3,
                           "tflops": v["work"] / (v["ms"] * 1e-3) / 1e12} for t, v in ks.items()},
              "gemm_ms_per_step": gemm_ms,
              "gemm_mfma_util": gemm_flops / (gemm_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
              "layer_tflops": flops["total"] / (ms_step * 1e-3) / 1e12,
-             "layer_algorithmic_tflop": flops["total"] / 1e12}
+             "layer_algorithmic_tflop": flops["total"] / 1e12,
+             "step_kernels": step_k}
     if not args.no_extras:
         log("standalone dequant / SwiGLU bandwidth")
         extra.update(bandwidth_extras(torch, dev, kernels, workloads))
@@ -445,7 +512,8 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": dom_tag, "achieved": achieved, "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS, "traffic": traffic,
-                     "avg_launch_us": avg_ms * 1e3, "algorithmic_flops_per_launch": avg_flops},
+                     "avg_launch_us": avg_ms * 1e3, "algorithmic_flops_per_launch": avg_flops,
+                     "kernel_avg_us_profiler": dom_kernel_us},
         "cpu_baseline": cpu,
         "extra": extra,
     }

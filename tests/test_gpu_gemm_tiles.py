@@ -79,7 +79,7 @@ CASES = [  # (gather, lora, odd)
 ]
 
 
-@pytest.mark.parametrize("cfg", [0, 20, 22, 25])
+@pytest.mark.parametrize("cfg", [0, 4, 22])
 @pytest.mark.parametrize("gather,lora,odd", CASES)
 def test_forward_tiles(dev, cfg, gather, lora, odd):
     g, ref, rd, gi = _routing(dev, 11)
@@ -105,7 +105,7 @@ def test_forward_tiles(dev, cfg, gather, lora, odd):
     assert not bad.any(), float(bad.float().mean())
 
 
-@pytest.mark.parametrize("cfg", [0, 21, 23])
+@pytest.mark.parametrize("cfg", [0, 4, 23])
 @pytest.mark.parametrize("gather,lora,odd", CASES)
 def test_dgrad_tiles(dev, cfg, gather, lora, odd):
     g, ref, rd, gi = _routing(dev, 12)
