@@ -2,13 +2,15 @@
 
 Command line (run from the repository root on the MI355X box)::
 
-    python -m agent_factory_3_amd.profiling ktrace  <run>_kernel_trace.csv
+    python -m agent_factory_3_amd.profiling ktrace  <run>_kernel_trace.csv [<run>_marker_api_trace.csv RANGE]
     python -m agent_factory_3_amd.profiling traffic <fetch>_counter_collection.csv \\
                                                      <write>_counter_collection.csv
 
 ``ktrace`` turns a ``rocprofv3 --kernel-trace --output-format csv`` trace into
 a markdown table (one row per kernel name and grid size: calls, average /
-minimum / total duration).
+minimum / total duration), optionally restricted to the dispatches that start
+inside the roctx range RANGE of a ``--marker-trace`` (``bench.py`` wraps its
+timed steps in the range ``bench_timed``).
 
 ``traffic`` takes two ``rocprofv3 --pmc FETCH_SIZE`` / ``--pmc WRITE_SIZE``
 counter collections of ``bench.py --probe traffic`` (which runs one plain
@@ -52,18 +54,41 @@ def short_name(name: str) -> str:
     return "".join(out).strip()
 
 
-def ktrace(path: str) -> str:
+def marker_window(path: str, name: str) -> tuple[int, int]:
+    """(start, end) timestamps of the roctx range ``name`` in a ``rocprofv3
+    --marker-trace`` CSV (the earliest start and latest end of the rows that
+    carry the name in any column)."""
+    spans = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in csv.DictReader(open(path))
+             if name in r.values()]
+    if not spans:
+        raise SystemExit(f"no marker named {name!r} in {path}")
+    return min(s for s, _ in spans), max(e for _, e in spans)
+
+
+def ktrace(path: str, window: tuple[int, int] | None = None) -> str:
+    """Markdown table of a kernel trace, one row per (kernel, grid); with
+    ``window`` only the dispatches that start inside it.  A second table gives
+    the average duration over all grids of each grouped-GEMM entry point's
+    kernel, the per-launch figure bench.py reports as ``roofline.avg_launch_us``."""
     rows = list(csv.DictReader(open(path)))
     agg = collections.defaultdict(list)
     for r in rows:
+        if window and not window[0] <= int(r["Start_Timestamp"]) <= window[1]:
+            continue
         grid = r.get("Grid_Size_X") or r.get("Grid_Size") or ""
         dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
         agg[(short_name(r["Kernel_Name"]), grid)].append(dur)
     tot = sum(sum(v) for v in agg.values()) or 1.0
     lines = ["| kernel | grid | calls | avg us | min us | total us | % |", "|---|---:|---:|---:|---:|---:|---:|"]
     for (k, g), v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        k = k if len(k) <= 100 else k[:96] + " ..."  # library kernels (hipBLASLt's Cijk_*) carry very long names
         lines.append(f"| `{k}` | {g} | {len(v)} | {sum(v) / len(v):.2f} | {min(v):.2f} | {sum(v):.1f} | "
                      f"{100 * sum(v) / tot:.2f} |")
+    lines += ["", "| entry point | kernel | launches | avg us per launch (all grids) |", "|---|---|---:|---:|"]
+    for tag, kname in GEMM_KERNELS.items():
+        v = [d for (k, _), ds in agg.items() if k.startswith(kname) for d in ds]
+        if v:
+            lines.append(f"| {tag} | `{kname}` | {len(v)} | {sum(v) / len(v):.2f} |")
     return "\n".join(lines)
 
 
@@ -123,8 +148,8 @@ def read_traffic(md_path: str) -> dict | None:
 
 
 def main(argv: list[str]) -> int:
-    if len(argv) >= 2 and argv[0] == "ktrace":
-        print(ktrace(argv[1]))
+    if len(argv) in (2, 4) and argv[0] == "ktrace":
+        print(ktrace(argv[1], marker_window(argv[2], argv[3]) if len(argv) == 4 else None))
         return 0
     if len(argv) >= 3 and argv[0] == "traffic":
         print(traffic(argv[1], argv[2]))

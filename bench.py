@@ -108,20 +108,35 @@ def _short(name):
     return short_name(name)
 
 
-def _device_kernels(torch, fn, reps):
+def _device_kernels(torch, fn, reps, warm=3):
     """Device-side kernel durations (us) of ``reps`` calls of ``fn``, from the
-    profiler's kernel records (roctracer on ROCm): {kernel: [durations]}."""
+    profiler's kernel records (roctracer on ROCm): {kernel: [durations]}.
+    ``warm`` more calls run first under the same profiler and are dropped (each
+    call launches the same kernels, so each kernel keeps its last
+    ``reps / (warm + reps)`` share of launches by start time): the clock drops
+    while the GPU idles during the profiler's start, and the first launches
+    after that run up to 40% slower.  The profiler's own warm-up phase does not
+    help here: on ROCm the kernel records of that phase arrive with the active
+    one."""
+    if os.environ.get("ROCP_TOOL_LIBRARIES"):
+        # under rocprofv3 both tracers share rocprofiler-sdk and torch's reads ~1 us per kernel
+        raise RuntimeError("running under rocprofv3: its own kernel trace has the durations")
     from torch.profiler import ProfilerActivity, profile
     torch.cuda.synchronize()
     with profile(activities=[ProfilerActivity.CUDA]) as prof:
-        for _ in range(reps):
+        for _ in range(warm + reps):
             fn()
         torch.cuda.synchronize()
-    out = {}
+    recs = {}
     for ev in prof.events():
         if ev.device_type == torch.autograd.DeviceType.CUDA:
             t = getattr(ev, "device_time", None)
-            out.setdefault(_short(ev.name), []).append(t if t is not None else ev.cuda_time)
+            recs.setdefault(_short(ev.name), []).append((ev.time_range.start, t if t is not None else ev.cuda_time))
+    out = {}
+    for k, v in recs.items():
+        v.sort()
+        keep = max(1, round(len(v) * reps / (warm + reps)))
+        out[k] = [d for _, d in v[-keep:]]
     return out
 
 
@@ -406,6 +421,7 @@ def main():
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    torch.cuda.nvtx.range_push("bench_timed")  # roctx range: rocprofv3 --marker-trace finds the timed steps by it
     timer.on = True
     t_start.record()
     for _ in range(args.steps):
@@ -413,6 +429,7 @@ def main():
     t_end.record()
     torch.cuda.synchronize()
     timer.on = False
+    torch.cuda.nvtx.range_pop()
     quantization.KERNEL_TIMER = None
     ms_total = t_start.elapsed_time(t_end)
     ms_step = ms_total / args.steps
@@ -442,8 +459,8 @@ def main():
     # the step's kernels from the profiler's device timestamps (outside the timed region)
     step_k = {}
     try:
-        ks_dev = _device_kernels(torch, step, 2)
-        step_k = {k: {"calls_per_step": len(v) / 2, "us_per_step": sum(v) / 2, "avg_us": sum(v) / len(v)}
+        ks_dev = _device_kernels(torch, step, 4)
+        step_k = {k: {"calls_per_step": len(v) / 4, "us_per_step": sum(v) / 4, "avg_us": sum(v) / len(v)}
                   for k, v in sorted(ks_dev.items(), key=lambda kv: -sum(kv[1]))}
     except Exception as ex:  # noqa: BLE001
         log(f"kernel breakdown unavailable: {ex}")

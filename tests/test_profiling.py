@@ -33,3 +33,26 @@ def test_committed_traffic_profile_parses():
     names = [k.split("|")[0] for k in tj["kernels"]]
     for kernel in profiling.GEMM_KERNELS.values():   # the kernels bench.py reads traffic for
         assert any(kernel in n for n in names), kernel
+
+
+def test_ktrace_window_and_entry_point_average(tmp_path):
+    kt, mk = tmp_path / "kt.csv", tmp_path / "mk.csv"
+    with open(kt, "w", newline="") as f:
+        w = csv.DictWriter(f, ["Kernel_Name", "Grid_Size_X", "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        # one dispatch before the range (slow, cold), two inside: grids of both GEMM shapes
+        for s, e, g in ((0, 9000, 64), (10000, 12000, 64), (20000, 21000, 32), (30000, 39000, 64)):
+            w.writerow({"Kernel_Name": "void gemm4_fwd_kernel<2, 4, 0>(Params)", "Grid_Size_X": g,
+                        "Start_Timestamp": s, "End_Timestamp": e})
+    with open(mk, "w", newline="") as f:
+        w = csv.DictWriter(f, ["Domain", "Function", "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        w.writerow({"Domain": "MARKER_CORE_API", "Function": "other", "Start_Timestamp": 0, "End_Timestamp": 50000})
+        w.writerow({"Domain": "MARKER_CORE_API", "Function": "bench_timed", "Start_Timestamp": 9500,
+                    "End_Timestamp": 25000})
+    win = profiling.marker_window(str(mk), "bench_timed")
+    assert win == (9500, 25000)
+    table = profiling.ktrace(str(kt), win)
+    assert "| `gemm4_fwd_kernel<2, 4, 0>` | 64 | 1 | 2.00 |" in table
+    assert "| moe_gemm_fwd | `gemm4_fwd_kernel` | 2 | 1.50 |" in table
+    assert "| moe_gemm_fwd | `gemm4_fwd_kernel` | 4 | 5.25 |" in profiling.ktrace(str(kt))
