@@ -9,16 +9,25 @@ and ``weight``), over gfx950 kernels instead of its Triton ones
 * forward: ``af3_lm_head_logprobs`` — a bf16 MFMA GEMM whose epilogue keeps
   only per-row softmax statistics of each 256-column vocabulary tile, then a
   per-row combine; the [tokens, vocab] logits are never written;
-* backward: ``af3_lm_head_dlogits`` recomputes the logits tile by tile and
-  writes the logits gradient (bf16), then ``d_hidden = dz @ W`` and
-  ``d_weight = dz^T @ hidden`` run as plain GEMMs (hipBLASLt through torch).
+* backward: the vocabulary is cut into splits of at most ``SPLIT_BYTES`` of
+  bf16 gradient ([tokens, split]); per split ``af3_lm_head_dlogits_range``
+  recomputes the logits tile by tile and writes that split's logits gradient
+  dz (bf16), then ``d_hidden += dz @ W[split]`` (fp32 accumulation across the
+  splits, one bf16 rounding at the end) and ``d_weight[split] = dz^T @ hidden``
+  run as plain GEMMs (hipBLASLt through torch).  This is the reference's
+  default backward (``BackwardEnum._Split_Dlogits_N``, kernels.py:1528-1585);
+  the [tokens, vocab] gradient is never formed, and at the default 128 MiB a
+  split stays in the 256 MB Infinity Cache between its write and the GEMMs'
+  reads.
 
 ``logprobs`` = z[label] - logsumexp(z), ``entropy`` = logsumexp(z) - E_p[z],
 z = hidden @ W^T / temperature, fp32 (reduction "none"; "sum" / "mean"
 return the scalar of the log-probabilities, as the reference does).
 Differences: one rank only (``dist_process_group`` must be None: the
 vocabulary-parallel form is not built), a label outside [0, V) counts as
-z = 0 (the reference leaves that entry unwritten).
+z = 0 (the reference leaves that entry unwritten), and d_hidden sums the
+splits in fp32 (the reference adds each split's bf16 product into a bf16
+d_hidden, kernels.py:1575-1582).
 """
 from __future__ import annotations
 
@@ -29,6 +38,16 @@ import torch
 from . import _capi
 
 _REDUCTIONS = {"none": 0, "sum": 1, "mean": 2}
+
+# bytes of bf16 logits gradient one vocabulary split of the backward may hold
+SPLIT_BYTES = 128 << 20
+
+
+def vocab_split(M: int, V: int) -> int:
+    """Vocabulary columns per backward split: the [M, split] bf16 gradient
+    within SPLIT_BYTES, a multiple of the kernel's 256-column tile."""
+    n = max(256, (SPLIT_BYTES // (2 * max(M, 1))) // 256 * 256)
+    return min(n, V)
 
 
 def _check(hidden, weight, labels):
@@ -81,6 +100,40 @@ def lm_head_dlogits(hidden, weight, labels, temperature, lse, ez, dlogprobs, den
     return dz
 
 
+def lm_head_backward(hidden, weight, labels, temperature, lse, ez, dlogprobs, dentropy, reduction=0,
+                     need_hidden=True, need_weight=True):
+    """-> (d_hidden, d_weight) in bf16 (None where not needed), the logits
+    gradient formed one vocabulary split at a time."""
+    h, w = hidden.contiguous(), weight.contiguous()
+    lab = labels.to(torch.int64).contiguous()
+    M, H = h.shape
+    V = w.shape[0]
+    dev = h.device
+    dlp = dlogprobs.float().contiguous()
+    dent = (dentropy.float().contiguous() if dentropy is not None
+            else torch.zeros(M, dtype=torch.float32, device=dev))
+    stride = 1 if reduction == 0 else 0
+    scale = 1.0 / M if reduction == 2 else 1.0
+    d_hidden = torch.zeros(M, H, dtype=torch.float32, device=dev) if need_hidden else None
+    d_weight = torch.empty(V, H, dtype=torch.bfloat16, device=dev) if need_weight else None
+    if M == 0 or not (need_hidden or need_weight):
+        return (d_hidden.to(torch.bfloat16) if need_hidden else None), (d_weight.zero_() if need_weight else None)
+    split = vocab_split(M, V)
+    dz = torch.empty(M, split, dtype=torch.bfloat16, device=dev)
+    stream = _capi.stream_of(dev)
+    for v0 in range(0, V, split):
+        n = min(split, V - v0)
+        dzc = dz[:, :n]
+        _capi.call("af3_lm_head_dlogits_range", h.data_ptr(), h.stride(0), w.data_ptr(), w.stride(0), M, v0, n, H,
+                   lab.data_ptr(), float(temperature), lse.data_ptr(), ez.data_ptr(), dlp.data_ptr(), stride, scale,
+                   dent.data_ptr(), dzc.data_ptr(), dz.stride(0), stream)
+        if need_hidden:
+            torch.addmm(d_hidden, dzc, w[v0:v0 + n], out_dtype=torch.float32, out=d_hidden)
+        if need_weight:
+            torch.mm(dzc.t(), h, out=d_weight[v0:v0 + n])
+    return (d_hidden.to(torch.bfloat16) if need_hidden else None), d_weight
+
+
 class LinearCrossEntropy(torch.autograd.Function):
     """trainer/losses/linear_cross_entropy.py:LinearCrossEntropy on gfx950."""
 
@@ -114,12 +167,10 @@ class LinearCrossEntropy(torch.autograd.Function):
         if dlogprobs is None:
             dlogprobs = torch.zeros(M if ctx.red == 0 else (), dtype=torch.float32, device=h.device)
         dlp = dlogprobs.reshape(-1) if ctx.red == 0 else dlogprobs.reshape(1)
-        dz = lm_head_dlogits(h, w, lab, ctx.temperature, lse, ez, dlp, dentropy, ctx.red)
-        d_hidden = d_weight = None
-        if ctx.needs_input_grad[0]:
-            d_hidden = torch.mm(dz, w).view(ctx.shape)
-        if ctx.needs_input_grad[1]:
-            d_weight = torch.mm(dz.t(), h)
+        d_hidden, d_weight = lm_head_backward(h, w, lab, ctx.temperature, lse, ez, dlp, dentropy, ctx.red,
+                                              ctx.needs_input_grad[0], ctx.needs_input_grad[1])
+        if d_hidden is not None:
+            d_hidden = d_hidden.view(ctx.shape)
         return d_hidden, d_weight, None, None, None, None
 
 

@@ -107,7 +107,7 @@ __global__ __launch_bounds__(kLmThreads, 1) void lmh_gemm_kernel(
     float4* __restrict__ partials, float* __restrict__ zlab,
     // MODE 1
     const float* __restrict__ lse, const float* __restrict__ ez, const float* __restrict__ dlp, int64_t dlp_stride,
-    float dlp_scale, const float* __restrict__ dent, uint16_t* __restrict__ dz, int64_t lddz) {
+    float dlp_scale, const float* __restrict__ dent, uint16_t* __restrict__ dz, int64_t lddz, int64_t voff) {
   using Ring = LmRing<BK>;
   constexpr int kLmBK = BK, kLmRowB = Ring::kRowB, kLmCh = Ring::kCh, kLmStage = Ring::kStage;
   constexpr int kLmStages = Ring::kStages, kLmCopies = Ring::kCopies;
@@ -262,7 +262,8 @@ __global__ __launch_bounds__(kLmThreads, 1) void lmh_gemm_kernel(
       rs[tid * 5 + 2] = dlp[(int64_t)row * dlp_stride] * dlp_scale;
       rs[tid * 5 + 3] = dent[row];
       const int64_t lab = labels[row];
-      rs[tid * 5 + 4] = __int_as_float(lab >= 0 && lab < V ? (int)lab : -1);
+      // the tile's columns are vocabulary entries voff .. voff + V - 1
+      rs[tid * 5 + 4] = __int_as_float(lab >= voff && lab < voff + V ? (int)(lab - voff) : -1);
     }
     __syncthreads();
 #pragma unroll
@@ -357,11 +358,11 @@ extern "C" int af3_lm_head_logprobs(const uint16_t* hidden, int64_t ldh, const u
   if (H % 64 == 0)
     hipLaunchKernelGGL((lmh_gemm_kernel<0, 64>), dim3(grid), dim3(kLmThreads), 0, stream, hidden, ldh, weight, ldw, M, V, H,
                        1.f / temperature, labels, nm, nv, px, partials, zlab, nullptr, nullptr, nullptr, 0, 0.f,
-                       nullptr, nullptr, 0);
+                       nullptr, nullptr, 0, 0);
   else
     hipLaunchKernelGGL((lmh_gemm_kernel<0, 32>), dim3(grid), dim3(kLmThreads), 0, stream, hidden, ldh, weight, ldw, M, V, H,
                        1.f / temperature, labels, nm, nv, px, partials, zlab, nullptr, nullptr, nullptr, 0, 0.f,
-                       nullptr, nullptr, 0);
+                       nullptr, nullptr, 0, 0);
   int rc = af3::check_launch("lm_head_logprobs (gemm)");
   if (rc) return rc;
   hipLaunchKernelGGL(lmh_reduce_kernel, dim3((unsigned)af3_cdiv(M, 256)), dim3(256), 0, stream, partials, M, nv, zlab,
@@ -369,27 +370,38 @@ extern "C" int af3_lm_head_logprobs(const uint16_t* hidden, int64_t ldh, const u
   return af3::check_launch("lm_head_logprobs (reduce)");
 }
 
-extern "C" int af3_lm_head_dlogits(const uint16_t* hidden, int64_t ldh, const uint16_t* weight, int64_t ldw, int M,
-                                   int V, int H, const int64_t* labels, float temperature, const float* lse,
-                                   const float* ez, const float* dlogprobs, int64_t dlp_stride, float dlp_scale,
-                                   const float* dentropy, uint16_t* dz, int64_t lddz, void* stream_) {
+extern "C" int af3_lm_head_dlogits_range(const uint16_t* hidden, int64_t ldh, const uint16_t* weight, int64_t ldw,
+                                         int M, int v_begin, int v_count, int H, const int64_t* labels,
+                                         float temperature, const float* lse, const float* ez, const float* dlogprobs,
+                                         int64_t dlp_stride, float dlp_scale, const float* dentropy, uint16_t* dz,
+                                         int64_t lddz, void* stream_) {
   hipStream_t stream = (hipStream_t)stream_;
-  AF3_REQUIRE(M >= 0 && V > 0 && H > 0 && H % 32 == 0, "lm_head_dlogits: H must be a positive multiple of 32");
+  AF3_REQUIRE(M >= 0 && v_begin >= 0 && v_count > 0 && H > 0 && H % 32 == 0,
+              "lm_head_dlogits: need v_begin >= 0, v_count > 0 and H a positive multiple of 32");
   if (M == 0) return 0;
   AF3_REQUIRE(hidden && weight && labels && lse && ez && dlogprobs && dentropy && dz, "lm_head_dlogits: null pointer");
   AF3_REQUIRE(temperature > 0.f, "lm_head_dlogits: temperature must be positive");
   AF3_REQUIRE(ldh % 8 == 0 && ldw % 8 == 0 && ((uintptr_t)hidden & 15) == 0 && ((uintptr_t)weight & 15) == 0 &&
-                  lddz >= V,
+                  lddz >= v_count,
               "lm_head_dlogits: rows must be 16-byte aligned");
+  const uint16_t* wr = weight + (int64_t)v_begin * ldw;  // vocabulary rows v_begin .. v_begin + v_count - 1
   int nm, nv, px;
-  const int grid = lmh_grid(M, V, nm, nv, px);
+  const int grid = lmh_grid(M, v_count, nm, nv, px);
   if (H % 64 == 0)
-    hipLaunchKernelGGL((lmh_gemm_kernel<1, 64>), dim3(grid), dim3(kLmThreads), 0, stream, hidden, ldh, weight, ldw, M, V, H,
-                       1.f / temperature, labels, nm, nv, px, nullptr, nullptr, lse, ez, dlogprobs, dlp_stride,
-                       dlp_scale, dentropy, dz, lddz);
+    hipLaunchKernelGGL((lmh_gemm_kernel<1, 64>), dim3(grid), dim3(kLmThreads), 0, stream, hidden, ldh, wr, ldw, M,
+                       v_count, H, 1.f / temperature, labels, nm, nv, px, nullptr, nullptr, lse, ez, dlogprobs,
+                       dlp_stride, dlp_scale, dentropy, dz, lddz, (int64_t)v_begin);
   else
-    hipLaunchKernelGGL((lmh_gemm_kernel<1, 32>), dim3(grid), dim3(kLmThreads), 0, stream, hidden, ldh, weight, ldw, M, V, H,
-                       1.f / temperature, labels, nm, nv, px, nullptr, nullptr, lse, ez, dlogprobs, dlp_stride,
-                       dlp_scale, dentropy, dz, lddz);
+    hipLaunchKernelGGL((lmh_gemm_kernel<1, 32>), dim3(grid), dim3(kLmThreads), 0, stream, hidden, ldh, wr, ldw, M,
+                       v_count, H, 1.f / temperature, labels, nm, nv, px, nullptr, nullptr, lse, ez, dlogprobs,
+                       dlp_stride, dlp_scale, dentropy, dz, lddz, (int64_t)v_begin);
   return af3::check_launch("lm_head_dlogits");
+}
+
+extern "C" int af3_lm_head_dlogits(const uint16_t* hidden, int64_t ldh, const uint16_t* weight, int64_t ldw, int M,
+                                   int V, int H, const int64_t* labels, float temperature, const float* lse,
+                                   const float* ez, const float* dlogprobs, int64_t dlp_stride, float dlp_scale,
+                                   const float* dentropy, uint16_t* dz, int64_t lddz, void* stream) {
+  return af3_lm_head_dlogits_range(hidden, ldh, weight, ldw, M, 0, V, H, labels, temperature, lse, ez, dlogprobs,
+                                   dlp_stride, dlp_scale, dentropy, dz, lddz, stream);
 }

@@ -343,6 +343,23 @@ def lm_head_extras(torch, dev, M=8192, H=2880, V=201088, reps=3):
         torch.autograd.backward([lp, ent], [dlp, dent])
     ms = timed(fwd_bwd)
     res["fwd_bwd"] = {"ms": ms, "tflops": 4 * flops / (ms * 1e-3) / 1e12}
+    # the backward alone (logits recomputed, split gradient, two GEMMs per split) and its
+    # memory beyond the inputs, against forming the whole [M, V] gradient first
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    ms = timed(lambda: lce.lm_head_backward(h, w, lab, 1.0, lse, ez, dlp, dent))
+    res["backward_split"] = {"ms": ms, "tflops": 3 * flops / (ms * 1e-3) / 1e12, "split": lce.vocab_split(M, V),
+                             "peak_extra_bytes": torch.cuda.max_memory_allocated(dev) - base}
+
+    def whole():
+        dz = lce.lm_head_dlogits(h, w, lab, 1.0, lse, ez, dlp, dent)
+        return torch.mm(dz, w), torch.mm(dz.t(), h)
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
+    ms = timed(whole)
+    res["backward_whole_vocab"] = {"ms": ms, "tflops": 3 * flops / (ms * 1e-3) / 1e12,
+                                   "peak_extra_bytes": torch.cuda.max_memory_allocated(dev) - base}
     ms = timed(lambda: torch.mm(h, w.t()))
     res["hipblaslt_logits_gemm"] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12}
     return res

@@ -279,6 +279,16 @@ int af3_lm_head_dlogits(const uint16_t* hidden, int64_t ldh, const uint16_t* wei
                         const float* dlogprobs, int64_t dlp_stride, float dlp_scale, const float* dentropy,
                         uint16_t* dz, int64_t lddz, void* stream);
 
+/* The same logits gradient for the vocabulary entries v_begin .. v_begin + v_count - 1
+ * only (dz [M][lddz], column j = entry v_begin + j): the per-split d_logits of the
+ * reference's default backward, BackwardEnum._Split_Dlogits_N
+ * (trainer/losses/kernels.py:1528-1585, kernel 1278-1380), which bounds the
+ * gradient buffer to [M][split] and runs the two GEMMs per split. */
+int af3_lm_head_dlogits_range(const uint16_t* hidden, int64_t ldh, const uint16_t* weight, int64_t ldw, int M,
+                              int v_begin, int v_count, int H, const int64_t* labels, float temperature,
+                              const float* lse, const float* ez, const float* dlogprobs, int64_t dlp_stride,
+                              float dlp_scale, const float* dentropy, uint16_t* dz, int64_t lddz, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

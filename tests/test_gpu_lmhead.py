@@ -1,14 +1,18 @@
 """Fused LM-head log-probabilities / entropy (linear_cross_entropy) on the GPU
 against oracle/lmhead.py on the same bf16 inputs: forward values (the GEMM
 accumulates in fp32, so only summation order separates it from float64),
-gradients of hidden and weight through the bf16 logits gradient, the three
+the logits gradient per vocabulary split (bit-equal to the whole-vocabulary
+kernel), gradients of hidden and weight through the split backward, the three
 reductions, out-of-range labels, partial row / vocabulary tiles and the full
 gpt-oss vocabulary (201,088)."""
 import pytest
 import torch
 
+from agent_factory_3_amd import _capi
+from agent_factory_3_amd import linear_cross_entropy as lce
 from agent_factory_3_amd.linear_cross_entropy import linear_cross_entropy
 from oracle import lmhead
+from tests._tol import check_close
 
 pytestmark = pytest.mark.gpu
 
@@ -26,11 +30,39 @@ def _close(got, ref, atol, rtol):
     return float(((got - ref).abs() > atol + rtol * ref.abs()).float().mean())
 
 
-@pytest.mark.parametrize("M,H,V,T", [(300, 128, 1000, 1.0), (257, 96, 513, 0.7), (64, 64, 256, 1.3)])
-def test_forward_and_backward(dev, M, H, V, T):
+def _split(monkeypatch, M, cols):
+    """Force backward splits of ``cols`` vocabulary columns for M rows."""
+    monkeypatch.setattr(lce, "SPLIT_BYTES", 2 * M * cols)
+    assert lce.vocab_split(M, 10 ** 6) == cols
+
+
+def _check_grads(hd, wd, h, w, lab, T, dlp, dent, hr, wr, lse, ez, what):
+    """d_hidden / d_weight against (1) the exact float64 gradients, within the
+    north-star tolerance scaled to the gradient's size (the bf16 logits gradient
+    is the only rounding that separates them), and (2) the same GEMMs in float64
+    over the GPU's own bf16 logits gradient (whole-vocabulary kernel), within a
+    bf16 output rounding plus the fp32 accumulation allowance."""
+    for got, ref in ((hd.grad, hr.grad), (wd.grad, wr.grad)):
+        scale = float(ref.abs().max())
+        check_close(got, ref, rtol=2e-2, atol=1e-2 * scale, what=f"{what} vs float64")
+    dz = lce.lm_head_dlogits(hd.detach(), wd.detach(), lab.to(hd.device), T, lse, ez, dlp.to(hd.device),
+                             dent.to(hd.device)).double().cpu()
+    h64, w64 = h.double(), w.double()
+    V = w.shape[0]
+    check_close(hd.grad, dz @ w64, rtol=2.0 ** -8, atol=1e-9, mag=dz.abs() @ w64.abs(), n=V,
+                what=f"{what} d_hidden vs the GEMM over the GPU logits gradient")
+    check_close(wd.grad, dz.t() @ h64, rtol=2.0 ** -8, atol=1e-9, mag=dz.abs().t() @ h64.abs(), n=h.shape[0],
+                what=f"{what} d_weight vs the GEMM over the GPU logits gradient")
+
+
+@pytest.mark.parametrize("M,H,V,T,cols", [(300, 128, 1000, 1.0, 256), (257, 96, 513, 0.7, 512),
+                                          (64, 64, 256, 1.3, 256), (300, 128, 1000, 1.0, 1024)])
+def test_forward_and_backward(dev, monkeypatch, M, H, V, T, cols):
     h, w, lab = _inputs(M, H, V, seed=M + V)
     lab[5] = -100
-    print(f"lm_head M={M} H={H} V={V} T={T}", flush=True)
+    lab[6], lab[7], lab[8] = 255, 256, V - 1  # the last and first column of two splits, the last entry
+    _split(monkeypatch, M, cols)
+    print(f"lm_head M={M} H={H} V={V} T={T} split={cols}", flush=True)
     hd = h.to(dev).requires_grad_(True)
     wd = w.to(dev).requires_grad_(True)
     lp, ent = linear_cross_entropy(hd, wd, lab.to(dev), T, "none")
@@ -46,17 +78,38 @@ def test_forward_and_backward(dev, M, H, V, T):
     ((lpr * dlp.double()).sum() + (entr * dent.double()).sum()).backward()
     assert _close(lp, lpr.detach(), 1e-3, 1e-3) == 0.0
     assert _close(ent, entr.detach(), 1e-3, 1e-3) == 0.0
-    for got, ref in ((hd.grad, hr.grad), (wd.grad, wr.grad)):
-        scale = float(ref.abs().max())
-        assert _close(got, ref, 1e-2 * scale, 2e-2) < 1e-2
-        d = (got.float().cpu().double() - ref).norm() / ref.norm()
-        assert float(d) < 1e-2
+    _, _, lse, ez = lce.lm_head_forward(hd.detach(), wd.detach(), lab.to(dev), T)
+    _check_grads(hd, wd, h, w, lab, T, dlp, dent, hr, wr, lse, ez, f"M={M} V={V} split={cols}")
+
+
+def test_dlogits_range_equals_whole_vocabulary_columns(dev):
+    """The per-split kernel reproduces the whole-vocabulary logits gradient's
+    columns bit for bit (same 256-column tiles, same k order), labels mapped
+    into the split, for splits that start on any 256-column tile."""
+    M, H, V, T = 200, 96, 1300, 0.9
+    h, w, lab = _inputs(M, H, V, seed=21)
+    lab[:6] = torch.tensor([0, 255, 256, 511, 512, V - 1])
+    hd, wd, labd = h.to(dev), w.to(dev), lab.to(dev)
+    _, _, lse, ez = lce.lm_head_forward(hd, wd, labd, T)
+    g = torch.Generator().manual_seed(3)
+    dlp = torch.randn(M, generator=g).to(dev)
+    dent = torch.randn(M, generator=g).to(dev)
+    full = lce.lm_head_dlogits(hd, wd, labd, T, lse, ez, dlp, dent)
+    for v0, n in ((0, 256), (256, 256), (512, 768), (1280, 20), (768, 532)):
+        dz = torch.full((M, n + 8), 7.0, dtype=torch.bfloat16, device=dev)
+        _capi.call("af3_lm_head_dlogits_range", hd.data_ptr(), hd.stride(0), wd.data_ptr(), wd.stride(0), M, v0, n,
+                   H, labd.data_ptr(), T, lse.data_ptr(), ez.data_ptr(), dlp.data_ptr(), 1, 1.0, dent.data_ptr(),
+                   dz.data_ptr(), dz.stride(0), _capi.stream_of(dev))
+        torch.cuda.synchronize()
+        assert torch.equal(dz[:, :n].view(torch.int16), full[:, v0:v0 + n].view(torch.int16)), (v0, n)
+        assert (dz[:, n:] == 7.0).all(), "columns past the split untouched"
 
 
 @pytest.mark.parametrize("reduction", ["sum", "mean"])
-def test_reductions(dev, reduction):
+def test_reductions(dev, monkeypatch, reduction):
     M, H, V = 200, 64, 700
     h, w, lab = _inputs(M, H, V, seed=9)
+    _split(monkeypatch, M, 256)
     hd = h.to(dev).requires_grad_(True)
     wd = w.to(dev).requires_grad_(True)
     lp, ent = linear_cross_entropy(hd, wd, lab.to(dev), 1.0, reduction)
@@ -68,16 +121,31 @@ def test_reductions(dev, reduction):
     red = lpr.sum() if reduction == "sum" else lpr.mean()
     red.backward()
     assert abs(lp.item() - red.item()) <= 1e-3 * max(1.0, abs(red.item()))
-    d = (hd.grad.float().cpu().double() - hr.grad).norm() / hr.grad.norm()
-    assert float(d) < 1e-2
+    for got, ref in ((hd.grad, hr.grad), (wd.grad, wr.grad)):
+        check_close(got, ref, rtol=2e-2, atol=1e-2 * float(ref.abs().max()), what=f"{reduction} gradients")
 
 
-def test_full_vocabulary(dev):
+def test_full_vocabulary(dev, monkeypatch):
+    """Forward and backward over the whole gpt-oss vocabulary, the backward in
+    22 splits of 9472 columns (the last one ragged)."""
     M, H, V = 96, 256, 201088
     h, w, lab = _inputs(M, H, V, seed=4, scale=0.1)
+    lab[:3] = torch.tensor([9471, 9472, V - 1])
+    _split(monkeypatch, M, 9472)
     print("lm_head full vocabulary", flush=True)
-    lp, ent = linear_cross_entropy(h.to(dev), w.to(dev), lab.to(dev), 1.0, "none")
+    hd = h.to(dev).requires_grad_(True)
+    wd = w.to(dev).requires_grad_(True)
+    lp, ent = linear_cross_entropy(hd, wd, lab.to(dev), 1.0, "none")
+    g = torch.Generator().manual_seed(5)
+    dlp = torch.randn(M, generator=g)
+    dent = torch.randn(M, generator=g)
+    (lp * dlp.to(dev)).sum().add((ent * dent.to(dev)).sum()).backward()
     torch.cuda.synchronize()
-    lpr, entr = lmhead.lm_head(h, w, lab, 1.0)
-    assert _close(lp, lpr, 2e-3, 1e-3) == 0.0
-    assert _close(ent, entr, 2e-3, 1e-3) == 0.0
+    hr = h.double().requires_grad_(True)
+    wr = w.double().requires_grad_(True)
+    lpr, entr = lmhead.lm_head(hr, wr, lab, 1.0)
+    ((lpr * dlp.double()).sum() + (entr * dent.double()).sum()).backward()
+    assert _close(lp, lpr.detach(), 2e-3, 1e-3) == 0.0
+    assert _close(ent, entr.detach(), 2e-3, 1e-3) == 0.0
+    _, _, lse, ez = lce.lm_head_forward(hd.detach(), wd.detach(), lab.to(dev), 1.0)
+    _check_grads(hd, wd, h, w, lab, 1.0, dlp, dent, hr, wr, lse, ez, "full vocabulary")
