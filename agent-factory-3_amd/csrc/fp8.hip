@@ -113,28 +113,43 @@ __global__ __launch_bounds__(256) void e5m2_cols_kernel(const uint8_t* __restric
 // rebiased fp32 pattern with round-to-nearest-even; results below 2^-6 are
 // multiples of 2^-9, rounded with v_rndne_f32 on the exact product by 512.
 __device__ __forceinline__ uint32_t f8_e4m3_rne_sat(float v) {
+  // every case computed and selected (no divergent branches in the caller's loop)
   const uint32_t u = __float_as_uint(v);
   const uint32_t sign = (u >> 24) & 0x80u;
   const uint32_t a = u & 0x7FFFFFFFu;
-  if (a > 0x7F800000u) return sign | 0x7Fu;            // NaN
-  if (a >= 0x43E80000u) return sign | 0x7Eu;           // >= 464 (and inf): saturate to 448
-  if (a < 0x3C800000u) {                               // < 2^-6: subnormal (or zero)
-    const float t = __builtin_rintf(__uint_as_float(a) * 512.0f);
-    return sign | (uint32_t)t;                         // 0..8 (8 = the smallest normal, 0x08)
-  }
-  const uint32_t r = (a + 0x7FFFFu + ((a >> 20) & 1u)) >> 20;  // RNE to 3 mantissa bits
-  return sign | (r - (120u << 3));                     // rebias 127 -> 7
+  const uint32_t sub = (uint32_t)__builtin_rintf(__uint_as_float(a) * 512.0f);  // |v| < 2^-6: 0..8 (8 = 0x08)
+  const uint32_t nrm = ((a + 0x7FFFFu + ((a >> 20) & 1u)) >> 20) - (120u << 3);  // RNE to 3 mantissa bits, rebias
+  uint32_t r = a < 0x3C800000u ? sub : nrm;
+  r = a >= 0x43E80000u ? 0x7Eu : r;  // >= 464 (and inf): saturate to 448
+  r = a > 0x7F800000u ? 0x7Fu : r;   // NaN
+  return sign | r;
 }
 
 // E4M3FN code -> bf16 bits (exact)
 __device__ __forceinline__ uint32_t f8_e4m3_to_bf16(uint32_t c) {
   const uint32_t sign = (c & 0x80u) << 8, ex = (c >> 3) & 0xFu, m = c & 7u;
-  if (ex == 0) {
-    if (m == 0) return sign;
-    const float f = (float)m * (1.0f / 512.0f);  // exact
-    return sign | (__float_as_uint(f) >> 16);
-  }
-  return sign | ((ex + 120u) << 7) | (m << 4);
+  const uint32_t sub = __float_as_uint((float)m * (1.0f / 512.0f)) >> 16;  // exact; 0 for m = 0
+  const uint32_t nrm = ((ex + 120u) << 7) | (m << 4);
+  return sign | (ex == 0 ? sub : nrm);
+}
+
+// Four values -> their E4M3FN codes in bytes 0..3 (v_cvt_pk_fp8_f32: round to
+// nearest even, subnormals kept; equal to f8_e4m3_rne_sat for every finite value
+// below 464 in magnitude, the only values the quantizer feeds it: x / scale with
+// scale = amax / 448 stays within 448 (1 + 2^-22)).
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
+// the bf16 values of four E4M3FN codes (bytes 0..3 of w) as two bf16 pairs (exact:
+// every E4M3 value is a bf16 value, so the fp32 conversion's high half is it)
+__device__ __forceinline__ void e4m3x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  typedef __attribute__((ext_vector_type(2))) float f32x2;
+  const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false), b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  lo = __builtin_amdgcn_perm(__float_as_uint(a[1]), __float_as_uint(a[0]), 0x07060302u);
+  hi = __builtin_amdgcn_perm(__float_as_uint(b[1]), __float_as_uint(b[0]), 0x07060302u);
 }
 
 // One row per block: amax over the row (fp32), scale = max(amax, 1e-12) / 448,
@@ -176,22 +191,21 @@ __global__ __launch_bounds__(256) void quant_e4m3_rows_kernel(const uint16_t* __
   for (int j = 0; j < CPL; ++j) {
     const int c = lane + 64 * j;
     if (c >= nch) break;
-    uint32_t q[8];
+    float f[8];
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
-      q[2 * h] = f8_e4m3_rne_sat(af3_bf16_to_f32(v[j][h] & 0xFFFFu) * inv);
-      q[2 * h + 1] = f8_e4m3_rne_sat(af3_bf16_to_f32(v[j][h] >> 16) * inv);
+      f[2 * h] = af3_bf16_to_f32(v[j][h] & 0xFFFFu) * inv;
+      f[2 * h + 1] = af3_bf16_to_f32(v[j][h] >> 16) * inv;
     }
+    const uint32_t w0 = e4m3x4(f[0], f[1], f[2], f[3]), w1 = e4m3x4(f[4], f[5], f[6], f[7]);
     typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
-    __builtin_nontemporal_store((u32x2){q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24),
-                                        q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24)},
-                                (u32x2*)(orow + c * 8));
-    if (brow)
-      __builtin_nontemporal_store(af3_u32x4{f8_e4m3_to_bf16(q[0]) | (f8_e4m3_to_bf16(q[1]) << 16),
-                                            f8_e4m3_to_bf16(q[2]) | (f8_e4m3_to_bf16(q[3]) << 16),
-                                            f8_e4m3_to_bf16(q[4]) | (f8_e4m3_to_bf16(q[5]) << 16),
-                                            f8_e4m3_to_bf16(q[6]) | (f8_e4m3_to_bf16(q[7]) << 16)},
-                                  (af3_u32x4*)(brow + c * 8));
+    __builtin_nontemporal_store((u32x2){w0, w1}, (u32x2*)(orow + c * 8));
+    if (brow) {
+      uint32_t b0, b1, b2, b3;
+      e4m3x4_to_bf16(w0, b0, b1);
+      e4m3x4_to_bf16(w1, b2, b3);
+      __builtin_nontemporal_store(af3_u32x4{b0, b1, b2, b3}, (af3_u32x4*)(brow + c * 8));
+    }
   }
 }
 

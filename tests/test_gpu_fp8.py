@@ -62,6 +62,32 @@ def test_quantize_per_token(dev, M, K):
     assert c2.dtype == torch.float8_e4m3fn and torch.equal(s2, scale)
 
 
+@pytest.mark.parametrize("shift", [0, 9, -20])
+def test_quantize_every_bf16_value(dev, shift):
+    """Every finite bf16 value of magnitude <= 448 2^shift, in rows whose
+    maximum is 448 2^shift (so the scale is 2^shift and x / scale is the bf16
+    value times a power of two): every E4M3 rounding tie, the subnormal codes
+    and the top of the range, bit-exact against the oracle's round-to-nearest-
+    even rule, with the codes' bf16 values."""
+    bits = torch.arange(0, 1 << 16, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    v = bits.float()
+    lim = 448.0 * 2.0 ** shift
+    vals = bits[torch.isfinite(v) & (v.abs() <= lim)]
+    K = 2880
+    n = vals.numel()
+    M = (n + K - 2) // (K - 1)
+    x = torch.zeros(M, K, dtype=torch.bfloat16)
+    x[:, 0] = lim
+    flat = torch.zeros(M * (K - 1), dtype=torch.bfloat16)
+    flat[:n] = vals
+    x[:, 1:] = flat.view(M, K - 1)
+    codes, scale, out_bf16 = kernels.quantize_per_token_e4m3(x.to(dev), with_bf16=True)
+    rc, rs = fp8.quantize_per_token(x.float().numpy())
+    assert np.array_equal(scale.cpu().numpy(), rs) and np.all(rs == np.float32(2.0 ** shift))
+    assert np.array_equal(_u8(codes.contiguous()), rc)
+    assert np.array_equal(out_bf16.float().cpu().numpy(), fp8.e4m3_to_f32(rc).astype(np.float32))
+
+
 def _fp8_rows(x, W, offs, gather, k, trans, bias=None, gammas=None):
     """oracle: (sum_k E4M3(x/s)[a(r)] W[e]) * s[a(r)] + bias, then gammas, bf16."""
     codes, s = fp8.quantize_per_token(x.float().numpy())
