@@ -44,8 +44,8 @@ _SIGNATURES = {
                                    _f32, _f32, _p]),
     "af3_moe_gemm_rowscale": (_i32, [_p, _i64, _p, _i32, _p, _p, _i32, _p, _p, _i32, _p, _p, _p, _i32, _i32,
                                      _i32, _i32, _i32, _i32, _p, _i64, _p, _p]),
-    "af3_moe_gemm_f8": (_i32, [_p, _i64, _p, _i32, _p, _p, _p, _p, _i32, _p, _p, _p, _i32, _i32, _i32, _i32, _i32,
-                               _i32, _p, _i64, _p, _p]),
+    "af3_moe_gemm_f8": (_i32, [_p, _i64, _p, _i32, _p, _p, _i32, _p, _p, _i32, _p, _p, _p, _i32, _i32, _i32, _i32,
+                               _i32, _i32, _p, _i64, _p, _p]),
     "af3_moe_combine": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _p, _i64, _p]),
     "af3_mxfp4_to_fp8_e5m2": (_i32, [_p, _p, _p, _i64, _p]),
     "af3_mxfp4_to_fp8_e5m2_colmajor": (_i32, [_p, _p, _p, _i32, _i32, _i32, _p]),

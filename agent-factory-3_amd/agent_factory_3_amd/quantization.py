@@ -283,14 +283,17 @@ def moe_combine(rows, scatter_indx, n_expts_act):
     return out
 
 
-def moe_rows_f8(codes, a_row_scale, blocks, scales, bias, routing_data, gather_indx=None, gammas=None):
-    """Forward rows of the fp8 mode on the block-scaled MFMA: per-token E4M3
-    ``codes`` [Tx, K] (float8_e4m3fn, rows 16-byte aligned) times the MXFP4
-    weights, ``(acc * a_row_scale[a(r)] + bias[e]) * gammas`` in bf16.  None
-    when the kernel's requirements do not hold (the caller then runs the
-    bf16-operand form of the same arithmetic)."""
+def moe_rows_f8(codes, a_row_scale, blocks, scales, bias, routing_data, gather_indx=None, gammas=None,
+                trans_w=False):
+    """Rows of the fp8 mode on the block-scaled MFMA: per-token E4M3 ``codes``
+    [Tx, K] (float8_e4m3fn, rows 16-byte aligned) times the MXFP4 weights
+    (``trans_w`` as in ``moe_rows``: False for the forward, True for the input
+    gradient, whose weights the kernel converts to E5M2), ``(acc *
+    a_row_scale[a(r)] + bias[e]) * gammas`` in bf16.  None when the kernel's
+    requirements do not hold (the caller then runs the bf16-operand form of
+    the same arithmetic)."""
     dev = codes.device
-    E, N, K = _weight_dims(blocks, False)
+    E, N, K = _weight_dims(blocks, trans_w)
     if codes.shape[-1] != K:
         raise ValueError(f"codes have {codes.shape[-1]} columns, weight reduction dim is {K}")
     g = _gather_ptr(gather_indx)
@@ -305,7 +308,8 @@ def moe_rows_f8(codes, a_row_scale, blocks, scales, bias, routing_data, gather_i
     if R == 0 or pid_map.numel() == 0:
         return y
     ld = codes.stride(0) if codes.shape[0] > 1 else K
-    if codes.stride(-1) != 1 or ld % 16 or codes.data_ptr() % 16 or K % 64 or GEMM_TILE["tile_cfg"] not in (0, 22):
+    if (codes.stride(-1) != 1 or ld % 16 or codes.data_ptr() % 16 or K % 64 or (trans_w and N % 64)
+            or GEMM_TILE["tile_cfg"] not in ((0, 23) if trans_w else (0, 22))):
         return None
     blocks = blocks if blocks.data_ptr() % 16 == 0 else blocks.clone()
     b = bias.to(torch.float32).contiguous() if bias is not None else None
@@ -317,19 +321,20 @@ def moe_rows_f8(codes, a_row_scale, blocks, scales, bias, routing_data, gather_i
 
     def launch():
         return _capi.try_call("af3_moe_gemm_f8", codes.data_ptr(), ld, _capi.ptr(g),
-                              k_act if g is not None else 1, blocks.data_ptr(), scales.data_ptr(), _capi.ptr(b),
+                              k_act if g is not None else 1, blocks.data_ptr(), scales.data_ptr(), int(trans_w),
+                              _capi.ptr(b),
                               _capi.ptr(gm), gm_f32, ed.token_offs_raw.data_ptr(), pid_map.data_ptr(),
                               ed.token_offs_pad[bm].data_ptr(), pid_map.numel(), bm, 0, E, N, K, y.data_ptr(), N,
                               s.data_ptr(), _capi.stream_of(dev))
     if KERNEL_TIMER is None:
         ok = launch()
     else:
-        with KERNEL_TIMER("moe_gemm_fwd_f8", 2 * R * N * K):
+        with KERNEL_TIMER("moe_gemm_dgrad_f8" if trans_w else "moe_gemm_fwd_f8", 2 * R * N * K):
             ok = launch()
     return y if ok else None
 
 
-FP8_BLOCK_SCALED = True  # fp8-mode forward on the block-scaled MFMA (else: E4M3 values as bf16 operands)
+FP8_BLOCK_SCALED = True  # fp8 mode on the block-scaled MFMA (else: E4M3 values as bf16 operands)
 
 
 def matmul_ogs(x, w_blocks_scales, bias, routing_data=None, gather_indx=None, scatter_indx=None, gammas=None,
@@ -426,9 +431,18 @@ class DequantMoEMatmul(torch.autograd.Function):
         with on_device(grad_output.device):
             g = grad_output.to(torch.bfloat16).contiguous()
             if ctx.dequant_dtype == "fp8":  # quantization.py:382-408
-                _, gs, gq = kernels.quantize_per_token_e4m3(g, with_bf16=True)
-                grad_x = matmul_ogs(gq, (blocks, scales), None, ctx.routing_data, ctx.bwd_gather_indx,
-                                    ctx.bwd_scatter_indx, ctx.bwd_gammas, trans_w=True, a_row_scale=gs)
+                grad_x = None
+                if FP8_BLOCK_SCALED:
+                    gc, gs = kernels.quantize_per_token_e4m3(g)
+                    y = moe_rows_f8(gc, gs, blocks, scales, None, ctx.routing_data, ctx.bwd_gather_indx,
+                                    ctx.bwd_gammas, trans_w=True)
+                    if y is not None:
+                        k = ctx.routing_data.n_expts_act if ctx.routing_data is not None else 1
+                        grad_x = y if ctx.bwd_scatter_indx is None else moe_combine(y, ctx.bwd_scatter_indx, k)
+                if grad_x is None:
+                    _, gs, gq = kernels.quantize_per_token_e4m3(g, with_bf16=True)
+                    grad_x = matmul_ogs(gq, (blocks, scales), None, ctx.routing_data, ctx.bwd_gather_indx,
+                                        ctx.bwd_scatter_indx, ctx.bwd_gammas, trans_w=True, a_row_scale=gs)
             else:
                 grad_x = matmul_ogs(g, (blocks, scales), None, ctx.routing_data, ctx.bwd_gather_indx,
                                     ctx.bwd_scatter_indx, ctx.bwd_gammas, trans_w=True)

@@ -114,6 +114,17 @@ __device__ __forceinline__ void af3_dequant_u32_int(uint32_t v, uint32_t scale, 
   }
 }
 
+// E5M2 byte of one e2m1 nibble under e8m0 scale byte S by the reference's
+// integer rule (kernels.py:21-37: exponent field ee + S - 113, mantissa m << 1
+// for ee > 0; zero magnitude or an exponent below 1 gives the signed zero),
+// truncated to a byte as its column-major store does (kernels.py:272-285)
+__device__ __forceinline__ uint32_t af3_e2m1_to_e5m2_byte(uint32_t nib, uint32_t scale) {
+  const uint32_t sign = (nib >> 3) & 1u, ee = (nib >> 1) & 3u, m = nib & 1u;
+  const int exp = (int)ee + (int)scale - 113;
+  const uint32_t r = (sign << 7) | ((uint32_t)exp << 2) | (ee ? (m << 1) : 0u);
+  return ((nib & 7u) == 0u || exp < 1) ? (sign << 7) : (r & 0xFFu);
+}
+
 __host__ __device__ __forceinline__ int64_t af3_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // gpt-oss clamped SwiGLU per element (kernels.py:431-441 forward, 533-545

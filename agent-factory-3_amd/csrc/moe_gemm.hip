@@ -1711,6 +1711,276 @@ __global__ __launch_bounds__(256) void gemm5_dgrad_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------
+// fp8-mode input gradient (the reference's fp8 backward, quantization.py:382-408:
+// per-token E4M3 gradient x the weights' E5M2 form): A = E4M3 codes [rows][K]
+// bytes, B = the packed MXFP4 weights of gemm5 (W[e][k][n/32][16], scales
+// [e][k][n/32]), converted to E5M2 in registers, on the block-scaled MFMA
+// v_mfma_scale_f32_32x32x64_f8f6f4 (A format E4M3, B format E5M2, block scales
+// 2^0); the per-token scale multiplies the fp32 accumulator in gemm5's epilogue.
+// Work items, wave layout (wave w: all rows x columns 64 w .. 64 w + 63, or the
+// NARROW 128 x 512 item with 128 columns per wave) and the epilogue are gemm5's.
+// The k permutation is the MFMA's own: lane (r, h) holds k 16 h .. 16 h + 15 in
+// bytes 0-15 and 32 + 16 h .. in bytes 16-31 of its 32-byte operand.
+//   A   [RM rows][64 k] codes, 16-byte chunk c of row r in slot c ^ ((r >> 2) & 3)
+//       (the fp8 forward's layout); a lane's operand is two 16-byte reads.
+//   B   gemm5's packed rows; four ds_read_b64_tr_b8 per pair group (rows 16 h +
+//       {0, 8, 32, 40} .. + 7) give a lane the bytes of its column pair at the 32
+//       k of its operand; per byte (one k row) v_cvt_scalef32_pk_f32_fp4 with the
+//       row's scale yields the (even, odd) column values and v_cvt_pk_bf8_f32
+//       packs four rows of each into E5M2 bytes.  That is exact and equal to the
+//       reference's integer rule for scale bytes 114 .. 140 (every value an E5M2
+//       normal); a wave's k-step holding another scale byte rebuilds its
+//       fragments with the integer rule (af3_e2m1_to_e5m2_byte).
+//   S   the scales as zero-extended dwords [blocks][64 k] (gemm5's copy).
+// Four-stage ring, copies issued three k-steps ahead; the barrier at k-step kt
+// publishes stage kt + 1, whose B fragments are read and converted during the
+// MFMAs of k-step kt (double-buffered B), and the A operands are read one row
+// group ahead of their MFMAs.
+// ---------------------------------------------------------------------------
+constexpr int kD8Stages = 4;
+constexpr int kD8Stage = 28 * 1024;  // A 16 + B 8 + S 2 KB, NARROW A 8 + B 16 + S 4 KB
+static_assert(kD8Stages * kD8Stage <= kD5LdsBytes, "fp8 dgrad ring inside gemm5's LDS area");
+
+typedef __attribute__((ext_vector_type(2))) float af3_f32x2;
+
+// E5M2 bytes of the 8 packed bytes (w0: k rows 0..3, w1: rows 4..7) of one
+// transposing read: even columns -> e[0..1], odd -> o[0..1]; s[q] = scale dword of row q
+template <bool EXACT>
+__device__ __forceinline__ void d8_cvt(uint32_t w0, uint32_t w1, const uint32_t s[8], uint32_t e[2], uint32_t o[2]) {
+  if constexpr (EXACT) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t ev = 0, od = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t byte = ((h ? w1 : w0) >> (8 * q)) & 0xFFu;
+        ev |= af3_e2m1_to_e5m2_byte(byte & 0xFu, s[4 * h + q]) << (8 * q);
+        od |= af3_e2m1_to_e5m2_byte(byte >> 4, s[4 * h + q]) << (8 * q);
+      }
+      e[h] = ev;
+      o[h] = od;
+    }
+  } else {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t src = h ? w1 : w0;
+      af3_f32x2 r[4];
+      r[0] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(src, __uint_as_float(s[4 * h + 0] << 23), 0);
+      r[1] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(src, __uint_as_float(s[4 * h + 1] << 23), 1);
+      r[2] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(src, __uint_as_float(s[4 * h + 2] << 23), 2);
+      r[3] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(src, __uint_as_float(s[4 * h + 3] << 23), 3);
+      int ev = __builtin_amdgcn_cvt_pk_bf8_f32(r[0][0], r[1][0], 0, false);
+      ev = __builtin_amdgcn_cvt_pk_bf8_f32(r[2][0], r[3][0], ev, true);
+      int od = __builtin_amdgcn_cvt_pk_bf8_f32(r[0][1], r[1][1], 0, false);
+      od = __builtin_amdgcn_cvt_pk_bf8_f32(r[2][1], r[3][1], od, true);
+      e[h] = (uint32_t)ev;
+      o[h] = (uint32_t)od;
+    }
+  }
+}
+
+template <bool NARROW>
+__device__ __forceinline__ void d8_tile(const Params& p, uint8_t* lds, int e, int row_lo, int nrows, int n0, int ncols) {
+  constexpr int RM = NARROW ? 128 : 256;  // tile rows
+  constexpr int CN = NARROW ? 512 : 256;  // tile columns
+  constexpr int TM = RM / 32;
+  constexpr int WC = CN / 4;              // columns per wave
+  constexpr int PG = WC / 64;             // pair groups (64 columns each) per wave
+  constexpr int TN = 2 * PG;
+  constexpr int BRB = CN / 2;             // packed bytes per weight row
+  constexpr int NCH = BRB / 16;           // 16-byte chunks per weight row
+  constexpr int NBLK = CN / 32;           // scale blocks
+  constexpr int AI = RM / 64, BI = BRB / 64, SI = NBLK / 4;  // copies per wave per k-step
+  constexpr int DPW = AI + BI + SI;
+  static_assert(DPW == 8 || DPW == 10, "copy schedule");
+  constexpr int AOFF = 0, BOFF = RM * 64, SOFF = BOFF + 64 * BRB;
+  static_assert(SOFF + NBLK * 256 <= kD8Stage, "stage layout");
+  auto bswz = [](int k) { return NARROW ? ((k & 7) << 1) : (k & 7); };
+
+  const int nk = p.K / kBK;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = lane & 31, lh = lane >> 5;
+  const int wn0 = wave * WC;
+
+  // ---- global -> LDS copy sources ----
+  const uint8_t* arow[AI];  // 16 rows of 64 codes per copy
+#pragma unroll
+  for (int i = 0; i < AI; ++i) {
+    const int row = (wave * AI + i) * 16 + (lane >> 2);
+    int64_t src = row_lo + (row < nrows ? row : 0);
+    if (p.a.gather) src = p.a.gather[src] / p.a.gdiv;
+    arow[i] = (const uint8_t*)p.a.ptr + src * p.a.ld + (f8_chunk(row, lane & 3) << 4);
+  }
+  const uint8_t* bsrc[BI];
+#pragma unroll
+  for (int j = 0; j < BI; ++j) {
+    const int kr = (wave * BI + j) * (1024 / BRB) + lane / NCH;
+    int c = (lane % NCH) ^ bswz(kr);
+    if (c * 32 >= ncols) c = 0;  // columns past the tile: any valid bytes (never stored)
+    bsrc[j] = (const uint8_t*)p.b.ptr + e * p.b.estride + (int64_t)kr * p.b.ld + (n0 >> 1) + c * 16;
+  }
+  const uint8_t* ssrc[SI];
+#pragma unroll
+  for (int j = 0; j < SI; ++j) {
+    int q = wave * SI + j;
+    if (q * 32 >= ncols) q = 0;
+    ssrc[j] = p.b.scales + e * p.b.sestride + (int64_t)lane * p.b.sld + (n0 >> 5) + q;
+  }
+  const int64_t bstep = (int64_t)kBK * p.b.ld, sstep = (int64_t)kBK * p.b.sld;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+  auto issue_one = [&](int kc, int j) {
+    const uint32_t st = lds0 + (uint32_t)((kc % kD8Stages) * kD8Stage);
+    if (j < AI) {
+      g4_dma16(arow[j] + kc * kBK, st + (uint32_t)(AOFF + (wave * AI + j) * 1024));
+    } else if (j < AI + BI) {
+      g4_dma16(bsrc[j - AI] + kc * bstep, st + (uint32_t)(BOFF + (wave * BI + j - AI) * 1024));
+    } else {
+      asm volatile("s_nop 0\n\tglobal_load_lds_ubyte %0, off" ::"v"(ssrc[j - AI - BI] + kc * sstep), "{m0}"(st + (uint32_t)(SOFF + (wave * SI + j - AI - BI) * 256)) : "memory");
+    }
+  };
+
+  // ---- lane-fixed LDS byte offsets inside a stage ----
+  const int ach = (lr >> 2) & 3;
+  const int aoff_lo = AOFF + lr * 64 + ((lh ^ ach) << 4), aoff_hi = AOFF + lr * 64 + (((2 + lh) ^ ach) << 4);
+  const int gi = lane & 15, gg = lane >> 4;
+  int boff[PG], soff[PG];
+#pragma unroll
+  for (int pg = 0; pg < PG; ++pg) {
+    const int chunk = wn0 / 32 + 2 * pg + (gg & 1);
+    const int kr = 16 * (gg >> 1) + (gi >> 1);
+    boff[pg] = BOFF + kr * BRB + ((chunk ^ bswz(kr)) << 4) + (gi & 1) * 8;  // + BRB (8 (i & 1) + 32 (i >> 1))
+    soff[pg] = SOFF + (chunk * 64 + 16 * (gg >> 1)) * 4;                   // + 4 (8 (i & 1) + 32 (i >> 1))
+  }
+  constexpr int CW = WC / 32;  // scale dwords per lane for the wave's range check
+  const int coff = SOFF + (wn0 / 32 * 64 + CW * lane) * 4;
+
+  af3_f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  // B operands of the stage at stg: tr reads, scales, range check, conversion
+  auto load_b = [&](const uint8_t* stg, af3_i32x8 (&bf)[TN]) {
+    uint32_t chk[CW];
+    if constexpr (CW == 2) {
+      const uint2 cv = *(const uint2*)(stg + coff);
+      chk[0] = cv.x;
+      chk[1] = cv.y;
+    } else {
+      const af3_u32x4 cv = *(const af3_u32x4*)(stg + coff);
+#pragma unroll
+      for (int q = 0; q < CW; ++q) chk[q] = cv[q];
+    }
+    bool lane_odd = false;
+#pragma unroll
+    for (int q = 0; q < CW; ++q) lane_odd |= chk[q] - 114u > 26u;
+    const bool odd = __builtin_amdgcn_ballot_w64(lane_odd) != 0;
+#pragma unroll
+    for (int pg = 0; pg < PG; ++pg) {
+      uint32_t ev[8], od[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int radd = 8 * (i & 1) + 32 * (i >> 1);
+        const af3_i32x2 wv = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (__attribute__((address_space(3))) af3_i32x2*)(stg + boff[pg] + BRB * radd));
+        const af3_u32x4 s0 = *(const af3_u32x4*)(stg + soff[pg] + 4 * radd);
+        const af3_u32x4 s1 = *(const af3_u32x4*)(stg + soff[pg] + 4 * radd + 16);
+        const uint32_t sc[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+        if (odd)
+          d8_cvt<true>((uint32_t)wv[0], (uint32_t)wv[1], sc, ev + 2 * i, od + 2 * i);
+        else
+          d8_cvt<false>((uint32_t)wv[0], (uint32_t)wv[1], sc, ev + 2 * i, od + 2 * i);
+      }
+      bf[2 * pg] = af3_i32x8{(int)ev[0], (int)ev[1], (int)ev[2], (int)ev[3], (int)ev[4], (int)ev[5], (int)ev[6],
+                             (int)ev[7]};
+      bf[2 * pg + 1] = af3_i32x8{(int)od[0], (int)od[1], (int)od[2], (int)od[3], (int)od[4], (int)od[5], (int)od[6],
+                                 (int)od[7]};
+    }
+  };
+  auto load_a = [&](const uint8_t* stg, int tm) {
+    const af3_u32x4 lo = *(const af3_u32x4*)(stg + aoff_lo + tm * 2048);
+    const af3_u32x4 hi = *(const af3_u32x4*)(stg + aoff_hi + tm * 2048);
+    return af3_i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  };
+
+  // prologue: stages 0..2 in flight, stage 0 published, its B operands converted
+#pragma unroll
+  for (int kc = 0; kc < 3; ++kc)
+    if (kc < nk) {
+#pragma unroll
+      for (int j = 0; j < DPW; ++j) issue_one(kc, j);
+    }
+  if (nk > 2) {
+    if constexpr (DPW == 8) AF3_ASM_WAIT_VM(16); else AF3_ASM_WAIT_VM(20);
+  } else if (nk > 1) {
+    if constexpr (DPW == 8) AF3_ASM_WAIT_VM(8); else AF3_ASM_WAIT_VM(10);
+  } else {
+    AF3_ASM_WAIT_VM(0);
+  }
+  AF3_ASM_LDS_BARRIER();
+  af3_i32x8 bfA[TN], bfB[TN];
+  load_b(lds, bfA);
+  // k-step kt: publish stage kt + 1 (its copies in, those of kt + 2 still in flight),
+  // issue k-step kt + 3 into the slot of kt - 1, then the MFMAs of kt with the A
+  // operands read one row group ahead, while stage kt + 1's B operands are converted
+  auto kstep = [&](int kt, af3_i32x8 (&bcur)[TN], af3_i32x8 (&bnxt)[TN]) {
+    if (kt + 2 < nk) {
+      if constexpr (DPW == 8) AF3_ASM_WAIT_VM(8); else AF3_ASM_WAIT_VM(10);
+    } else {
+      AF3_ASM_WAIT_VM(0);
+    }
+    AF3_ASM_LDS_BARRIER();
+    if (kt + 3 < nk) {
+#pragma unroll
+      for (int j = 0; j < DPW; ++j) issue_one(kt + 3, j);
+    }
+    const uint8_t* stg = lds + (kt % kD8Stages) * kD8Stage;
+    af3_i32x8 a0 = load_a(stg, 0), a1;
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+      if (tm + 1 < TM) a1 = load_a(stg, tm + 1);
+      if (tm == TM / 2 && kt + 1 < nk) load_b(lds + ((kt + 1) % kD8Stages) * kD8Stage, bnxt);
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+        acc[tm][tn] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a0, bcur[tn], acc[tm][tn], 0, 1, 0, 127, 0,
+                                                                       127);
+      a0 = a1;
+    }
+  };
+  int kt = 0;
+#pragma nounroll
+  for (; kt + 1 < nk; kt += 2) {
+    kstep(kt, bfA, bfB);
+    kstep(kt + 1, bfB, bfA);
+  }
+  if (kt < nk) kstep(kt, bfA, bfB);
+  d5_epilogue<RM, CN>(p, lds, acc, e, row_lo, nrows, n0, ncols, wn0);
+}
+
+__global__ __launch_bounds__(256) void gemm5_f8_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kD5LdsBytes];
+  int mt, nt;
+  if (!g4_work_item(p, mt, nt)) return;
+  const int32_t ent = p.tile_map[mt];
+  if (ent < 0) return;
+  const int e = ent & 0xFFFF, blk = ent >> 16;
+  const int row_lo = p.offs[e] + blk * kG4Rows;
+  const int nrows = min(kG4Rows, p.offs[e + 1] - row_lo);
+  if (nrows <= 0) return;
+  const int n0 = nt * kG4Rows;
+  if (nrows <= 128) {
+    if (nt & 1) return;
+    d8_tile<true>(p, lds, e, row_lo, nrows, n0, min(2 * kG4Rows, p.N - n0));
+  } else {
+    d8_tile<false>(p, lds, e, row_lo, nrows, n0, min(kG4Rows, p.N - n0));
+  }
+}
+
+// ---------------------------------------------------------------------------
 // row-tile kernel: main GEMMs and the skinny LoRA row products
 // ---------------------------------------------------------------------------
 template <int BM, int BN, int WM, int WN, int AK, int BK_, int AXK, int BXK>
@@ -2028,10 +2298,23 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
   }
   const bool bm_ok = (cfg == 4 || cfg == 22 || cfg == 23) ? block_m == 256 : block_m == 128;
   AF3_REQUIRE(bm_ok, "moe_gemm: tile_cfg %d does not match block_m %d", cfg, block_m);
-  if (a_fp8) {  // E4M3 activations x MXFP4 weights on the block-scaled MFMA (forward, 256-row map)
-    if (trans || block_m != 256 || K % kBK != 0 || K / 32 > kG4MaxG || !al16(w_scales) || !al16(y) || ldy % 8 != 0 ||
+  if (a_fp8) {  // E4M3 activations x MXFP4 weights on the block-scaled MFMA (256-row map)
+    if (trans) {  // input gradient: the weights converted to E5M2 in registers
+      if (block_m != 256 || K % kBK != 0 || N % 64 != 0 || !al16(y) || ldy % 8 != 0 || ldx % 16 != 0 || !al16(x) ||
+          !a_row_scale || lora_r != 0 || epi != 0 || !(cfg == 23 || cfg == 0)) {
+        af3::set_error("moe_gemm_f8 (trans_w 1): needs block_m 256, K %% 64 == 0, N %% 64 == 0, 16-byte aligned "
+                       "rows, a row scale");
+        return AF3_EUNSUPPORTED;
+      }
+      p.group_m = group_m;
+      p.n_nblk = (N + kG4Rows - 1) / kG4Rows;
+      dim3 grid(g4_grid(max_tiles, p.n_nblk, p.group_m));
+      hipLaunchKernelGGL(gemm5_f8_kernel, grid, dim3(256), 0, stream, p);
+      return af3::check_launch("moe_gemm_f8 (input gradient)");
+    }
+    if (block_m != 256 || K % kBK != 0 || K / 32 > kG4MaxG || !al16(w_scales) || !al16(y) || ldy % 8 != 0 ||
         ldx % 16 != 0 || !al16(x) || !a_row_scale || lora_r != 0 || epi != 0 || !(cfg == 22 || cfg == 0)) {
-      af3::set_error("moe_gemm_f8: needs trans_w 0, block_m 256, K %% 64 == 0, 16-byte aligned rows, a row scale");
+      af3::set_error("moe_gemm_f8: needs block_m 256, K %% 64 == 0, 16-byte aligned rows, a row scale");
       return AF3_EUNSUPPORTED;
     }
     p.group_m = group_m;
@@ -2112,12 +2395,13 @@ extern "C" int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gathe
 // E4M3 codes x MXFP4 weights on the block-scaled MFMA.  trans_w 0, block_m
 // 256, no LoRA; AF3_EUNSUPPORTED when a requirement fails.
 extern "C" int af3_moe_gemm_f8(const uint8_t* x_e4m3, int64_t ldx, const int32_t* gather_indx, int gather_div,
-                               const uint8_t* w_blocks, const uint8_t* w_scales, const float* bias, const void* gammas,
-                               int gammas_f32, const int32_t* token_offs, const int32_t* block_pid_map,
-                               const int32_t* tile_offs, int max_tiles, int block_m, int tile_cfg, int n_expts, int N,
-                               int K, uint16_t* y, int64_t ldy, const float* a_row_scale, void* stream) {
+                               const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
+                               const void* gammas, int gammas_f32, const int32_t* token_offs,
+                               const int32_t* block_pid_map, const int32_t* tile_offs, int max_tiles, int block_m,
+                               int tile_cfg, int n_expts, int N, int K, uint16_t* y, int64_t ldy,
+                               const float* a_row_scale, void* stream) {
   AF3_REQUIRE(a_row_scale, "moe_gemm_f8: null row scale");
-  return moe_gemm_impl((const uint16_t*)x_e4m3, ldx, gather_indx, gather_div, w_blocks, w_scales, 0, bias, gammas,
+  return moe_gemm_impl((const uint16_t*)x_e4m3, ldx, gather_indx, gather_div, w_blocks, w_scales, trans_w, bias, gammas,
                        gammas_f32, nullptr, 0, nullptr, 0, token_offs, block_pid_map, tile_offs, max_tiles, block_m,
                        tile_cfg, n_expts, N, K, y, ldy, 0, nullptr, 0, 0.f, 0.f, a_row_scale, stream, 1);
 }

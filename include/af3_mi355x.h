@@ -172,18 +172,24 @@ int af3_moe_gemm_rowscale(const uint16_t* x, int64_t ldx, const int32_t* gather_
                           const int32_t* tile_offs, int max_tiles, int block_m, int tile_cfg, int n_expts, int N,
                           int K, uint16_t* y, int64_t ldy, const float* a_row_scale, void* stream);
 
-/* fp8-mode forward on the block-scaled MFMA (v_mfma_scale_f32_32x32x64_f8f6f4):
+/* fp8 mode on the block-scaled MFMA (v_mfma_scale_f32_32x32x64_f8f6f4):
  * x_e4m3 [rows][ldx bytes] per-token E4M3 codes (ldx % 16 == 0) times the
- * MXFP4 weights (trans_w 0 layout; each 16-byte group and its e8m0 byte go to
- * the MFMA unconverted), y = bf16((acc * a_row_scale[a(r)] + bias) * gammas).
- * Replaces matmul_ogs(x_fp8, w_fp8_t, ...) with the per-token PrecisionConfig
- * at quantization.py:331-356 (the reference's E5M2 weights hold the same
- * values).  block_m 256, no LoRA; AF3_EUNSUPPORTED when a requirement fails. */
+ * MXFP4 weights, y = bf16((acc * a_row_scale[a(r)] + bias) * gammas), products
+ * and layouts as af3_moe_gemm.
+ *   trans_w 0 (forward): each 16-byte group and its e8m0 byte go to the MFMA
+ *   unconverted.  Replaces matmul_ogs(x_fp8, w_fp8_t, ...) with the per-token
+ *   PrecisionConfig at quantization.py:331-356 (the reference's E5M2 weights
+ *   hold the same values).
+ *   trans_w 1 (input gradient, N % 64 == 0): the weights converted to E5M2 in
+ *   registers (the reference's mxfp4_to_fp8_e5m2_colmajor values, kernels.py:
+ *   238-312, for every scale byte).  Replaces matmul_ogs(grad_fp8, w_fp8, ...)
+ *   at quantization.py:382-408.
+ * block_m 256, no LoRA; AF3_EUNSUPPORTED when a requirement fails. */
 int af3_moe_gemm_f8(const uint8_t* x_e4m3, int64_t ldx, const int32_t* gather_indx, int gather_div,
-                    const uint8_t* w_blocks, const uint8_t* w_scales, const float* bias, const void* gammas,
-                    int gammas_f32, const int32_t* token_offs, const int32_t* block_pid_map, const int32_t* tile_offs,
-                    int max_tiles, int block_m, int tile_cfg, int n_expts, int N, int K, uint16_t* y, int64_t ldy,
-                    const float* a_row_scale, void* stream);
+                    const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
+                    const void* gammas, int gammas_f32, const int32_t* token_offs, const int32_t* block_pid_map,
+                    const int32_t* tile_offs, int max_tiles, int block_m, int tile_cfg, int n_expts, int N, int K,
+                    uint16_t* y, int64_t ldy, const float* a_row_scale, void* stream);
 
 /* MXFP4 -> fp8 E5M2, row-major.  Replaces kernels.py:20-108
  * (mxfp4_to_fp8_e5m2_triton): blocks [n_groups][16], scales [n_groups] ->

@@ -173,3 +173,31 @@ def test_block_scaled_forward_tiles(dev, gather, odd):
     assert torch.isfinite(a[~skip]).all()
     ok = ((a - b).abs() <= 1e-2 + 2e-2 * b.abs()) | skip
     assert ok.all(), float((~ok).float().mean())
+
+
+@pytest.mark.parametrize("gather,odd", [(True, False), (False, False), (True, True)])
+def test_block_scaled_dgrad_tiles(dev, gather, odd):
+    """The fp8 input-gradient kernel (weights converted to E5M2 in registers) on
+    the tile shapes of the bf16 kernels' tests, against the oracle over the
+    reference's E5M2 weight bytes (kernels.py:238-312) and the per-token E4M3
+    gradient.  ``odd`` plants e8m0 bytes 0, 1, 254, 255, which the kernel's
+    exact integer path turns into the reference's flushed / wrapped bytes, so
+    every output is compared."""
+    from test_gpu_gemm_tiles import KRED, NOUT, T, TOPK, _routing, _weights
+    g, ref, rd, gi = _routing(dev, 22)
+    blocks, scales = _weights(g, KRED, NOUT, odd)          # W [E, K, N], packed along N
+    Rr = T * TOPK
+    x = torch.randn(T if gather else Rr, KRED, generator=g).to(torch.bfloat16)
+    gam = rd.gate_scal if gather else None
+    codes, s = kernels.quantize_per_token_e4m3(x.to(dev))
+    y = Q.moe_rows_f8(codes, s, blocks.to(dev), scales.to(dev), None, rd, gi if gather else None, gam, trans_w=True)
+    assert y is not None and y.shape == (Rr, NOUT)
+    w8 = fp8.e5m2_colmajor(blocks.numpy(), scales.numpy())            # [E, N, K] bytes
+    W8 = torch.from_numpy(fp8.e5m2_to_f32(w8)).transpose(1, 2)        # [E, K, N] values
+    assert torch.isfinite(W8).all()
+    yr = _fp8_rows(x, W8, ref["offs"], ref["topk_indx"] if gather else None, TOPK, True,
+                   gammas=gam.cpu() if gather else None)
+    a, b = y.float().cpu().double(), yr.double()
+    assert torch.isfinite(a).all()
+    ok = (a - b).abs() <= 1e-2 + 2e-2 * b.abs()
+    assert ok.all(), float((~ok).float().mean())
