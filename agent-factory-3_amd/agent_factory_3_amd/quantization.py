@@ -96,7 +96,11 @@ def mxfp4_to_bf16(blocks, scales):
 def convert_moe_packed_tensors(blocks, scales, *, dtype=torch.bfloat16, rows_per_chunk=None):
     """Dequantize to a full weight, transposed to [E, K, N] (quantization.py:137-172).
 
-    Used by the dequantize-at-load fallback of the quantizer.
+    Used by the dequantize-at-load fallback of the quantizer.  Scale bytes
+    2..252 give the reference's LUT + ldexp values bit for bit; bytes 0, 1 and
+    253..255 follow the kernels' flush-to-signed-zero rule (kernels.py:151-156)
+    where ldexp would give bf16 subnormals, inf or NaN, so a loaded weight
+    equals what the fused GEMMs compute with.
     """
     if dtype != torch.bfloat16:
         raise TypeError("only bf16 dequantisation is implemented")

@@ -516,15 +516,26 @@ def main():
             r.update(cpu_baseline.host_info())
         else:
             r = cpu_baseline.run_layer(inp_cpu, warmup=1, runs=1)
+            bwd = inp_cpu.dy is not None
             sample = (f"the whole layer (after one untimed warm-up pass): all {E} experts' MXFP4 weights dequantized "
-                      f"(LUT + ldexp) for the forward and again for the backward ({r['dequant_s']:.1f} s), then the "
-                      f"per-expert bf16 loop over all {T * k} routed rows, fwd+bwd with LoRA ({r['loop_s']:.1f} s); "
+                      f"(LUT + ldexp) for the forward{' and again for the backward' if bwd else ''} "
+                      f"({r['dequant_s']:.1f} s), then the per-expert bf16 loop over all {T * k} routed rows, "
+                      f"{'fwd+bwd' if bwd else 'forward'}{' with LoRA' if lora_r else ''} ({r['loop_s']:.1f} s); "
                       f"wall {r['t_layer_s']:.1f} s")
         cpu = {"value": r["tokens_per_s"], "unit": "tokens/s", "cores": r["threads"], "kind": "port",
                "sample": sample, "cpu_model": r["cpu_model"], "affinity_cores": r["affinity_cores"],
                "omp_num_threads": r["omp_num_threads"], "dequant_s_per_expert": r["dequant_s_per_expert"],
                "loop_s_per_row": r["loop_s_per_row"]}
         log(f"cpu baseline {r['tokens_per_s']:.1f} tokens/s")
+        if not args.no_extras:  # the standalone configurations on the same cores
+            blocks, scales = workloads.cfg0()
+            d = cpu_baseline.run_dequant(blocks, scales)
+            cpu["cfg0_dequant"] = {"seconds": d["seconds"],
+                                   "GBps": (8294400 + 518400 + 33177600) / d["seconds"] / 1e9}
+            gu, dout = workloads.cfg1()
+            sw = cpu_baseline.run_swiglu(gu, dout)
+            cpu["cfg1_swiglu_fwd_bwd"] = {"seconds": sw["seconds"]}
+            log(f"cpu cfg0 dequant {d['seconds'] * 1e3:.1f} ms, cfg1 SwiGLU fwd+bwd {sw['seconds'] * 1e3:.1f} ms")
 
     line = {
         "metric": METRIC,

@@ -10,7 +10,10 @@ autograd for the backward.  Test/bench infrastructure only.
 ``run_layer`` times the whole layer once, unscaled: every expert's weights
 dequantized for the forward, the per-expert loop (forward + autograd
 backward) over all routed rows, and every expert's weights dequantized again
-for the backward (DequantMoEMatmul re-derives them, quantization.py:364-373).
+for the backward (DequantMoEMatmul re-derives them, quantization.py:364-373);
+a forward-only workload (no output gradient) runs the forward part alone.
+``run_dequant`` / ``run_swiglu`` time the standalone dequant (cfg0) and
+SwiGLU forward + backward (cfg1).
 ``run_sample`` times a bounded sample (the rows of a few experts, fwd + bwd,
 plus the dequant of those experts) and scales it to the whole layer:
     t_layer = t_dequant_per_expert * E * 2   (forward and backward re-dequant,
@@ -61,11 +64,19 @@ def host_info() -> dict:
 
 
 def _expert_step(inp, e, W, ids, gam, s):
-    """Forward + autograd backward of expert e's routed rows; returns the row count."""
+    """Forward (+ autograd backward when the workload has an output gradient) of
+    expert e's routed rows; returns the row count."""
     lora = inp.lora
     tok, slot = torch.nonzero(ids == e, as_tuple=True)
     if tok.numel() == 0:
         return 0
+    if inp.dy is None:
+        with torch.no_grad():
+            Wgu, Wdn = W
+            xe = inp.x[tok]
+            act = _swiglu(xe @ Wgu.T + inp.gu_bias[e])
+            _ = (act @ Wdn.T + inp.dn_bias[e]) * gam[tok, slot, None]
+        return tok.numel()
     xe = inp.x[tok].clone().requires_grad_(True)
     Wgu, Wdn = W
     gu = xe @ Wgu.T + inp.gu_bias[e]
@@ -110,14 +121,46 @@ def _layer_once(inp) -> dict:
     rows = sum(_expert_step(inp, e, W[e], ids, gam, s) for e in range(E))
     t2 = time.perf_counter()
     del W
-    W = dequant_all()  # the backward re-dequant
+    if inp.dy is not None:
+        W = dequant_all()  # the backward re-dequant
+        del W
     t3 = time.perf_counter()
-    del W
     t_layer = t3 - t0
     t_deq = (t1 - t0) + (t3 - t2)
-    return dict(tokens_per_s=T / t_layer, t_layer_s=t_layer, dequant_s=t_deq, dequant_s_per_expert=t_deq / (2 * E),
+    n_deq = 2 * E if inp.dy is not None else E
+    return dict(tokens_per_s=T / t_layer, t_layer_s=t_layer, dequant_s=t_deq, dequant_s_per_expert=t_deq / n_deq,
                 loop_s=t2 - t1, loop_s_per_row=(t2 - t1) / max(1, rows), rows=rows,
                 threads_used=torch.get_num_threads())
+
+
+def _median_time(fn, warmup=1, runs=3) -> float:
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def run_dequant(blocks, scales) -> dict:
+    """cfg0 on the CPU: the LUT + ldexp dequant of one weight (median of 3 after a warm-up)."""
+    torch.set_num_threads(threads())
+    t = _median_time(lambda: _mx.dequant_lut_ldexp(blocks, scales))
+    return dict(seconds=t, threads=torch.get_num_threads())
+
+
+def run_swiglu(gate_up, dout) -> dict:
+    """cfg1 on the CPU: the clamped SwiGLU forward + autograd backward in bf16 eager
+    (median of 3 after a warm-up)."""
+    torch.set_num_threads(threads())
+
+    def once():
+        g = gate_up.clone().requires_grad_(True)
+        _swiglu(g).backward(dout)
+    t = _median_time(once)
+    return dict(seconds=t, threads=torch.get_num_threads())
 
 
 def run_sample(inp, ranks=(0, 10, 60, 110)) -> dict:
