@@ -876,9 +876,72 @@ def enable_expert_lora(experts: Mxfp4Bf16DequantGptOssExperts, r: int = 16, lora
     return experts
 
 
+EXPERT_LORA_PARAMS = ("gate_up_proj_lora_A", "gate_up_proj_lora_B", "down_proj_lora_A", "down_proj_lora_B")
+
+
 def _full(t):
     """The whole tensor of a (possibly FSDP2-sharded) parameter: DTensor.full_tensor() is a collective."""
     return t.full_tensor() if hasattr(t, "full_tensor") else t
+
+
+def expert_lora_state_dict(model, to_cpu: bool = True) -> dict:
+    """The expert-LoRA adapters of every experts module, for saving with the
+    attention adapters.
+
+    The reference saves adapters through PEFT (``get_peft_model_state_dict``,
+    model_trainer.py:573, or ``save_pretrained``), which keeps only keys that
+    name the adapter, so these parameters, registered on the experts module,
+    would be left out.  Keys are the module path plus the parameter name, the
+    form PEFT gives its own saved keys (adapter name removed); each module also
+    stores ``<path>.expert_lora_scaling`` (lora_alpha / r) as a 0-d fp32 tensor.
+    Merge the result into the adapter dict before writing it (safetensors /
+    ``torch.save``); ``load_expert_lora_state_dict`` restores it.  Under FSDP2
+    every rank must call this (``full_tensor`` is a collective)."""
+    out = {}
+    for name, mod in model.named_modules():
+        if isinstance(mod, Mxfp4Bf16DequantGptOssExperts) and getattr(mod, "expert_lora_r", 0):
+            for p in EXPERT_LORA_PARAMS:
+                t = _full(getattr(mod, p)).detach()
+                out[f"{name}.{p}"] = t.cpu().contiguous() if to_cpu else t
+            out[f"{name}.expert_lora_scaling"] = torch.tensor(float(mod.expert_lora_scaling), dtype=torch.float32)
+    return out
+
+
+def load_expert_lora_state_dict(model, state_dict: dict, strict: bool = True) -> list:
+    """Restore expert-LoRA adapters saved by ``expert_lora_state_dict``: each
+    experts module whose path has adapters in ``state_dict`` gets expert LoRA
+    at the saved rank and scaling (``enable_expert_lora`` if it has none yet)
+    and the saved tensors copied in.  Keys may carry PEFT's
+    ``base_model.model.`` prefix.  Returns the paths restored; with ``strict``
+    a module path in the dict that the model does not have raises."""
+    def strip(k):
+        return k[len("base_model.model."):] if k.startswith("base_model.model.") else k
+    sd = {strip(k): v for k, v in state_dict.items()}
+    paths = sorted({k.rsplit(".", 1)[0] for k in sd if k.rsplit(".", 1)[-1] in EXPERT_LORA_PARAMS})
+    modules = dict(model.named_modules())
+    done = []
+    for path in paths:
+        mod = modules.get(path)
+        if not isinstance(mod, Mxfp4Bf16DequantGptOssExperts):
+            if strict:
+                raise KeyError(f"{path}: no experts module at this path to load expert LoRA into")
+            continue
+        A = sd[f"{path}.gate_up_proj_lora_A"]
+        r = A.shape[1]
+        scaling = float(sd[f"{path}.expert_lora_scaling"]) if f"{path}.expert_lora_scaling" in sd else None
+        if getattr(mod, "expert_lora_r", 0) != r:
+            enable_expert_lora(mod, r=r, lora_alpha=(scaling if scaling is not None else 1.0) * r)
+        elif scaling is not None:
+            mod.expert_lora_scaling = scaling
+        with torch.no_grad():
+            for p in EXPERT_LORA_PARAMS:
+                dst = getattr(mod, p)
+                src = sd[f"{path}.{p}"]
+                if tuple(src.shape) != tuple(dst.shape):
+                    raise ValueError(f"{path}.{p}: saved shape {tuple(src.shape)}, module {tuple(dst.shape)}")
+                dst.copy_(src.to(device=dst.device, dtype=dst.dtype))
+        done.append(path)
+    return done
 
 
 def merge_expert_lora(experts: Mxfp4Bf16DequantGptOssExperts, proj: str, layout: str = "hf") -> torch.Tensor:
