@@ -218,3 +218,34 @@ def test_saved_activations(dev, lora):
                                  (Rr, 192), (Rr, 96), (6, 16, 96), (6, 128, 16), (Rr, 16)])  # down: GU, act, A, B, L
     y.backward(inp.dy.to(dev))
     assert torch.isfinite(x.grad.float()).all()
+
+
+@pytest.mark.parametrize("T", [0, 1, 3])
+def test_empty_and_tiny_batches(dev, T):
+    """A micro-batch of 0, 1 or 3 tokens, E = 32, top-4, LoRA r = 16: nearly
+    every expert idle, padding-only tile maps.  Empty (at the gpt-oss-20b
+    width, H = I = 2880): outputs and gradients are empty, the LoRA gradients
+    exactly zero.  1 and 3 tokens (H = 256, I = 192, so the float64 oracle
+    stays quick): Y, dX and the LoRA gradients against the float64 layer as in
+    the end-to-end test."""
+    inp = workloads.layer(3, T=T, E=32) if T == 0 else workloads.layer(3, T=T, E=32, H=256, I=192)
+    print(f"tiny batch T={T}", flush=True)
+    m, x, y = _run_module(inp, dev)
+    torch.cuda.synchronize()
+    assert y.shape == (T, inp.x.shape[1]) and x.grad.shape == inp.x.shape
+    names = ("gate_up_proj_lora_A", "gate_up_proj_lora_B", "down_proj_lora_A", "down_proj_lora_B")
+    if T == 0:
+        for pn in names:
+            g = getattr(m, pn).grad
+            assert g is None or not bool(g.any()), pn
+        return
+    rt = O.routing_replay(inp.logits, inp.expt_indx, inp.k)
+    p, lo = _params(inp), _lora_of(inp)
+    st = moe.layer_forward(inp.x, p, rt, inp.k, lora=lo)
+    gr = moe.layer_backward(inp.x, p, rt, inp.k, st, inp.dy, lora=lo)
+    st64 = moe.layer_forward(inp.x, p, rt, inp.k, lora=lo, rd=torch.float64)
+    gr64 = moe.layer_backward(inp.x, p, rt, inp.k, st64, inp.dy, lora=lo, rd=torch.float64)
+    _e2e_check(y, st["Y"], st64["Y"], "Y")
+    _e2e_check(x.grad, gr["dX"], gr64["dX"], "dX")
+    for pn, key in zip(names, ("dAgu", "dBgu", "dAdn", "dBdn")):
+        _e2e_check(getattr(m, pn).grad, gr[key], gr64[key], pn)
