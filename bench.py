@@ -208,6 +208,25 @@ def bandwidth_extras(torch, dev, kernels, workloads, reps=50):
     return res
 
 
+def hbm_probe(torch, dev, kernels, workloads, inp_cpu):
+    """One call of each standalone HBM-bound kernel, each on buffers no earlier
+    call touched (the 256 MB MALL holds nothing of them), for the counter runs."""
+    blocks, scales = workloads.cfg0()
+    big = torch.empty(512 << 20, dtype=torch.uint8, device=dev)  # evicts the calibration copy's lines
+    big.fill_(1)
+    del big
+    b, s_ = blocks.to(dev), scales.to(dev)
+    kernels.mxfp4_to_bf16_hip(b, s_)
+    b, s_ = blocks.to(dev), scales.to(dev)
+    kernels.mxfp4_to_fp8_e5m2(b, s_)
+    gu, dout = workloads.cfg1()
+    gu, dout = gu.to(dev), dout.to(dev)
+    kernels.swiglu_forward(gu, 1.702, 7.0)
+    gu2, dout2 = gu.clone(), dout.clone()
+    kernels.swiglu_backward_raw(dout2, gu2, 1.702, 7.0)
+    kernels.quantize_per_token_e4m3(inp_cpu.x.to(dev))
+
+
 def _kern_bw(kern, byts):
     if not kern:
         return None
@@ -375,9 +394,11 @@ def main():
     ap.add_argument("--cpu-sample", action="store_true",
                     help="CPU baseline on a 4-expert sample scaled to the layer (default: the whole layer)")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--probe", choices=("traffic",),
-                    help="traffic: one plain 512 MiB device copy (counter calibration) then one layer step, for "
-                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs; prints no JSON line")
+    ap.add_argument("--probe", choices=("traffic", "hbm"),
+                    help="traffic: one plain 512 MiB device copy (counter calibration) then one layer step; hbm: the "
+                         "same copy, then one call of each standalone HBM-bound kernel on cold buffers (cfg0 "
+                         "dequant and E5M2, cfg1 SwiGLU fwd / bwd, per-token E4M3 of x); for rocprofv3 --pmc "
+                         "FETCH_SIZE / WRITE_SIZE runs; prints no JSON line")
     ap.add_argument("--traffic-profile", default=str(ROOT / "profiles" / "traffic_cfg4.md"),
                     help="rocprofv3 traffic summary (agent_factory_3_amd.profiling traffic) read for roofline.traffic")
     args = ap.parse_args()
@@ -416,15 +437,19 @@ def main():
             with torch.no_grad():
                 m(x0, rd, gi, si)
 
-    if args.probe == "traffic":
+    if args.probe in ("traffic", "hbm"):
         from agent_factory_3_amd.profiling import COPY_BYTES
         src = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
         torch.mul(src, 1.0, out=dst)  # an elementwise kernel (a plain dst.copy_ may run on a copy engine)
         torch.cuda.synchronize()
-        step()
+        del src, dst
+        if args.probe == "traffic":
+            step()
+        else:
+            hbm_probe(torch, dev, kernels, workloads, inp_cpu)
         torch.cuda.synchronize()
-        log("traffic probe done")
+        log(f"{args.probe} probe done")
         return
 
     log(f"warmup {args.warmup}")
