@@ -63,6 +63,9 @@ _SIGNATURES = {
     "af3_lora_wgrad_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "af3_lora_wgrad": (_i32, [_p, _i64, _p, _i32, _p, _p, _i64, _p, _i32, _f32, _p, _i32, _i32,
                               _i32, _p, _p, _i32, _i32, _p, _sz, _p, _p]),
+    "af3_lora_u_wgrad_workspace_bytes": (_sz, [_i32, _i64, _i32, _i32]),
+    "af3_lora_u_wgrad": (_i32, [_p, _i64, _p, _i32, _p, _p, _p, _f32, _p, _i32, _i64, _i32, _i32,
+                                _p, _p, _i32, _i32, _p, _sz, _p, _p, _p]),
 }
 
 _lib = None

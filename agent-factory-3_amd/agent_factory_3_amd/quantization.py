@@ -516,6 +516,32 @@ def _lora_wgrad(a, a_gather, a_div, a_rowscale, b, b_gather, b_div, ed, E, M, N)
     return g
 
 
+def _lora_u_and_dB(big, gather, gdiv, rowscale, L, Bw, scale, ed, E, W):
+    """The two LoRA backward products that read the wide gradient ``big``:
+    u[i] = scale * big[b(i)] @ Bw[e]  and  dB[e] = sum_i bf16(rs(i) big[b(i)])^T L[i],
+    in one pass over ``big`` (af3_lora_u_wgrad); shapes it declines go through
+    _lora_rows and _lora_wgrad."""
+    dev = big.device
+    R, r = L.shape
+    u = torch.empty(R, r, dtype=torch.bfloat16, device=dev)
+    g = torch.empty(E, W, r, dtype=torch.bfloat16, device=dev)
+    cmap = ed.block_pid_map[WGRAD_CHUNK]
+    coffs = ed.token_offs_pad[WGRAD_CHUNK]
+    nch = cmap.numel()
+    ws_n = int(_capi.load().af3_lora_u_wgrad_workspace_bytes(nch, R, W, r))
+    ws = torch.empty(max(ws_n, 1), dtype=torch.uint8, device=dev)
+    L = L.contiguous()
+    Bw = Bw.contiguous()
+    if _capi.try_call("af3_lora_u_wgrad", big.data_ptr(), big.stride(0) if big.shape[0] > 1 else W,
+                      _capi.ptr(gather), gdiv, _capi.ptr(rowscale), L.data_ptr(), Bw.data_ptr(), float(scale),
+                      ed.token_offs_raw.data_ptr(), E, R, W, r, cmap.data_ptr(), coffs.data_ptr(), nch,
+                      WGRAD_CHUNK, ws.data_ptr(), ws_n, u.data_ptr(), g.data_ptr(), _capi.stream_of(dev)):
+        return u, g
+    del ws
+    u = _lora_rows(big, gather, gdiv, Bw, 1, scale, ed, r, W)
+    return u, _lora_wgrad(big, gather, gdiv, rowscale, L, None, 1, ed, E, W, r)
+
+
 class LoraDequantMoEMatmul(torch.autograd.Function):
     """Frozen-MXFP4 grouped GEMM plus a trainable per-expert LoRA term.
 
@@ -585,13 +611,12 @@ class LoraDequantMoEMatmul(torch.autograd.Function):
         if gam is not None:
             gam = gam.to(torch.bfloat16).contiguous()
         with on_device(dY.device):
-            u = _lora_rows(dY, bg, k_act, B, 1, ctx.scaling, ed, r, N)
+            u, dB = _lora_u_and_dB(dY, bg, k_act if bg is not None else 1, gam, L, B, ctx.scaling, ed, E, N)
             dx = moe_rows(dY, blocks, scales, None, ctx.routing_data, ctx.bwd_gather_indx, gam, True, u, A)
             if ctx.bwd_scatter_indx is not None:
                 dx = moe_combine(dx, ctx.bwd_scatter_indx, k_act)
             dA = _lora_wgrad(u, None, 1, gam, xg, ctx.fwd_gather, k_act if ctx.fwd_gather is not None else 1,
                              ed, E, r, K)
-            dB = _lora_wgrad(dY, bg, k_act if bg is not None else 1, gam, L, None, 1, ed, E, N, r)
         dA = dA.to(ctx.lora_dtypes[0])
         dB = dB.to(ctx.lora_dtypes[1])
         return (dx, dA, dB) + (None,) * 13
@@ -681,7 +706,8 @@ class _GateUpSwiGLU(torch.autograd.Function):
         dA = dB = u = None
         with on_device(dGU.device):
             if A is not None:
-                u = _lora_rows(dGU, None, k_act, B, 1, ctx.scaling, ed, A.shape[1], N)
+                u, dB = _lora_u_and_dB(dGU, None, 1, None, L, B, ctx.scaling, ed, E, N)
+                dB = dB.to(ctx.lora_dtypes[1])
             dx = moe_rows(dGU, blocks, scales, None, ctx.routing_data, None, None, True, u, A)
             if ctx.scatter_indx is not None:
                 dx = moe_combine(dx, ctx.scatter_indx, k_act)
@@ -689,7 +715,6 @@ class _GateUpSwiGLU(torch.autograd.Function):
                 r = A.shape[1]
                 dA = _lora_wgrad(u, None, 1, None, xg, ctx.fwd_gather,
                                  k_act if ctx.fwd_gather is not None else 1, ed, E, r, K).to(ctx.lora_dtypes[0])
-                dB = _lora_wgrad(dGU, None, 1, None, L, None, 1, ed, E, N, r).to(ctx.lora_dtypes[1])
         return (dx, dA, dB) + (None,) * 11
 
 
@@ -747,7 +772,8 @@ class _SwiGLUDown(torch.autograd.Function):
         dA = dB = u = None
         with on_device(dY.device):
             if A is not None:
-                u = _lora_rows(dY, bg, k_act, B, 1, ctx.scaling, ed, A.shape[1], N)
+                u, dB = _lora_u_and_dB(dY, bg, k_act if bg is not None else 1, gam, L, B, ctx.scaling, ed, E, N)
+                dB = dB.to(ctx.lora_dtypes[1])
             dgu = d_gam = None
             want_gam = ctx.needs_input_grad[10]  # routing-weight gradient (routing.GAMMA_GRAD)
             if FUSED_SWIGLU_BWD and not want_gam:
@@ -762,8 +788,6 @@ class _SwiGLUDown(torch.autograd.Function):
             if A is not None:
                 r = A.shape[1]
                 dA = _lora_wgrad(u, None, 1, gam, act, None, 1, ed, E, r, K).to(ctx.lora_dtypes[0])
-                dB = _lora_wgrad(dY, bg, k_act if bg is not None else 1, gam, L, None, 1, ed, E, N,
-                                 r).to(ctx.lora_dtypes[1])
         return (dgu, None, dA, dB) + (None,) * 6 + (d_gam,) + (None,) * 5
 
 

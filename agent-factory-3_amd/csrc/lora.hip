@@ -168,8 +168,8 @@ __global__ __launch_bounds__(256) void lrows_kernel(LrParams p) {
 // point (the Small side in MODE 1, the Big side in MODE 0) as bf16(rs(r) * A).
 // Block = (chunk of chunk_rows expert-sorted rows, 256 Big columns); 4 waves of
 // 64 columns x 32.  Per 32-row step: Big rows [32][256] (512 B rows, 16-byte
-// chunks XOR-swizzled by 2 (row & 3) so the transposing reads of 4 rows hit
-// distinct banks) and Small rows [32][SR bytes] go global->LDS through a
+// chunks XOR-swizzled by lw_swz(row) so the transposing reads hit distinct
+// banks) and Small rows [32][SR bytes] go global->LDS through a
 // 4-stage ring, three steps ahead.  The gather indices and the per-row scales
 // of the chunk are staged in LDS once, so no copy waits on an index load.
 // The row scales are applied in registers to the MFMA operands (each lane
@@ -199,8 +199,14 @@ constexpr int kLwStage = kLwBig + kLwSmall;
 constexpr int kLwMaxChunk = 512;          // rows per chunk (gather indices and scales staged in LDS)
 constexpr int kLwTPad = 260;              // floats per row of the MODE 1 output transpose
 
+// XOR applied to the 16-byte chunk index of a 512-byte Big row: bits 2-3 are
+// row & 3 and bits 0-1 are (row >> 2) & 3, so the transposing reads (4 rows x
+// 4 consecutive chunks per half wave) and row reads (16 rows x 1 chunk per
+// quarter wave) both touch 16 distinct 16-byte bank groups
+__device__ __forceinline__ int lw_swz(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
+
 __device__ __forceinline__ int lw_big_off(int row, int col) {  // byte offset of Big[row][col] (col % 4 == 0)
-  return row * 512 + ((((col >> 3) ^ ((row & 3) << 1))) << 4) + ((col & 7) << 1);
+  return row * 512 + (((col >> 3) ^ lw_swz(row)) << 4) + ((col & 7) << 1);
 }
 
 // bf16(rs[i] * v[i]) for the 8 values of an MFMA operand
@@ -251,7 +257,7 @@ __global__ __launch_bounds__(256, 2) void lwg_kernel(LwParams p) {
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
     const int rr = (wave * NB + i) * 2 + (lane >> 5);
-    const int lc = (lane & 31) ^ ((rr & 3) << 1);
+    const int lc = (lane & 31) ^ lw_swz(rr);
     bcol[i] = p.big + (lc * 8 < ncols ? c0 + lc * 8 : c0);  // row part added per step (rows are gathered)
   }
   const uint8_t* ssrc = (const uint8_t*)p.small;
@@ -381,6 +387,265 @@ __global__ __launch_bounds__(256) void lwg_reduce_kernel(const float* __restrict
   *(uint2*)(g + (int64_t)e * MN + i) = o;
 }
 
+// ---------------------------------------------------------------------------
+// One pass over the wide gradient Big for both LoRA backward products that
+// read it (the two products otherwise stream Big separately):
+//   u[i][n]  = scale_u * sum_k Big[b(i)][k] Bl[e][k][n]            (rows, Bl = B [E][W][r])
+//   P[chunk] = sum_{i in chunk} bf16(rs(i) Big[b(i)][k]) (x) Small[i][n]   (dB partials, [W][r])
+// Block = (chunk of <= 512 expert-sorted rows, group of kLuG 256-column
+// slices).  Row steps of 32 rows outer, slices inner: ring step g = s kLuG + j
+// copies Big[32 rows of step s][256 columns of slice j] and the step's Small
+// rows global->LDS through a kLuStages-stage ring (the stage layout of
+// lwg_kernel), kLuStages - 1 steps ahead: one block per CU, so the ring depth
+// is what keeps enough bytes in flight.
+// dB: the slice's 4 waves x 64 columns x r accumulate over all row steps in
+//   registers (one accumulator pair per slice), as in lwg_kernel MODE 0.
+// u:  wave w multiplies columns 64 w .. 64 w + 63 of each slice (a K split);
+//   its Bl operands for those columns are loaded once per block and stay in
+//   registers.  After the kLuG slices of a row step the four waves' partial
+//   sums meet in LDS, are added in wave order and stored as fp32 into
+//   u_part[group][row][n]; lu_sum_kernel adds the groups in order.
+// The Big tile has lwg_kernel's layout (lw_big_off), which keeps both the
+// transposing reads (dB) and the row reads (u) free of bank conflicts.
+// ---------------------------------------------------------------------------
+struct LuParams {
+  const uint16_t* big;
+  int64_t ld_big;
+  const int32_t* big_gather;
+  int big_div;
+  const uint16_t* small;     // [rows][r], compact
+  const uint16_t* rowscale;  // Big-side row scale of dB (u has none), optional
+  const uint16_t* bl;        // [E][W][r]
+  const int32_t* offs;
+  const int32_t* chunk_map;
+  int chunk_rows, W, r, ngrp;
+  int64_t n_rows;
+  float* partials;  // [chunk][W][r]
+  float* u_part;    // [ngrp][n_rows][r]
+};
+
+constexpr int kLuG = 2;          // 256-column slices per block
+constexpr int kLuStages = 3;     // ring stages (two steps in flight per block)
+constexpr int kLuMinBlocks = 2;  // resident blocks per CU (registers <= 256, LDS <= 80 KB per block)
+
+template <int SR>
+__global__ __launch_bounds__(256, kLuMinBlocks) void lug_kernel(LuParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kLuStages * kLwStage];
+  __shared__ __attribute__((aligned(16))) float red[4 * 32 * 32];  // [wave][qq / 4][lane][4]
+  __shared__ int32_t gsrc[kLwMaxChunk];
+  __shared__ __attribute__((aligned(16))) float rs_small[kLwMaxChunk];
+  __shared__ __attribute__((aligned(16))) float rs_big[kLwMaxChunk];
+  static_assert(256 * SR <= kLuStages * kLwStage && kLuG >= 2 && kLuStages >= 2 && kLuStages <= 7,
+                "slab slice must fit the ring; u's LDS buffer needs a barrier between rows steps' uses");
+  const int chunk = blockIdx.x / p.ngrp, cg = blockIdx.x % p.ngrp;
+  const int32_t ent = p.chunk_map[chunk];
+  if (ent < 0) return;
+  const int e = ent & 0xFFFF, cb = ent >> 16;
+  const int kb = p.offs[e] + cb * p.chunk_rows;
+  const int kend = min(p.chunk_rows, p.offs[e + 1] - kb);
+  if (kend <= 0) return;
+  const int nsteps = (kend + kLwRows - 1) / kLwRows;
+  const int NT = nsteps * kLuG;  // ring steps
+  const bool big_rs = p.rowscale != nullptr;
+  for (int i = threadIdx.x; i < nsteps * kLwRows; i += 256) {
+    const bool valid = i < kend;
+    const int64_t src = kb + (valid ? i : 0);  // rows past the chunk read its first row
+    gsrc[i] = p.big_gather ? p.big_gather[src] / p.big_div : (int32_t)src;
+    rs_small[i] = valid ? 1.f : 0.f;
+    rs_big[i] = big_rs ? af3_bf16_to_f32(p.rowscale[src]) : 1.f;
+  }
+  const int gc0 = cg * (kLuG * 256);  // first column of the group (< W)
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gi = lane >> 4, q = lane & 15, lr = lane & 31, lh = lane >> 5;
+
+  // Bl[e][gc0 + 256 j ..][0 .. r), one slice at a time -> LDS [256][SR] (rows past W zero) -> registers:
+  // bw[j][m] = Bl rows 256 j + 64 wave + 16 m + 8 lh + (0..7), column lr (the B operand)
+  af3_bf16x8 bw[kLuG][4];
+  {
+    const int col = (gi & 1) * 16 + 4 * (q & 3);
+#pragma unroll
+    for (int j = 0; j < kLuG; ++j) {
+      const int nbytes = min(256, p.W - gc0 - 256 * j) * SR;  // <= 0 for a slice past W
+      const uint8_t* src = (const uint8_t*)(p.bl + ((int64_t)e * p.W + gc0 + 256 * j) * p.r);
+      for (int o = threadIdx.x * 16; o < 256 * SR; o += 256 * 16) {
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (o < nbytes) v = *(const uint4*)(src + o);
+        *(uint4*)(lds + o) = v;
+      }
+      __syncthreads();  // (the first one also publishes gsrc / rs_*)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int kr = wave * 64 + m * 16 + (gi >> 1) * 8 + (q >> 2);
+        bw[j][m] = l_tr8(lds + kr * SR + col * 2, lds + (kr + 4) * SR + col * 2);
+      }
+      __syncthreads();  // the slab area is rewritten (next slice, then the ring)
+    }
+  }
+
+  constexpr int NS = (kLwRows * SR) / 1024;  // Small copies per step (block)
+  constexpr int NB = kLwBig / 1024 / 4;      // Big copies per step and wave
+  const bool has_s = wave < NS;
+  int lcs[NB];  // logical 16-byte chunk of each Big copy of this lane
+#pragma unroll
+  for (int i = 0; i < NB; ++i) lcs[i] = (lane & 31) ^ lw_swz((wave * NB + i) * 2 + lh);
+  const uint8_t* ssrc = (const uint8_t*)p.small;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(l_lds_addr(lds));
+  auto issue = [&](int g, int slot) {
+    const int s = g / kLuG, j = g % kLuG;
+    const uint32_t st = lds0 + (uint32_t)(slot * kLwStage);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int rr = (wave * NB + i) * 2 + lh;
+      const int64_t src = gsrc[s * kLwRows + rr];
+      int col = gc0 + j * 256 + lcs[i] * 8;
+      col = col < p.W ? col : 0;
+      l_dma16(p.big + src * p.ld_big + col, st + (uint32_t)((wave * NB + i) * 1024));
+    }
+    if (has_s) {
+      const int off = wave * 1024 + lane * 16;  // byte offset inside the step's Small rows
+      const int rl = s * kLwRows + off / SR;
+      const int64_t srow = kb + (rl < kend ? rl : 0);
+      l_dma16(ssrc + srow * SR + (off % SR), st + (uint32_t)(kLwBig + wave * 1024));
+    }
+  };
+  // u of row step sp: sum the four waves' K-partials, store the chunk's valid rows
+  auto u_store = [&](int sp) {
+    const int t = threadIdx.x, i = t >> 6, l = t & 63;
+    const float4* r4 = (const float4*)red;
+    const float4 v0 = r4[0 * 256 + i * 64 + l], v1 = r4[1 * 256 + i * 64 + l];
+    const float4 v2 = r4[2 * 256 + i * 64 + l], v3 = r4[3 * 256 + i * 64 + l];
+    const float s4[4] = {((v0.x + v1.x) + v2.x) + v3.x, ((v0.y + v1.y) + v2.y) + v3.y,
+                         ((v0.z + v1.z) + v2.z) + v3.z, ((v0.w + v1.w) + v2.w) + v3.w};
+    const int n = l & 31;
+    if (n < p.r) {
+      float* up = p.u_part + ((int64_t)cg * p.n_rows + kb) * p.r + n;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int row = sp * kLwRows + i * 8 + (l >> 5) * 4 + c;
+        if (row < kend) up[(int64_t)row * p.r] = s4[c];
+      }
+    }
+  };
+
+  af3_f32x16 accb[kLuG][2], accu;
+#pragma unroll
+  for (int q2 = 0; q2 < 16; ++q2) {
+    accu[q2] = 0.f;
+#pragma unroll
+    for (int j = 0; j < kLuG; ++j) accb[j][0][q2] = accb[j][1][q2] = 0.f;
+  }
+  constexpr int D = kLuStages - 1;  // steps in flight
+#pragma unroll
+  for (int g = 0; g < D; ++g)
+    if (g < NT) issue(g, g);
+  int slot = 0;                      // ring slot of step g
+  const int lrow = 8 * lh;  // first of the lane's 8 operand rows inside a 16-row slice
+  for (int s = 0; s < nsteps; ++s) {
+    const bool scale_s = (s + 1) * kLwRows > kend;
+#pragma unroll
+    for (int j = 0; j < kLuG; ++j) {
+      const int g = s * kLuG + j;
+      // this step's copies are in once at most those of the later issued steps are outstanding
+      // (NB + has_s copies per step and wave; stores issued since only make the wait stricter)
+      const int ahead = min(D - 1, NT - 1 - g);
+      if (has_s) {
+        switch (ahead) {
+          case 5: L_WAIT_VM(25); break;
+          case 4: L_WAIT_VM(20); break;
+          case 3: L_WAIT_VM(15); break;
+          case 2: L_WAIT_VM(10); break;
+          case 1: L_WAIT_VM(5); break;
+          default: L_WAIT_VM(0); break;
+        }
+      } else {
+        switch (ahead) {
+          case 5: L_WAIT_VM(20); break;
+          case 4: L_WAIT_VM(16); break;
+          case 3: L_WAIT_VM(12); break;
+          case 2: L_WAIT_VM(8); break;
+          case 1: L_WAIT_VM(4); break;
+          default: L_WAIT_VM(0); break;
+        }
+      }
+      L_BARRIER();
+      // the slot of step g + D is the one step g - 1 read (all waves are past it)
+      const int prev = slot == 0 ? D : slot - 1;
+      if (g + D < NT) issue(g + D, prev);
+      if (j == 0 && s > 0) u_store(s - 1);
+      const uint8_t* bs = lds + slot * kLwStage;
+      slot = slot == D ? 0 : slot + 1;
+      const uint8_t* ss = bs + kLwBig;
+#pragma unroll
+      for (int h = 0; h < kLwRows / 16; ++h) {
+        const int kr = h * 16 + (gi >> 1) * 8 + (q >> 2);
+        const int scol = (gi & 1) * 16 + 4 * (q & 3);
+        const int r0 = s * kLwRows + h * 16 + lrow;
+        af3_bf16x8 b = l_tr8(ss + kr * SR + scol * 2, ss + (kr + 4) * SR + scol * 2);
+        if (scale_s) b = lw_scale8(b, *(const float4*)&rs_small[r0], *(const float4*)&rs_small[r0 + 4]);
+        float4 g0, g1;
+        if (big_rs) {
+          g0 = *(const float4*)&rs_big[r0];
+          g1 = *(const float4*)&rs_big[r0 + 4];
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int bc = wave * 64 + t * 32 + (gi & 1) * 16 + 4 * (q & 3);
+          af3_bf16x8 a = l_tr8(bs + lw_big_off(kr, bc), bs + lw_big_off(kr + 4, bc));
+          if (big_rs) a = lw_scale8(a, g0, g1);
+          accb[j][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, accb[j][t], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int c = wave * 8 + m * 2 + lh;  // 16-byte chunk of columns 64 wave + 16 m + 8 lh ..
+        const af3_bf16x8 a = *(const af3_bf16x8*)(bs + lr * 512 + ((c ^ lw_swz(lr)) << 4));
+        accu = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bw[j][m], accu, 0, 0, 0);
+      }
+    }
+    // K-partial of row step s -> red (the last readers of red were in step (s, 0))
+    float4* rw = (float4*)red + wave * 256;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      rw[i * 64 + lane] = make_float4(accu[4 * i], accu[4 * i + 1], accu[4 * i + 2], accu[4 * i + 3]);
+      accu[4 * i] = accu[4 * i + 1] = accu[4 * i + 2] = accu[4 * i + 3] = 0.f;
+    }
+  }
+  L_BARRIER();
+  u_store(nsteps - 1);
+  // accb[j][t][qq]: Big column gc0 + 256 j + 64 wave + 32 t + 8 (qq / 4) + 4 lh + qq % 4, Small column lr
+  if (lr >= p.r) return;
+  float* P = p.partials + (int64_t)chunk * p.W * p.r;
+#pragma unroll
+  for (int j = 0; j < kLuG; ++j)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int qq = 0; qq < 16; ++qq) {
+        const int col = gc0 + j * 256 + wave * 64 + t * 32 + (qq >> 2) * 8 + lh * 4 + (qq & 3);
+        if (col < p.W) P[(int64_t)col * p.r + lr] = accb[j][t][qq];
+      }
+}
+
+// u[i][n] = bf16(scale * sum_g u_part[g][i][n]), groups in order
+__global__ __launch_bounds__(256) void lu_sum_kernel(const float* __restrict__ u_part, int64_t n_elems, int ngrp,
+                                                     float scale, uint16_t* __restrict__ u) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= n_elems) return;
+  float4 a = *(const float4*)(u_part + i);
+  for (int g = 1; g < ngrp; ++g) {
+    const float4 v = *(const float4*)(u_part + (int64_t)g * n_elems + i);
+    a.x += v.x;
+    a.y += v.y;
+    a.z += v.z;
+    a.w += v.w;
+  }
+  uint2 o;
+  o.x = af3_pack_bf16x2(a.x * scale, a.y * scale);
+  o.y = af3_pack_bf16x2(a.z * scale, a.w * scale);
+  *(uint2*)(u + i) = o;
+}
+
 inline bool l_al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
@@ -460,3 +725,67 @@ int lora_wgrad_fast(const uint16_t* big, int64_t ld_big, const int32_t* big_gath
 }
 
 }  // namespace af3
+
+namespace {
+constexpr int kLuGroupCols = kLuG * 256;
+int64_t lu_ngrp(int W) { return (W + kLuGroupCols - 1) / kLuGroupCols; }
+size_t lu_align(size_t n) { return (n + 255) & ~(size_t)255; }
+}  // namespace
+
+extern "C" size_t af3_lora_u_wgrad_workspace_bytes(int max_chunks, int64_t n_rows, int W, int r) {
+  if (W <= 0 || r <= 0 || n_rows < 0) return 0;
+  const size_t part = (size_t)(max_chunks > 0 ? max_chunks : 1) * (size_t)W * (size_t)r * sizeof(float);
+  return lu_align(part) + (size_t)lu_ngrp(W) * (size_t)n_rows * (size_t)r * sizeof(float);
+}
+
+extern "C" int af3_lora_u_wgrad(const uint16_t* big, int64_t ld_big, const int32_t* big_gather, int big_div,
+                                const uint16_t* big_rowscale, const uint16_t* small, const uint16_t* bl,
+                                float scale_u, const int32_t* token_offs, int n_expts, int64_t n_rows, int W, int r,
+                                const int32_t* chunk_map, const int32_t* chunk_offs, int max_chunks, int chunk_rows,
+                                void* workspace, size_t ws_bytes, uint16_t* u, uint16_t* g, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  AF3_REQUIRE(W > 0 && r > 0 && n_expts > 0 && n_rows >= 0 && max_chunks >= 0 && chunk_rows > 0,
+              "lora_u_wgrad: bad sizes");
+  if (!(r == 16 || r == 32) || W % 8 != 0 || ld_big % 8 != 0 || chunk_rows > kLwMaxChunk ||
+      chunk_rows % kLwRows != 0 || !l_al16(big) || !l_al16(small) || !l_al16(bl) || !l_al16(u) || !l_al16(g) ||
+      !l_al16(workspace))
+    return AF3_EUNSUPPORTED;
+  AF3_REQUIRE(workspace && ws_bytes >= af3_lora_u_wgrad_workspace_bytes(max_chunks, n_rows, W, r),
+              "lora_u_wgrad: workspace too small");
+  LuParams p{};
+  p.big = big;
+  p.ld_big = ld_big;
+  p.big_gather = big_gather;
+  p.big_div = big_div > 0 ? big_div : 1;
+  p.small = small;
+  p.rowscale = big_rowscale;
+  p.bl = bl;
+  p.offs = token_offs;
+  p.chunk_map = chunk_map;
+  p.chunk_rows = chunk_rows;
+  p.W = W;
+  p.r = r;
+  p.ngrp = (int)lu_ngrp(W);
+  p.n_rows = n_rows;
+  p.partials = (float*)workspace;
+  p.u_part = (float*)((uint8_t*)workspace +
+                      lu_align((size_t)(max_chunks > 0 ? max_chunks : 1) * (size_t)W * (size_t)r * sizeof(float)));
+  if (max_chunks > 0 && n_rows > 0) {
+    const dim3 grid((unsigned)max_chunks * (unsigned)p.ngrp), block(256);
+    if (r == 32)
+      hipLaunchKernelGGL((lug_kernel<64>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((lug_kernel<32>), grid, block, 0, stream, p);
+    int rc = af3::check_launch("lora_u_wgrad/partial");
+    if (rc) return rc;
+    const int64_t nu = n_rows * r;  // multiple of 16
+    hipLaunchKernelGGL(lu_sum_kernel, dim3((unsigned)af3_cdiv(nu / 4, 256)), dim3(256), 0, stream, p.u_part, nu,
+                       p.ngrp, scale_u, u);
+    rc = af3::check_launch("lora_u_wgrad/u");
+    if (rc) return rc;
+  }
+  const int64_t MN = (int64_t)W * r;
+  hipLaunchKernelGGL(lwg_reduce_kernel, dim3((unsigned)af3_cdiv(MN / 4, 256), n_expts), dim3(256), 0, stream,
+                     p.partials, chunk_offs, MN, 1.f, g);
+  return af3::check_launch("lora_u_wgrad/reduce");
+}

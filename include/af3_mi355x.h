@@ -239,6 +239,23 @@ int af3_lora_wgrad(const uint16_t* a, int64_t lda, const int32_t* a_gather, int 
                    const int32_t* chunk_offs, int max_chunks, int chunk_rows, float* partials, size_t partial_bytes,
                    uint16_t* g, void* stream);
 
+/* Both expert-LoRA backward products that read the wide gradient, in one pass
+ * over it (no counterpart in the reference):
+ *   u[i][n]    = bf16(scale_u * sum_k Big[b(i)][k] Bl[e(i)][k][n])        = af3_lora_rows, trans_b 1
+ *   G[e][k][n] = bf16(sum_{i in rows(e)} bf16(rs(i) Big[b(i)][k]) Small[i][n]) = af3_lora_wgrad
+ * Big [.][ld_big] bf16 (W columns) with rows b(i) = big_gather[i] / big_div
+ * (identity when big_gather is NULL), rs = optional bf16 big_rowscale [n_rows],
+ * Small [n_rows][r] bf16 compact, Bl [E][W][r], u [n_rows][r], G [E][W][r];
+ * r = 16 or 32, W % 8 == 0.  Chunking and the fp32 partial sums follow
+ * af3_lora_wgrad; the workspace also holds u's per-column-group partial sums.
+ * Returns AF3_EUNSUPPORTED (nothing launched) for shapes it does not cover. */
+size_t af3_lora_u_wgrad_workspace_bytes(int max_chunks, int64_t n_rows, int W, int r);
+int af3_lora_u_wgrad(const uint16_t* big, int64_t ld_big, const int32_t* big_gather, int big_div,
+                     const uint16_t* big_rowscale, const uint16_t* small, const uint16_t* bl, float scale_u,
+                     const int32_t* token_offs, int n_expts, int64_t n_rows, int W, int r, const int32_t* chunk_map,
+                     const int32_t* chunk_offs, int max_chunks, int chunk_rows, void* workspace, size_t ws_bytes,
+                     uint16_t* u, uint16_t* g, void* stream);
+
 /* Expert-LoRA merge for weight sync.  The reference merges attention LoRA
  * into bf16 weights for sglang (model_trainer.py:653-719: fp32 base + fp32
  * (B @ A) * scaling, one cast to bf16); this is the same merge for the expert

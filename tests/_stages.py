@@ -22,7 +22,8 @@ from agent_factory_3_amd import workloads
 from oracle import moe, mxfp4, swiglu
 from tests._tol import check_close, check_equal
 
-_RECORDED = ("moe_rows", "moe_combine", "_lora_rows", "_lora_wgrad", "swiglu_backward_raw", "swiglu_forward")
+_RECORDED = ("moe_rows", "moe_combine", "_lora_rows", "_lora_wgrad", "_lora_u_and_dB", "swiglu_backward_raw",
+             "swiglu_forward")
 
 
 @contextmanager
@@ -144,8 +145,10 @@ def check_call_structure(run):
     lora = bool(run.lora_grads)
     assert names.count("moe_rows") == (4 if run.backward else 2)
     assert names.count("moe_combine") == (2 if run.backward else 1)
-    assert names.count("_lora_rows") == ((4 if run.backward else 2) if lora else 0)
-    assert names.count("_lora_wgrad") == (4 if lora and run.backward else 0)
+    # forward: L of both projections; backward: one pass (u, dB) and dA per projection
+    assert names.count("_lora_rows") == (2 if lora else 0)
+    assert names.count("_lora_u_and_dB") == (2 if lora and run.backward else 0)
+    assert names.count("_lora_wgrad") == (2 if lora and run.backward else 0)
     combines = run.of("moe_combine")
     check_equal(run.y, combines[0][1], "Y is the forward combine")
     if run.backward:
@@ -208,12 +211,29 @@ def check_lora_rows(run, experts, tag=""):
             idx = _src_rows(a["gather"], a["k_act"], lo, hi)
             ref, mag = moe.expert_lora_rows(a["x"], a["wl"][e], idx, a["scale"], trans=trans)
             check_close(out[lo:hi], ref, mag=mag, n=a["K"], what=f"{tag} LoRA rows trans={trans} e{e}")
+    for a, (u, _) in run.of("_lora_u_and_dB"):
+        for e in experts:
+            lo, hi = run.rows(e)
+            idx = _src_rows(a["gather"], a["gdiv"], lo, hi)
+            ref, mag = moe.expert_lora_rows(a["big"], a["Bw"][e], idx, a["scale"], trans=True)
+            check_close(u[lo:hi], ref, mag=mag, n=a["W"], what=f"{tag} LoRA u (one pass) e{e}")
 
 
 def check_lora_wgrads(run, experts, tag=""):
     """dA / dB of both projections: the experts' gradients vs the oracle, idle experts exactly zero,
     and the module's parameter gradients are the recorded ones."""
     w = run.of("_lora_wgrad")
+    ub = run.of("_lora_u_and_dB")
+    for a, (_, G) in ub:
+        assert torch.isfinite(G.float()).all()
+        for e in run.idle:
+            assert not bool(G[e].any()), f"{tag} idle expert {e} has a nonzero LoRA gradient"
+        for e in experts:
+            lo, hi = run.rows(e)
+            ib = _src_rows(a["gather"], a["gdiv"], lo, hi)
+            rs = None if a["rowscale"] is None else a["rowscale"][lo:hi]
+            ref, mag = moe.expert_wgrad(a["big"][ib], a["L"][lo:hi], rs)
+            check_close(G[e], ref, mag=mag, n=hi - lo, what=f"{tag} LoRA dB (one pass) [{a['W']}x{a['L'].shape[1]}] e{e}")
     for a, G in w:
         assert torch.isfinite(G.float()).all()
         for e in run.idle:
@@ -227,6 +247,6 @@ def check_lora_wgrads(run, experts, tag=""):
             check_close(G[e], ref, mag=mag, n=hi - lo, what=f"{tag} LoRA wgrad [{a['M']}x{a['N']}] e{e}")
     g = run.lora_grads
     check_equal(g["down_proj_lora_A"], w[0][1], "dA down")
-    check_equal(g["down_proj_lora_B"], w[1][1], "dB down")
-    check_equal(g["gate_up_proj_lora_A"], w[2][1], "dA gate_up")
-    check_equal(g["gate_up_proj_lora_B"], w[3][1], "dB gate_up")
+    check_equal(g["down_proj_lora_B"], ub[0][1][1], "dB down")
+    check_equal(g["gate_up_proj_lora_A"], w[1][1], "dA gate_up")
+    check_equal(g["gate_up_proj_lora_B"], ub[1][1][1], "dB gate_up")

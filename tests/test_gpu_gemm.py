@@ -151,6 +151,47 @@ def test_lora_wgrad(dev, M, N, gather_a, gather_b, rowscale):
         check_close(out[e], refo, mag=mag, n=hi - lo, what=f"wgrad expert {e}")
 
 
+@pytest.mark.parametrize("W,r,gather,rowscale", [
+    (2880, 32, True, True),     # the down projection's form: dY gathered, gammas on dB
+    (5760, 16, False, False),   # gate_up's form; the last column group has one empty slice
+    (264, 32, False, True),     # one group, a 8-column last slice
+    (1288, 16, True, False),    # two groups, the second with 264 columns
+])
+def test_lora_u_and_dB_one_pass(dev, W, r, gather, rowscale):
+    """u = s big[b] @ B[e] and dB[e] = sum bf16(rs big[b])^T L in one pass over big: u against the
+    oracle, dB against the oracle and bit for bit against the two-pass kernels (same sums in the
+    same order).  Expert 0 holds > 512 rows (several chunks), the last expert none."""
+    g, x, logits, blocks, scales, bias = _problem(T=700, seed=11)
+    K = 4
+    ref, (rd, gi, si) = _route(logits, K, dev)
+    E, R_ = blocks.shape[0], x.shape[0] * K
+    assert int(ref["hist"][0]) > 512 and int(ref["hist"][-1]) == 0
+    big = torch.randn(x.shape[0] if gather else R_, W, generator=g).to(torch.bfloat16)
+    L = torch.randn(R_, r, generator=g).to(torch.bfloat16)
+    Bw = (torch.randn(E, W, r, generator=g) * 0.1).to(torch.bfloat16)
+    rs = rd.gate_scal.to(torch.bfloat16) if rowscale else None
+    gx = gi.src_indx if gather else None
+    div = K if gather else 1
+    ed = rd.expt_data
+    u, dB = Q._lora_u_and_dB(big.to(dev), gx, div, rs, L.to(dev), Bw.to(dev), 0.5, ed, E, W)
+    u2 = Q._lora_rows(big.to(dev), gx, div, Bw.to(dev), 1, 0.5, ed, r, W)
+    dB2 = Q._lora_wgrad(big.to(dev), gx, div, rs, L.to(dev), None, 1, ed, E, W, r)
+    u, dB, u2, dB2 = u.cpu(), dB.cpu(), u2.cpu(), dB2.cpu()
+    assert torch.equal(dB.view(torch.int16), dB2.view(torch.int16))
+    assert dB[-1].abs().max() == 0
+    offs, ti = ref["offs"], ref["topk_indx"].long()
+    for e in range(E):
+        lo, hi = int(offs[e]), int(offs[e + 1])
+        if hi == lo:
+            continue
+        ib = ti[lo:hi] // K if gather else torch.arange(lo, hi)
+        uref, umag = moe.expert_lora_rows(big, Bw[e], ib, 0.5, trans=True)
+        check_close(u[lo:hi], uref, mag=umag, n=W, what=f"u expert {e}")
+        check_close(u2[lo:hi], uref, mag=umag, n=W, what=f"u (two-pass) expert {e}")
+        dref, dmag = moe.expert_wgrad(big[ib], L[lo:hi], rs.cpu()[lo:hi] if rowscale else None)
+        check_close(dB[e], dref, mag=dmag, n=hi - lo, what=f"dB expert {e}")
+
+
 def test_dense_routing_none(dev):
     """matmul_ogs with routing_data=None: one expert, plain GEMM."""
     g = torch.Generator().manual_seed(9)
