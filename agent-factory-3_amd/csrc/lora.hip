@@ -393,18 +393,19 @@ __global__ __launch_bounds__(256) void lwg_reduce_kernel(const float* __restrict
 //   u[i][n]  = scale_u * sum_k Big[b(i)][k] Bl[e][k][n]            (rows, Bl = B [E][W][r])
 //   P[chunk] = sum_{i in chunk} bf16(rs(i) Big[b(i)][k]) (x) Small[i][n]   (dB partials, [W][r])
 // Block = (chunk of <= 512 expert-sorted rows, group of kLuG 256-column
-// slices).  Row steps of 32 rows outer, slices inner: ring step g = s kLuG + j
-// copies Big[32 rows of step s][256 columns of slice j] and the step's Small
-// rows global->LDS through a kLuStages-stage ring (the stage layout of
-// lwg_kernel), kLuStages - 1 steps ahead: one block per CU, so the ring depth
-// is what keeps enough bytes in flight.
+// slices); two blocks per CU.  Row steps of 32 rows outer, slices inner: ring
+// step g = s kLuG + j copies Big[32 rows of step s][256 columns of slice j] and
+// the step's Small rows global->LDS through a kLuStages-stage ring (the stage
+// layout of lwg_kernel), kLuStages - 1 steps ahead.
 // dB: the slice's 4 waves x 64 columns x r accumulate over all row steps in
 //   registers (one accumulator pair per slice), as in lwg_kernel MODE 0.
-// u:  wave w multiplies columns 64 w .. 64 w + 63 of each slice (a K split);
-//   its Bl operands for those columns are loaded once per block and stay in
-//   registers.  After the kLuG slices of a row step the four waves' partial
-//   sums meet in LDS, are added in wave order and stored as fp32 into
-//   u_part[group][row][n]; lu_sum_kernel adds the groups in order.
+// u:  on v_mfma_f32_16x16x32_bf16, one 16-row x 16-column tile of a row step
+//   per wave over all the group's columns (r = 32: four tiles, every wave,
+//   every step; r = 16: two tiles, waves 0-1 on even steps and 2-3 on odd
+//   ones), so no partial sums cross waves.  A wave's Bl operands for its 16
+//   columns of u are loaded once per block and stay in registers; after the
+//   kLuG slices of a row step the tile goes to u_part[group][row][n] (fp32)
+//   and lu_sum_kernel adds the groups in order.
 // The Big tile has lwg_kernel's layout (lw_big_off), which keeps both the
 // transposing reads (dB) and the row reads (u) free of bank conflicts.
 // ---------------------------------------------------------------------------
@@ -424,19 +425,22 @@ struct LuParams {
   float* u_part;    // [ngrp][n_rows][r]
 };
 
+typedef __attribute__((ext_vector_type(4))) float lu_f32x4;
+
 constexpr int kLuG = 2;          // 256-column slices per block
-constexpr int kLuStages = 3;     // ring stages (two steps in flight per block)
+constexpr int kLuStages = 4;     // ring stages (three steps in flight per block)
 constexpr int kLuMinBlocks = 2;  // resident blocks per CU (registers <= 256, LDS <= 80 KB per block)
 
 template <int SR>
 __global__ __launch_bounds__(256, kLuMinBlocks) void lug_kernel(LuParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLuStages * kLwStage];
-  __shared__ __attribute__((aligned(16))) float red[4 * 32 * 32];  // [wave][qq / 4][lane][4]
   __shared__ int32_t gsrc[kLwMaxChunk];
   __shared__ __attribute__((aligned(16))) float rs_small[kLwMaxChunk];
   __shared__ __attribute__((aligned(16))) float rs_big[kLwMaxChunk];
-  static_assert(256 * SR <= kLuStages * kLwStage && kLuG >= 2 && kLuStages >= 2 && kLuStages <= 7,
-                "slab slice must fit the ring; u's LDS buffer needs a barrier between rows steps' uses");
+  static_assert(256 * SR <= kLwStage && kLuStages >= 2 && kLuStages <= 7,
+                "a Bl slice must fit a ring slot; the waits below cover up to 6 steps in flight");
+  static_assert(kLuStages * kLwStage + 3 * kLwMaxChunk * 4 <= 80 * 1024, "two blocks per CU");
+  constexpr bool R32 = SR == 64;  // r = 32 (else 16)
   const int chunk = blockIdx.x / p.ngrp, cg = blockIdx.x % p.ngrp;
   const int32_t ent = p.chunk_map[chunk];
   if (ent < 0) return;
@@ -454,34 +458,14 @@ __global__ __launch_bounds__(256, kLuMinBlocks) void lug_kernel(LuParams p) {
     rs_small[i] = valid ? 1.f : 0.f;
     rs_big[i] = big_rs ? af3_bf16_to_f32(p.rowscale[src]) : 1.f;
   }
+  __syncthreads();  // gsrc / rs_* published
   const int gc0 = cg * (kLuG * 256);  // first column of the group (< W)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int gi = lane >> 4, q = lane & 15, lr = lane & 31, lh = lane >> 5;
-
-  // Bl[e][gc0 + 256 j ..][0 .. r), one slice at a time -> LDS [256][SR] (rows past W zero) -> registers:
-  // bw[j][m] = Bl rows 256 j + 64 wave + 16 m + 8 lh + (0..7), column lr (the B operand)
-  af3_bf16x8 bw[kLuG][4];
-  {
-    const int col = (gi & 1) * 16 + 4 * (q & 3);
-#pragma unroll
-    for (int j = 0; j < kLuG; ++j) {
-      const int nbytes = min(256, p.W - gc0 - 256 * j) * SR;  // <= 0 for a slice past W
-      const uint8_t* src = (const uint8_t*)(p.bl + ((int64_t)e * p.W + gc0 + 256 * j) * p.r);
-      for (int o = threadIdx.x * 16; o < 256 * SR; o += 256 * 16) {
-        uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (o < nbytes) v = *(const uint4*)(src + o);
-        *(uint4*)(lds + o) = v;
-      }
-      __syncthreads();  // (the first one also publishes gsrc / rs_*)
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const int kr = wave * 64 + m * 16 + (gi >> 1) * 8 + (q >> 2);
-        bw[j][m] = l_tr8(lds + kr * SR + col * 2, lds + (kr + 4) * SR + col * 2);
-      }
-      __syncthreads();  // the slab area is rewritten (next slice, then the ring)
-    }
-  }
+  // the wave's u tile: rows 16 uh of a row step, columns 16 un
+  const int uh = R32 ? wave >> 1 : wave & 1;
+  const int un = R32 ? wave & 1 : 0;
 
   constexpr int NS = (kLwRows * SR) / 1024;  // Small copies per step (block)
   constexpr int NB = kLwBig / 1024 / 4;      // Big copies per step and wave
@@ -509,40 +493,49 @@ __global__ __launch_bounds__(256, kLuMinBlocks) void lug_kernel(LuParams p) {
       l_dma16(ssrc + srow * SR + (off % SR), st + (uint32_t)(kLwBig + wave * 1024));
     }
   };
-  // u of row step sp: sum the four waves' K-partials, store the chunk's valid rows
-  auto u_store = [&](int sp) {
-    const int t = threadIdx.x, i = t >> 6, l = t & 63;
-    const float4* r4 = (const float4*)red;
-    const float4 v0 = r4[0 * 256 + i * 64 + l], v1 = r4[1 * 256 + i * 64 + l];
-    const float4 v2 = r4[2 * 256 + i * 64 + l], v3 = r4[3 * 256 + i * 64 + l];
-    const float s4[4] = {((v0.x + v1.x) + v2.x) + v3.x, ((v0.y + v1.y) + v2.y) + v3.y,
-                         ((v0.z + v1.z) + v2.z) + v3.z, ((v0.w + v1.w) + v2.w) + v3.w};
-    const int n = l & 31;
-    if (n < p.r) {
-      float* up = p.u_part + ((int64_t)cg * p.n_rows + kb) * p.r + n;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int row = sp * kLwRows + i * 8 + (l >> 5) * 4 + c;
-        if (row < kend) up[(int64_t)row * p.r] = s4[c];
-      }
-    }
-  };
 
-  af3_f32x16 accb[kLuG][2], accu;
+  af3_f32x16 accb[kLuG][2];
+  lu_f32x4 accu = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int q2 = 0; q2 < 16; ++q2) {
-    accu[q2] = 0.f;
+  for (int q2 = 0; q2 < 16; ++q2)
 #pragma unroll
     for (int j = 0; j < kLuG; ++j) accb[j][0][q2] = accb[j][1][q2] = 0.f;
-  }
   constexpr int D = kLuStages - 1;  // steps in flight
 #pragma unroll
   for (int g = 0; g < D; ++g)
     if (g < NT) issue(g, g);
-  int slot = 0;                      // ring slot of step g
+  // Bl[e][gc0 + 256 j ..][0 .. r), one slice at a time -> the ring slot D, which the copies issued so far
+  // leave free (rows past W zero) -> registers:
+  // bw[j][kk] = Bl rows 256 j + 32 kk + 8 gi + (0..7), column 16 un + q (the 16x16x32 B operand)
+  af3_bf16x8 bw[kLuG][8];
+  {
+    uint8_t* slab = lds + D * kLwStage;
+    const int col = un * 16 + 4 * (q & 3);
+#pragma unroll
+    for (int j = 0; j < kLuG; ++j) {
+      const int nbytes = min(256, p.W - gc0 - 256 * j) * SR;  // <= 0 for a slice past W
+      const uint8_t* src = (const uint8_t*)(p.bl + ((int64_t)e * p.W + gc0 + 256 * j) * p.r);
+      for (int o = threadIdx.x * 16; o < 256 * SR; o += 256 * 16) {
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (o < nbytes) v = *(const uint4*)(src + o);
+        *(uint4*)(slab + o) = v;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const int kr = kk * 32 + gi * 8 + (q >> 2);
+        bw[j][kk] = l_tr8(slab + kr * SR + col * 2, slab + (kr + 4) * SR + col * 2);
+      }
+      __syncthreads();  // slot D is rewritten (next slice, then the ring's step D)
+    }
+  }
+
+  int slot = 0;             // ring slot of step g
   const int lrow = 8 * lh;  // first of the lane's 8 operand rows inside a 16-row slice
+  const int urow = uh * 16 + q;  // the lane's row of the u A operand
   for (int s = 0; s < nsteps; ++s) {
     const bool scale_s = (s + 1) * kLwRows > kend;
+    const bool u_here = R32 || (wave >> 1) == (s & 1);  // this wave owns a u tile of step s
 #pragma unroll
     for (int j = 0; j < kLuG; ++j) {
       const int g = s * kLuG + j;
@@ -572,7 +565,6 @@ __global__ __launch_bounds__(256, kLuMinBlocks) void lug_kernel(LuParams p) {
       // the slot of step g + D is the one step g - 1 read (all waves are past it)
       const int prev = slot == 0 ? D : slot - 1;
       if (g + D < NT) issue(g + D, prev);
-      if (j == 0 && s > 0) u_store(s - 1);
       const uint8_t* bs = lds + slot * kLwStage;
       slot = slot == D ? 0 : slot + 1;
       const uint8_t* ss = bs + kLwBig;
@@ -596,23 +588,26 @@ __global__ __launch_bounds__(256, kLuMinBlocks) void lug_kernel(LuParams p) {
           accb[j][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, accb[j][t], 0, 0, 0);
         }
       }
+      if (u_here) {
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const int c = wave * 8 + m * 2 + lh;  // 16-byte chunk of columns 64 wave + 16 m + 8 lh ..
-        const af3_bf16x8 a = *(const af3_bf16x8*)(bs + lr * 512 + ((c ^ lw_swz(lr)) << 4));
-        accu = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bw[j][m], accu, 0, 0, 0);
+        for (int kk = 0; kk < 8; ++kk) {  // columns 32 kk .. 32 kk + 31 of the slice; lane: 8 of them
+          const int c = kk * 4 + gi;
+          const af3_bf16x8 a = *(const af3_bf16x8*)(bs + urow * 512 + ((c ^ lw_swz(urow)) << 4));
+          accu = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bw[j][kk], accu, 0, 0, 0);
+        }
       }
     }
-    // K-partial of row step s -> red (the last readers of red were in step (s, 0))
-    float4* rw = (float4*)red + wave * 256;
+    // accu[i]: row 16 uh + 4 gi + i of row step s, column 16 un + q
+    if (u_here) {
+      float* up = p.u_part + ((int64_t)cg * p.n_rows + kb) * p.r + un * 16 + q;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      rw[i * 64 + lane] = make_float4(accu[4 * i], accu[4 * i + 1], accu[4 * i + 2], accu[4 * i + 3]);
-      accu[4 * i] = accu[4 * i + 1] = accu[4 * i + 2] = accu[4 * i + 3] = 0.f;
+      for (int i = 0; i < 4; ++i) {
+        const int row = s * kLwRows + uh * 16 + gi * 4 + i;
+        if (row < kend) up[(int64_t)row * p.r] = accu[i];
+      }
+      accu = lu_f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
-  L_BARRIER();
-  u_store(nsteps - 1);
   // accb[j][t][qq]: Big column gc0 + 256 j + 64 wave + 32 t + 8 (qq / 4) + 4 lh + qq % 4, Small column lr
   if (lr >= p.r) return;
   float* P = p.partials + (int64_t)chunk * p.W * p.r;
