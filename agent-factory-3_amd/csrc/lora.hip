@@ -176,6 +176,8 @@ __global__ __launch_bounds__(256) void lrows_kernel(LrParams p) {
 // holds 8 consecutive rows of one column of either operand); rows past the
 // chunk get scale 0 on the Small side.  MODE 0 writes P as [W][r] (dB),
 // MODE 1 as [r][W] (dA; transposed through LDS so the stores are row runs).
+// The chunk of an expert that has only one writes bf16(scale * P) into G
+// directly (what lwg_reduce_kernel would compute from it) and no partial.
 // ---------------------------------------------------------------------------
 struct LwParams {
   const uint16_t* big;
@@ -186,9 +188,12 @@ struct LwParams {
   const uint16_t* rowscale;
   const int32_t* offs;
   const int32_t* chunk_map;
+  const int32_t* chunk_offs;  // per-expert chunk ranges: an expert of one chunk skips the partials
   int chunk_rows;
   int W, r, nbb;
+  float scale;
   float* partials;
+  uint16_t* g;  // output, written here directly for one-chunk experts
 };
 
 constexpr int kLwRows = 32;               // rows per pipeline step
@@ -337,6 +342,8 @@ __global__ __launch_bounds__(256, 2) void lwg_kernel(LwParams p) {
   const int lr = lane & 31, lh = lane >> 5;
   const int j = lr;
   float* P = p.partials + (int64_t)chunk * p.W * p.r;
+  const bool direct = p.chunk_offs[e + 1] - p.chunk_offs[e] == 1;
+  uint16_t* G = p.g + (int64_t)e * p.W * p.r;
   if (MODE == 0) {
     if (j >= p.r) return;
 #pragma unroll
@@ -344,7 +351,13 @@ __global__ __launch_bounds__(256, 2) void lwg_kernel(LwParams p) {
 #pragma unroll
       for (int qq = 0; qq < 16; ++qq) {
         const int col = wave * 64 + t * 32 + (qq >> 2) * 8 + lh * 4 + (qq & 3);
-        if (col < ncols) P[(int64_t)(c0 + col) * p.r + j] = acc[t][qq];
+        if (col < ncols) {
+          const int64_t o = (int64_t)(c0 + col) * p.r + j;
+          if (direct)
+            G[o] = (uint16_t)af3_f32_to_bf16(acc[t][qq] * p.scale);
+          else
+            P[o] = acc[t][qq];
+        }
       }
     }
   } else {
@@ -361,7 +374,17 @@ __global__ __launch_bounds__(256, 2) void lwg_kernel(LwParams p) {
     L_BARRIER();
     for (int i = threadIdx.x; i < p.r * 64; i += 256) {
       const int jj = i >> 6, c = (i & 63) * 4;
-      if (c < ncols) *(float4*)(P + (int64_t)jj * p.W + c0 + c) = *(const float4*)(T + jj * kLwTPad + c);
+      if (c >= ncols) continue;
+      const float4 v = *(const float4*)(T + jj * kLwTPad + c);
+      const int64_t o = (int64_t)jj * p.W + c0 + c;
+      if (direct) {
+        uint2 b;
+        b.x = af3_pack_bf16x2(v.x * p.scale, v.y * p.scale);
+        b.y = af3_pack_bf16x2(v.z * p.scale, v.w * p.scale);
+        *(uint2*)(G + o) = b;
+      } else {
+        *(float4*)(P + o) = v;
+      }
     }
   }
 }
@@ -373,6 +396,7 @@ __global__ __launch_bounds__(256) void lwg_reduce_kernel(const float* __restrict
   const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (i >= MN) return;
   const int c0 = chunk_offs[e], c1 = chunk_offs[e + 1];
+  if (c1 - c0 == 1) return;  // the chunk's kernel wrote G itself
   float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
   for (int c = c0; c < c1; ++c) {
     const float4 v = *(const float4*)(partials + (int64_t)c * MN + i);
@@ -419,10 +443,12 @@ struct LuParams {
   const uint16_t* bl;        // [E][W][r]
   const int32_t* offs;
   const int32_t* chunk_map;
+  const int32_t* chunk_offs;  // per-expert chunk ranges: an expert of one chunk skips the dB partials
   int chunk_rows, W, r, ngrp;
   int64_t n_rows;
   float* partials;  // [chunk][W][r]
   float* u_part;    // [ngrp][n_rows][r]
+  uint16_t* g;      // dB, written here directly for one-chunk experts
 };
 
 typedef __attribute__((ext_vector_type(4))) float lu_f32x4;
@@ -609,8 +635,11 @@ __global__ __launch_bounds__(256, kLuMinBlocks) void lug_kernel(LuParams p) {
     }
   }
   // accb[j][t][qq]: Big column gc0 + 256 j + 64 wave + 32 t + 8 (qq / 4) + 4 lh + qq % 4, Small column lr
+  // (an expert of one chunk: bf16 straight into dB, as lwg_kernel)
   if (lr >= p.r) return;
   float* P = p.partials + (int64_t)chunk * p.W * p.r;
+  uint16_t* G = p.g + (int64_t)e * p.W * p.r;
+  const bool direct = p.chunk_offs[e + 1] - p.chunk_offs[e] == 1;
 #pragma unroll
   for (int j = 0; j < kLuG; ++j)
 #pragma unroll
@@ -618,7 +647,12 @@ __global__ __launch_bounds__(256, kLuMinBlocks) void lug_kernel(LuParams p) {
 #pragma unroll
       for (int qq = 0; qq < 16; ++qq) {
         const int col = gc0 + j * 256 + wave * 64 + t * 32 + (qq >> 2) * 8 + lh * 4 + (qq & 3);
-        if (col < p.W) P[(int64_t)col * p.r + lr] = accb[j][t][qq];
+        if (col < p.W) {
+          if (direct)
+            G[(int64_t)col * p.r + lr] = (uint16_t)af3_f32_to_bf16(accb[j][t][qq]);
+          else
+            P[(int64_t)col * p.r + lr] = accb[j][t][qq];
+        }
       }
 }
 
@@ -691,11 +725,14 @@ int lora_wgrad_fast(const uint16_t* big, int64_t ld_big, const int32_t* big_gath
   p.rowscale = rowscale;
   p.offs = token_offs;
   p.chunk_map = chunk_map;
+  p.chunk_offs = chunk_offs;
   p.chunk_rows = chunk_rows;
   p.W = W;
   p.r = r;
   p.nbb = (W + 255) / 256;
+  p.scale = scale;
   p.partials = partials;
+  p.g = g;
   if (max_chunks > 0) {
     const dim3 grid((unsigned)max_chunks * p.nbb), block(256);
     // small_is_a: G = Small^T Big ([r][W], the dA form); else G = Big^T Small ([W][r], dB)
@@ -757,10 +794,12 @@ extern "C" int af3_lora_u_wgrad(const uint16_t* big, int64_t ld_big, const int32
   p.bl = bl;
   p.offs = token_offs;
   p.chunk_map = chunk_map;
+  p.chunk_offs = chunk_offs;
   p.chunk_rows = chunk_rows;
   p.W = W;
   p.r = r;
   p.ngrp = (int)lu_ngrp(W);
+  p.g = g;
   p.n_rows = n_rows;
   p.partials = (float*)workspace;
   p.u_part = (float*)((uint8_t*)workspace +
