@@ -53,7 +53,7 @@ from . import _capi, kernels
 from .kernels import mxfp4_to_bf16_hip, swiglu_backward_raw, swiglu_forward
 from .routing import (  # noqa: F401  (re-exported names of the routing layer)
     ExptData, GatherIndx, RoutingData, ScatterIndx, compute_expt_data, compute_expt_data_torch,
-    dense_routing, router_linear, routing, routing_replay,
+    dense_routing, max_tiles, router_linear, routing, routing_replay,
 )
 
 GEMM_BLOCK_M = 128
@@ -501,12 +501,21 @@ def _lora_rows(x, gather, k_act, wl, trans_b, scale, ed, n_out, K):
 WGRAD_CHUNK = 512
 
 
+def _wgrad_chunks(ed, R, E):
+    """Entries of the WGRAD_CHUNK tile map the weight-gradient kernels visit:
+    R expert-sorted rows over E experts make at most max_tiles(R, E,
+    WGRAD_CHUNK) chunks, listed first (the map itself is sized for the smallest
+    tile), so the grid and the fp32 partial workspace are sized by that bound."""
+    return min(ed.block_pid_map[WGRAD_CHUNK].numel(), max_tiles(R, E, WGRAD_CHUNK))
+
+
 def _lora_wgrad(a, a_gather, a_div, a_rowscale, b, b_gather, b_div, ed, E, M, N):
     dev = a.device
     g = torch.empty(E, M, N, dtype=torch.bfloat16, device=dev)
     cmap = ed.block_pid_map[WGRAD_CHUNK]
     coffs = ed.token_offs_pad[WGRAD_CHUNK]
-    nch = cmap.numel()
+    R = a_gather.shape[0] if a_gather is not None else (b_gather.shape[0] if b_gather is not None else a.shape[0])
+    nch = _wgrad_chunks(ed, R, E)
     ws_n = int(_capi.load().af3_lora_wgrad_workspace_bytes(nch, M, N))
     ws = torch.empty(ws_n // 4, dtype=torch.float32, device=dev)
     _capi.call("af3_lora_wgrad", a.data_ptr(), a.stride(0) if a.shape[0] > 1 else M, _capi.ptr(a_gather), a_div,
@@ -527,7 +536,7 @@ def _lora_u_and_dB(big, gather, gdiv, rowscale, L, Bw, scale, ed, E, W):
     g = torch.empty(E, W, r, dtype=torch.bfloat16, device=dev)
     cmap = ed.block_pid_map[WGRAD_CHUNK]
     coffs = ed.token_offs_pad[WGRAD_CHUNK]
-    nch = cmap.numel()
+    nch = _wgrad_chunks(ed, R, E)
     ws_n = int(_capi.load().af3_lora_u_wgrad_workspace_bytes(nch, R, W, r))
     ws = torch.empty(max(ws_n, 1), dtype=torch.uint8, device=dev)
     L = L.contiguous()
