@@ -1315,10 +1315,12 @@ __device__ __forceinline__ void d5_cvt_exact(uint32_t w0, uint32_t w1, const uin
 // through LDS as [RM][CN] bf16 rows (16-byte chunks XOR-swizzled by row bit 2
 // so the two row groups of an MFMA output store hit disjoint banks), then one
 // 16-byte global store per chunk.
-template <int RM, int CN>
-__device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f32x16 (&acc)[RM / 32][CN / 128],
-                                            int e, int row_lo, int nrows, int n0, int ncols, int wn0) {
-  constexpr int TM = RM / 32, TN = CN / 128, RB = CN * 2;
+// acc[tm][tn] of a wave holds rows rb + 32 tm .. and the column pairs of
+// sub-tile tn from column wn0 (TM row groups per wave)
+template <int RM, int CN, int TM = RM / 32>
+__device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f32x16 (&acc)[TM][CN / 128],
+                                            int e, int row_lo, int nrows, int n0, int ncols, int wn0, int rb = 0) {
+  constexpr int TN = CN / 128, RB = CN * 2;
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
   float* const gl = (float*)(lds + RM * RB);
@@ -1345,7 +1347,7 @@ __device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f
   for (int tm = 0; tm < TM; ++tm) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int row0 = tm * 32 + j * 8 + lh * 4;
+      const int row0 = rb + tm * 32 + j * 8 + lh * 4;
       const float4 g = *(const float4*)(gl + row0);
       const float gq[4] = {g.x, g.y, g.z, g.w};
       const float4 a = *(const float4*)(al + row0);
@@ -1402,11 +1404,19 @@ __device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f
 // wave w owns columns 128 w .. 128 w + 127 (4 x 4 sub-tiles, two pair groups),
 // so a short expert tile still gives every wave 16 MFMAs per sub-step.  Both
 // copy 12 instructions per wave per k-step (A / B / S = 8 / 2 / 2 or 4 / 4 / 4).
-template <bool NARROW, int BXK>
+// SPLIT = 2 / 4 (256-row tiles with only 128 / 64 columns: the last n-tile
+// when N % 256 is 128 / 64): SPLIT waves share a 64-column group, each taking
+// 256 / SPLIT of the rows, so the tail tile's MFMAs are spread over all four
+// SIMDs instead of running on one; copies, LDS layouts and the slot schedule
+// are those of SPLIT = 1 (the A reads and MFMAs of the missing row groups
+// drop out of their slots).
+template <bool NARROW, int BXK, int SPLIT = 1>
 __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, int row_lo, int nrows, int n0, int ncols) {
+  static_assert(SPLIT == 1 || (!NARROW && (SPLIT == 2 || SPLIT == 4)), "row split only for 256-row tiles");
   constexpr int RM = NARROW ? 128 : 256;  // tile rows
   constexpr int CN = NARROW ? 512 : 256;  // tile columns
-  constexpr int TM = RM / 32;
+  constexpr int TM = RM / 32;             // row groups of the tile
+  constexpr int TMW = TM / SPLIT;         // row groups of one wave
   constexpr int PG = CN / 256;            // pair groups (64 columns each) per wave
   constexpr int TN = 2 * PG;
   constexpr int WC = CN / 4;              // columns per wave
@@ -1424,7 +1434,8 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lr = lane & 31, lh = lane >> 5;
-  const int wn0 = wave * WC;
+  const int wn0 = (wave / SPLIT) * WC;         // first column of the wave
+  const int rb = (wave % SPLIT) * (RM / SPLIT);  // first row of the wave
   const int tm_live = min(TM, (nrows + 31) >> 5);
   const int pg_live = min(PG, max(0, (ncols - wn0) >> 6));  // ncols is a multiple of 64
   const bool wave_live = pg_live > 0;
@@ -1473,11 +1484,13 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
 
   // ---- lane-fixed LDS byte offsets inside a stage ----
   const int ax = (lr ^ (lr >> 3)) & 7;
-  int aoff[2][4];  // A fragment of row group tm at sub-step s: aoff[tm & 1][s] + 4096 tm
+  // A fragment of the wave's row group tm at sub-step s: aoff[tm & 1][s] + 4096 tm
+  // (the wave's first row group rb / 32 is even, so tm & 1 is the tile row group's parity)
+  int aoff[2][4];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) aoff[t][s] = AOFF + lr * 128 + ((((lh * 4 + s) ^ ax) ^ (t << 2)) << 4);
+    for (int s = 0; s < 4; ++s) aoff[t][s] = AOFF + rb * 128 + lr * 128 + ((((lh * 4 + s) ^ ax) ^ (t << 2)) << 4);
   // B transposed read of pair group pg: lane group g = lane / 16 (k half g / 2,
   // chunk (2 pg + g % 2) of the wave's columns), i = lane % 16
   const int gi = lane & 15, gg = lane >> 4;
@@ -1492,9 +1505,9 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
   constexpr int CW = WC / 32;  // scale dwords per lane for the wave's check (its blocks x 64 k / 64 lanes)
   const int coff = SOFF + (wn0 / 32 * 64 + CW * lane) * 4;
 
-  af3_f32x16 acc[TM][TN];
+  af3_f32x16 acc[TMW][TN];
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int i = 0; i < TMW; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
@@ -1505,7 +1518,7 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
 
   auto kloop = [&](auto full_c) {
     constexpr bool FULL = decltype(full_c)::value;
-    af3_bf16x8 af[2][TM], bf[2][TN];
+    af3_bf16x8 af[2][TMW], bf[2][TN];
     // one k-step: iterations s = -1 (the carried sub-step of the previous
     // k-step, skipped at kt = 0) and 0..2; iteration s runs the MFMAs of
     // sub-step s while reading and converting the fragments of s + 1
@@ -1538,7 +1551,7 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int tm = i / TN, tn = i % TN;
-          if (!(s < 0 && first) && (FULL || (tm < tm_live && (tn >> 1) < pg_live)))
+          if (i < TMW * TN && !(s < 0 && first) && (FULL || (tm < tm_live && (tn >> 1) < pg_live)))
             acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[c][tm], bf[c][tn], acc[tm][tn], 0, 0, 0);
           if (FULL || wave_live) {
             if (i < SB) {
@@ -1564,7 +1577,7 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
                   for (int q = 0; q < CW; ++q) chk[q] = cv[q];
                 }
               }
-            } else if (i < SA + TM) {
+            } else if (i < SA + TMW) {
               const int t = i - SA;
               if (FULL || t < tm_live) af[nx][t] = *(const af3_bf16x8*)(stg + aoff[t & 1][o] + 4096 * t);
             }
@@ -1622,7 +1635,7 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
     };
     const af3_bf16x8 zf = __builtin_bit_cast(af3_bf16x8, zero4());
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm) af[1][tm] = zf;
+    for (int tm = 0; tm < TMW; ++tm) af[1][tm] = zf;
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) bf[1][tn] = zf;
     if (nk > 1)
@@ -1642,7 +1655,7 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
     }
     // the last k-step's sub-step 3
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < TMW * TN; ++i) {
       const int tm = i / TN, tn = i % TN;
       if (FULL || (tm < tm_live && (tn >> 1) < pg_live))
         acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[1][tm], bf[1][tn], acc[tm][tn], 0, 0, 0);
@@ -1671,14 +1684,14 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
         __syncthreads();
 #pragma unroll
         for (int ks = 0; ks < kBK / 16; ++ks) {
-          af3_bf16x8 af[TM], bf[TN];
+          af3_bf16x8 af[TMW], bf[TN];
 #pragma unroll
-          for (int tm = 0; tm < TM; ++tm) af[tm] = *(const af3_bf16x8*)(As + lds_off(tm * 32 + lr, ks * 2 + lh));
+          for (int tm = 0; tm < TMW; ++tm) af[tm] = *(const af3_bf16x8*)(As + lds_off(rb + tm * 32 + lr, ks * 2 + lh));
 #pragma unroll
           for (int tn = 0; tn < TN; ++tn)
             bf[tn] = *(const af3_bf16x8*)(Bs + lds_off(wn0 + 64 * (tn >> 1) + 2 * lr + (tn & 1), ks * 2 + lh));
 #pragma unroll
-          for (int tm = 0; tm < TM; ++tm)
+          for (int tm = 0; tm < TMW; ++tm)
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn)
               acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[tm], bf[tn], acc[tm][tn], 0, 0, 0);
@@ -1686,7 +1699,7 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
       }
     }
   }
-  d5_epilogue<RM, CN>(p, lds, acc, e, row_lo, nrows, n0, ncols, wn0);
+  d5_epilogue<RM, CN, TMW>(p, lds, acc, e, row_lo, nrows, n0, ncols, wn0, rb);
 }
 
 template <int BXK>
@@ -1706,7 +1719,14 @@ __global__ __launch_bounds__(256) void gemm5_dgrad_kernel(Params p) {
     if (nt & 1) return;
     d5_tile<true, BXK>(p, lds, e, row_lo, nrows, n0, min(2 * kG4Rows, p.N - n0));
   } else {
-    d5_tile<false, BXK>(p, lds, e, row_lo, nrows, n0, min(kG4Rows, p.N - n0));
+    // N % 64 == 0: the last n-tile of N % 256 == 64 / 128 splits its columns' rows over the waves
+    const int ncols = min(kG4Rows, p.N - n0);
+    if (ncols <= 64)
+      d5_tile<false, BXK, 4>(p, lds, e, row_lo, nrows, n0, ncols);
+    else if (ncols <= 128)
+      d5_tile<false, BXK, 2>(p, lds, e, row_lo, nrows, n0, ncols);
+    else
+      d5_tile<false, BXK, 1>(p, lds, e, row_lo, nrows, n0, ncols);
   }
 }
 

@@ -79,16 +79,18 @@ CASES = [  # (gather, lora, odd)
 ]
 
 
-@pytest.mark.parametrize("cfg", [0, 4, 22])
+@pytest.mark.parametrize("cfg,nout", [(0, NOUT), (4, NOUT), (22, NOUT), (22, 640)])
 @pytest.mark.parametrize("gather,lora,odd", CASES)
-def test_forward_tiles(dev, cfg, gather, lora, odd):
+def test_forward_tiles(dev, cfg, nout, gather, lora, odd):
+    """N = 576 / 640 end in a 64- / 128-column n-tile (waves past the tile's
+    columns keep only the copy / barrier protocol)."""
     g, ref, rd, gi = _routing(dev, 11)
-    blocks, scales = _weights(g, NOUT, KRED, odd)          # W [E, N, K]
+    blocks, scales = _weights(g, nout, KRED, odd)          # W [E, N, K]
     Rr = T * TOPK
     x = torch.randn(T if gather else Rr, KRED, generator=g).to(torch.bfloat16)
-    bias = (torch.randn(E, NOUT, generator=g) * 0.1).to(torch.bfloat16)
+    bias = (torch.randn(E, nout, generator=g) * 0.1).to(torch.bfloat16)
     L = (torch.randn(Rr, 32, generator=g) * 0.3).to(torch.bfloat16) if lora else None
-    Bx = (torch.randn(E, NOUT, 32, generator=g) * 0.3).to(torch.bfloat16) if lora else None
+    Bx = (torch.randn(E, nout, 32, generator=g) * 0.3).to(torch.bfloat16) if lora else None
     old = dict(Q.GEMM_TILE)
     Q.GEMM_TILE.update(block_m=256, tile_cfg=cfg)
     try:
@@ -105,15 +107,17 @@ def test_forward_tiles(dev, cfg, gather, lora, odd):
     assert not bad.any(), float(bad.float().mean())
 
 
-@pytest.mark.parametrize("cfg", [0, 4, 23])
+@pytest.mark.parametrize("cfg,nout", [(0, NOUT), (4, NOUT), (23, NOUT), (23, 640)])
 @pytest.mark.parametrize("gather,lora,odd", CASES)
-def test_dgrad_tiles(dev, cfg, gather, lora, odd):
+def test_dgrad_tiles(dev, cfg, nout, gather, lora, odd):
+    """N = 576 / 640 end in a 64- / 128-column n-tile, which the default kernel
+    (tile_cfg 23) runs with the tile's rows split over the waves."""
     g, ref, rd, gi = _routing(dev, 12)
-    blocks, scales = _weights(g, KRED, NOUT, odd)          # W [E, K, N] packed along N
+    blocks, scales = _weights(g, KRED, nout, odd)          # W [E, K, N] packed along N
     Rr = T * TOPK
     x = torch.randn(T if gather else Rr, KRED, generator=g).to(torch.bfloat16)
     L = (torch.randn(Rr, 32, generator=g) * 0.3).to(torch.bfloat16) if lora else None
-    Ax = (torch.randn(E, 32, NOUT, generator=g) * 0.3).to(torch.bfloat16) if lora else None
+    Ax = (torch.randn(E, 32, nout, generator=g) * 0.3).to(torch.bfloat16) if lora else None
     gam = rd.gate_scal if gather else None
     old = dict(Q.GEMM_TILE)
     Q.GEMM_TILE.update(block_m=256, tile_cfg=cfg)
@@ -126,7 +130,7 @@ def test_dgrad_tiles(dev, cfg, gather, lora, odd):
     W = mxfp4.dequant_f32(blocks, scales)
     yr = moe.rows(x, W, ref["offs"], ref["topk_indx"] if gather else None, TOPK,
                   gammas=gam.cpu() if gather else None, trans=True, lora_l=L, lora_b=Ax)
-    assert y.shape == (Rr, NOUT)
+    assert y.shape == (Rr, nout)
     a = y.float().cpu().double()
     assert torch.isfinite(a).all()
     bad = (a - yr.double()).abs() > ATOL + RTOL * yr.double().abs()
