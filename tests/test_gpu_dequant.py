@@ -64,3 +64,21 @@ def test_convert_moe_packed_tensors_transposed(dev):
     w = quantization.convert_moe_packed_tensors(blocks.to(dev), scales.to(dev))
     ref = mxfp4.dequant_lut_ldexp(blocks, scales).transpose(1, 2)
     assert w.shape == (2, 96, 64) and torch.equal(w.cpu(), ref)
+
+
+def test_convert_moe_packed_tensors_every_scale_byte(dev):
+    """All 256 e8m0 bytes, each over every nibble pair: bit-equal to the kernels'
+    rule everywhere, and to the reference's LUT + ldexp (quantization.py:137-172)
+    for bytes 2..252; bytes 0, 1 and 253..255 flush where ldexp gives bf16
+    subnormals, inf or NaN."""
+    blocks = torch.arange(256, dtype=torch.uint8).reshape(1, 1, 1, 16, 16).expand(1, 256, 1, 16, 16)
+    blocks = blocks.reshape(1, 256, 16, 16).contiguous()                 # [E, N, G, 16]: G blocks of all 256 bytes
+    scales = torch.arange(256, dtype=torch.uint8).reshape(1, 256, 1).expand(1, 256, 16).contiguous()
+    w = quantization.convert_moe_packed_tensors(blocks.to(dev), scales.to(dev)).cpu()   # [E, K, N]
+    rule = torch.from_numpy(mxfp4.dequant_bits(blocks.numpy(), scales.numpy()).view("int16")).view(
+        torch.bfloat16).transpose(1, 2)
+    assert torch.equal(w.view(torch.int16), rule.contiguous().view(torch.int16))
+    ldexp = mxfp4.dequant_lut_ldexp(blocks, scales).transpose(1, 2).contiguous()
+    normal = ((scales >= 2) & (scales <= 252)).repeat_interleave(32, dim=-1).transpose(1, 2)
+    assert torch.equal(w.view(torch.int16)[normal], ldexp.view(torch.int16)[normal])
+    assert int((~normal).sum()) == 5 * 16 * 32
