@@ -215,39 +215,65 @@ __global__ void fill_tail_kernel(const int32_t* __restrict__ offs, int E, int64_
 }
 
 // ---- expert data: padded tile offsets and block -> (block, expert) map -----
-__global__ void tile_scan_kernel(const int32_t* __restrict__ hist, int E, const int32_t* __restrict__ block_ms,
-                                 int n_bm, int32_t* __restrict__ offs_pad /* n_bm x (E+1) */) {
-  int b = threadIdx.x;
-  if (b >= n_bm) return;
-  int bm = block_ms[b];
-  int32_t run = 0;
-  for (int e = 0; e < E; ++e) {
-    offs_pad[b * (E + 1) + e] = run;
-    run += (hist[e] + bm - 1) / bm;
-  }
-  offs_pad[b * (E + 1) + E] = run;
-}
+// per tile size (one 1024-thread block each): the exclusive prefix of the
+// experts' tile counts -> offs_pad, then the tile -> (expert, tile) map
+constexpr int kScanMaxE = 4096;
 
-__global__ void tile_map_kernel(const int32_t* __restrict__ offs_pad, int E, int max_tiles,
-                                int32_t* __restrict__ map /* n_bm x max_tiles */) {
-  int b = blockIdx.y;
-  int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= max_tiles) return;
-  const int32_t* op = offs_pad + b * (E + 1);
-  int32_t val = -1;
-  if (i < op[E]) {
-    // largest e with op[e] <= i (experts with zero tiles have op[e] == op[e+1])
-    int lo = 0, hi = E - 1;
-    while (lo < hi) {
-      int mid = (lo + hi + 1) >> 1;
-      if (op[mid] <= i)
-        lo = mid;
-      else
-        hi = mid - 1;
+__global__ __launch_bounds__(1024) void tile_scan_map_kernel(const int32_t* __restrict__ hist, int E,
+                                                             const int32_t* __restrict__ block_ms, int max_tiles,
+                                                             int32_t* __restrict__ offs_pad /* n_bm x (E+1) */,
+                                                             int32_t* __restrict__ map /* n_bm x max_tiles */) {
+  __shared__ int32_t op[kScanMaxE + 1];
+  __shared__ int32_t part[1024];
+  const int b = blockIdx.x, t = threadIdx.x;
+  const int bm = block_ms[b];
+  // thread t owns experts [t * per, (t + 1) * per)
+  const int per = (E + 1023) / 1024;
+  int32_t run = 0;
+  for (int i = 0; i < per; ++i) {
+    const int e = t * per + i;
+    if (e < E) {
+      const int32_t n = (hist[e] + bm - 1) / bm;
+      op[e] = n;
+      run += n;
     }
-    val = ((i - op[lo]) << 16) | lo;
   }
-  map[(int64_t)b * max_tiles + i] = val;
+  part[t] = run;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int32_t v = t >= off ? part[t - off] : 0;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
+  }
+  int32_t pos = part[t] - run;
+  for (int i = 0; i < per; ++i) {
+    const int e = t * per + i;
+    if (e < E) {
+      const int32_t n = op[e];
+      op[e] = pos;
+      pos += n;
+    }
+  }
+  if (t == 1023) op[E] = part[1023];
+  __syncthreads();
+  for (int e = t; e <= E; e += 1024) offs_pad[b * (E + 1) + e] = op[e];
+  for (int i = t; i < max_tiles; i += 1024) {
+    int32_t val = -1;
+    if (i < op[E]) {
+      // largest e with op[e] <= i (experts with zero tiles have op[e] == op[e+1])
+      int lo = 0, hi = E - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (op[mid] <= i)
+          lo = mid;
+        else
+          hi = mid - 1;
+      }
+      val = ((i - op[lo]) << 16) | lo;
+    }
+    map[(int64_t)b * max_tiles + i] = val;
+  }
 }
 
 // ---- grouped-GEMM tile order: full tiles first (expert order), then the
@@ -260,7 +286,8 @@ __global__ __launch_bounds__(1024) void tile_order_kernel(const int32_t* __restr
   __shared__ int32_t nfull[kSchedMaxE];
   __shared__ int32_t tail[kSchedMaxE];
   __shared__ int32_t start[kSchedMaxBM + 1];  // tails of size s start at start[s]
-  __shared__ int32_t part[1024];
+  __shared__ int32_t part[1024];               // prefix of full-tile counts
+  __shared__ int32_t suf[1024];                // suffix of the tail-size histogram
   const int t = threadIdx.x;
   for (int e = t; e < E; e += 1024) {
     const int h = hist[e];
@@ -281,21 +308,22 @@ __global__ __launch_bounds__(1024) void tile_order_kernel(const int32_t* __restr
   }
   part[t] = run;
   __syncthreads();
+  // thread t holds the count of tail size t (sizes 1 .. bm - 1; bm <= 1024)
+  const int32_t cnt = (t >= 1 && t < bm) ? start[t] : 0;
+  suf[t] = cnt;
+  __syncthreads();
   for (int off = 1; off < 1024; off <<= 1) {
     const int32_t v = t >= off ? part[t - off] : 0;
+    const int32_t w = t + off < 1024 ? suf[t + off] : 0;
     __syncthreads();
     part[t] += v;
+    suf[t] += w;
     __syncthreads();
   }
   const int32_t total_full = part[1023];
-  if (t == 0) {  // descending exclusive scan of the tail-size histogram
-    int32_t acc = 0;
-    for (int s = bm - 1; s >= 1; --s) {
-      const int32_t c = start[s];
-      start[s] = acc;
-      acc += c;
-    }
-  }
+  const int32_t n_tiles = total_full + suf[0];  // full tiles + one partial tile per expert with a tail
+  // partial tiles by decreasing size: size s starts after every larger one
+  if (t >= 1 && t < bm) start[t] = suf[t] - cnt;
   __syncthreads();
   int32_t pos = part[t] - run;
   for (int i = 0; i < per; ++i) {
@@ -310,12 +338,7 @@ __global__ __launch_bounds__(1024) void tile_order_kernel(const int32_t* __restr
       order[total_full + rank] = (nfull[e] << 16) | e;
     }
   }
-}
-
-__global__ void tile_order_pad_kernel(const int32_t* __restrict__ offs_pad, int E, int max_tiles,
-                                      int32_t* __restrict__ order) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < max_tiles && i >= offs_pad[E]) order[i] = -1;
+  for (int i = n_tiles + t; i < max_tiles; i += 1024) order[i] = -1;
 }
 
 }  // namespace
@@ -462,14 +485,11 @@ extern "C" int af3_routing_topk(const uint16_t* logits, int64_t ld_logits, int64
 extern "C" int af3_expt_data(const int32_t* hist, int n_expts_tot, const int32_t* block_ms_dev, int n_block_ms,
                              int max_tiles, int32_t* token_offs_pad, int32_t* block_pid_map, void* stream_) {
   hipStream_t stream = (hipStream_t)stream_;
-  AF3_REQUIRE(n_expts_tot > 0 && n_block_ms > 0 && n_block_ms <= 64 && max_tiles >= 0, "expt_data: bad sizes");
-  hipLaunchKernelGGL(tile_scan_kernel, dim3(1), dim3(64), 0, stream, hist, n_expts_tot, block_ms_dev, n_block_ms,
-                     token_offs_pad);
-  int rc = af3::check_launch("expt_data/scan");
-  if (rc || max_tiles == 0) return rc;
-  hipLaunchKernelGGL(tile_map_kernel, dim3((unsigned)af3_cdiv(max_tiles, 256), n_block_ms), dim3(256), 0, stream,
-                     token_offs_pad, n_expts_tot, max_tiles, block_pid_map);
-  return af3::check_launch("expt_data/map");
+  AF3_REQUIRE(n_expts_tot > 0 && n_expts_tot <= kScanMaxE && n_block_ms > 0 && n_block_ms <= 64 && max_tiles >= 0,
+              "expt_data: bad sizes (E=%d, block sizes %d, max_tiles %d)", n_expts_tot, n_block_ms, max_tiles);
+  hipLaunchKernelGGL(tile_scan_map_kernel, dim3(n_block_ms), dim3(1024), 0, stream, hist, n_expts_tot, block_ms_dev,
+                     max_tiles, token_offs_pad, block_pid_map);
+  return af3::check_launch("expt_data");
 }
 
 // Order of the BM-row tiles for the grouped GEMM's work list (same entries as
@@ -484,10 +504,7 @@ extern "C" int af3_tile_order(const int32_t* hist, int n_expts_tot, int block_m,
               block_m, max_tiles);
   AF3_REQUIRE(max_tiles == 0 || (hist && token_offs_pad && order), "tile_order: null pointer");
   if (max_tiles == 0) return 0;
+  (void)token_offs_pad;  // the kernel counts the tiles itself (the same total as token_offs_pad[E])
   hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(1024), 0, stream, hist, n_expts_tot, block_m, max_tiles, order);
-  int rc = af3::check_launch("tile_order");
-  if (rc) return rc;
-  hipLaunchKernelGGL(tile_order_pad_kernel, dim3((unsigned)af3_cdiv(max_tiles, 256)), dim3(256), 0, stream,
-                     token_offs_pad, n_expts_tot, max_tiles, order);
-  return af3::check_launch("tile_order/pad");
+  return af3::check_launch("tile_order");
 }

@@ -18,10 +18,11 @@ def _check(rt_gpu, gi_gpu, si_gpu, ref, max_tiles_bm=128):
     assert torch.equal(si_gpu.src_indx.cpu(), ref["gate_indx"])
     assert torch.equal(si_gpu.dst_indx.cpu(), ref["topk_indx"])
     assert torch.allclose(rd.gate_scal.float().cpu(), ref["gate_scal"].float(), rtol=1e-2, atol=4e-3)
-    pid = rd.expt_data.block_pid_map[128].cpu()
-    offs_pad, ref_pid = O.expt_data(ref["hist"], 128, pid.numel())
-    assert torch.equal(rd.expt_data.token_offs_pad[128].cpu(), offs_pad)
-    assert torch.equal(pid, ref_pid)
+    for bm in R.BLOCK_MS:  # every tile size's padded offsets and tile map (one launch builds them all)
+        pid = rd.expt_data.block_pid_map[bm].cpu()
+        offs_pad, ref_pid = O.expt_data(ref["hist"], bm, pid.numel())
+        assert torch.equal(rd.expt_data.token_offs_pad[bm].cpu(), offs_pad)
+        assert torch.equal(pid, ref_pid)
 
 
 @pytest.mark.parametrize("T,E,K", [(1, 4, 2), (300, 6, 4), (4096, 32, 4), (5000, 128, 4)])
