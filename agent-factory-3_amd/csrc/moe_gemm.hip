@@ -2158,6 +2158,10 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restri
 // ---------------------------------------------------------------------------
 // combine: out[t] = sum_j rows[src[t*K + j]] (fp32 sum, bf16 out), -1 skipped
 // ---------------------------------------------------------------------------
+// KU > 0: K <= KU, the K row indices and then the K rows loaded before any
+// sum (KU rows in flight per lane); KU = 0: any K, one row at a time.  The
+// fp32 sum runs over j = 0 .. K - 1 in order either way.
+template <int KU>
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ rows, int64_t ld_rows,
                                                       const int32_t* __restrict__ src, int K, int N,
                                                       uint16_t* __restrict__ out, int64_t ld_out, int vec_per_row,
@@ -2167,14 +2171,28 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   int64_t t = v / vec_per_row;
   int c = (int)(v - t * vec_per_row) * 8;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int j = 0; j < K; ++j) {
-    int32_t r = src[t * K + j];
-    if (r < 0) continue;
-    af3_u32x4 x = *(const af3_u32x4*)(rows + (int64_t)r * ld_rows + c);
+  auto add = [&](const af3_u32x4 x) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       acc[2 * q] += af3_bf16_to_f32(x[q] & 0xFFFFu);
       acc[2 * q + 1] += af3_bf16_to_f32(x[q] >> 16);
+    }
+  };
+  if constexpr (KU > 0) {
+    int32_t r[KU];
+#pragma unroll
+    for (int j = 0; j < KU; ++j) r[j] = j < K ? src[t * K + j] : -1;
+    af3_u32x4 x[KU];
+#pragma unroll
+    for (int j = 0; j < KU; ++j) x[j] = r[j] >= 0 ? *(const af3_u32x4*)(rows + (int64_t)r[j] * ld_rows + c) : zero4();
+#pragma unroll
+    for (int j = 0; j < KU; ++j)
+      if (r[j] >= 0) add(x[j]);
+  } else {
+    for (int j = 0; j < K; ++j) {
+      int32_t r = src[t * K + j];
+      if (r < 0) continue;
+      add(*(const af3_u32x4*)(rows + (int64_t)r * ld_rows + c));
     }
   }
   af3_u32x4 o;
@@ -2589,7 +2607,14 @@ extern "C" int af3_moe_combine(const uint16_t* rows, int64_t ld_rows, const int3
               "moe_combine: rows/out must be 16-byte aligned with N % 8 == 0");
   int vpr = N / 8;
   int64_t nv = n_tokens * vpr;
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)af3_cdiv(nv, 256)), dim3(256), 0, stream, rows, ld_rows, src_indx,
-                     K, N, out, ld_out, vpr, nv);
+  if (K <= 4)
+    hipLaunchKernelGGL(combine_kernel<4>, dim3((unsigned)af3_cdiv(nv, 256)), dim3(256), 0, stream, rows, ld_rows,
+                       src_indx, K, N, out, ld_out, vpr, nv);
+  else if (K <= 8)
+    hipLaunchKernelGGL(combine_kernel<8>, dim3((unsigned)af3_cdiv(nv, 256)), dim3(256), 0, stream, rows, ld_rows,
+                       src_indx, K, N, out, ld_out, vpr, nv);
+  else
+    hipLaunchKernelGGL(combine_kernel<0>, dim3((unsigned)af3_cdiv(nv, 256)), dim3(256), 0, stream, rows, ld_rows,
+                       src_indx, K, N, out, ld_out, vpr, nv);
   return af3::check_launch("moe_combine");
 }

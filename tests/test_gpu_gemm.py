@@ -66,6 +66,22 @@ def test_down_forward_gammas_and_combine(dev):
     assert torch.equal(out.cpu(), moe.combine(rows_dev.cpu(), ref["gate_indx"], K))
 
 
+@pytest.mark.parametrize("K", [1, 3, 6, 10])
+def test_combine_any_k_bit_exact(dev, K):
+    """af3_moe_combine at k = 1 .. 10 (all rows in flight for k <= 4 and <= 8,
+    one at a time beyond), with dropped (-1) entries: bit-equal to the
+    oracle's in-order fp32 sum of the bf16 rows."""
+    import types
+    g = torch.Generator().manual_seed(40 + K)
+    T, N = 300, 264
+    rows = torch.randn(T * K + 5, N, generator=g).to(torch.bfloat16)
+    src = torch.randperm(T * K + 5, generator=g)[:T * K].to(torch.int32)
+    src[torch.randint(0, T * K, (T // 3,), generator=g)] = -1
+    out = Q.moe_combine(rows.to(dev), types.SimpleNamespace(src_indx=src.to(dev)), K)
+    assert out.shape == (T, N)
+    assert torch.equal(out.cpu(), moe.combine(rows, src, K))
+
+
 @pytest.mark.parametrize("gather", [True, False])
 def test_dgrad_transposed_weights(dev, gather):
     g, x, logits, blocks, scales, bias = _problem(H=160, N=224, seed=2)  # W [E, 224, 160]
