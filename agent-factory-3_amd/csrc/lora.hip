@@ -397,13 +397,22 @@ __global__ __launch_bounds__(256) void lwg_reduce_kernel(const float* __restrict
   if (i >= MN) return;
   const int c0 = chunk_offs[e], c1 = chunk_offs[e + 1];
   if (c1 - c0 == 1) return;  // the chunk's kernel wrote G itself
+  // chunks in order, eight partial loads in flight per lane
   float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-  for (int c = c0; c < c1; ++c) {
-    const float4 v = *(const float4*)(partials + (int64_t)c * MN + i);
-    a0 += v.x;
-    a1 += v.y;
-    a2 += v.z;
-    a3 += v.w;
+  for (int cb = c0; cb < c1; cb += 8) {
+    float4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      v[j] = cb + j < c1 ? *(const float4*)(partials + (int64_t)(cb + j) * MN + i) : float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (cb + j < c1) {
+        a0 += v[j].x;
+        a1 += v[j].y;
+        a2 += v[j].z;
+        a3 += v[j].w;
+      }
+    }
   }
   uint2 o;
   o.x = af3_pack_bf16x2(a0 * scale, a1 * scale);
