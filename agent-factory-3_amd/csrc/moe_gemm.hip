@@ -1410,13 +1410,17 @@ __device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f
 // SIMDs instead of running on one; copies, LDS layouts and the slot schedule
 // are those of SPLIT = 1 (the A reads and MFMAs of the missing row groups
 // drop out of their slots).
-template <bool NARROW, int BXK, int SPLIT = 1>
+// RG > 0 (SPLIT = 1): only the first RG row groups of the tile hold rows (an
+// expert's last, partial m-tile), so the waves run the MFMAs and A reads of
+// those alone; the rows past them are never stored either way.
+template <bool NARROW, int BXK, int SPLIT = 1, int RG = 0>
 __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, int row_lo, int nrows, int n0, int ncols) {
   static_assert(SPLIT == 1 || (!NARROW && (SPLIT == 2 || SPLIT == 4)), "row split only for 256-row tiles");
+  static_assert(RG == 0 || (SPLIT == 1 && RG >= 1 && RG <= (NARROW ? 4 : 8)), "row groups of a tile");
   constexpr int RM = NARROW ? 128 : 256;  // tile rows
   constexpr int CN = NARROW ? 512 : 256;  // tile columns
   constexpr int TM = RM / 32;             // row groups of the tile
-  constexpr int TMW = TM / SPLIT;         // row groups of one wave
+  constexpr int TMW = RG ? RG : TM / SPLIT;  // row groups of one wave
   constexpr int PG = CN / 256;            // pair groups (64 columns each) per wave
   constexpr int TN = 2 * PG;
   constexpr int WC = CN / 4;              // columns per wave
@@ -1717,7 +1721,11 @@ __global__ __launch_bounds__(256) void gemm5_dgrad_kernel(Params p) {
   if (nrows <= 128) {
     // short tile: even n-tiles take the next n-tile too, odd ones have no work
     if (nt & 1) return;
-    d5_tile<true, BXK>(p, lds, e, row_lo, nrows, n0, min(2 * kG4Rows, p.N - n0));
+    const int ncols = min(2 * kG4Rows, p.N - n0);
+    if (nrows <= 64)
+      d5_tile<true, BXK, 1, 2>(p, lds, e, row_lo, nrows, n0, ncols);
+    else
+      d5_tile<true, BXK>(p, lds, e, row_lo, nrows, n0, ncols);
   } else {
     // N % 64 == 0: the last n-tile of N % 256 == 64 / 128 splits its columns' rows over the waves
     const int ncols = min(kG4Rows, p.N - n0);
@@ -1725,6 +1733,12 @@ __global__ __launch_bounds__(256) void gemm5_dgrad_kernel(Params p) {
       d5_tile<false, BXK, 4>(p, lds, e, row_lo, nrows, n0, ncols);
     else if (ncols <= 128)
       d5_tile<false, BXK, 2>(p, lds, e, row_lo, nrows, n0, ncols);
+    else if (nrows <= 160)  // a partial m-tile: only its live row groups
+      d5_tile<false, BXK, 1, 5>(p, lds, e, row_lo, nrows, n0, ncols);
+    else if (nrows <= 192)
+      d5_tile<false, BXK, 1, 6>(p, lds, e, row_lo, nrows, n0, ncols);
+    else if (nrows <= 224)
+      d5_tile<false, BXK, 1, 7>(p, lds, e, row_lo, nrows, n0, ncols);
     else
       d5_tile<false, BXK, 1>(p, lds, e, row_lo, nrows, n0, ncols);
   }
