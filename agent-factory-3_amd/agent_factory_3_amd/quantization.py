@@ -641,13 +641,12 @@ class LoraDequantMoEMatmul(torch.autograd.Function):
 # values and gradients are those of the reference's DequantMoEMatmul ->
 # SwiGLUFunction -> DequantMoEMatmul chain (quantization.py:507-544), bit for
 # bit; FUSED_SWIGLU = False restores that chain of separate kernels.
-# The fused backward is off by default: it trades the separate SwiGLU
-# backward pass for loads of the saved pre-activation inside each dX work
-# item's epilogue, where one work item per CU leaves their latency exposed
-# (measured on MI355X at the gpt-oss-120b layer: +0.42 ms in the dX kernel
-# against 0.31 ms for the separate pass).
+# The fused backward replaces the separate SwiGLU backward pass (and the dI
+# round trip through HBM) by loads of the saved pre-activation inside each dX
+# work item's epilogue, issued in two batches ahead of their use.  With the
+# routing-weight gradient on, dI itself is needed and the separate pass runs.
 FUSED_SWIGLU = True
-FUSED_SWIGLU_BWD = False
+FUSED_SWIGLU_BWD = True
 
 
 def _weights_of(ctx):

@@ -1326,6 +1326,30 @@ __device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f
   float* const gl = (float*)(lds + RM * RB);
   float* const al = gl + 256;  // per-row A scales
   auto coff = [&](int row, int col) { return row * RB + ((((col >> 3) ^ (((row >> 2) & 1) << 2))) << 4) + ((col & 7) << 1); };
+  // SwiGLU backward (epi 1): the saved pre-activation of the lane's first NB
+  // output chunks is loaded before the staging below, the rest one batch at a
+  // time, so a work item waits on NI / NB loads in flight instead of one
+  // chunk group after another (addresses clamped to the tile's first valid
+  // row and column; those values are never used)
+  constexpr int CH = CN / 8;              // 16-byte chunks per row
+  constexpr int NI = RM * CH / 256;       // chunks per lane
+  constexpr int NB = NI < 16 ? NI : 16;   // chunks per prefetch batch
+  const bool swb = p.epi == 1;
+  af3_u32x4 gx[NB][2];
+  auto gu_load = [&](int i, af3_u32x4 (&d)[2]) {
+    const int id = i * 256 + threadIdx.x;
+    const int row = id / CH, ch = id % CH;
+    const bool ok = row < nrows && ch * 8 < ncols;
+    const int64_t grow = row_lo + (ok ? row : 0);
+    const int64_t col2 = 2 * (int64_t)(n0 + (ok ? ch * 8 : 0));
+    const uint16_t* gu = (const uint16_t*)p.glu + grow * p.ld_glu + col2;
+    d[0] = *(const af3_u32x4*)gu;
+    d[1] = *(const af3_u32x4*)(gu + 8);
+  };
+  if (swb) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) gu_load(j, gx[j]);
+  }
   __syncthreads();
   for (int t = threadIdx.x; t < RM; t += 256) {
     float gv = 1.f;
@@ -1365,35 +1389,47 @@ __device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f
     }
   }
   __syncthreads();
-  constexpr int CH = CN / 8;  // 16-byte chunks per row
+  if (swb) {
+    for (int b0 = 0; b0 < NI; b0 += NB) {
+      if (b0 > 0) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) gu_load(b0 + j, gx[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const int id = (b0 + j) * 256 + threadIdx.x;
+        const int row = id / CH, ch = id % CH;
+        if (row < nrows && ch * 8 < ncols) {  // dI (the bf16 values v) and the saved pre-activation -> dGU
+          const af3_u32x4 v = *(const af3_u32x4*)(lds + row * RB + ((ch ^ (((row >> 2) & 1) << 2)) << 4));
+          const int64_t grow = row_lo + row;
+          const int64_t col2 = 2 * (int64_t)(n0 + ch * 8);
+          const uint32_t xw[8] = {gx[j][0][0], gx[j][0][1], gx[j][0][2], gx[j][0][3],
+                                  gx[j][1][0], gx[j][1][1], gx[j][1][2], gx[j][1][3]};
+          uint32_t o[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const float d = af3_bf16_to_f32(q & 1 ? v[q >> 1] >> 16 : v[q >> 1] & 0xFFFFu);
+            const float g = fminf(af3_bf16_to_f32(xw[q] & 0xFFFFu), p.limit);
+            const float u = fminf(fmaxf(af3_bf16_to_f32(xw[q] >> 16), -p.limit), p.limit);
+            float dg, du;
+            af3_swiglu_bwd_elem(d, g, u, p.alpha, p.limit, dg, du);
+            o[q] = af3_pack_bf16x2(dg, du);
+          }
+          af3_u32x4* dst = (af3_u32x4*)(p.c + grow * p.ldc + col2);
+          dst[0] = af3_u32x4{o[0], o[1], o[2], o[3]};
+          dst[1] = af3_u32x4{o[4], o[5], o[6], o[7]};
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll 4
-  for (int i = 0; i < RM * CH / 256; ++i) {
+  for (int i = 0; i < NI; ++i) {
     const int id = i * 256 + threadIdx.x;
     const int row = id / CH, ch = id % CH;
     if (row < nrows && ch * 8 < ncols) {
       const af3_u32x4 v = *(const af3_u32x4*)(lds + row * RB + ((ch ^ (((row >> 2) & 1) << 2)) << 4));
-      const int64_t grow = row_lo + row;
-      if (p.epi == 1) {  // SwiGLU backward: dI (the bf16 values v) and the saved pre-activation -> dGU
-        const int64_t col2 = 2 * (int64_t)(n0 + ch * 8);
-        const uint16_t* gu = (const uint16_t*)p.glu + grow * p.ld_glu + col2;
-        const af3_u32x4 x0 = *(const af3_u32x4*)gu, x1 = *(const af3_u32x4*)(gu + 8);
-        const uint32_t xw[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-        uint32_t o[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const float d = af3_bf16_to_f32(q & 1 ? v[q >> 1] >> 16 : v[q >> 1] & 0xFFFFu);
-          const float g = fminf(af3_bf16_to_f32(xw[q] & 0xFFFFu), p.limit);
-          const float u = fminf(fmaxf(af3_bf16_to_f32(xw[q] >> 16), -p.limit), p.limit);
-          float dg, du;
-          af3_swiglu_bwd_elem(d, g, u, p.alpha, p.limit, dg, du);
-          o[q] = af3_pack_bf16x2(dg, du);
-        }
-        af3_u32x4* dst = (af3_u32x4*)(p.c + grow * p.ldc + col2);
-        dst[0] = af3_u32x4{o[0], o[1], o[2], o[3]};
-        dst[1] = af3_u32x4{o[4], o[5], o[6], o[7]};
-      } else {
-        *(af3_u32x4*)(p.c + grow * p.ldc + n0 + ch * 8) = v;
-      }
+      *(af3_u32x4*)(p.c + (row_lo + row) * p.ldc + n0 + ch * 8) = v;
     }
   }
 }

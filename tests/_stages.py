@@ -62,17 +62,36 @@ class LayerRun:
         m = workloads.make_experts(inp, dev)
         rd, gi, si = R.routing_replay(inp.logits.to(dev), inp.expt_indx.to(dev), inp.k)
         calls = []
-        x = inp.x.to(dev).requires_grad_(self.backward)
-        with recording(calls):
-            y = m(x, rd, gi, si)
-            if self.backward:
-                y.backward(inp.dy.to(dev))
+        lora_names = [n for n in ("gate_up_proj_lora_A", "gate_up_proj_lora_B", "down_proj_lora_A",
+                                  "down_proj_lora_B") if hasattr(m, n)]
+        # the recorded run keeps the SwiGLU backward a stage of its own (dI and
+        # its SwiGLU backward each checked against the oracle) ...
+        saved_bwd = Q.FUSED_SWIGLU_BWD
+        Q.FUSED_SWIGLU_BWD = False
+        try:
+            x = inp.x.to(dev).requires_grad_(self.backward)
+            with recording(calls):
+                y = m(x, rd, gi, si)
+                if self.backward:
+                    y.backward(inp.dy.to(dev))
+        finally:
+            Q.FUSED_SWIGLU_BWD = saved_bwd
         torch.cuda.synchronize()
         self.y = _cpu(y)
         self.dx = _cpu(x.grad) if self.backward else None
-        self.lora_grads = {n: _cpu(getattr(m, n).grad) for n in ("gate_up_proj_lora_A", "gate_up_proj_lora_B",
-                                                                  "down_proj_lora_A", "down_proj_lora_B")
-                           if hasattr(m, n)}
+        self.lora_grads = {n: _cpu(getattr(m, n).grad) for n in lora_names}
+        # ... and the module's default composition (the SwiGLU backward inside
+        # the down projection's dX epilogue) runs again on the same inputs
+        self.default = None
+        if self.backward:
+            for prm in m.parameters():
+                prm.grad = None
+            x2 = inp.x.to(dev).requires_grad_(True)
+            y2 = m(x2, rd, gi, si)
+            y2.backward(inp.dy.to(dev))
+            torch.cuda.synchronize()
+            self.default = dict(y=_cpu(y2), dx=_cpu(x2.grad), lora={n: _cpu(getattr(m, n).grad) for n in lora_names})
+            del x2, y2
         self.offs = _cpu(rd.expt_data.token_offs_raw).long()
         self.rt_gpu = dict(gate_scal=_cpu(rd.gate_scal), hist=_cpu(rd.expt_hist), topk_indx=_cpu(gi.src_indx),
                            gate_indx=_cpu(si.src_indx))

@@ -17,6 +17,11 @@ recorded inputs (tests/_stages.py; reference quantization.py:507-544,
 * the k-way combines: every token, bit-exact; idle experts' LoRA gradients
   exactly zero; every stage's output finite;
 * routing: indices bit-exact against the oracle's routing_replay.
+
+The recorded run keeps the SwiGLU backward a separate stage; the module's
+default composition (that backward inside the down projection's dX epilogue)
+runs again on the same inputs and must give the same output and gradients,
+bit for bit.
 """
 import pytest
 import torch
@@ -77,3 +82,14 @@ def test_lora_weight_grads_match_oracle(run):
     if not run.lora_grads or not run.backward:
         pytest.skip("configuration without expert-LoRA gradients")
     S.check_lora_wgrads(run, run.subset, f"cfg{run.cfg}")
+
+
+def test_default_composition_matches_staged_run(run):
+    """Output, input gradient and LoRA gradients of the module's default
+    composition equal the staged run's bit for bit."""
+    if run.default is None:
+        pytest.skip("forward-only configuration")
+    check_equal(run.default["y"], run.y, f"cfg{run.cfg} Y (default composition)")
+    check_equal(run.default["dx"], run.dx, f"cfg{run.cfg} dX (default composition)")
+    for n, g in run.lora_grads.items():
+        check_equal(run.default["lora"][n], g, f"cfg{run.cfg} {n} grad (default composition)")

@@ -172,12 +172,13 @@ def test_fused_swiglu_module_matches_unfused_chain(dev, lora):
     DequantMoEMatmul -> SwiGLUFunction -> DequantMoEMatmul chain."""
     inp = workloads.layer(4, T=1024, E=16, H=256, I=192, lora_r=16 if lora else 0, zipf=False)
     outs = []
+    saved = (Q.FUSED_SWIGLU, Q.FUSED_SWIGLU_BWD)
     for fused, fused_bwd in ((True, True), (True, False), (False, False)):
         Q.FUSED_SWIGLU, Q.FUSED_SWIGLU_BWD = fused, fused_bwd
         try:
             m, x, y = _run_module(inp, dev)
         finally:
-            Q.FUSED_SWIGLU, Q.FUSED_SWIGLU_BWD = True, False
+            Q.FUSED_SWIGLU, Q.FUSED_SWIGLU_BWD = saved
         grads = [x.grad] + ([getattr(m, n).grad for n in ("gate_up_proj_lora_A", "gate_up_proj_lora_B",
                                                         "down_proj_lora_A", "down_proj_lora_B")] if lora else [])
         outs.append((y.detach(), grads))
