@@ -27,6 +27,9 @@ def test_layer_inputs_small():
     assert int(inp.gu_scales.min()) >= 118 and int(inp.gu_scales.max()) <= 130
 
 
-def test_flops_match_survey():
+def test_cfg4_flops_closed_form():
+    """cfg4 work: the forward's 2 R H 2I + 2 R I H and the same again for
+    the input gradients (6.523 TFLOP in all), and 6 R r (K + N) per LoRA
+    projection (0.1812 TFLOP), R = 65,536 rows, H = I = 2880, r = 32."""
     f = workloads.layer_flops(16384, 4, lora_r=32)
     assert abs(f["base"] / 1e12 - 6.523) < 1e-3 and abs(f["lora"] / 1e12 - 0.1812) < 1e-3
