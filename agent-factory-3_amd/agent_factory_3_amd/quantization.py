@@ -62,7 +62,7 @@ GEMM_BLOCK_M = 128
 GEMM_TILE = {"block_m": 256, "tile_cfg": 0}
 
 # Optional launch timer for the grouped GEMM (set by benchmark harnesses):
-# callable(tag: str, flops: int) -> context manager wrapping the launch.
+# callable(tag: str, flops: int, detail: str) -> context manager wrapping the launch.
 KERNEL_TIMER = None
 
 FP4_VALUES = [
@@ -267,7 +267,8 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
     if KERNEL_TIMER is None:
         ok = launch()
     else:
-        with KERNEL_TIMER("moe_gemm_dgrad" if trans_w else "moe_gemm_fwd", 2 * R * N * (K + lr)):
+        detail = f"{'dX' if trans_w else 'fwd'} N={N} K={K}" + {0: "", 1: " +SwiGLU bwd", 2: " +SwiGLU fwd"}[epi]
+        with KERNEL_TIMER("moe_gemm_dgrad" if trans_w else "moe_gemm_fwd", 2 * R * N * (K + lr), detail):
             ok = launch()
     if not ok:
         return None

@@ -45,7 +45,7 @@ class EventTimer:
         self.on = False
 
     @contextmanager
-    def __call__(self, tag, work):
+    def __call__(self, tag, work, detail=None):
         if not self.on:
             yield
             return
@@ -54,12 +54,12 @@ class EventTimer:
         s.record()
         yield
         e.record()
-        self.recs.append((tag, work, s, e))
+        self.recs.append((tag, work, s, e, detail))
 
-    def summary(self):
+    def summary(self, by_detail=False):
         out = {}
-        for tag, work, s, e in self.recs:
-            d = out.setdefault(tag, {"n": 0, "ms": 0.0, "work": 0})
+        for tag, work, s, e, detail in self.recs:
+            d = out.setdefault(f"{tag}: {detail}" if by_detail else tag, {"n": 0, "ms": 0.0, "work": 0})
             d["n"] += 1
             d["ms"] += s.elapsed_time(e)
             d["work"] += work
@@ -512,8 +512,12 @@ def main():
         if durs:
             dom_kernel_us = sum(d["us_per_step"] for d in durs) / sum(d["calls_per_step"] for d in durs)
 
+    kd = timer.summary(by_detail=True)
     extra = {"gemm": {t: {"launches_per_step": v["n"] / args.steps, "avg_us": v["ms"] / v["n"] * 1e3,
                           "tflops": v["work"] / (v["ms"] * 1e-3) / 1e12} for t, v in ks.items()},
+             # per projection (N = output columns, K = reduction; "+SwiGLU" = that work in the launch's epilogue)
+             "gemm_launches": {t: {"launches_per_step": v["n"] / args.steps, "avg_us": v["ms"] / v["n"] * 1e3,
+                                   "tflops": v["work"] / (v["ms"] * 1e-3) / 1e12} for t, v in kd.items()},
              "gemm_ms_per_step": gemm_ms,
              "gemm_mfma_util": gemm_flops / (gemm_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
              "layer_tflops": flops["total"] / (ms_step * 1e-3) / 1e12,
@@ -583,7 +587,10 @@ def main():
         "roofline": {"bound": "mfma", "kernel": dom_tag, "achieved": achieved, "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS, "traffic": traffic,
                      "avg_launch_us": avg_ms * 1e3, "algorithmic_flops_per_launch": avg_flops,
-                     "kernel_avg_us_profiler": dom_kernel_us},
+                     "kernel_avg_us_profiler": dom_kernel_us,
+                     "note": ("achieved counts GEMM flops only; launches marked +SwiGLU in extra.gemm_launches "
+                              "also run the SwiGLU forward / backward (HBM work) in their epilogue")
+                     if any("SwiGLU" in t for t in kd if t.startswith(dom_tag + ":")) else None},
         "cpu_baseline": cpu,
         "extra": extra,
     }
