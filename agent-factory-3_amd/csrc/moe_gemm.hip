@@ -1327,10 +1327,10 @@ __device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f
   float* const al = gl + 256;  // per-row A scales
   auto coff = [&](int row, int col) { return row * RB + ((((col >> 3) ^ (((row >> 2) & 1) << 2))) << 4) + ((col & 7) << 1); };
   // SwiGLU backward (epi 1): the saved pre-activation of the lane's first NB
-  // output chunks is loaded before the staging below, the rest one batch at a
-  // time, so a work item waits on NI / NB loads in flight instead of one
-  // chunk group after another (addresses clamped to the tile's first valid
-  // row and column; those values are never used)
+  // output chunks is loaded before the staging below and the rest as one more
+  // batch, so a work item waits for NI / NB batches of loads instead of one
+  // small group after another (chunks past the tile load from its first row
+  // and column, valid addresses whose values are never used)
   constexpr int CH = CN / 8;              // 16-byte chunks per row
   constexpr int NI = RM * CH / 256;       // chunks per lane
   constexpr int NB = NI < 16 ? NI : 16;   // chunks per prefetch batch
