@@ -170,3 +170,46 @@ def test_fused_swiglu_epilogues_bit_equal(dev, lora):
     d_act = Q.moe_rows(dy, db, ds, None, rd, gi, gam, True, u, Ax)
     assert dgu is not None and dgu.shape == (Rr, 2 * I_)
     assert torch.equal(dgu, kernels.swiglu_backward_raw(d_act, gu, alpha, limit))
+
+
+# expert sizes whose last m-tile lands on every row-group variant of the
+# input-gradient kernel and its boundaries: tails of 225 (all 8 row groups),
+# 193 / 224 (7), 161 / 188 (6), 160 (5), and 47 / 64 (2 of 4) / 65 (4) rows
+# in the 128x512 item
+COUNTS_RG = [481, 449, 160, 161, 193, 224, 64, 65, 700, 303]
+
+
+@pytest.mark.parametrize("gather", [True, False])
+def test_dgrad_row_group_tails(dev, gather):
+    """gemm5's row-group variants (partial m-tiles run only their live 32-row
+    groups) against the oracle, LoRA segment and routing weights included."""
+    Ec = len(COUNTS_RG)
+    g = torch.Generator().manual_seed(21)
+    assert sum(COUNTS_RG) == T * TOPK and max(COUNTS_RG) <= T
+    order = sorted(range(Ec), key=lambda e: -COUNTS_RG[e])
+    multiset = [e for e in order for _ in range(COUNTS_RG[e])]
+    ids = torch.empty(T, TOPK, dtype=torch.int32)
+    for j, e in enumerate(multiset):
+        ids[j % T, j // T] = e
+    ids = ids[torch.randperm(T, generator=g)].sort(dim=1).values
+    logits = torch.randn(T, Ec, generator=g).to(torch.bfloat16)
+    ref = O.routing_replay(logits, ids, TOPK)
+    rd, gi, si = R.routing_replay(logits.to(dev), ids.to(dev), TOPK)
+    assert ref["hist"].tolist() == COUNTS_RG
+    G = NOUT // 32
+    blocks = torch.randint(0, 256, (Ec, KRED, G, 16), generator=g).to(torch.uint8)   # W [E, K, N] packed along N
+    scales = torch.randint(118, 125, (Ec, KRED, G), generator=g).to(torch.uint8)
+    Rr = T * TOPK
+    x = torch.randn(T if gather else Rr, KRED, generator=g).to(torch.bfloat16)
+    L = (torch.randn(Rr, 32, generator=g) * 0.3).to(torch.bfloat16)
+    Ax = (torch.randn(Ec, 32, NOUT, generator=g) * 0.3).to(torch.bfloat16)
+    gam = rd.gate_scal if gather else None
+    y = Q.moe_rows(x.to(dev), blocks.to(dev), scales.to(dev), None, rd, gi if gather else None, gam, True,
+                   L.to(dev), Ax.to(dev))
+    W = mxfp4.dequant_f32(blocks, scales)
+    yr = moe.rows(x, W, ref["offs"], ref["topk_indx"] if gather else None, TOPK,
+                  gammas=gam.cpu() if gather else None, trans=True, lora_l=L, lora_b=Ax)
+    a = y.float().cpu().double()
+    assert torch.isfinite(a).all()
+    bad = (a - yr.double()).abs() > ATOL + RTOL * yr.double().abs()
+    assert not bad.any(), float(bad.float().mean())
