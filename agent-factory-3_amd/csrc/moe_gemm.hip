@@ -352,11 +352,12 @@ struct Loader<TR, COLS_FP4, NT> {
 // ---------------------------------------------------------------------------
 template <int TM, int TN>
 __device__ __forceinline__ void mma_kstep(const uint16_t* As, const uint16_t* Bs, int wm0, int wn0,
-                                          af3_f32x16 acc[TM][TN]) {
+                                          af3_f32x16 acc[TM][TN], int nks = kBK / 16) {
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lk = lane >> 5;
 #pragma unroll
   for (int ks = 0; ks < kBK / 16; ++ks) {
+    if (ks >= nks) break;  // (wave-uniform) sub-steps past a short k segment hold only zero padding
     af3_bf16x8 af[TM], bf[TN];
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm)
@@ -1001,7 +1002,7 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
         la.store(As);
         lb.store(As + RM * kBK);
         __syncthreads();
-        mma_kstep<TM, TN>(As, As + RM * kBK, wm0, wn0, acc);
+        mma_kstep<TM, TN>(As, As + RM * kBK, wm0, wn0, acc, (min(kBK, p.kx - k0) + 15) / 16);
       }
     }
   }
@@ -1722,8 +1723,10 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
         la.store(As);
         lb.store(Bs);
         __syncthreads();
+        const int nks = (min(kBK, p.kx - k0) + 15) / 16;  // sub-steps past the rank hold only zero padding
 #pragma unroll
         for (int ks = 0; ks < kBK / 16; ++ks) {
+          if (ks >= nks) break;
           af3_bf16x8 af[TMW], bf[TN];
 #pragma unroll
           for (int tm = 0; tm < TMW; ++tm) af[tm] = *(const af3_bf16x8*)(As + lds_off(rb + tm * 32 + lr, ks * 2 + lh));
