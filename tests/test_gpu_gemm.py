@@ -101,9 +101,12 @@ def test_dgrad_transposed_weights(dev, gather):
 
 
 @pytest.mark.parametrize("trans", [False, True])
-def test_lora_extension_segment(dev, trans):
-    g, x, logits, blocks, scales, bias = _problem(H=128, N=192, seed=3)
-    K, r = 4, 16
+@pytest.mark.parametrize("r", [8, 16, 24, 40, 64])
+def test_lora_extension_segment(dev, trans, r):
+    """The rank-r segment after the main k-loop: ranks that end inside a
+    16-deep MFMA sub-step (8, 24, 40) and that fill the whole 64-deep step."""
+    g, x, logits, blocks, scales, bias = _problem(H=128, N=192, seed=3 + r)
+    K = 4
     ref, (rd, gi, si) = _route(logits, K, dev)
     E = blocks.shape[0]
     W = mxfp4.dequant_f32(blocks, scales)
