@@ -5,6 +5,7 @@ Command line (run from the repository root on the MI355X box)::
     python -m agent_factory_3_amd.profiling ktrace  <run>_kernel_trace.csv [<run>_marker_api_trace.csv RANGE]
     python -m agent_factory_3_amd.profiling traffic <fetch>_counter_collection.csv \\
                                                      <write>_counter_collection.csv
+    python -m agent_factory_3_amd.profiling mfma <run>_counter_collection.csv <run>_agent_info.csv
 
 ``ktrace`` turns a ``rocprofv3 --kernel-trace --output-format csv`` trace into
 a markdown table (one row per kernel name and grid size: calls, average /
@@ -19,6 +20,13 @@ HBM-side bytes per dispatch: each counter (KiB per dispatch) is scaled by
 the factor that makes the copy kernel's reading equal its known size.  The
 last line is a machine-readable JSON comment that ``bench.py`` reads for the
 ``roofline.traffic`` field.
+
+``mfma`` takes one ``rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES
+GRBM_GUI_ACTIVE`` collection and the run's agent info and reports, per kernel
+and grid, the share of the SIMDs' active cycles with the MFMA pipe busy:
+SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / XCDs x CUs x SIMDs per CU)
+(GRBM_GUI_ACTIVE comes summed over the XCDs), and the CUs' busy share
+SQ_BUSY_CU_CYCLES / (GRBM_GUI_ACTIVE / XCDs x CUs).
 """
 from __future__ import annotations
 
@@ -147,12 +155,40 @@ def read_traffic(md_path: str) -> dict | None:
     return json.loads(m.group(1)) if m else None
 
 
+def _gpu_agent(agent_csv: str) -> tuple[int, int, int]:
+    """(XCDs, CUs, SIMDs per CU) of the first GPU agent of a rocprofv3 agent-info CSV."""
+    for r in csv.DictReader(open(agent_csv)):
+        if r.get("Agent_Type", "").strip('"').upper() == "GPU":
+            return int(r["Num_Xcc"]), int(r["Cu_Count"]), int(r["Simd_Per_Cu"])
+    raise SystemExit("no GPU agent in the agent info")
+
+
+def mfma(counters_csv: str, agent_csv: str, kernels: tuple[str, ...] = ("gemm", "lug_", "lwg_", "lrows_")) -> str:
+    xcd, cus, simds = _gpu_agent(agent_csv)
+    busy = _counter_means(counters_csv, "SQ_VALU_MFMA_BUSY_CYCLES")
+    cu = _counter_means(counters_csv, "SQ_BUSY_CU_CYCLES")
+    gui = _counter_means(counters_csv, "GRBM_GUI_ACTIVE")
+    lines = [f"GPU: {xcd} XCDs, {cus} CUs, {simds} SIMDs per CU.", "",
+             "| kernel | grid | GUI-active cycles per XCD | MFMA busy share | CU busy share |",
+             "|---|---:|---:|---:|---:|"]
+    for k in sorted(set(busy) & set(gui), key=lambda k: -gui[k]):
+        if not any(n in k[0] for n in kernels) or gui[k] <= 0:
+            continue
+        g = gui[k] / xcd
+        cu_s = f"{cu[k] / (g * cus):.3f}" if k in cu else "-"
+        lines.append(f"| `{k[0]}` | {k[1]} | {g:.4g} | {busy[k] / (g * cus * simds):.3f} | {cu_s} |")
+    return "\n".join(lines)
+
+
 def main(argv: list[str]) -> int:
     if len(argv) in (2, 4) and argv[0] == "ktrace":
         print(ktrace(argv[1], marker_window(argv[2], argv[3]) if len(argv) == 4 else None))
         return 0
     if len(argv) >= 3 and argv[0] == "traffic":
         print(traffic(argv[1], argv[2]))
+        return 0
+    if len(argv) == 3 and argv[0] == "mfma":
+        print(mfma(argv[1], argv[2]))
         return 0
     print(__doc__, file=sys.stderr)
     return 2

@@ -56,3 +56,26 @@ def test_ktrace_window_and_entry_point_average(tmp_path):
     assert "| `gemm4_fwd_kernel<2, 4, 0>` | 64 | 1 | 2.00 |" in table
     assert "| moe_gemm_fwd | `gemm4_fwd_kernel` | 2 | 1.50 |" in table
     assert "| moe_gemm_fwd | `gemm4_fwd_kernel` | 4 | 5.25 |" in profiling.ktrace(str(kt))
+
+
+def test_mfma_busy_share_normalisation(tmp_path):
+    """GRBM_GUI_ACTIVE comes summed over the XCDs; the MFMA-busy counter over
+    every SIMD: a kernel whose MFMA pipes are busy half of the active cycles
+    on every SIMD reads 0.5."""
+    ag, pc = tmp_path / "agent.csv", tmp_path / "pmc.csv"
+    with open(ag, "w", newline="") as f:
+        w = csv.DictWriter(f, ["Agent_Type", "Num_Xcc", "Cu_Count", "Simd_Per_Cu"])
+        w.writeheader()
+        w.writerow({"Agent_Type": "CPU", "Num_Xcc": 1, "Cu_Count": 16, "Simd_Per_Cu": 0})
+        w.writerow({"Agent_Type": "GPU", "Num_Xcc": 8, "Cu_Count": 256, "Simd_Per_Cu": 4})
+    active = 1000.0  # cycles per XCD
+    with open(pc, "w", newline="") as f:
+        w = csv.DictWriter(f, ["Dispatch_Id", "Kernel_Name", "Grid_Size", "Counter_Name", "Counter_Value"])
+        w.writeheader()
+        for name, v in (("GRBM_GUI_ACTIVE", 8 * active), ("SQ_VALU_MFMA_BUSY_CYCLES", 0.5 * active * 256 * 4),
+                        ("SQ_BUSY_CU_CYCLES", 0.9 * active * 256)):
+            w.writerow({"Dispatch_Id": 1, "Kernel_Name": "void gemm4_fwd_kernel<2, 4, 0>(Params)",
+                        "Grid_Size": 512, "Counter_Name": name, "Counter_Value": v})
+    table = profiling.mfma(str(pc), str(ag))
+    assert "GPU: 8 XCDs, 256 CUs, 4 SIMDs per CU." in table
+    assert "| `gemm4_fwd_kernel<2, 4, 0>` | 512 | 1000 | 0.500 | 0.900 |" in table
