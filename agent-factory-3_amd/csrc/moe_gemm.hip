@@ -2237,7 +2237,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
     for (int j = 0; j < KU; ++j) r[j] = j < K ? src[t * K + j] : -1;
     af3_u32x4 x[KU];
 #pragma unroll
-    for (int j = 0; j < KU; ++j) x[j] = r[j] >= 0 ? *(const af3_u32x4*)(rows + (int64_t)r[j] * ld_rows + c) : zero4();
+    for (int j = 0; j < KU; ++j)
+      x[j] = r[j] >= 0 ? __builtin_nontemporal_load((const af3_u32x4*)(rows + (int64_t)r[j] * ld_rows + c)) : zero4();
 #pragma unroll
     for (int j = 0; j < KU; ++j)
       if (r[j] >= 0) add(x[j]);
@@ -2251,7 +2252,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   af3_u32x4 o;
 #pragma unroll
   for (int q = 0; q < 4; ++q) o[q] = af3_pack_bf16x2(acc[2 * q], acc[2 * q + 1]);
-  *(af3_u32x4*)(out + t * ld_out + c) = o;
+  __builtin_nontemporal_store(o, (af3_u32x4*)(out + t * ld_out + c));
 }
 
 Operand make_bf16(const uint16_t* ptr, int64_t ld, int64_t estride, const int32_t* gather, int gdiv,
