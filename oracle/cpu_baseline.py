@@ -9,9 +9,11 @@ autograd for the backward.  Test/bench infrastructure only.
 
 ``run_layer`` times the whole layer once, unscaled: every expert's weights
 dequantized for the forward, the per-expert loop (forward + autograd
-backward) over all routed rows, and every expert's weights dequantized again
-for the backward (DequantMoEMatmul re-derives them, quantization.py:364-373);
-a forward-only workload (no output gradient) runs the forward part alone.
+backward) over all routed rows with each token's k weighted rows added into
+the layer output and the rows' input gradients added into dX, and every
+expert's weights dequantized again for the backward (DequantMoEMatmul
+re-derives them, quantization.py:364-373); a forward-only workload (no output
+gradient) runs the forward part alone.
 ``run_dequant`` / ``run_swiglu`` time the standalone dequant (cfg0) and
 SwiGLU forward + backward (cfg1).
 ``run_sample`` times a bounded sample (the rows of a few experts, fwd + bwd,
@@ -63,22 +65,27 @@ def host_info() -> dict:
             "omp_num_threads": os.environ.get("OMP_NUM_THREADS"), "threads": threads()}
 
 
-def _expert_step(inp, e, W, ids, gam, s):
+def _expert_step(inp, e, W, ids, gam, s, acc):
     """Forward (+ autograd backward when the workload has an output gradient) of
-    expert e's routed rows; returns the row count."""
+    expert e's routed rows, combined into the layer's outputs the way
+    GptOssExperts.forward does (``next_states.index_add_`` of the weighted rows
+    in the activation dtype): ``acc["Y"]`` [T, H] bf16, and with a gradient
+    ``acc["dX"]`` [T, H] fp32 (the expert's input-row gradients added at their
+    tokens) and the expert's LoRA gradients in ``acc["lora"]``.  Returns the
+    row count."""
     lora = inp.lora
     tok, slot = torch.nonzero(ids == e, as_tuple=True)
     if tok.numel() == 0:
         return 0
+    Wgu, Wdn = W
     if inp.dy is None:
         with torch.no_grad():
-            Wgu, Wdn = W
             xe = inp.x[tok]
             act = _swiglu(xe @ Wgu.T + inp.gu_bias[e])
-            _ = (act @ Wdn.T + inp.dn_bias[e]) * gam[tok, slot, None]
+            y = (act @ Wdn.T + inp.dn_bias[e]) * gam[tok, slot, None]
+            acc["Y"].index_add_(0, tok, y.to(acc["Y"].dtype))
         return tok.numel()
     xe = inp.x[tok].clone().requires_grad_(True)
-    Wgu, Wdn = W
     gu = xe @ Wgu.T + inp.gu_bias[e]
     if lora:
         A, B = (lora["Agu"][e].clone().requires_grad_(True), lora["Bgu"][e].clone().requires_grad_(True))
@@ -89,7 +96,12 @@ def _expert_step(inp, e, W, ids, gam, s):
         A2, B2 = (lora["Adn"][e].clone().requires_grad_(True), lora["Bdn"][e].clone().requires_grad_(True))
         y = y + ((act @ A2.T) @ B2.T) * s
     y = y * gam[tok, slot, None]
+    acc["Y"].index_add_(0, tok, y.detach().to(acc["Y"].dtype))
     y.backward(inp.dy[tok])
+    acc["dX"].index_add_(0, tok, xe.grad.float())
+    if lora:
+        for name, t in (("Agu", A), ("Bgu", B), ("Adn", A2), ("Bdn", B2)):
+            acc["lora"][name][e] = t.grad
     return tok.numel()
 
 
@@ -104,12 +116,19 @@ def run_layer(inp, warmup: int = 1, runs: int = 1) -> dict:
     return out
 
 
-def _layer_once(inp) -> dict:
+def _layer_once(inp, keep: bool = False) -> dict:
+    """One timed pass over the whole layer.  ``keep``: also return the layer's
+    outputs (Y, and with a gradient dX and the LoRA gradients) for checking."""
     E = inp.gu_blocks.shape[0]
     ids = inp.expt_indx.long()
     T = inp.x.shape[0]
     gam = torch.softmax(torch.take_along_dim(inp.logits, ids, 1), dim=-1)
     s = (inp.lora["alpha"] / inp.lora["r"]) if inp.lora else 0.0
+    acc = {"Y": torch.zeros_like(inp.x)}
+    if inp.dy is not None:
+        acc["dX"] = torch.zeros(inp.x.shape, dtype=torch.float32)
+        if inp.lora:
+            acc["lora"] = {k: torch.zeros_like(inp.lora[k]) for k in ("Agu", "Bgu", "Adn", "Bdn")}
 
     def dequant_all():
         return [(_mx.dequant_lut_ldexp(inp.gu_blocks[e], inp.gu_scales[e]),
@@ -118,7 +137,8 @@ def _layer_once(inp) -> dict:
     t0 = time.perf_counter()
     W = dequant_all()
     t1 = time.perf_counter()
-    rows = sum(_expert_step(inp, e, W[e], ids, gam, s) for e in range(E))
+    rows = sum(_expert_step(inp, e, W[e], ids, gam, s, acc) for e in range(E))
+    dX = acc["dX"].to(inp.x.dtype) if "dX" in acc else None
     t2 = time.perf_counter()
     del W
     if inp.dy is not None:
@@ -128,9 +148,12 @@ def _layer_once(inp) -> dict:
     t_layer = t3 - t0
     t_deq = (t1 - t0) + (t3 - t2)
     n_deq = 2 * E if inp.dy is not None else E
-    return dict(tokens_per_s=T / t_layer, t_layer_s=t_layer, dequant_s=t_deq, dequant_s_per_expert=t_deq / n_deq,
-                loop_s=t2 - t1, loop_s_per_row=(t2 - t1) / max(1, rows), rows=rows,
-                threads_used=torch.get_num_threads())
+    out = dict(tokens_per_s=T / t_layer, t_layer_s=t_layer, dequant_s=t_deq, dequant_s_per_expert=t_deq / n_deq,
+               loop_s=t2 - t1, loop_s_per_row=(t2 - t1) / max(1, rows), rows=rows,
+               threads_used=torch.get_num_threads())
+    if keep:
+        out["outputs"] = dict(Y=acc["Y"], dX=dX, lora=acc.get("lora"))
+    return out
 
 
 def _median_time(fn, warmup=1, runs=3) -> float:

@@ -46,27 +46,63 @@ def combined_slack(rows, gate_indx, k):
     return 2.0 ** -7 * out
 
 
+def _lowp(t) -> bool:
+    return t.dtype in (torch.bfloat16, torch.float16)
+
+
 def check_close(got, ref, *, rtol=RTOL, atol=ATOL, mag=None, n=None, extra=None, what=""):
     """Assert |got - ref| <= atol + rtol*|ref| (+ the accumulation allowance for
     n-term sums of magnitude ``mag``) (+ ``extra``, a derived per-element or
-    scalar slack) for every element."""
-    g = got.detach().to("cpu", torch.float64)
-    r = ref.detach().to("cpu", torch.float64)
-    assert g.shape == r.shape, f"{what}: shape {tuple(g.shape)} != {tuple(r.shape)}"
-    assert torch.isfinite(g).all(), f"{what}: non-finite values"
-    tol = atol + rtol * r.abs()
-    if mag is not None:
-        tol = tol + accum_allowance(mag, n)
-    if extra is not None:
-        tol = tol + (extra.to(torch.float64) if isinstance(extra, torch.Tensor) else float(extra))
-    err = (g - r).abs()
-    bad = err > tol
-    if bool(bad.any()):
-        idx = bad.nonzero()[:5].tolist()
-        ex = [(i, float(g[tuple(i)]), float(r[tuple(i)]), float(tol[tuple(i)])) for i in idx]
-        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.numel()} elements outside tolerance; "
-                             f"(index, got, ref, tol) {ex}")
-    return float((err / tol).max()) if err.numel() else 0.0
+    scalar slack) for every element.  Returns the largest error / tolerance.
+
+    When both sides are 16-bit floats the comparison runs in float32, chunk by
+    chunk: the difference of two bf16 values is exact in float32 unless their
+    exponents are more than 16 apart (then it is within 2^-24 of the larger),
+    and the tolerance only needs a few significant bits."""
+    g0, r0 = got.detach().cpu(), ref.detach().cpu()
+    assert g0.shape == r0.shape, f"{what}: shape {tuple(g0.shape)} != {tuple(r0.shape)}"
+    wd = torch.float32 if _lowp(g0) and _lowp(r0) else torch.float64
+    if g0.dim() == 0 or g0.numel() == 0:
+        g0, r0 = g0.reshape(-1), r0.reshape(-1)
+    ex = extra.detach().cpu() if isinstance(extra, torch.Tensor) else extra
+    mg = mag.detach().cpu() if mag is not None else None
+    c = 2.0 * math.sqrt(max(n or 1, 1)) * U32
+    rows = g0.shape[0]
+    per_row = max(1, g0[0].numel()) if rows else 1
+    step = max(1, (1 << 24) // per_row)
+    worst, n_bad, first = 0.0, 0, []
+
+    def part(t, lo, hi):
+        if not isinstance(t, torch.Tensor):
+            return t
+        if t.dim() == g0.dim() and t.shape[0] == rows and rows > 1:
+            return t[lo:hi]
+        return t
+
+    for lo in range(0, rows, step):
+        hi = min(rows, lo + step)
+        g = g0[lo:hi].to(wd)
+        r = r0[lo:hi].to(wd)
+        assert torch.isfinite(g).all(), f"{what}: non-finite values"
+        err = (g - r).abs_()
+        tol = r.abs().mul_(rtol).add_(atol)
+        if mg is not None:
+            tol.add_(part(mg, lo, hi).to(wd), alpha=c)
+        if ex is not None:
+            e = part(ex, lo, hi)
+            tol.add_(e.to(wd) if isinstance(e, torch.Tensor) else float(e))
+        bad = err > tol
+        if bool(bad.any()):
+            n_bad += int(bad.sum())
+            for i in bad.nonzero()[:5 - len(first)].tolist():
+                i = tuple(i)
+                first.append(((lo + i[0],) + i[1:], float(g[i]), float(r[i]), float(tol[i])))
+        if err.numel():
+            worst = max(worst, float((err / tol).max()))
+    if n_bad:
+        raise AssertionError(f"{what}: {n_bad} of {g0.numel()} elements outside tolerance; "
+                             f"(index, got, ref, tol) {first}")
+    return worst
 
 
 def check_equal(got, ref, what=""):

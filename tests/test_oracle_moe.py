@@ -203,3 +203,120 @@ def test_gate_scal_backward_is_the_softmax_backward():
     gs = R._GateScal.apply(lg2, gs_ref.detach().float(), topk.to(torch.int32), hist, K)
     (gs.double() * w).sum().backward()
     assert torch.allclose(lg2.grad, lg.grad, rtol=1e-5, atol=1e-6)
+
+
+# --- the per-expert helpers the full-size GPU checks call (tests/_stages.py) ---
+# Each is pinned twice: bit for bit against the expert's slice of the whole-layer
+# function it restates (rows / lora_rows / wgrad, pinned above by float64
+# autograd of the dense layer), and directly against float64 sums of the same
+# bf16 inputs (one bf16 rounding plus the fp32 accumulation allowance).
+
+import pytest  # noqa: E402
+
+from tests._tol import check_close, check_equal  # noqa: E402
+
+
+def _expert_case(seed=12, T=50, K=96, N=72, E=4, k=2, r=8):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(T, K, generator=g).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)])
+    rt = routing.routing_replay(torch.randn(T, E, generator=g).to(torch.bfloat16), ids, k)
+    offs = rt["offs"].long()
+    assert int((offs[1:] - offs[:-1]).min()) > 0      # every expert live
+    W = mxfp4.dequant_f32(torch.randint(0, 256, (E, N, K // 32, 16), generator=g, dtype=torch.uint8),
+                          torch.randint(120, 126, (E, N, K // 32), generator=g, dtype=torch.uint8))
+    return g, x, rt, offs, W
+
+
+def _src(rt, offs, e, k, gathered):
+    lo, hi = int(offs[e]), int(offs[e + 1])
+    return lo, hi, (rt["topk_indx"][lo:hi].long() // k) if gathered else torch.arange(lo, hi)
+
+
+@pytest.mark.parametrize("trans", [False, True])
+@pytest.mark.parametrize("gathered", [False, True])
+def test_expert_rows_is_the_expert_slice_of_rows(trans, gathered):
+    g, x, rt, offs, W = _expert_case()
+    k = 2
+    R = rt["topk_indx"].numel()
+    Wt = W if not trans else W[:, :, :72]                        # trans: y = x W[e], W [E, N, K'] with N = K_x
+    xin = x if gathered else torch.randn(R, 96, generator=g).to(torch.bfloat16)
+    if trans:
+        xin = xin[:, :72].contiguous()
+    bias = (torch.randn(W.shape[0], Wt.shape[2] if trans else Wt.shape[1], generator=g) * 0.1).to(torch.bfloat16)
+    gam = torch.rand(R, generator=g).to(torch.bfloat16)
+    gi = rt["topk_indx"] if gathered else None
+    whole = moe.rows(xin, Wt, offs, gi, k, bias=bias, gammas=gam, trans=trans)
+    for e in range(W.shape[0]):
+        lo, hi, idx = _src(rt, offs, e, k, gathered)
+        got, mag = moe.expert_rows(xin, Wt[e], idx, trans=trans, bias=bias[e], gammas=gam[lo:hi])
+        check_equal(got, whole[lo:hi], f"expert_rows e{e}")
+        xe = xin[idx].double()
+        We = Wt[e].double()
+        exact = ((xe @ (We if trans else We.T)) + bias[e].double()) * gam[lo:hi].double()[:, None]
+        n = xin.shape[1]
+        check_close(got, exact, rtol=2 ** -8, atol=0.0, mag=mag, n=n, what=f"expert_rows vs float64 e{e}")
+        mag64 = (xe.abs() @ (We.abs() if trans else We.abs().T)) * gam[lo:hi].double().abs()[:, None]
+        assert torch.allclose(mag.double(), mag64, rtol=1e-5, atol=0)
+
+
+@pytest.mark.parametrize("trans", [False, True])
+@pytest.mark.parametrize("gathered", [False, True])
+def test_expert_lora_rows_is_the_expert_slice_of_lora_rows(trans, gathered):
+    g, x, rt, offs, _ = _expert_case()
+    k, r, E, s = 2, 8, 4, 1.75
+    R = rt["topk_indx"].numel()
+    xin = x if gathered else torch.randn(R, 96, generator=g).to(torch.bfloat16)
+    Wl = (torch.randn(E, 96, r, generator=g) if trans else torch.randn(E, r, 96, generator=g)).to(torch.bfloat16)
+    gi = rt["topk_indx"] if gathered else None
+    whole = moe.lora_rows(xin, Wl, offs, gi, k, s, trans=trans)
+    for e in range(E):
+        lo, hi, idx = _src(rt, offs, e, k, gathered)
+        got, mag = moe.expert_lora_rows(xin, Wl[e], idx, s, trans=trans)
+        assert got.shape == (hi - lo, r)
+        check_equal(got, whole[lo:hi], f"expert_lora_rows e{e}")
+        xe, We = xin[idx].double(), Wl[e].double()
+        exact = s * (xe @ (We if trans else We.T))
+        check_close(got, exact, rtol=2 ** -8, atol=0.0, mag=mag, n=96, what=f"expert_lora_rows vs float64 e{e}")
+        mag64 = abs(s) * (xe.abs() @ (We.abs() if trans else We.abs().T))
+        assert torch.allclose(mag.double(), mag64, rtol=1e-5, atol=0)
+
+
+@pytest.mark.parametrize("rowscale", [False, True])
+@pytest.mark.parametrize("gathered", [False, True])
+def test_expert_wgrad_is_the_expert_slice_of_wgrad(rowscale, gathered):
+    g, x, rt, offs, _ = _expert_case()
+    k, E, r = 2, 4, 8
+    R = rt["topk_indx"].numel()
+    a = torch.randn(R, r, generator=g).to(torch.bfloat16)                   # the rank side, sorted rows
+    b = x if gathered else torch.randn(R, 96, generator=g).to(torch.bfloat16)
+    rs = torch.rand(R, generator=g).add(0.1).to(torch.bfloat16) if rowscale else None
+    gi = rt["topk_indx"] if gathered else None
+    whole = moe.wgrad(a, b, offs, a_rowscale=rs, b_gather=gi, b_div=k)
+    for e in range(E):
+        lo, hi, ib = _src(rt, offs, e, k, gathered)
+        got, mag = moe.expert_wgrad(a[lo:hi], b[ib], None if rs is None else rs[lo:hi])
+        check_equal(got, whole[e], f"expert_wgrad e{e}")
+        ae = a[lo:hi].double()
+        if rs is not None:   # the row-scaled operand is rounded to bf16 (autograd of a bf16 multiply)
+            ae = (a[lo:hi].float() * rs[lo:hi].float()[:, None]).to(torch.bfloat16).double()
+        exact = ae.T @ b[ib].double()
+        check_close(got, exact, rtol=2 ** -8, atol=0.0, mag=mag, n=hi - lo, what=f"expert_wgrad vs float64 e{e}")
+    # the a-side gather form of wgrad (dB of the down projection) is the same sum
+    whole_a = moe.wgrad(b, a, offs, a_gather=gi, a_div=k, a_rowscale=rs)
+    for e in range(E):
+        lo, hi, ia = _src(rt, offs, e, k, gathered)
+        got, _ = moe.expert_wgrad(b[ia], a[lo:hi], None if rs is None else rs[lo:hi])
+        check_equal(got, whole_a[e], f"expert_wgrad (a gathered) e{e}")
+
+
+def test_expert_helpers_reject_a_planted_transpose():
+    """A transposed weight (the kind of mistake a GEMM's operand layout makes)
+    fails the float64 check the helpers are held to."""
+    g, x, rt, offs, _ = _expert_case()
+    Wl = torch.randn(4, 96, 96, generator=g).to(torch.bfloat16)
+    idx = torch.arange(0, 20)
+    got, mag = moe.expert_lora_rows(x, Wl[0].T.contiguous(), idx, 1.0)
+    exact = x[idx].double() @ Wl[0].double().T
+    with pytest.raises(AssertionError):
+        check_close(got, exact, rtol=2 ** -8, atol=0.0, mag=mag, n=96, what="planted transpose")
