@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede the library load: shared HIP runtime)
 
 _LIB_PATH = Path(__file__).resolve().parent / "libaf3_mi355x.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _p = C.c_void_p
 _i32 = C.c_int

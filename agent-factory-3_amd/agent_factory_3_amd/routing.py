@@ -285,6 +285,23 @@ class RouterLinear(torch.autograd.Function):
         return dh, dw, db
 
 
+def router_kernel_supports(hidden: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> bool:
+    """Whether af3_router_logits takes these operands: GPU tensors, all bf16,
+    hidden [T, H] / weight [E, H] with H % 64 == 0 and E <= 256."""
+    ts = (hidden, weight) + ((bias,) if bias is not None else ())
+    return (all(t.is_cuda and t.dtype == torch.bfloat16 for t in ts) and hidden.dim() == 2 and weight.dim() == 2
+            and weight.shape[1] == hidden.shape[1] and hidden.shape[1] % 64 == 0 and 0 < weight.shape[0] <= 256
+            and (bias is None or bias.shape == (weight.shape[0],)))
+
+
 def router_linear(hidden: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
-    """The router's nn.functional.linear on the HIP kernel (autograd-aware)."""
+    """The router's nn.functional.linear (quantization.py:654), on the HIP
+    kernel (autograd-aware) for the operands it takes (gpt-oss: bf16, H = 2880,
+    E = 32 / 128).  Other GPU operands (another dtype, H % 64 != 0, E > 256)
+    go to nn.functional.linear as in the reference, so such a router still
+    works; CPU operands raise, as the expert layer after it needs the GPU."""
+    if not hidden.is_cuda:
+        raise RuntimeError("router_logits: hidden must be a GPU tensor (no CPU implementation)")
+    if not router_kernel_supports(hidden, weight, bias):
+        return torch.nn.functional.linear(hidden, weight, bias)
     return RouterLinear.apply(hidden, weight, bias)

@@ -10,7 +10,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#define AF3_ABI_VERSION 1
+#define AF3_ABI_VERSION 2
 
 // ---------------------------------------------------------------------------
 // error reporting (host side)

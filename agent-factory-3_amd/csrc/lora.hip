@@ -665,11 +665,18 @@ __global__ __launch_bounds__(256, kLuMinBlocks) void lug_kernel(LuParams p) {
       }
 }
 
-// u[i][n] = bf16(scale * sum_g u_part[g][i][n]), groups in order
+// u[i][n] = bf16(scale * sum_g u_part[g][i][n]), groups in order, for the
+// routed rows i < offs[E]; rows past them (entries dropped for an expert id
+// outside [0, E)) have no partials and are written as zeros
 __global__ __launch_bounds__(256) void lu_sum_kernel(const float* __restrict__ u_part, int64_t n_elems, int ngrp,
-                                                     float scale, uint16_t* __restrict__ u) {
+                                                     const int32_t* __restrict__ offs, int E, int r, float scale,
+                                                     uint16_t* __restrict__ u) {
   const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (i >= n_elems) return;
+  if (i >= (int64_t)offs[E] * r) {  // r % 4 == 0: the 4 elements lie in one row
+    *(uint2*)(u + i) = uint2{0u, 0u};
+    return;
+  }
   float4 a = *(const float4*)(u_part + i);
   for (int g = 1; g < ngrp; ++g) {
     const float4 v = *(const float4*)(u_part + (int64_t)g * n_elems + i);
@@ -823,7 +830,7 @@ extern "C" int af3_lora_u_wgrad(const uint16_t* big, int64_t ld_big, const int32
     if (rc) return rc;
     const int64_t nu = n_rows * r;  // multiple of 16
     hipLaunchKernelGGL(lu_sum_kernel, dim3((unsigned)af3_cdiv(nu / 4, 256)), dim3(256), 0, stream, p.u_part, nu,
-                       p.ngrp, scale_u, u);
+                       p.ngrp, token_offs, n_expts, r, scale_u, u);
     rc = af3::check_launch("lora_u_wgrad/u");
     if (rc) return rc;
   }

@@ -329,13 +329,16 @@ __global__ __launch_bounds__(1024) void tile_order_kernel(const int32_t* __restr
   for (int i = 0; i < per; ++i) {
     const int e = t * per + i;
     if (e >= E) break;
-    for (int b = 0; b < nfull[e]; ++b) order[pos + b] = (b << 16) | e;
+    // (a max_tiles below the real tile count truncates the order instead of
+    // writing past it)
+    for (int b = 0; b < nfull[e]; ++b)
+      if (pos + b < max_tiles) order[pos + b] = (b << 16) | e;
     pos += nfull[e];
     const int s = tail[e];
     if (s) {
       int rank = start[s];
       for (int f = 0; f < e; ++f) rank += tail[f] == s;
-      order[total_full + rank] = (nfull[e] << 16) | e;
+      if (total_full + rank < max_tiles) order[total_full + rank] = (nfull[e] << 16) | e;
     }
   }
   for (int i = n_tiles + t; i < max_tiles; i += 1024) order[i] = -1;
@@ -450,28 +453,46 @@ extern "C" int af3_routing_replay_noalloc(const uint16_t* logits, int64_t ld_log
               "routing_replay_noalloc: T=%lld E=%d K=%d needs %zu scratch bytes, the built-in buffer holds %zu "
               "(use af3_routing_replay with a workspace)",
               (long long)n_tokens, n_expts_tot, n_expts_act, need, kRoutingScratchBytes);
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
+  // the array of the device the stream belongs to (the null stream: the
+  // current device), taken with that device current
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
   if (e != hipSuccess) {
     af3::set_error("routing_replay_noalloc: hipGetDevice: %s", hipGetErrorString(e));
     return (int)e;
   }
-  AF3_REQUIRE(dev >= 0 && dev < kMaxDevices, "routing_replay_noalloc: device %d out of range", dev);
+  hipDevice_t dev = cur;
+  if (stream) {
+    e = hipStreamGetDevice((hipStream_t)stream, &dev);
+    if (e != hipSuccess) {
+      af3::set_error("routing_replay_noalloc: hipStreamGetDevice: %s", hipGetErrorString(e));
+      return (int)e;
+    }
+  }
+  AF3_REQUIRE(dev >= 0 && dev < kMaxDevices, "routing_replay_noalloc: device %d out of range", (int)dev);
+  if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) {
+    af3::set_error("routing_replay_noalloc: hipSetDevice(%d): %s", (int)dev, hipGetErrorString(e));
+    return (int)e;
+  }
   void* ws = nullptr;
   {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_ptr[dev]) {  // first call on this device: its copy of the array
       e = hipGetSymbolAddress(&g_scratch_ptr[dev], HIP_SYMBOL(scratch));
-      if (e != hipSuccess) {
-        g_scratch_ptr[dev] = nullptr;
-        af3::set_error("routing_replay_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
-        return (int)e;
-      }
+      if (e != hipSuccess) g_scratch_ptr[dev] = nullptr;
     }
     ws = g_scratch_ptr[dev];
   }
-  return routing_common(false, logits, ld_logits, expt_indx, n_tokens, n_expts_tot, n_expts_act, gate_scal, hist,
+  int rc = 0;
+  if (!ws) {
+    af3::set_error("routing_replay_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+    rc = (int)e;
+  } else {
+    rc = routing_common(false, logits, ld_logits, expt_indx, n_tokens, n_expts_tot, n_expts_act, gate_scal, hist,
                         topk_indx, gate_indx, token_offs_raw, ws, kRoutingScratchBytes, (hipStream_t)stream);
+  }
+  if (dev != cur) hipSetDevice(cur);  // the caller's current device, as it was
+  return rc;
 }
 
 extern "C" int af3_routing_topk(const uint16_t* logits, int64_t ld_logits, int64_t n_tokens, int n_expts_tot,

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-/* ABI version (1). */
+/* ABI version (2: af3_moe_gemm_f8 takes trans_w after w_scales; 1 had no trans_w). */
 int af3_abi_version(void);
 
 /* Message of the last failing call on this host thread. */
@@ -115,7 +115,9 @@ int af3_expt_data(const int32_t* hist, int n_expts_tot, const int32_t* block_ms_
  * each expert's partial last tile follows by decreasing row count, -1 past
  * the tile count.  No counterpart in the reference (its block_pid_map,
  * compute_expt_data_torch, is in expert order and that order is kept there);
- * the grouped GEMM takes either map.  n_expts_tot <= 4096, block_m <= 512. */
+ * the grouped GEMM takes either map.  n_expts_tot <= 4096, block_m <= 512.
+ * max_tiles should be >= sum_e ceil(hist[e] / block_m); a smaller one gives a
+ * truncated order (no write past order[max_tiles - 1]). */
 int af3_tile_order(const int32_t* hist, int n_expts_tot, int block_m, const int32_t* token_offs_pad, int max_tiles,
                    int32_t* order, void* stream);
 
@@ -248,6 +250,8 @@ int af3_lora_wgrad(const uint16_t* a, int64_t lda, const int32_t* a_gather, int 
  * Small [n_rows][r] bf16 compact, Bl [E][W][r], u [n_rows][r], G [E][W][r];
  * r = 16 or 32, W % 8 == 0.  Chunking and the fp32 partial sums follow
  * af3_lora_wgrad; the workspace also holds u's per-column-group partial sums.
+ * Rows of u at or past token_offs[n_expts] (entries dropped for an expert id
+ * outside [0, E)) are written as zeros.
  * Returns AF3_EUNSUPPORTED (nothing launched) for shapes it does not cover. */
 size_t af3_lora_u_wgrad_workspace_bytes(int max_chunks, int64_t n_rows, int W, int r);
 int af3_lora_u_wgrad(const uint16_t* big, int64_t ld_big, const int32_t* big_gather, int big_div,

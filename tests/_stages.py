@@ -128,19 +128,6 @@ class LayerRun:
         self.all_experts = [e for e in range(self.hist.numel()) if int(self.hist[e]) > 0]
         self._wcache = {}
 
-    def pick_subset(self):
-        """The largest, a mid-size, a one-tile (129-256 rows), a <=128-row and the smallest live expert."""
-        order = torch.argsort(self.hist, descending=True, stable=True).tolist()
-        live = [e for e in order if int(self.hist[e]) > 0]
-        pick = [live[0], live[len(live) // 2], live[-1]]
-        one_tile = [e for e in live if 128 < int(self.hist[e]) <= 256]
-        small = [e for e in live if int(self.hist[e]) <= 128]
-        if one_tile:
-            pick.append(one_tile[0])
-        if small:
-            pick.append(small[len(small) // 2])
-        return sorted(set(pick))
-
     def W(self, proj, e):
         key = (proj, e)
         if key not in self._wcache:
@@ -175,16 +162,18 @@ def check_call_structure(run):
 
 
 def check_gemm_rows(run, experts, tag=""):
-    """Every grouped-GEMM launch: the rows of ``experts`` vs oracle rows on the same inputs."""
+    """Every grouped-GEMM launch: the rows of ``experts`` vs oracle rows on the same inputs.
+    Experts outer, launches inner, so only one expert's dequantised weights are held at a time."""
+    launches = run.of("moe_rows")
     checked = 0
-    for a, out in run.of("moe_rows"):
-        y = out[0] if isinstance(out, tuple) else out
-        trans = bool(a["trans_w"])
-        k_div = a["n_expts_act"] if a["gather_indx"] is not None else 1
-        L, B = a["lora_l"], a["lora_b"]
-        n_red = a["x"].shape[1] + (L.shape[1] if L is not None else 0)
-        for e in experts:
-            lo, hi = run.rows(e)
+    for e in experts:
+        lo, hi = run.rows(e)
+        for a, out in launches:
+            y = out[0] if isinstance(out, tuple) else out
+            trans = bool(a["trans_w"])
+            k_div = a["n_expts_act"] if a["gather_indx"] is not None else 1
+            L, B = a["lora_l"], a["lora_b"]
+            n_red = a["x"].shape[1] + (L.shape[1] if L is not None else 0)
             idx = _src_rows(a["gather_indx"], k_div, lo, hi)
             ref, mag = moe.expert_rows(a["x"], run.W(a["proj"], e), idx, trans=trans,
                                        lora_l=None if L is None else L[lo:hi], lora_b=None if B is None else B[e],
@@ -193,6 +182,9 @@ def check_gemm_rows(run, experts, tag=""):
             check_close(y[lo:hi], ref, mag=mag, n=n_red,
                         what=f"{tag} {a['proj']} trans={trans} expert {e} ({hi - lo} rows)")
             checked += hi - lo
+        run._wcache.clear()
+    for a, out in launches:
+        y = out[0] if isinstance(out, tuple) else out
         assert torch.isfinite(y.float()).all()
     return checked
 

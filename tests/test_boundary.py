@@ -90,3 +90,17 @@ def test_replace_and_routing_replay_plumbing():
     layer(h, routing_indices=ri)
     assert torch.equal(seen[layer.mlp], ri[:, :, 1, :])
     assert routing_replay.current_router_indices(layer.mlp) is None  # cleared after the layer call
+
+
+def test_router_kernel_predicate_on_cpu_tensors():
+    """The router kernel's operand check (routing.router_kernel_supports): CPU
+    tensors never qualify; router_linear refuses them."""
+    import pytest
+    import torch
+
+    from agent_factory_3_amd import routing as R
+    x = torch.zeros(4, 128, dtype=torch.bfloat16)
+    w = torch.zeros(8, 128, dtype=torch.bfloat16)
+    assert not R.router_kernel_supports(x, w, None)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        R.router_linear(x, w, None)

@@ -9,10 +9,10 @@ recorded inputs (tests/_stages.py; reference quantization.py:507-544,
 376-421, 442-444):
 
 * grouped-GEMM rows (gate_up, down and both input gradients), the LoRA row
-  products and the LoRA weight gradients: every row / gradient of an expert
-  subset (the largest expert, a mid-size one, a one-tile expert of 129-256
-  rows, an expert of at most 128 rows, the smallest), element-wise at rtol
-  2e-2 / atol 1e-2 plus the fp32 accumulation allowance of tests/_tol.py;
+  products and the LoRA weight gradients: every row and gradient of every
+  live expert (cfg4: 120 experts from the 14,924-row expert down to
+  single-digit ones), element-wise at rtol 2e-2 / atol 1e-2 plus the fp32
+  accumulation allowance of tests/_tol.py;
 * SwiGLU forward / backward: every row, element-wise;
 * the k-way combines: every token, bit-exact; idle experts' LoRA gradients
   exactly zero; every stage's output finite;
@@ -31,7 +31,7 @@ from oracle import routing as O
 from tests import _stages as S
 from tests._tol import check_close, check_equal
 
-pytestmark = [pytest.mark.gpu, pytest.mark.timeout(300)]
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(600)]
 
 
 @pytest.fixture(scope="module", params=[2, 3, 4], ids=lambda c: f"cfg{c}")
@@ -39,7 +39,6 @@ def run(request, dev):
     cfg = request.param
     r = S.LayerRun(workloads.layer(cfg), dev)
     r.cfg = cfg
-    r.subset = r.pick_subset()
     yield r
 
 
@@ -61,7 +60,8 @@ def test_stage_calls_cover_the_layer(run):
 
 
 def test_gemm_rows_match_oracle(run):
-    assert S.check_gemm_rows(run, run.subset, f"cfg{run.cfg}") > 0
+    n_launch = len(run.of("moe_rows"))
+    assert S.check_gemm_rows(run, run.all_experts, f"cfg{run.cfg}") == n_launch * int(run.offs[-1])
 
 
 def test_swiglu_stages_match_oracle(run):
@@ -75,13 +75,13 @@ def test_combines_exact(run):
 def test_lora_rows_match_oracle(run):
     if not run.lora_grads:
         pytest.skip("configuration without expert LoRA")
-    S.check_lora_rows(run, run.subset, f"cfg{run.cfg}")
+    S.check_lora_rows(run, run.all_experts, f"cfg{run.cfg}")
 
 
 def test_lora_weight_grads_match_oracle(run):
     if not run.lora_grads or not run.backward:
         pytest.skip("configuration without expert-LoRA gradients")
-    S.check_lora_wgrads(run, run.subset, f"cfg{run.cfg}")
+    S.check_lora_wgrads(run, run.all_experts, f"cfg{run.cfg}")
 
 
 def test_default_composition_matches_staged_run(run):

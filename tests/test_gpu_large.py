@@ -1,0 +1,244 @@
+"""Past 2^31 bytes and 2^31 elements: the reference's packing budget.
+
+The reference packs up to max_capacity = 128,000 tokens per micro-batch
+(examples/wordle/train.py:163) and its kernels take int64 offsets for tensors
+over 2 GB (kernels.py:7,278,427).  At T = 128,000 and top-4 (R = 512,000
+expert-sorted rows) the gate_up rows and their gradient [R, 5760] bf16 hold
+2.95e9 elements (5.9 GB): they pass 2^31 bytes at row 186,414 and 2^31
+elements at row 372,828; the [R, 2880] tensors (SwiGLU output, down rows,
+their input gradient, the gate_up input-gradient rows) pass 2^31 bytes at row
+372,828.  The expert module (8 experts, expert LoRA r = 16) runs forward and
+backward through the drop-in API with every HIP stage recorded; the rows in
+windows at the start, at both boundaries and at the end are checked against
+the oracle on the stage's own inputs (grouped-GEMM rows of all four launches,
+the fused SwiGLU forward, the SwiGLU backward, LoRA rows), the k-way combines
+bit-exact on the tokens that own those rows plus a random sample, and the
+LoRA weight gradients of the experts whose rows straddle the boundaries.  The
+module's default composition (SwiGLU backward inside the down input-gradient
+epilogue) must give the same dX and LoRA gradients bit for bit.
+
+Also the standalone dequant of a 130-expert gate_up stack (4.31 GB of bf16
+output, 2.16e9 elements) with whole experts checked on both sides of the
+2^31-byte and 2^31-element boundaries.
+"""
+import numpy as np
+import pytest
+import torch
+
+from agent_factory_3_amd import kernels
+from agent_factory_3_amd import quantization as Q
+from agent_factory_3_amd import routing as R
+from agent_factory_3_amd import workloads
+from oracle import moe, mxfp4, swiglu
+from tests._stages import recording
+from tests._tol import check_close, check_equal
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(600)]
+
+T, E, K = 128_000, 8, 4
+ROWS = T * K
+B31 = 2 ** 31
+
+
+def _windows():
+    wide_byte = B31 // (5760 * 2)         # first row of [R, 5760] bf16 past 2^31 bytes (186,413 starts below it)
+    elem = B31 // 5760                    # first row past 2^31 elements (and [R, 2880] bf16 past 2^31 bytes)
+    rows = set(range(0, 48))
+    for c in (wide_byte, elem):
+        rows |= set(range(c - 40, c + 40))
+    rows |= set(range(ROWS - 48, ROWS))
+    return torch.tensor(sorted(rows), dtype=torch.long)
+
+
+@pytest.fixture(scope="module")
+def big_run(dev):
+    inp = workloads.layer(3, T=T, E=E, lora_r=16, zipf=False)
+    m = workloads.make_experts(inp, dev)
+    rd, gi, si = R.routing_replay(inp.logits.to(dev), inp.expt_indx.to(dev), K)
+    calls = []
+    saved = Q.FUSED_SWIGLU_BWD
+    Q.FUSED_SWIGLU_BWD = False
+    try:
+        x = inp.x.to(dev).requires_grad_(True)
+        with recording(calls):
+            y = m(x, rd, gi, si)
+            y.backward(inp.dy.to(dev))
+    finally:
+        Q.FUSED_SWIGLU_BWD = saved
+    torch.cuda.synchronize()
+    lora_names = ("gate_up_proj_lora_A", "gate_up_proj_lora_B", "down_proj_lora_A", "down_proj_lora_B")
+    staged = dict(dx=x.grad.cpu(), lora={n: getattr(m, n).grad.cpu() for n in lora_names})
+    for prm in m.parameters():
+        prm.grad = None
+    x2 = inp.x.to(dev).requires_grad_(True)
+    y2 = m(x2, rd, gi, si)
+    y2.backward(inp.dy.to(dev))
+    torch.cuda.synchronize()
+    default = dict(dx=x2.grad.cpu(), lora={n: getattr(m, n).grad.cpu() for n in lora_names})
+    del x2, y2
+    wptr = {m._get_uint8_weights(p)[0].data_ptr(): p for p in ("gate_up_proj", "down_proj")}
+    offs = rd.expt_data.token_offs_raw.cpu().long()
+    yield dict(inp=inp, calls=calls, offs=offs, wptr=wptr, staged=staged, default=default,
+               topk=gi.src_indx.cpu().long(), gate=si.src_indx.cpu().long(), rows=_windows(), y=y, x=x)
+    del m, calls, x, y
+    torch.cuda.empty_cache()
+
+
+def _of(run, name):
+    return [(a, o) for n, a, o in run["calls"] if n == name]
+
+
+def _expert_of(offs, rows):
+    return torch.searchsorted(offs, rows, right=True) - 1
+
+
+def _weights(run, proj, e):
+    inp = run["inp"]
+    b, s = (inp.gu_blocks, inp.gu_scales) if proj == "gate_up_proj" else (inp.dn_blocks, inp.dn_scales)
+    return mxfp4.dequant_f32_table(b[e], s[e])
+
+
+def test_sizes_cross_the_boundaries(big_run):
+    offs = big_run["offs"]
+    assert int(offs[-1]) == ROWS and ROWS * 5760 > B31 and ROWS * 2880 * 2 > B31
+    (a, (gu, act)), = [(a, o) for a, o in _of(big_run, "moe_rows") if a["swiglu"] is not None]
+    assert gu.shape == (ROWS, 5760) and gu.numel() > B31 and act.shape == (ROWS, 2880)
+
+
+def test_gemm_rows_at_the_boundaries(big_run):
+    rows = big_run["rows"]
+    offs = big_run["offs"]
+    ex = _expert_of(offs, rows)
+    n_launch = 0
+    for a, out in _of(big_run, "moe_rows"):
+        y = out[0] if isinstance(out, tuple) else out
+        trans = bool(a["trans_w"])
+        proj = big_run["wptr"][a["blocks"].data_ptr()]
+        gather = a["gather_indx"].src_indx.long() if a["gather_indx"] is not None else None
+        kd = a["routing_data"].n_expts_act if gather is not None else 1
+        L, Bx = a["lora_l"], a["lora_b"]
+        n_red = a["x"].shape[1] + (L.shape[1] if L is not None else 0)
+        for e in ex.unique().tolist():
+            rr = rows[ex == e]
+            src = (gather[rr.to(gather.device)] // kd) if gather is not None else rr
+            xe = a["x"][src.to(a["x"].device)].cpu()
+            ref, mag = moe.expert_rows(xe, _weights(big_run, proj, e), torch.arange(rr.numel()), trans=trans,
+                                       lora_l=None if L is None else L[rr.to(L.device)].cpu(),
+                                       lora_b=None if Bx is None else Bx[e].cpu(),
+                                       bias=None if a["bias"] is None else a["bias"][e].cpu(),
+                                       gammas=None if a["gammas"] is None else a["gammas"][rr.to(y.device)].cpu())
+            check_close(y[rr.to(y.device)].cpu(), ref, mag=mag, n=n_red,
+                        what=f"{proj} trans={trans} expert {e} rows {int(rr[0])}..{int(rr[-1])}")
+        n_launch += 1
+    assert n_launch == 4
+
+
+def test_swiglu_at_the_boundaries(big_run):
+    rows = big_run["rows"]
+    (a, (gu, act)), = [(a, o) for a, o in _of(big_run, "moe_rows") if a["swiglu"] is not None]
+    rg = rows.to(gu.device)
+    ref = swiglu.forward(gu[rg].cpu(), a["swiglu"][1], a["swiglu"][2])[0]
+    check_close(act[rg].cpu(), ref, what="fused SwiGLU forward")
+    (b, dgu), = _of(big_run, "swiglu_backward_raw")
+    ref = swiglu.backward_from_raw(b["grad_output"][rg].cpu(), b["gate_up_raw"][rg].cpu(), b["alpha"], b["limit"])
+    check_close(dgu[rg].cpu(), ref, what="SwiGLU backward")
+
+
+def test_lora_rows_at_the_boundaries(big_run):
+    rows = big_run["rows"]
+    ex = _expert_of(big_run["offs"], rows)
+    n_calls = 0
+    for a, out in _of(big_run, "_lora_rows"):
+        gather = a["gather"].long() if a["gather"] is not None else None
+        for e in ex.unique().tolist():
+            rr = rows[ex == e]
+            src = (gather[rr.to(gather.device)] // a["k_act"]) if gather is not None else rr
+            xe = a["x"][src.to(a["x"].device)].cpu()
+            ref, mag = moe.expert_lora_rows(xe, a["wl"][e].cpu(), torch.arange(rr.numel()), a["scale"],
+                                            trans=bool(a["trans_b"]))
+            check_close(out[rr.to(out.device)].cpu(), ref, mag=mag, n=a["K"], what=f"LoRA rows e{e}")
+        n_calls += 1
+    assert n_calls == 2
+    # u = s * Big B of the one-pass LoRA backward (the LoRA operand of the input gradients)
+    for a, (u, _) in _of(big_run, "_lora_u_and_dB"):
+        gather = a["gather"].long() if a["gather"] is not None else None
+        for e in ex.unique().tolist():
+            rr = rows[ex == e]
+            src = (gather[rr.to(gather.device)] // a["gdiv"]) if gather is not None else rr
+            big = a["big"][src.to(a["big"].device)].cpu()
+            ref, mag = moe.expert_lora_rows(big, a["Bw"][e].cpu(), torch.arange(rr.numel()), a["scale"], trans=True)
+            check_close(u[rr.to(u.device)].cpu(), ref, mag=mag, n=a["W"], what=f"LoRA u e{e}")
+        n_calls += 1
+    assert n_calls == 4
+
+
+def test_lora_grads_of_the_boundary_experts(big_run):
+    """dB (one pass over the wide gradient) and dA of the experts holding the
+    boundary rows and the last rows, against the oracle over all their rows."""
+    offs = big_run["offs"]
+    experts = sorted(set(_expert_of(offs, big_run["rows"][48:]).tolist()))
+    for a, (u, G) in _of(big_run, "_lora_u_and_dB"):
+        gather = a["gather"].long() if a["gather"] is not None else None
+        for e in experts:
+            lo, hi = int(offs[e]), int(offs[e + 1])
+            rr = torch.arange(lo, hi)
+            src = (gather[rr.to(gather.device)] // a["gdiv"]) if gather is not None else rr
+            big = a["big"][src.to(a["big"].device)].cpu()
+            rs = None if a["rowscale"] is None else a["rowscale"][lo:hi].cpu()
+            ref, mag = moe.expert_wgrad(big, a["L"][lo:hi].cpu(), rs)
+            check_close(G[e].cpu(), ref, mag=mag, n=hi - lo, what=f"LoRA dB [{a['W']}x16] e{e}")
+            del big
+    for a, G in _of(big_run, "_lora_wgrad"):
+        ag = a["a_gather"].long() if a["a_gather"] is not None else None
+        bg = a["b_gather"].long() if a["b_gather"] is not None else None
+        for e in experts:
+            lo, hi = int(offs[e]), int(offs[e + 1])
+            rr = torch.arange(lo, hi)
+            ia = (ag[rr.to(ag.device)] // a["a_div"]) if ag is not None else rr
+            ib = (bg[rr.to(bg.device)] // a["b_div"]) if bg is not None else rr
+            rs = None if a["a_rowscale"] is None else a["a_rowscale"][lo:hi].cpu()
+            ref, mag = moe.expert_wgrad(a["a"][ia.to(a["a"].device)].cpu(), a["b"][ib.to(a["b"].device)].cpu(), rs)
+            check_close(G[e].cpu(), ref, mag=mag, n=hi - lo, what=f"LoRA dA [{a['M']}x{a['N']}] e{e}")
+
+
+def test_combines_on_the_boundary_tokens(big_run):
+    """Each token's k-way sum, bit-exact: fp32 sum of its bf16 rows in slot order."""
+    rows = big_run["rows"]
+    gate = big_run["gate"].view(T, K)
+    g = torch.Generator().manual_seed(3)
+    tokens = torch.cat([big_run["topk"][rows] // K, torch.randint(0, T, (2048,), generator=g),
+                        torch.arange(T - 16, T)]).unique()
+    n = 0
+    for a, out in _of(big_run, "moe_combine"):
+        gi = gate[tokens]                                            # [n, K] rows of each token
+        r = a["rows"][gi.reshape(-1).to(a["rows"].device)].cpu()     # the tokens' rows, slot order
+        ref = moe.combine(r, torch.arange(gi.numel(), dtype=torch.int32), K)
+        check_equal(out[tokens.to(out.device)].cpu(), ref, f"combine {n}")
+        n += 1
+    assert n == 2
+
+
+def test_default_composition_matches_staged_run(big_run):
+    check_equal(big_run["default"]["dx"], big_run["staged"]["dx"], "dX (default composition)")
+    for name, gr in big_run["staged"]["lora"].items():
+        check_equal(big_run["default"]["lora"][name], gr, f"{name} grad (default composition)")
+
+
+def test_whole_stack_dequant_past_2_31_elements(dev):
+    """130 experts' gate_up weights [130, 5760, 2880]: 2.16e9 bf16 outputs (4.31 GB)."""
+    E2, N, Kd = 130, 5760, 2880
+    gen = torch.Generator(device=dev).manual_seed(11)
+    blocks = torch.randint(0, 256, (E2, N, Kd // 32, 16), generator=gen, dtype=torch.uint8, device=dev)
+    scales = torch.randint(118, 131, (E2, N, Kd // 32), generator=gen, dtype=torch.uint8, device=dev)
+    out = kernels.mxfp4_to_bf16_hip(blocks, scales)
+    torch.cuda.synchronize()
+    assert out.shape == (E2, N, Kd) and out.numel() > B31
+    per = N * Kd
+    # experts around 2^31 bytes (64 / 65), 2^31 elements (129: starts below, ends past) and the first
+    checked = {0, (B31 // 2) // per, (B31 // 2) // per + 1, B31 // per, E2 - 2}
+    for e in sorted(checked):
+        ref = mxfp4.dequant_f32_table(blocks[e].cpu(), scales[e].cpu())
+        got = out[e].cpu().view(torch.int16).numpy().view(np.uint16).astype(np.uint32) << 16
+        assert (got == ref.numpy().view(np.uint32)).all(), f"expert {e}"   # bits: -0.0 is not +0.0
+    del out, blocks, scales
+    torch.cuda.empty_cache()

@@ -7,7 +7,8 @@ term.  End-to-end (module outputs and gradients against the float64 dense
 layer): the intermediates are rounded to bf16 at the same points on the GPU
 and in the oracle's bf16 chain, so the oracle's own deviation from float64
 bounds what rounding alone can do; the test allows rtol 2e-2 / atol 1e-2
-plus twice the oracle chain's largest deviation from float64 in that tensor.
+plus twice the oracle chain's largest deviation from float64 in the same row
+(token of Y / dX, expert of a LoRA gradient).
 """
 from pathlib import Path
 from types import SimpleNamespace
@@ -81,10 +82,17 @@ def test_stagewise_official_distribution(dev, lora_r):
     _check_all_stages(S.LayerRun(inp, dev), f"official r={lora_r}")
 
 
+def _row_slack(bf, f64):
+    """Twice the oracle bf16 chain's largest deviation from float64 in each row
+    of the first dimension (a token of Y / dX, an expert of a LoRA gradient),
+    so a large entry in one row sets no slack for the others."""
+    d = (bf.double() - f64.double()).abs()
+    return 2.0 * d.reshape(d.shape[0], -1).max(1).values.view(-1, *([1] * (d.dim() - 1)))
+
+
 def _e2e_check(got, bf, f64, what):
-    """got vs float64 with twice the oracle bf16 chain's largest deviation from float64 as extra slack."""
-    dev_oracle = float((bf.double() - f64.double()).abs().max())
-    check_close(got, f64, extra=2.0 * dev_oracle, what=what)
+    """got vs float64 with the per-row slack of the oracle bf16 chain (_row_slack)."""
+    check_close(got, f64, extra=_row_slack(bf, f64), what=what)
 
 
 @pytest.mark.parametrize("lora", [False, True])

@@ -61,3 +61,20 @@ def test_router_rejects_unsupported_shapes(dev):
         R.router_logits_hip(x, w, None)
     with pytest.raises(TypeError):
         R.router_logits_hip(x.float(), w.float(), None)
+
+
+@pytest.mark.parametrize("case", ["h96", "fp32_weight", "e300"])
+def test_router_linear_falls_back_for_operands_the_kernel_does_not_take(dev, case):
+    """router_linear (what mlp_forward calls) still gives the reference's
+    nn.functional.linear for a router the kernel does not take."""
+    g = torch.Generator().manual_seed(11)
+    T, H, E = 33, (96 if case == "h96" else 128), (300 if case == "e300" else 16)
+    x = workloads.normal_bf16(g, (T, H), 1.0).to(dev)
+    w = workloads.normal_bf16(g, (E, H), 0.05).to(dev)
+    b = workloads.normal_bf16(g, (E,), 0.05).to(dev)
+    if case == "fp32_weight":
+        x, w, b = x.float(), w.float(), b.float()
+    assert not R.router_kernel_supports(x, w, b)
+    got = R.router_linear(x, w, b)
+    ref = torch.nn.functional.linear(x, w, b)
+    assert got.dtype == ref.dtype and torch.equal(got, ref)

@@ -28,7 +28,7 @@ def _args(o):
             o["offs"].data_ptr())
 
 
-def _case(T, E, K, seed, dev, zipf):
+def _case(T, E, K, seed, dev, zipf, own_stream=False):
     g = torch.Generator().manual_seed(seed)
     logits = workloads.normal_bf16(g, (T, E), 1.0).to(dev)
     if zipf:
@@ -36,6 +36,9 @@ def _case(T, E, K, seed, dev, zipf):
     else:
         ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)]).to(torch.int32).to(dev)
     stream = _capi.stream_of(dev)
+    side = torch.cuda.Stream(device=dev) if own_stream else None   # default priority
+    if side is not None:
+        torch.cuda.synchronize()
     ref = _outputs(T, E, K, dev)
     ws = torch.empty(_capi.workspace_bytes(T, E, K), dtype=torch.uint8, device=dev)
     _capi.call("af3_routing_replay", logits.data_ptr(), E, ids.data_ptr(), T, E, K, *_args(ref), ws.data_ptr(),
@@ -43,7 +46,10 @@ def _case(T, E, K, seed, dev, zipf):
     got = _outputs(T, E, K, dev)
     for o in got.values():
         o.fill_(0x55) if o.dtype != torch.bfloat16 else o.fill_(-3.0)
-    _capi.call("af3_routing_replay_noalloc", logits.data_ptr(), E, ids.data_ptr(), T, E, K, *_args(got), stream)
+    torch.cuda.synchronize()
+    # (a stream object of its own: the scratch array is the one of the stream's device)
+    _capi.call("af3_routing_replay_noalloc", logits.data_ptr(), E, ids.data_ptr(), T, E, K, *_args(got),
+               side.cuda_stream if side is not None else stream)
     torch.cuda.synchronize()
     for k in ref:
         a, b = got[k].cpu(), ref[k].cpu()
@@ -57,4 +63,5 @@ def test_noalloc_matches_workspace_entry_point_two_calls(dev):
     _case(16384, 128, 4, 1, dev, zipf=True)    # the 120b layer's routing (Zipf, idle experts)
     _case(3000, 32, 4, 2, dev, zipf=False)     # smaller, over the first call's leftovers
     _case(37, 6, 2, 3, dev, zipf=False)
+    _case(2000, 64, 4, 4, dev, zipf=False, own_stream=True)
 
