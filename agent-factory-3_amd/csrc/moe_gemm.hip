@@ -630,16 +630,16 @@ __device__ __forceinline__ int g4_col(int tn, int lr) {
   return PAIRED ? 64 * (tn >> 1) + 2 * lr + (tn & 1) : tn * 32 + lr;
 }
 
-template <bool PAIRED = false, int TM = 4, int TN = 4, int NT = 256, int CN = 256>
+template <bool PAIRED = false, int TM = 4, int TN = 4, int NT = 256, int CN = 256, int RM = 256>
 __device__ __forceinline__ void g4_epilogue(const Params& p, uint8_t* lds, af3_f32x16 acc[TM][TN], int e, int row_lo,
                                             int nrows, int n0, int ncols, int wm0, int wn0) {
   constexpr int CH = CN / 8;  // 16-byte chunks per tile row
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
-  float* const gl = (float*)(lds + 256 * 512);  // per-row gammas
-  float* const al = gl + 256;                    // per-row A scales
+  float* const gl = (float*)(lds + RM * CN * 2);  // per-row gammas
+  float* const al = gl + RM;                        // per-row A scales
   __syncthreads();
-  for (int t = threadIdx.x; t < 256; t += NT) {
+  for (int t = threadIdx.x; t < RM; t += NT) {
     float gv = 1.f;
     if (p.gammas && t < nrows) {
       const int64_t gr = row_lo + t;
@@ -678,7 +678,7 @@ __device__ __forceinline__ void g4_epilogue(const Params& p, uint8_t* lds, af3_f
   }
   __syncthreads();
 #pragma unroll 4
-  for (int i = 0; i < 32 * 256 / NT; ++i) {
+  for (int i = 0; i < RM * CH / NT; ++i) {
     const int id = i * NT + threadIdx.x;
     const int row = id / CH, ch = id % CH;
     if (row < nrows && ch * 8 < ncols) {
@@ -764,8 +764,9 @@ __device__ __forceinline__ af3_bf16x8 g4_bfrag(uint32_t v, uint32_t sc, float sc
 // first MFMAs to land), the k-step's DPW global->LDS copies are spread
 // between the MFMAs, and the A-fragment LDS reads of sub-step s + 1 are
 // issued ahead of the MFMAs of sub-step s.
-template <int TM, int TN, int DPW, bool FULL, bool EXACT, class Dma>
-__device__ __forceinline__ void g4_kstep(const uint16_t* as, const uint8_t* bs, const uint8_t* ss, int G, int kt,
+template <int TM, int TN, int DPW, bool FULL, bool EXACT, bool BG, class Dma>
+__device__ __forceinline__ void g4_kstep(const uint16_t* as, const uint8_t* bs, const af3_u32x4 (&bqv)[TN],
+                                         const uint8_t* ss, int G, int kt,
                                          bool more, int wm0, int wn0, int tm_live, int tn_live,
                                          af3_f32x16 acc[TM][TN], af3_bf16x8 af[2][TM], af3_bf16x8 bf[2][TN],
                                          uint32_t sc[TN], Dma&& dma) {
@@ -781,7 +782,10 @@ __device__ __forceinline__ void g4_kstep(const uint16_t* as, const uint8_t* bs, 
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) {
     const int n = wn0 + tn * 32 + lr;
-    bp[tn] = (FULL || tn < tn_live) ? *(const af3_u32x4*)(bs + g4_b_off(n, lh)) : zero4();
+    if constexpr (BG)
+      bp[tn] = (FULL || tn < tn_live) ? bqv[tn] : zero4();
+    else
+      bp[tn] = (FULL || tn < tn_live) ? *(const af3_u32x4*)(bs + g4_b_off(n, lh)) : zero4();
     scf[tn] = __uint_as_float(sc[tn] << 23);
     sc_next[tn] = 127u;
   }
@@ -824,25 +828,46 @@ __device__ __forceinline__ void g4_kstep(const uint16_t* as, const uint8_t* bs, 
   for (int tn = 0; tn < TN; ++tn) sc[tn] = sc_next[tn];
 }
 
+// Packed weight words global -> registers (inline assembly, counted by the
+// k-loop's explicit vmcnt waits), and the marker that ties the registers to
+// the wait that covers them: every later use depends on its output.
+template <int TN>
+__device__ __forceinline__ void g7_load_words(af3_u32x4 (&dst)[TN], const uint8_t* const (&src)[TN], int off) {
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn)
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(dst[tn]) : "v"(src[tn] + off) : "memory");
+}
+template <int TN>
+__device__ __forceinline__ void g7_landed(af3_u32x4 (&r)[TN]) {
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) asm volatile("" : "+v"(r[tn]));
+}
+
 // One work item of the forward kernel: a RM x CN output tile (256 x 256, or
 // NARROW 128 x 512 for the partial tiles of short experts, so a tail tile of
 // <= 128 rows converts each weight byte once per 128 rows instead of per 256).
 // The 8 waves are WM x WN (NARROW: 1 x 8) of the same 128 x 64 wave tile.
-template <int WM, int WN, int BXK, bool NARROW>
+// SHAPE 0: 256 x 256 (WM x WN waves), 1 (NARROW): 128 x 512 (8 waves side by
+// side), 2 (HALF): 128 x 256 (4 waves side by side; two blocks per CU)
+template <int WM, int WN, int BXK, int SHAPE, bool BG = false>
 __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, int row_lo, int nrows, int n0,
                                          int ncols) {
-  constexpr int NW = WM * WN, NT = NW * 64;
-  constexpr int RM = NARROW ? 128 : kG4Rows, CN = NARROW ? 512 : kG4Rows;
-  constexpr int WMX = NARROW ? 1 : WM, WNX = NARROW ? NW : WN;
+  constexpr bool NARROW = SHAPE == 1, HALF = SHAPE == 2;
+  static_assert(!HALF || BG, "the 128 x 256 shape takes the packed weights from registers");
+  constexpr int NW = HALF ? 4 : WM * WN, NT = NW * 64;
+  constexpr int RM = (NARROW || HALF) ? 128 : kG4Rows, CN = NARROW ? 512 : kG4Rows;
+  constexpr int WMX = (NARROW || HALF) ? 1 : WM, WNX = (NARROW || HALF) ? NW : WN;
   constexpr int TM = RM / WMX / 32, TN = CN / WNX / 32;
   constexpr int ASTAGE = RM * kBK;  // bf16 elements per A stage
   constexpr int BSTAGE = CN * 32;   // bytes per packed-B stage
-  constexpr int API = RM / 8 / NW, BPI = CN / 32 / NW, DPW = API + BPI;  // copies per wave per k-step
-  static_assert(API >= 1 && BPI >= 1 && (DPW == 10 || DPW == 8 || DPW == 5 || DPW == 4), "copy schedule");
+  // copies per wave per k-step (BG: the packed weights go straight to registers, no B copies)
+  constexpr int API = RM / 8 / NW, BPI = BG ? 0 : CN / 32 / NW, DPW = API + BPI;
+  static_assert(API >= 1 && (BG || BPI >= 1) && (DPW == 10 || DPW == 8 || DPW == 5 || DPW == 4 || DPW == 2),
+                "copy schedule");
   static_assert(kG4Stages * (ASTAGE * 2 + BSTAGE) <= kG4Stages * (kG4AStage * 2 + kG4BStage), "LDS ring");
   uint16_t* const As = (uint16_t*)lds;                    // 3 x RM x 64 bf16
-  uint8_t* const Bs = lds + kG4Stages * ASTAGE * 2;       // 3 x CN x 32 bytes
-  uint8_t* const Ss = Bs + kG4Stages * BSTAGE;            // CN x G scale bytes
+  uint8_t* const Bs = lds + kG4Stages * ASTAGE * 2;       // 3 x CN x 32 bytes (not with BG)
+  uint8_t* const Ss = BG ? Bs : Bs + kG4Stages * BSTAGE;  // CN x G scale bytes
   const int G = p.K >> 5;
   const int nk = p.K / kBK;
 
@@ -864,7 +889,7 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
     arow[i] = (const uint16_t*)p.a.ptr + src * p.a.ld + (((lane & 7) ^ swz(row)) << 3);
   }
   // packed B (BPI instructions per wave per stage, 32 weight rows each)
-  const uint8_t* bsrc[BPI];
+  const uint8_t* bsrc[BPI > 0 ? BPI : 1];
 #pragma unroll
   for (int j = 0; j < BPI; ++j) {
     const int row4 = (wave * BPI + j) * 8 + (lane >> 3);
@@ -888,9 +913,11 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));  // LDS byte address of the block's area
   auto issue_one = [&](int kt, int j) {
     const int st = kt % kG4Stages;
+    // BG: the k-steps past the end copy the last k-step's rows again (into a stage no wave reads again)
+    const int ks = BG ? min(kt, nk - 1) : kt;
     if (j < API)
-      g4_dma16(arow[j] + kt * kBK, lds0 + (uint32_t)(st * ASTAGE * 2 + (wave * API + j) * 8 * kBK * 2));
-    else
+      g4_dma16(arow[j] + ks * kBK, lds0 + (uint32_t)(st * ASTAGE * 2 + (wave * API + j) * 8 * kBK * 2));
+    else if constexpr (BPI > 0)
       g4_dma16(bsrc[j - API] + kt * 32,
                lds0 + (uint32_t)(kG4Stages * ASTAGE * 2 + st * BSTAGE + (wave * BPI + j - API) * 1024));
   };
@@ -909,9 +936,28 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
       AF3_ASM_WAIT_VM(8);
     else if constexpr (DPW == 5)
       AF3_ASM_WAIT_VM(5);
-    else
+    else if constexpr (DPW == 4)
       AF3_ASM_WAIT_VM(4);
+    else
+      AF3_ASM_WAIT_VM(2);
   };
+  // BG: the lane's packed weight words of a k-step (row wn0 + 32 tn + lr, MXFP4 block 2 kt + lh: the
+  // 16 bytes of its B fragments for the whole k-step) go global -> registers one k-step ahead, into
+  // bq[parity]; the loads are issued by inline assembly like the copies (so the k-step waits stay
+  // exact) and each k-step's registers pass through an empty asm after the vmcnt wait, so no use of
+  // them can be scheduled before it.  Rows past the tile read row 0 (their sub-tiles are skipped).
+  af3_u32x4 bq[2][TN];
+  const uint8_t* bgp[TN];
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) {
+    int nr = wn0 + tn * 32 + lr;
+    if (nr >= ncols) nr = 0;
+    bgp[tn] = (const uint8_t*)p.b.ptr + e * p.b.estride + (int64_t)(n0 + nr) * p.b.ld + lh * 16;
+    bq[0][tn] = zero4();
+    bq[1][tn] = zero4();
+  }
+  auto load_b = [&](int kt, auto par) { g7_load_words<TN>(bq[decltype(par)::value], bgp, kt * 32); };
+  const bool live = tm_live > 0 && tn_live > 0;
 
   af3_f32x16 acc[TM][TN];
 #pragma unroll
@@ -921,8 +967,11 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+  if constexpr (BG) {
+    if (live) load_b(0, std::integral_constant<int, 0>{});
+  }
   issue(0);
-  if (nk > 1) issue(1);
+  if (BG || nk > 1) issue(1);
   // does the tile hold a scale byte outside [2, 252]?  (then the whole work
   // item takes the exact integer dequantisation)
   bool odd = false;
@@ -954,16 +1003,41 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn)
       sc[tn] = (FULL || tn < tn_live) ? Ss[(wn0 + tn * 32 + lr) * G + lh] : 127u;
-    auto step = [&](int kt, bool last, auto&& dma) {
-      wait_stage(last);
-      AF3_ASM_LDS_BARRIER();
+    auto step = [&](int kt, auto last_c, auto par, auto&& dma) {
+      constexpr int P = decltype(par)::value;
+      constexpr bool last = decltype(last_c)::value;
+      if constexpr (BG) {
+        // uniform k-steps: API copies and TN weight loads were issued by every
+        // earlier k-step, so this k-step's data is everything but the newest API
+        wait_stage(false);
+        g7_landed<TN>(bq[P]);
+        AF3_ASM_LDS_BARRIER();
+        load_b(min(kt + 1, nk - 1), std::integral_constant<int, 1 - P>{});
+      } else {
+        wait_stage(last);
+        AF3_ASM_LDS_BARRIER();
+      }
       const int st = kt % kG4Stages;
-      g4_kstep<TM, TN, DPW, FULL, EXACT>(As + st * ASTAGE, Bs + st * BSTAGE, Ss, G, kt, !last, wm0, wn0, tm_live,
-                                         tn_live, acc, af, bf, sc, dma);
+      g4_kstep<TM, TN, DPW, FULL, EXACT, BG>(As + st * ASTAGE, Bs + st * BSTAGE, bq[P], Ss, G, kt, BG || !last, wm0,
+                                             wn0, tm_live, tn_live, acc, af, bf, sc, dma);
     };
+    constexpr std::integral_constant<int, 0> I0{};
+    constexpr std::integral_constant<int, 1> I1{};
+    constexpr std::false_type MORE{};
+    constexpr std::true_type LAST{};
     int kt = 0;
-    for (; kt + 2 < nk; ++kt) step(kt, false, [&](int j) { issue_one(kt + 2, j); });
-    for (; kt < nk; ++kt) step(kt, kt + 1 == nk, [](int) {});
+    if constexpr (BG) {
+      // pairs of k-steps (the register parity is static)
+      for (; kt < nk; kt += 2) {
+        step(kt, MORE, I0, [&](int j) { issue_one(kt + 2, j); });
+        if (kt + 1 < nk) step(kt + 1, MORE, I1, [&](int j) { issue_one(kt + 3, j); });
+      }
+      AF3_ASM_WAIT_VM(0);  // the redundant copies and loads past the end have landed before the LDS is reused
+    } else {
+      for (; kt + 2 < nk; ++kt) step(kt, MORE, I0, [&](int j) { issue_one(kt + 2, j); });
+      if (nk - kt == 2) step(kt++, MORE, I0, [](int) {});
+      step(kt, LAST, I0, [](int) {});
+    }
     // the last k-step's sub-step 3
 #pragma unroll
     for (int i = 0; i < TM * TN; ++i) {
@@ -983,10 +1057,17 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
     // partial tile) only keeps the copy / barrier protocol of the k-loop, so
     // the live wave sharing its SIMD runs alone
     for (int kt = 0; kt < nk; ++kt) {
-      wait_stage(kt + 1 == nk);
-      AF3_ASM_LDS_BARRIER();
-      if (kt + 2 < nk) issue(kt + 2);
+      if constexpr (BG) {
+        wait_stage(false);
+        AF3_ASM_LDS_BARRIER();
+        issue(kt + 2);
+      } else {
+        wait_stage(kt + 1 == nk);
+        AF3_ASM_LDS_BARRIER();
+        if (kt + 2 < nk) issue(kt + 2);
+      }
     }
+    if constexpr (BG) AF3_ASM_WAIT_VM(0);
   }
 
   if constexpr (BXK != NONE) {
@@ -1007,7 +1088,7 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
     }
   }
 
-  g4_epilogue<false, TM, TN, NT, CN>(p, lds, acc, e, row_lo, nrows, n0, ncols, wm0, wn0);
+  g4_epilogue<false, TM, TN, NT, CN, RM>(p, lds, acc, e, row_lo, nrows, n0, ncols, wm0, wn0);
 }
 
 // scale bytes of a NARROW work item (512 weight rows x G) fit behind its rings
@@ -1029,11 +1110,33 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm4_fwd_kernel(Params p) {
     if (nrows <= 128 && (p.K >> 5) <= kG4NarrowMaxG) {
       // tiles of <= 128 rows take n-tiles nt and nt + 1 as one 128 x 512 item
       if (nt & 1) return;
-      g4f_tile<WM, WN, BXK, true>(p, lds, e, row_lo, nrows, n0, min(512, p.N - n0));
+      g4f_tile<WM, WN, BXK, 1>(p, lds, e, row_lo, nrows, n0, min(512, p.N - n0));
       return;
     }
   }
-  g4f_tile<WM, WN, BXK, false>(p, lds, e, row_lo, nrows, n0, min(kG4Rows, p.N - n0));
+  g4f_tile<WM, WN, BXK, 0>(p, lds, e, row_lo, nrows, n0, min(kG4Rows, p.N - n0));
+}
+
+// Two independent blocks per CU: 128 x 256 items of 4 waves (one per SIMD per
+// block) on the 128-row tile map, packed weights from registers, so one
+// block's epilogue and barriers overlap the other block's k-loop.
+constexpr int kG7MaxG = 96;  // scale bytes per weight row (K <= 3072)
+constexpr int kG7LdsBytes = kG4Stages * 128 * kBK * 2 + 256 * kG7MaxG;  // 72 KB
+static_assert(kG7LdsBytes >= 128 * 256 * 2 + 1024, "the epilogue reuses the LDS for the bf16 tile + row gammas / scales");
+
+template <int BXK>
+__global__ __launch_bounds__(256, 2) void gemm7_fwd_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kG7LdsBytes];
+  int mt, nt;
+  if (!g4_work_item(p, mt, nt)) return;
+  const int32_t ent = p.tile_map[mt];
+  if (ent < 0) return;
+  const int e = ent & 0xFFFF, blk = ent >> 16;
+  const int row_lo = p.offs[e] + blk * 128;
+  const int nrows = min(128, p.offs[e + 1] - row_lo);
+  if (nrows <= 0) return;
+  const int n0 = nt * 256;
+  g4f_tile<1, 4, BXK, 2, true>(p, lds, e, row_lo, nrows, n0, min(256, p.N - n0));
 }
 
 // ---------------------------------------------------------------------------
@@ -1201,7 +1304,7 @@ __device__ __forceinline__ void g4f8_tile(const Params& p, uint8_t* lds, int e, 
     step(kt + 1, afB, bfB, scB, afA, bfA, scA);
   }
   if (kt < nk) step(kt, afA, bfA, scA, afB, bfB, scB);
-  g4_epilogue<false, TM, TN, NT, CN>(p, lds, acc, e, row_lo, nrows, n0, ncols, wm0, wn0);
+  g4_epilogue<false, TM, TN, NT, CN, RM>(p, lds, acc, e, row_lo, nrows, n0, ncols, wm0, wn0);
 }
 
 template <int BXK>
@@ -2288,6 +2391,12 @@ static void launch_gemm4_fwd(int max_tiles, int N, hipStream_t stream, Params p)
   hipLaunchKernelGGL((gemm4_fwd_kernel<WM, WN, ROWS_BF16>), grid, dim3(WM * WN * 64), 0, stream, p);
 }
 
+static void launch_gemm7_fwd(int max_tiles, int N, hipStream_t stream, Params p) {
+  p.n_nblk = (N + 255) / 256;
+  dim3 grid(g4_grid(max_tiles, p.n_nblk, p.group_m));
+  hipLaunchKernelGGL((gemm7_fwd_kernel<ROWS_BF16>), grid, dim3(256), 0, stream, p);
+}
+
 template <int BM, int BN, int WM, int WN>
 static void launch_gemm2(bool trans, int max_tiles, int N, hipStream_t stream, Params p) {
   p.n_nblk = (N + BN - 1) / BN;
@@ -2370,23 +2479,29 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
   p.limit = limit;
   const bool trans = trans_w != 0;
   // tile configurations:
+  //   26: gemm7 forward (128x256 work items on the 128-row map, 4 waves of
+  //       128x64, two blocks per CU; activation rows through a three-stage
+  //       global->LDS ring, the packed MXFP4 words straight into registers and
+  //       converted there); default for trans_w 0 with block_m 128
   //   22: gemm4 forward (256x256 work items, 8 waves of 128x64, two per SIMD,
   //       packed MXFP4 through a three-stage global->LDS ring, converted in
-  //       registers); default for trans_w 0 when its requirements hold
+  //       registers); default for trans_w 0 with block_m 256
   //   23: gemm5 input gradient (packed weight rows read with transposing LDS
   //       loads, one three-stage ring for A, B and scales; 4 waves of 256x64);
   //       default for trans_w 1 when its requirements hold
   //   4 / 2: gemm2, 256x256 / 128x256 tiles with the weight dequantised into
   //       LDS (general fallback for block_m 256 / 128)
   //   9: single-buffered 128x128 row tiles (any K % 32 == 0; used when K % 64 != 0)
-  //   tile_cfg / 100 = m-tiles per group of the 22 / 23 work order (default 4)
+  //   tile_cfg / 100 = m-tiles per group of the 22 / 23 / 26 work order (default 4; 2 for 26)
   int cfg = tile_cfg % 100;
   const int group_m = tile_cfg / 100 > 0 ? tile_cfg / 100 : 4;
   if (cfg == 0) {
     const bool g4_fwd = !trans && block_m == 256 && K % kBK == 0 && K / 32 <= kG4MaxG && al16(w_scales) && al16(y) &&
                         ldy % 8 == 0;
+    const bool g7_fwd = !trans && block_m == 128 && K % kBK == 0 && K / 32 <= kG7MaxG && al16(w_scales) && al16(y) &&
+                        ldy % 8 == 0;
     const bool g4_dgrad = trans && block_m == 256 && K % kBK == 0 && N % 64 == 0 && al16(y) && ldy % 8 == 0;
-    cfg = g4_fwd ? 22 : g4_dgrad ? 23 : (block_m == 256 ? 4 : 2);
+    cfg = g4_fwd ? 22 : g7_fwd ? 26 : g4_dgrad ? 23 : (block_m == 256 ? 4 : 2);
   }
   const bool bm_ok = (cfg == 4 || cfg == 22 || cfg == 23) ? block_m == 256 : block_m == 128;
   AF3_REQUIRE(bm_ok, "moe_gemm: tile_cfg %d does not match block_m %d", cfg, block_m);
@@ -2419,7 +2534,8 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
   if (epi != 0) {
     AF3_REQUIRE(glu && (epi == 1 || epi == 2), "moe_gemm: bad SwiGLU epilogue %d", epi);
     const bool ok = epi == 1 ? (trans && cfg == 23 && ld_glu % 8 == 0 && al16(glu) && ldy >= 2LL * N)
-                             : (!trans && cfg == 22 && N % 2 == 0 && ld_glu % 4 == 0 && ((uintptr_t)glu & 7) == 0);
+                             : (!trans && (cfg == 22 || cfg == 26) && N % 2 == 0 && ld_glu % 4 == 0 &&
+                                ((uintptr_t)glu & 7) == 0);
     if (!ok) {
       af3::set_error("moe_gemm: the fused SwiGLU epilogue %d is not available for tile_cfg %d / these operands", epi,
                      cfg);
@@ -2428,8 +2544,8 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
   }
   if (a_row_scale) {
     AF3_REQUIRE(lora_r == 0, "moe_gemm: a row scale cannot be combined with the LoRA extension segment");
-    if (!(cfg == 22 || cfg == 23)) {
-      af3::set_error("moe_gemm: the A row scale needs tile_cfg 22 / 23 (got %d)", cfg);
+    if (!(cfg == 22 || cfg == 23 || cfg == 26)) {
+      af3::set_error("moe_gemm: the A row scale needs tile_cfg 22, 23 or 26 (got %d)", cfg);
       return AF3_EUNSUPPORTED;
     }
   }
@@ -2447,6 +2563,13 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
                   "moe_gemm: tile_cfg 22 needs trans_w 0, block_m 256, K %% 64 == 0, K <= %d, 16-byte aligned scales/y",
                   kG4MaxG * 32);
       launch_gemm4_fwd<2, 4>(max_tiles, N, stream, p);
+      break;
+    case 26:
+      p.group_m = tile_cfg / 100 > 0 ? tile_cfg / 100 : 2;
+      AF3_REQUIRE(!trans && block_m == 128 && K % kBK == 0 && K / 32 <= kG7MaxG && al16(w_scales) && al16(y) &&
+                      ldy % 8 == 0,
+                  "moe_gemm: tile_cfg 26 needs trans_w 0, block_m 128, K %% 64 == 0, K <= %d, 16-byte aligned", kG7MaxG * 32);
+      launch_gemm7_fwd(max_tiles, N, stream, p);
       break;
     case 23:
       p.group_m = group_m;

@@ -79,11 +79,14 @@ CASES = [  # (gather, lora, odd)
 ]
 
 
-@pytest.mark.parametrize("cfg,nout", [(0, NOUT), (4, NOUT), (22, NOUT), (22, 640)])
+@pytest.mark.parametrize("cfg,nout", [(0, NOUT), (0, 640), (4, NOUT), (22, NOUT), (22, 640), (126, NOUT)])
 @pytest.mark.parametrize("gather,lora,odd", CASES)
 def test_forward_tiles(dev, cfg, nout, gather, lora, odd):
     """N = 576 / 640 end in a 64- / 128-column n-tile (waves past the tile's
-    columns keep only the copy / barrier protocol)."""
+    columns keep only the copy / barrier protocol).  The default forward
+    (tile_cfg 0 = 26: 128 x 256 items on the 128-row map, two blocks per CU,
+    packed weights loaded into registers) sees tails of 10, 44, 50, 60, 100
+    and 104 rows; 126 is the same kernel with one m-tile per work group."""
     g, ref, rd, gi = _routing(dev, 11)
     blocks, scales = _weights(g, nout, KRED, odd)          # W [E, N, K]
     Rr = T * TOPK
