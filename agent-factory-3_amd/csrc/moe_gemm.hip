@@ -1032,7 +1032,13 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
         step(kt, MORE, I0, [&](int j) { issue_one(kt + 2, j); });
         if (kt + 1 < nk) step(kt + 1, MORE, I1, [&](int j) { issue_one(kt + 3, j); });
       }
-      AF3_ASM_WAIT_VM(0);  // the redundant copies and loads past the end have landed before the LDS is reused
+      // the redundant copies and weight loads past the end have landed before
+      // the LDS is reused; both weight-register buffers stay allocated until
+      // this wait (a dead load's registers handed to another value before its
+      // data lands would be overwritten by it)
+      AF3_ASM_WAIT_VM(0);
+      g7_landed<TN>(bq[0]);
+      g7_landed<TN>(bq[1]);
     } else {
       for (; kt + 2 < nk; ++kt) step(kt, MORE, I0, [&](int j) { issue_one(kt + 2, j); });
       if (nk - kt == 2) step(kt++, MORE, I0, [](int) {});
