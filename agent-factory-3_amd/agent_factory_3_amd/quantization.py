@@ -57,12 +57,13 @@ from .routing import (  # noqa: F401  (re-exported names of the routing layer)
 )
 
 GEMM_BLOCK_M = 128
-# Grouped-GEMM tile selection (tuning knob): rows per tile (128 or 256) of the
-# input-gradient kernels and of explicitly selected forward configurations,
-# and the C library's tile_cfg (0 = default).  The default forward kernel
-# (tile_cfg 26) takes the map of fwd_block_m (128; 256 selects the 256 x 256
-# kernel, tile_cfg 22); the LoRA row products always use the 128-row map.
-GEMM_TILE = {"block_m": 256, "tile_cfg": 0, "fwd_block_m": 128}
+# Grouped-GEMM tile selection (tuning knob): rows per tile (128 or 256) of
+# explicitly selected configurations, and the C library's tile_cfg (0 =
+# default).  The default kernels take the map of fwd_block_m (forward, tile_cfg
+# 26) and dx_block_m (input gradient, tile_cfg 28), both 128; 256 there selects
+# the 256 x 256 kernels (tile_cfg 22 / 23).  The LoRA row products always use
+# the 128-row map.
+GEMM_TILE = {"block_m": 256, "tile_cfg": 0, "fwd_block_m": 128, "dx_block_m": 128}
 
 # Optional launch timer for the grouped GEMM (set by benchmark harnesses):
 # callable(tag: str, flops: int, detail: str) -> context manager wrapping the launch.
@@ -206,8 +207,12 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
     routing_data, k_act = _expt_data(routing_data, R, dev)
     ed = routing_data.expt_data
     bm = GEMM_TILE["block_m"] if K % 64 == 0 else 128
-    if not trans_w and K % 64 == 0 and GEMM_TILE["tile_cfg"] % 100 in (0, 26) and a_row_scale is None:
-        bm = GEMM_TILE.get("fwd_block_m", 128)   # the default forward (tile_cfg 26): 128-row map
+    if K % 64 == 0 and a_row_scale is None:
+        # the default kernels (tile_cfg 26 forward, 28 input gradient) run on the 128-row map
+        if not trans_w and GEMM_TILE["tile_cfg"] % 100 in (0, 26):
+            bm = GEMM_TILE.get("fwd_block_m", 128)
+        elif trans_w and GEMM_TILE["tile_cfg"] % 100 in (0, 28):
+            bm = GEMM_TILE.get("dx_block_m", 128)
     pid_map = getattr(ed, "gemm_order", {}).get(bm) if GEMM_TILE.get("order", True) else None
     if pid_map is None:
         pid_map = ed.block_pid_map[bm]

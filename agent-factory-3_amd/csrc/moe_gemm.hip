@@ -1371,6 +1371,12 @@ constexpr int kD5SOff = kD5BOff + 64 * 128;     // + 8 KB of packed B
 constexpr int kD5Stage = kD5SOff + 8 * 64 * 4;  // + 2 KB of scale dwords = 42 KB
 constexpr int kD5LdsBytes = kD5Stages * kD5Stage > 256 * 512 + 2048 ? kD5Stages * kD5Stage : 256 * 512 + 2048;
 static_assert(kD5LdsBytes <= 160 * 1024, "gemm5 dgrad LDS budget");
+// HALF work items (128 rows x 256 columns, two blocks per CU): A 16 KB, packed
+// B 8 KB and scales 2 KB per stage
+constexpr int kD5HStage = 128 * 64 * 2 + 64 * 128 + 8 * 64 * 4;  // 26 KB
+constexpr int kD5HLdsBytes = kD5Stages * kD5HStage;             // 78 KB
+static_assert(kD5HLdsBytes >= 128 * 512 + 2048, "the HALF epilogue reuses the ring's LDS");
+static_assert(2 * kD5HLdsBytes <= 160 * 1024, "two HALF blocks per CU");
 
 typedef __attribute__((ext_vector_type(2))) int af3_i32x2;
 
@@ -1427,7 +1433,7 @@ __device__ __forceinline__ void d5_cvt_exact(uint32_t w0, uint32_t w1, const uin
 // 16-byte global store per chunk.
 // acc[tm][tn] of a wave holds rows rb + 32 tm .. and the column pairs of
 // sub-tile tn from column wn0 (TM row groups per wave)
-template <int RM, int CN, int TM = RM / 32>
+template <int RM, int CN, int TM = RM / 32, int NBMAX = 16>
 __device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f32x16 (&acc)[TM][CN / 128],
                                             int e, int row_lo, int nrows, int n0, int ncols, int wn0, int rb = 0) {
   constexpr int TN = CN / 128, RB = CN * 2;
@@ -1443,7 +1449,7 @@ __device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f
   // and column, valid addresses whose values are never used)
   constexpr int CH = CN / 8;              // 16-byte chunks per row
   constexpr int NI = RM * CH / 256;       // chunks per lane
-  constexpr int NB = NI < 16 ? NI : 16;   // chunks per prefetch batch
+  constexpr int NB = NI < NBMAX ? NI : NBMAX;  // chunks per prefetch batch
   const bool swb = p.epi == 1;
   af3_u32x4 gx[NB][2];
   auto gu_load = [&](int i, af3_u32x4 (&d)[2]) {
@@ -1559,11 +1565,12 @@ __device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f
 // RG > 0 (SPLIT = 1): only the first RG row groups of the tile hold rows (an
 // expert's last, partial m-tile), so the waves run the MFMAs and A reads of
 // those alone; the rows past them are never stored either way.
-template <bool NARROW, int BXK, int SPLIT = 1, int RG = 0>
+template <bool NARROW, int BXK, int SPLIT = 1, int RG = 0, bool HALF = false>
 __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, int row_lo, int nrows, int n0, int ncols) {
-  static_assert(SPLIT == 1 || (!NARROW && (SPLIT == 2 || SPLIT == 4)), "row split only for 256-row tiles");
-  static_assert(RG == 0 || (SPLIT == 1 && RG >= 1 && RG <= (NARROW ? 4 : 8)), "row groups of a tile");
-  constexpr int RM = NARROW ? 128 : 256;  // tile rows
+  static_assert(!(NARROW && HALF), "one item shape");
+  static_assert(SPLIT == 1 || (!NARROW && !HALF && (SPLIT == 2 || SPLIT == 4)), "row split only for 256-row tiles");
+  static_assert(RG == 0 || (SPLIT == 1 && RG >= 1 && RG <= ((NARROW || HALF) ? 4 : 8)), "row groups of a tile");
+  constexpr int RM = (NARROW || HALF) ? 128 : 256;  // tile rows
   constexpr int CN = NARROW ? 512 : 256;  // tile columns
   constexpr int TM = RM / 32;             // row groups of the tile
   constexpr int TMW = RG ? RG : TM / SPLIT;  // row groups of one wave
@@ -1574,9 +1581,11 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
   constexpr int NCH = BRB / 16;           // 16-byte chunks per weight row
   constexpr int NBLK = CN / 32;           // scale blocks
   constexpr int AI = RM / 32, BI = BRB / 64, SI = NBLK / 4;  // copies per wave per k-step
-  static_assert(AI + BI + SI == 12, "12 copies per wave per k-step");
-  constexpr int AOFF = 0, BOFF = NARROW ? 16384 : 32768, SOFF = NARROW ? 32768 : 40960;
-  static_assert(SOFF + NBLK * 256 <= kD5Stage, "stage layout");
+  constexpr int NCP = AI + BI + SI;
+  static_assert(NCP == (HALF ? 8 : 12), "12 (HALF: 8) copies per wave per k-step");
+  constexpr int AOFF = 0, BOFF = (NARROW || HALF) ? 16384 : 32768, SOFF = NARROW ? 32768 : HALF ? 24576 : 40960;
+  constexpr int STAGE = HALF ? kD5HStage : kD5Stage;
+  static_assert(SOFF + NBLK * 256 <= STAGE, "stage layout");
   // slot of chunk c in weight row k (keeps the transposing reads conflict-free)
   auto bswz = [](int k) { return NARROW ? ((k & 7) << 1) : (k & 7); };
 
@@ -1618,7 +1627,7 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
   // copy j (0..11) of k-step kc: A, then B, then S
   auto issue_one = [&](int kc, int j) {
-    const uint32_t st = lds0 + (uint32_t)((kc % kD5Stages) * kD5Stage);
+    const uint32_t st = lds0 + (uint32_t)((kc % kD5Stages) * STAGE);
     if (j < AI) {
       g4_dma16(arow[j] + kc * kBK, st + (uint32_t)(AOFF + (wave * AI + j) * 1024));
     } else if (j < AI + BI) {
@@ -1629,7 +1638,7 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
   };
   auto issue = [&](int kc) {
 #pragma unroll
-    for (int j = 0; j < 12; ++j) issue_one(kc, j);
+    for (int j = 0; j < NCP; ++j) issue_one(kc, j);
   };
 
   // ---- lane-fixed LDS byte offsets inside a stage ----
@@ -1673,7 +1682,7 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
     // k-step, skipped at kt = 0) and 0..2; iteration s runs the MFMAs of
     // sub-step s while reading and converting the fragments of s + 1
     auto kstep = [&](int kt, bool first, bool pf) {
-      const uint8_t* stg = lds + (kt % kD5Stages) * kD5Stage;
+      const uint8_t* stg = lds + (kt % kD5Stages) * STAGE;
       const int nxt_copy = kt + 2;
       bool odd = false;
 #pragma unroll
@@ -1700,8 +1709,11 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int tm = i / TN, tn = i % TN;
-          if (i < TMW * TN && !(s < 0 && first) && (FULL || (tm < tm_live && (tn >> 1) < pg_live)))
+          // (HALF: the sub-step's 8 MFMAs in every other slot)
+          const int mi = HALF ? (i >> 1) : i;
+          const bool mslot = HALF ? ((i & 1) == 0 && mi < TMW * TN) : i < TMW * TN;
+          const int tm = mi / TN, tn = mi % TN;
+          if (mslot && !(s < 0 && first) && (FULL || (tm < tm_live && (tn >> 1) < pg_live)))
             acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[c][tm], bf[c][tn], acc[tm][tn], 0, 0, 0);
           if (FULL || wave_live) {
             if (i < SB) {
@@ -1765,7 +1777,11 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
               }
             }
           }
-          if (pf && (i == 2 || i == 7 || i == 12)) issue_one(nxt_copy, o * 3 + (i == 2 ? 0 : i == 7 ? 1 : 2));
+          if constexpr (HALF) {
+            if (pf && (i == 3 || i == 10)) issue_one(nxt_copy, o * 2 + (i == 3 ? 0 : 1));
+          } else {
+            if (pf && (i == 2 || i == 7 || i == 12)) issue_one(nxt_copy, o * 3 + (i == 2 ? 0 : i == 7 ? 1 : 2));
+          }
           __builtin_amdgcn_sched_barrier(0);
         }
         if (FULL || wave_live) {
@@ -1788,18 +1804,34 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
     for (int tm = 0; tm < TMW; ++tm) af[1][tm] = zf;
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) bf[1][tn] = zf;
-    if (nk > 1)
-      AF3_ASM_WAIT_VM(12);
-    else
-      AF3_ASM_WAIT_VM(0);
+    // a k-step's stage is complete once this wave's copies for it have landed
+    // (NCP newer ones outstanding, none for the last k-step)
+    if constexpr (HALF) {
+      if (nk > 1)
+        AF3_ASM_WAIT_VM(8);
+      else
+        AF3_ASM_WAIT_VM(0);
+    } else {
+      if (nk > 1)
+        AF3_ASM_WAIT_VM(12);
+      else
+        AF3_ASM_WAIT_VM(0);
+    }
     AF3_ASM_LDS_BARRIER();
     kstep(0, true, nk > 2);
 #pragma nounroll
     for (int kt = 1; kt < nk; ++kt) {
-      if (kt + 1 < nk)
-        AF3_ASM_WAIT_VM(12);
-      else
-        AF3_ASM_WAIT_VM(0);
+      if constexpr (HALF) {
+        if (kt + 1 < nk)
+          AF3_ASM_WAIT_VM(8);
+        else
+          AF3_ASM_WAIT_VM(0);
+      } else {
+        if (kt + 1 < nk)
+          AF3_ASM_WAIT_VM(12);
+        else
+          AF3_ASM_WAIT_VM(0);
+      }
       AF3_ASM_LDS_BARRIER();
       kstep(kt, false, kt + 2 < nk);
     }
@@ -1851,7 +1883,8 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
       }
     }
   }
-  d5_epilogue<RM, CN, TMW>(p, lds, acc, e, row_lo, nrows, n0, ncols, wn0, rb);
+  // (HALF: smaller batches of the SwiGLU-backward prefetch, within 256 registers)
+  d5_epilogue<RM, CN, TMW, HALF ? 4 : 16>(p, lds, acc, e, row_lo, nrows, n0, ncols, wn0, rb);
 }
 
 template <int BXK>
@@ -1890,6 +1923,33 @@ __global__ __launch_bounds__(256) void gemm5_dgrad_kernel(Params p) {
     else
       d5_tile<false, BXK, 1>(p, lds, e, row_lo, nrows, n0, ncols);
   }
+}
+
+// Input gradient on HALF work items: 128 x 256 tiles of the 128-row map, four
+// waves of 128 x 64 (each weight byte converted once per 128 rows), two blocks
+// per CU, so one block's epilogue (the fused SwiGLU backward's VALU work in
+// the down projection) overlaps the other block's k-loop.
+template <int BXK>
+__global__ __launch_bounds__(256, 2) void gemm8_dgrad_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kD5HLdsBytes];
+  int mt, nt;
+  if (!g4_work_item(p, mt, nt)) return;
+  const int32_t ent = p.tile_map[mt];
+  if (ent < 0) return;
+  const int e = ent & 0xFFFF, blk = ent >> 16;
+  const int row_lo = p.offs[e] + blk * 128;
+  const int nrows = min(128, p.offs[e + 1] - row_lo);
+  if (nrows <= 0) return;
+  const int n0 = nt * 256;
+  const int ncols = min(256, p.N - n0);
+  if (nrows <= 32)
+    d5_tile<false, BXK, 1, 1, true>(p, lds, e, row_lo, nrows, n0, ncols);
+  else if (nrows <= 64)
+    d5_tile<false, BXK, 1, 2, true>(p, lds, e, row_lo, nrows, n0, ncols);
+  else if (nrows <= 96)
+    d5_tile<false, BXK, 1, 3, true>(p, lds, e, row_lo, nrows, n0, ncols);
+  else
+    d5_tile<false, BXK, 1, 0, true>(p, lds, e, row_lo, nrows, n0, ncols);
 }
 
 // ---------------------------------------------------------------------------
@@ -2384,6 +2444,12 @@ inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // exported entry points
 // ---------------------------------------------------------------------------
 
+static void launch_gemm8_dgrad(int max_tiles, int N, hipStream_t stream, Params p) {
+  p.n_nblk = (N + 255) / 256;
+  dim3 grid(g4_grid(max_tiles, p.n_nblk, p.group_m));
+  hipLaunchKernelGGL(gemm8_dgrad_kernel<COLS_BF16>, grid, dim3(256), 0, stream, p);
+}
+
 static void launch_gemm5_dgrad(int max_tiles, int N, hipStream_t stream, Params p) {
   p.n_nblk = (N + kG4Rows - 1) / kG4Rows;
   dim3 grid(g4_grid(max_tiles, p.n_nblk, p.group_m));
@@ -2492,13 +2558,16 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
   //   22: gemm4 forward (256x256 work items, 8 waves of 128x64, two per SIMD,
   //       packed MXFP4 through a three-stage global->LDS ring, converted in
   //       registers); default for trans_w 0 with block_m 256
+  //   28: gemm8 input gradient (gemm5's k-loop on 128x256 items of the 128-row
+  //       map, 4 waves of 128x64, two blocks per CU); default for trans_w 1
+  //       with block_m 128
   //   23: gemm5 input gradient (packed weight rows read with transposing LDS
   //       loads, one three-stage ring for A, B and scales; 4 waves of 256x64);
-  //       default for trans_w 1 when its requirements hold
+  //       default for trans_w 1 with block_m 256
   //   4 / 2: gemm2, 256x256 / 128x256 tiles with the weight dequantised into
   //       LDS (general fallback for block_m 256 / 128)
   //   9: single-buffered 128x128 row tiles (any K % 32 == 0; used when K % 64 != 0)
-  //   tile_cfg / 100 = m-tiles per group of the 22 / 23 / 26 work order (default 4; 2 for 26)
+  //   tile_cfg / 100 = m-tiles per group of the 22 / 23 / 26 / 28 work order (default 4; 2 for 26 / 28)
   int cfg = tile_cfg % 100;
   const int group_m = tile_cfg / 100 > 0 ? tile_cfg / 100 : 4;
   if (cfg == 0) {
@@ -2507,7 +2576,8 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
     const bool g7_fwd = !trans && block_m == 128 && K % kBK == 0 && K / 32 <= kG7MaxG && al16(w_scales) && al16(y) &&
                         ldy % 8 == 0;
     const bool g4_dgrad = trans && block_m == 256 && K % kBK == 0 && N % 64 == 0 && al16(y) && ldy % 8 == 0;
-    cfg = g4_fwd ? 22 : g7_fwd ? 26 : g4_dgrad ? 23 : (block_m == 256 ? 4 : 2);
+    const bool g8_dgrad = trans && block_m == 128 && K % kBK == 0 && N % 64 == 0 && al16(y) && ldy % 8 == 0;
+    cfg = g4_fwd ? 22 : g7_fwd ? 26 : g4_dgrad ? 23 : g8_dgrad ? 28 : (block_m == 256 ? 4 : 2);
   }
   const bool bm_ok = (cfg == 4 || cfg == 22 || cfg == 23) ? block_m == 256 : block_m == 128;
   AF3_REQUIRE(bm_ok, "moe_gemm: tile_cfg %d does not match block_m %d", cfg, block_m);
@@ -2539,7 +2609,7 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
   if (K % kBK != 0) cfg = 9;  // direct A loads need whole 64-deep k-steps
   if (epi != 0) {
     AF3_REQUIRE(glu && (epi == 1 || epi == 2), "moe_gemm: bad SwiGLU epilogue %d", epi);
-    const bool ok = epi == 1 ? (trans && cfg == 23 && ld_glu % 8 == 0 && al16(glu) && ldy >= 2LL * N)
+    const bool ok = epi == 1 ? (trans && (cfg == 23 || cfg == 28) && ld_glu % 8 == 0 && al16(glu) && ldy >= 2LL * N)
                              : (!trans && (cfg == 22 || cfg == 26) && N % 2 == 0 && ld_glu % 4 == 0 &&
                                 ((uintptr_t)glu & 7) == 0);
     if (!ok) {
@@ -2550,8 +2620,8 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
   }
   if (a_row_scale) {
     AF3_REQUIRE(lora_r == 0, "moe_gemm: a row scale cannot be combined with the LoRA extension segment");
-    if (!(cfg == 22 || cfg == 23 || cfg == 26)) {
-      af3::set_error("moe_gemm: the A row scale needs tile_cfg 22, 23 or 26 (got %d)", cfg);
+    if (!(cfg == 22 || cfg == 23 || cfg == 26 || cfg == 28)) {
+      af3::set_error("moe_gemm: the A row scale needs tile_cfg 22, 23, 26 or 28 (got %d)", cfg);
       return AF3_EUNSUPPORTED;
     }
   }
@@ -2576,6 +2646,12 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
                       ldy % 8 == 0,
                   "moe_gemm: tile_cfg 26 needs trans_w 0, block_m 128, K %% 64 == 0, K <= %d, 16-byte aligned", kG7MaxG * 32);
       launch_gemm7_fwd(max_tiles, N, stream, p);
+      break;
+    case 28:
+      p.group_m = tile_cfg / 100 > 0 ? tile_cfg / 100 : 2;
+      AF3_REQUIRE(trans && block_m == 128 && K % kBK == 0 && N % 64 == 0 && al16(y) && ldy % 8 == 0,
+                  "moe_gemm: tile_cfg 28 needs trans_w 1, block_m 128, K %% 64 == 0, N %% 64 == 0, 16-byte aligned y");
+      launch_gemm8_dgrad(max_tiles, N, stream, p);
       break;
     case 23:
       p.group_m = group_m;

@@ -110,11 +110,14 @@ def test_forward_tiles(dev, cfg, nout, gather, lora, odd):
     assert not bad.any(), float(bad.float().mean())
 
 
-@pytest.mark.parametrize("cfg,nout", [(0, NOUT), (4, NOUT), (23, NOUT), (23, 640)])
+@pytest.mark.parametrize("cfg,nout", [(0, NOUT), (0, 640), (4, NOUT), (23, NOUT), (23, 640), (228, NOUT)])
 @pytest.mark.parametrize("gather,lora,odd", CASES)
 def test_dgrad_tiles(dev, cfg, nout, gather, lora, odd):
     """N = 576 / 640 end in a 64- / 128-column n-tile, which the default kernel
-    (tile_cfg 23) runs with the tile's rows split over the waves."""
+    (tile_cfg 23) runs with the tile's rows split over the waves; the default
+    (tile_cfg 0 = 28: 128 x 256 items on the 128-row map, two blocks per CU)
+    sees tails of 10, 44, 50, 60, 100 and 104 rows; 228 is it with two m-tiles
+    per work group."""
     g, ref, rd, gi = _routing(dev, 12)
     blocks, scales = _weights(g, KRED, nout, odd)          # W [E, K, N] packed along N
     Rr = T * TOPK
@@ -123,7 +126,7 @@ def test_dgrad_tiles(dev, cfg, nout, gather, lora, odd):
     Ax = (torch.randn(E, 32, nout, generator=g) * 0.3).to(torch.bfloat16) if lora else None
     gam = rd.gate_scal if gather else None
     old = dict(Q.GEMM_TILE)
-    Q.GEMM_TILE.update(block_m=256, tile_cfg=cfg)
+    Q.GEMM_TILE.update(block_m=128 if cfg % 100 == 28 else 256, tile_cfg=cfg)
     try:
         y = Q.moe_rows(x.to(dev), blocks.to(dev), scales.to(dev), None, rd, gi if gather else None, gam, True,
                        L.to(dev) if lora else None, Ax.to(dev) if lora else None)
@@ -140,8 +143,9 @@ def test_dgrad_tiles(dev, cfg, nout, gather, lora, odd):
     assert not bad.any(), float(bad.float().mean())
 
 
+@pytest.mark.parametrize("dx_cfg", [(0, 256), (23, 256)])
 @pytest.mark.parametrize("lora", [False, True])
-def test_fused_swiglu_epilogues_bit_equal(dev, lora):
+def test_fused_swiglu_epilogues_bit_equal(dev, lora, dx_cfg):
     """af3_moe_gemm_swiglu: the forward epilogue's SwiGLU and the input-gradient
     epilogue's SwiGLU backward equal the separate kernels bit for bit, on full,
     partial and short (two n-tiles per work item) tiles."""
@@ -169,8 +173,14 @@ def test_fused_swiglu_epilogues_bit_equal(dev, lora):
     Ax = (torch.randn(E, r, I_, generator=g) * 0.3).to(torch.bfloat16).to(dev) if lora else None
     gam = rd.gate_scal
     db, ds = dn_blocks.to(dev), dn_scales.to(dev)
-    dgu = Q.moe_rows(dy, db, ds, None, rd, gi, gam, True, u, Ax, swiglu=("bwd", gu, alpha, limit))
-    d_act = Q.moe_rows(dy, db, ds, None, rd, gi, gam, True, u, Ax)
+    old = dict(Q.GEMM_TILE)
+    Q.GEMM_TILE.update(block_m=dx_cfg[1], tile_cfg=dx_cfg[0])
+    try:
+        dgu = Q.moe_rows(dy, db, ds, None, rd, gi, gam, True, u, Ax, swiglu=("bwd", gu, alpha, limit))
+        d_act = Q.moe_rows(dy, db, ds, None, rd, gi, gam, True, u, Ax)
+    finally:
+        Q.GEMM_TILE.clear()
+        Q.GEMM_TILE.update(old)
     assert dgu is not None and dgu.shape == (Rr, 2 * I_)
     assert torch.equal(dgu, kernels.swiglu_backward_raw(d_act, gu, alpha, limit))
 
@@ -182,8 +192,9 @@ def test_fused_swiglu_epilogues_bit_equal(dev, lora):
 COUNTS_RG = [481, 449, 160, 161, 193, 224, 64, 65, 700, 303]
 
 
+@pytest.mark.parametrize("dx_cfg", [(0, 256), (23, 256)])
 @pytest.mark.parametrize("gather", [True, False])
-def test_dgrad_row_group_tails(dev, gather):
+def test_dgrad_row_group_tails(dev, gather, dx_cfg):
     """gemm5's row-group variants (partial m-tiles run only their live 32-row
     groups) against the oracle, LoRA segment and routing weights included."""
     Ec = len(COUNTS_RG)
@@ -207,8 +218,14 @@ def test_dgrad_row_group_tails(dev, gather):
     L = (torch.randn(Rr, 32, generator=g) * 0.3).to(torch.bfloat16)
     Ax = (torch.randn(Ec, 32, NOUT, generator=g) * 0.3).to(torch.bfloat16)
     gam = rd.gate_scal if gather else None
-    y = Q.moe_rows(x.to(dev), blocks.to(dev), scales.to(dev), None, rd, gi if gather else None, gam, True,
-                   L.to(dev), Ax.to(dev))
+    old = dict(Q.GEMM_TILE)
+    Q.GEMM_TILE.update(block_m=dx_cfg[1], tile_cfg=dx_cfg[0])
+    try:
+        y = Q.moe_rows(x.to(dev), blocks.to(dev), scales.to(dev), None, rd, gi if gather else None, gam, True,
+                       L.to(dev), Ax.to(dev))
+    finally:
+        Q.GEMM_TILE.clear()
+        Q.GEMM_TILE.update(old)
     W = mxfp4.dequant_f32(blocks, scales)
     yr = moe.rows(x, W, ref["offs"], ref["topk_indx"] if gather else None, TOPK,
                   gammas=gam.cpu() if gather else None, trans=True, lora_l=L, lora_b=Ax)
