@@ -108,8 +108,28 @@ def convert_moe_packed_tensors(blocks, scales, *, dtype=torch.bfloat16, rows_per
     """
     if dtype != torch.bfloat16:
         raise TypeError("only bf16 dequantisation is implemented")
-    w = mxfp4_to_bf16_hip(blocks.to(torch.uint8), scales.to(torch.uint8))
-    return w.transpose(1, 2).contiguous()
+    blocks, scales = blocks.to(torch.uint8), scales.to(torch.uint8)
+    try:
+        if not blocks.is_cuda:
+            blocks, scales = blocks.cuda(), scales.cuda()
+        return mxfp4_to_bf16_hip(blocks, scales).transpose(1, 2).contiguous()
+    except torch.OutOfMemoryError:
+        # quantization.py:166-172 retries on the CPU when the device runs out of
+        # memory; here the HIP kernel dequantizes one expert at a time and the
+        # weight is assembled in host memory (same values, returned on the CPU).
+        return _convert_per_expert_to_host(blocks, scales)
+
+
+def _convert_per_expert_to_host(blocks, scales):
+    """[E, N, G, 16] + [E, N, G] -> CPU bf16 [E, G*32, N], one expert's weight on the GPU at a time."""
+    dev = blocks.device if blocks.is_cuda else torch.device("cuda", torch.cuda.current_device())
+    E, N, G = scales.shape
+    out = torch.empty(E, G * 32, N, dtype=torch.bfloat16)
+    for e in range(E):
+        w = mxfp4_to_bf16_hip(blocks[e].to(dev), scales[e].to(dev)).t().contiguous()
+        out[e].copy_(w)      # synchronous device-to-host copy; w is freed with the next expert
+        del w
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -1135,8 +1155,6 @@ class Mxfp4Fp8DequantDequantize(_ConversionOps):
     def convert(self, input_dict, model=None, full_layer_name=None, missing_keys=None, **kwargs):
         blocks = _first(input_dict["_blocks"])
         scales = _first(input_dict["_scales"])
-        if not blocks.is_cuda:
-            blocks, scales = blocks.cuda(), scales.cuda()
         return {full_layer_name: convert_moe_packed_tensors(blocks, scales)}
 
 

@@ -82,3 +82,30 @@ def test_convert_moe_packed_tensors_every_scale_byte(dev):
     normal = ((scales >= 2) & (scales <= 252)).repeat_interleave(32, dim=-1).transpose(1, 2)
     assert torch.equal(w.view(torch.int16)[normal], ldexp.view(torch.int16)[normal])
     assert int((~normal).sum()) == 5 * 16 * 32
+
+
+def test_convert_moe_packed_tensors_out_of_memory_path(dev, monkeypatch):
+    """quantization.py:166-172: when the whole-stack dequant runs out of device
+    memory the weight is still produced, on the CPU.  The out-of-memory error is
+    raised from the host (the whole-stack call is refused); the per-expert HIP
+    path must give the same bytes as the normal path, for device and host input."""
+    g = torch.Generator().manual_seed(6)
+    blocks = torch.randint(0, 256, (3, 96, 5, 16), generator=g).to(torch.uint8)
+    scales = torch.randint(110, 140, (3, 96, 5), generator=g).to(torch.uint8)
+    full = quantization.convert_moe_packed_tensors(blocks.to(dev), scales.to(dev)).cpu()
+    real = quantization.mxfp4_to_bf16_hip
+    calls = []
+
+    def refuse_whole_stack(b, s):
+        calls.append(tuple(b.shape))
+        if b.dim() == 4:
+            raise torch.OutOfMemoryError("HIP out of memory (refused by the test)")
+        return real(b, s)
+
+    monkeypatch.setattr(quantization, "mxfp4_to_bf16_hip", refuse_whole_stack)
+    for src in (blocks.to(dev), blocks):
+        calls.clear()
+        w = quantization.convert_moe_packed_tensors(src, scales.to(src.device))
+        assert w.device.type == "cpu" and w.shape == (3, 160, 96)
+        assert torch.equal(w.view(torch.int16), full.view(torch.int16))
+        assert calls == [(3, 96, 5, 16)] + [(96, 5, 16)] * 3
