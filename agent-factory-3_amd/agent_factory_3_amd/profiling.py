@@ -43,8 +43,8 @@ COPY_BYTES = 512 * 1024 * 1024
 COPY_KERNEL = "MulFunctor"
 
 # grouped-GEMM entry points timed by bench.py -> the kernel their default tile
-# configuration launches (forward: tile_cfg 22, input gradient: tile_cfg 23)
-GEMM_KERNELS = {"moe_gemm_fwd": "gemm4_fwd_kernel", "moe_gemm_dgrad": "gemm5_dgrad_kernel"}
+# configuration launches (forward: tile_cfg 26, input gradient: tile_cfg 28)
+GEMM_KERNELS = {"moe_gemm_fwd": "gemm7_fwd_kernel", "moe_gemm_dgrad": "gemm8_dgrad_kernel"}
 
 
 def short_name(name: str) -> str:

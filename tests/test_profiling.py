@@ -42,7 +42,7 @@ def test_ktrace_window_and_entry_point_average(tmp_path):
         w.writeheader()
         # one dispatch before the range (slow, cold), two inside: grids of both GEMM shapes
         for s, e, g in ((0, 9000, 64), (10000, 12000, 64), (20000, 21000, 32), (30000, 39000, 64)):
-            w.writerow({"Kernel_Name": "void gemm4_fwd_kernel<2, 4, 0>(Params)", "Grid_Size_X": g,
+            w.writerow({"Kernel_Name": "void gemm7_fwd_kernel<0>(Params)", "Grid_Size_X": g,
                         "Start_Timestamp": s, "End_Timestamp": e})
     with open(mk, "w", newline="") as f:
         w = csv.DictWriter(f, ["Domain", "Function", "Start_Timestamp", "End_Timestamp"])
@@ -53,9 +53,9 @@ def test_ktrace_window_and_entry_point_average(tmp_path):
     win = profiling.marker_window(str(mk), "bench_timed")
     assert win == (9500, 25000)
     table = profiling.ktrace(str(kt), win)
-    assert "| `gemm4_fwd_kernel<2, 4, 0>` | 64 | 1 | 2.00 |" in table
-    assert "| moe_gemm_fwd | `gemm4_fwd_kernel` | 2 | 1.50 |" in table
-    assert "| moe_gemm_fwd | `gemm4_fwd_kernel` | 4 | 5.25 |" in profiling.ktrace(str(kt))
+    assert "| `gemm7_fwd_kernel<0>` | 64 | 1 | 2.00 |" in table
+    assert "| moe_gemm_fwd | `gemm7_fwd_kernel` | 2 | 1.50 |" in table
+    assert "| moe_gemm_fwd | `gemm7_fwd_kernel` | 4 | 5.25 |" in profiling.ktrace(str(kt))
 
 
 def test_mfma_busy_share_normalisation(tmp_path):
