@@ -133,7 +133,12 @@ int af3_tile_order(const int32_t* hist, int n_expts_tot, int block_m, const int3
  * are [token_offs[e], token_offs[e+1]); block_pid_map / tile_offs are the
  * af3_expt_data map and token_offs_pad for BM = block_m (128 or 256); the
  * number of valid m-tiles is read from tile_offs[n_expts] on the device.
- * tile_cfg picks the block tile (0 = default for block_m). */
+ * tile_cfg picks the block tile; 0 = the default for block_m and trans_w:
+ * block_m 128 -> 26 (forward, 128 x 256 work items, two blocks per CU) and
+ * 28 (input gradient, same shape); block_m 256 -> 22 / 23 (256 x 256); the
+ * general fallbacks 4 / 2 / 9 where a default's alignment or K % 64 == 0
+ * requirement fails.  tile_cfg / 100 = m-tiles per work group of the
+ * 22 / 23 / 26 / 28 order (default 4; 2 for 26 / 28). */
 int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
                  const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
                  const void* gammas, int gammas_f32, const uint16_t* lora_l, int64_t ld_l, const uint16_t* lora_b,
@@ -151,7 +156,8 @@ int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int
  * 516-525, 432-439: epi 2, trans_w 0, y <- the bf16 pre-activation [rows][N]
  * and glu <- its SwiGLU [rows][N/2]).  Results equal the unfused sequence bit
  * for bit.  Returns AF3_EUNSUPPORTED (-2) when the selected tile configuration
- * has no fused epilogue; the caller then runs the unfused pair. */
+ * has no fused epilogue (epi 2: tile_cfg 22 / 26, epi 1: 23 / 28); the caller
+ * then runs the unfused pair. */
 int af3_moe_gemm_swiglu(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
                         const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
                         const void* gammas, int gammas_f32, const uint16_t* lora_l, int64_t ld_l,
@@ -167,7 +173,7 @@ int af3_moe_gemm_swiglu(const uint16_t* x, int64_t ldx, const int32_t* gather_in
  * scale_mode="per_token")) in the fp8 mode, quantization.py:338-356 (forward)
  * and 382-408 (dX), fed with the E4M3 codes' values as bf16.  Returns
  * AF3_EUNSUPPORTED (-2) when the selected tile configuration has no scaled
- * epilogue (only the default kernels, tile_cfg 20-23, have one). */
+ * epilogue (only tile_cfg 22, 23, 26 and 28 have one). */
 int af3_moe_gemm_rowscale(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
                           const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
                           const void* gammas, int gammas_f32, const int32_t* token_offs, const int32_t* block_pid_map,
