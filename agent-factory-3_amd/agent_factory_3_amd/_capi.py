@@ -56,6 +56,9 @@ _SIGNATURES = {
                                    _i64, _p]),
     "af3_lm_head_dlogits_range": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _p, _f32, _p, _p, _p, _i64, _f32,
                                          _p, _p, _i64, _p]),
+    "af3_lm_head_chunk_stats": (_i32, [_p, _i64, _i32, _i32, _i32, _p, _f32, _p, _p, _p]),
+    "af3_lm_head_reduce": (_i32, [_p, _i32, _i32, _p, _p, _i32, _p, _p, _p, _p, _p]),
+    "af3_lm_head_dz_chunk": (_i32, [_p, _i64, _i32, _i32, _i32, _p, _f32, _p, _p, _p, _i64, _f32, _p, _p, _i64, _p]),
     "af3_gamma_grad": (_i32, [_p, _i64, _p, _i64, _i32, _p, _i64, _p, _i32, _p, _i32, _p, _i32, _p, _i64, _p, _p]),
     "af3_mxfp4_lora_merge": (_i32, [_p, _p, _p, _p, _f32, _p, _i32, _i32, _i32, _i32, _i32, _p]),
     "af3_lora_rows": (_i32, [_p, _i64, _p, _i32, _p, _i32, _f32, _p, _p, _i32, _i32, _i32, _i32,

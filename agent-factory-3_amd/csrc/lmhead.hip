@@ -26,7 +26,8 @@
 //   LDS) -> partials [n_vtiles][M] float4; the row's label logit is stored by
 //   the one lane that holds it.
 //   MODE 1: dz for the tile from the row statistics of the forward, bf16.
-// lmh_reduce_kernel combines the partials of a row (running max rescaling).
+// lmh_reduce_kernel combines the partials of a row (running max rescaling,
+// 16 lanes per row and a fixed merge tree).
 #include "af3_common.h"
 
 namespace {
@@ -291,28 +292,51 @@ __global__ __launch_bounds__(kLmThreads, 1) void lmh_gemm_kernel(
   }
 }
 
+// Combine of the per-tile (or per-chunk) partials of each row: block = 16 rows
+// x 16 lanes; lane q of a row merges partials q, q + 16, ... in order, then the
+// 16 lanes' results are merged pairwise by shuffles (a fixed tree, so the
+// result does not depend on timing).  Merge of (m1, s1, t1) and (m2, s2, t2):
+// m = max, s = s1 e^(m1 - m) + s2 e^(m2 - m), t likewise.
+__device__ __forceinline__ void lmh_merge(float& m, float& s, float& t, float m2, float s2, float t2) {
+  if (m2 == -INFINITY) return;
+  if (m2 > m) {
+    const float f = __expf(m - m2);  // 0 while m = -inf
+    s = s * f + s2;
+    t = t * f + t2;
+    m = m2;
+  } else {
+    const float f = __expf(m2 - m);
+    s += s2 * f;
+    t += t2 * f;
+  }
+}
+
 __global__ __launch_bounds__(256) void lmh_reduce_kernel(const float4* __restrict__ partials, int M, int n_vtiles,
                                                          const float* __restrict__ zlab,
                                                          const int64_t* __restrict__ labels, int V,
                                                          float* __restrict__ logprobs, float* __restrict__ entropy,
                                                          float* __restrict__ lse, float* __restrict__ ez) {
-  const int row = blockIdx.x * 256 + threadIdx.x;
-  if (row >= M) return;
+  const int q = threadIdx.x & 15;
+  const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int rr = min(row, M - 1);  // rows past the end take part in the shuffles, store nothing
   float mx = -INFINITY, s = 0.f, t = 0.f;
-  for (int j = 0; j < n_vtiles; ++j) {
-    const float4 p = partials[(int64_t)j * M + row];
-    if (p.x == -INFINITY) continue;
-    if (p.x > mx) {
-      const float f = __expf(mx - p.x);  // 0 on the first tile (mx = -inf)
-      s = s * f + p.y;
-      t = t * f + p.z;
-      mx = p.x;
+  for (int j = q; j < n_vtiles; j += 16) {
+    const float4 p = partials[(int64_t)j * M + rr];
+    lmh_merge(mx, s, t, p.x, p.y, p.z);
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) {
+    const float m2 = __shfl_xor(mx, o), s2 = __shfl_xor(s, o), t2 = __shfl_xor(t, o);
+    // both lanes of a pair merge in the same order (lower lane's values first)
+    if (q & o) {
+      float mm = m2, ss = s2, tt = t2;
+      lmh_merge(mm, ss, tt, mx, s, t);
+      mx = mm, s = ss, t = tt;
     } else {
-      const float f = __expf(p.x - mx);
-      s += p.y * f;
-      t += p.z * f;
+      lmh_merge(mx, s, t, m2, s2, t2);
     }
   }
+  if (q != 0 || row >= M) return;
   const float l = mx + __logf(s);
   const float e = t / s;
   const int64_t lab = labels[row];
@@ -321,6 +345,120 @@ __global__ __launch_bounds__(256) void lmh_reduce_kernel(const float4* __restric
   entropy[row] = l - e;
   lse[row] = l;
   ez[row] = e;
+}
+
+// Statistics of one vocabulary chunk of fp32 logits that a library GEMM wrote
+// (logits [M][ldl], column j = entry v_begin + j): one wave per row, each lane
+// a running (max, sum exp, sum exp * z) over its float4 groups (1 KB per wave
+// load), then the wave's max, each lane's sums rescaled to it, and the wave's
+// sums by shuffles; the row's label logit when its label lies in the chunk.
+// Same partial as one column tile of lmh_gemm_kernel<0>, so lmh_reduce_kernel
+// combines them.
+__device__ __forceinline__ float lmh_wave_max(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float lmh_wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__global__ __launch_bounds__(256) void lmh_chunk_stats_kernel(const float* __restrict__ logits, int64_t ldl, int M,
+                                                              int n, int v_begin, const int64_t* __restrict__ labels,
+                                                              float rcp_t, bool vec, float4* __restrict__ partial,
+                                                              float* __restrict__ zlab) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const float* zr = logits + (int64_t)row * ldl;
+  float m = -INFINITY, s = 0.f, t = 0.f;
+  auto add4 = [&](float x0, float x1, float x2, float x3) {
+    const float lm = fmaxf(fmaxf(x0, x1), fmaxf(x2, x3));
+    if (lm > m) {
+      const float f = __expf(m - lm);  // 0 while m = -inf
+      s *= f;
+      t *= f;
+      m = lm;
+    }
+    const float e0 = __expf(x0 - m), e1 = __expf(x1 - m), e2 = __expf(x2 - m), e3 = __expf(x3 - m);
+    s += (e0 + e1) + (e2 + e3);
+    t += (e0 * x0 + e1 * x1) + (e2 * x2 + e3 * x3);
+  };
+  int c0 = 0;
+  if (vec) {  // 16-byte aligned rows: float4 groups, four in flight per lane, the tail below
+    const int n4 = n >> 2;
+    const float4* z4 = (const float4*)zr;
+    int i = lane;
+    for (; i + 192 < n4; i += 256) {
+      const float4 a = z4[i], b = z4[i + 64], c = z4[i + 128], d = z4[i + 192];
+      add4(a.x * rcp_t, a.y * rcp_t, a.z * rcp_t, a.w * rcp_t);
+      add4(b.x * rcp_t, b.y * rcp_t, b.z * rcp_t, b.w * rcp_t);
+      add4(c.x * rcp_t, c.y * rcp_t, c.z * rcp_t, c.w * rcp_t);
+      add4(d.x * rcp_t, d.y * rcp_t, d.z * rcp_t, d.w * rcp_t);
+    }
+    for (; i < n4; i += 64) {
+      const float4 a = z4[i];
+      add4(a.x * rcp_t, a.y * rcp_t, a.z * rcp_t, a.w * rcp_t);
+    }
+    c0 = n4 * 4;
+  }
+  for (int c = c0 + lane; c < n; c += 64) {
+    const float x = zr[c] * rcp_t;
+    if (x > m) {
+      const float f = __expf(m - x);
+      s *= f;
+      t *= f;
+      m = x;
+    }
+    const float e = __expf(x - m);
+    s += e;
+    t += e * x;
+  }
+  const float mw = lmh_wave_max(m);
+  const float f = m == -INFINITY ? 0.f : __expf(m - mw);
+  const float sw = lmh_wave_sum(s * f);
+  const float tw = lmh_wave_sum(t * f);
+  if (lane == 0) {
+    partial[row] = make_float4(mw, sw, tw, 0.f);
+    const int64_t lab = labels[row];
+    if (lab >= v_begin && lab < (int64_t)v_begin + n) zlab[row] = zr[lab - v_begin] * rcp_t;
+  }
+}
+
+// Logits gradient of one vocabulary chunk from its fp32 logits (the formula of
+// lmh_gemm_kernel<1>'s epilogue): block = (row, 2048 columns), 8 columns per
+// thread, one 16-byte store of bf16 where the row allows it.
+__global__ __launch_bounds__(256) void lmh_chunk_dz_kernel(const float* __restrict__ logits, int64_t ldl, int n,
+                                                           int v_begin, int n_cb, const int64_t* __restrict__ labels,
+                                                           float rcp_t, const float* __restrict__ lse,
+                                                           const float* __restrict__ ez,
+                                                           const float* __restrict__ dlp, int64_t dlp_stride,
+                                                           float dlp_scale, const float* __restrict__ dent,
+                                                           uint16_t* __restrict__ dz, int64_t lddz, bool vec) {
+  const int row = blockIdx.x / n_cb;
+  const int c = (blockIdx.x % n_cb) * 2048 + threadIdx.x * 8;
+  if (c >= n) return;
+  const float l_ = lse[row], e_ = ez[row], g_ = dlp[(int64_t)row * dlp_stride] * dlp_scale, h_ = dent[row];
+  const int64_t lab64 = labels[row];
+  const int lab = lab64 >= v_begin && lab64 < (int64_t)v_begin + n ? (int)(lab64 - v_begin) : -1;
+  const float* zr = logits + (int64_t)row * ldl;
+  uint16_t* dr = dz + (int64_t)row * lddz;
+  auto grad = [&](float zv, int j) {
+    const float x = zv * rcp_t;
+    const float p = __expf(x - l_);
+    return (g_ * ((j == lab ? 1.f : 0.f) - p) - h_ * p * (x - e_)) * rcp_t;
+  };
+  if (vec && c + 8 <= n) {
+    const float4 a = *(const float4*)(zr + c), b = *(const float4*)(zr + c + 4);
+    af3_u32x4 o;
+    o[0] = af3_f32_to_bf16(grad(a.x, c)) | (af3_f32_to_bf16(grad(a.y, c + 1)) << 16);
+    o[1] = af3_f32_to_bf16(grad(a.z, c + 2)) | (af3_f32_to_bf16(grad(a.w, c + 3)) << 16);
+    o[2] = af3_f32_to_bf16(grad(b.x, c + 4)) | (af3_f32_to_bf16(grad(b.y, c + 5)) << 16);
+    o[3] = af3_f32_to_bf16(grad(b.z, c + 6)) | (af3_f32_to_bf16(grad(b.w, c + 7)) << 16);
+    *(af3_u32x4*)(dr + c) = o;
+  } else {
+    for (int j = c; j < min(c + 8, n); ++j) dr[j] = (uint16_t)af3_f32_to_bf16(grad(zr[j], j));
+  }
 }
 
 int lmh_grid(int M, int V, int& n_mtiles, int& n_vtiles, int& per_xcd) {
@@ -365,7 +503,7 @@ extern "C" int af3_lm_head_logprobs(const uint16_t* hidden, int64_t ldh, const u
                        nullptr, nullptr, 0, 0);
   int rc = af3::check_launch("lm_head_logprobs (gemm)");
   if (rc) return rc;
-  hipLaunchKernelGGL(lmh_reduce_kernel, dim3((unsigned)af3_cdiv(M, 256)), dim3(256), 0, stream, partials, M, nv, zlab,
+  hipLaunchKernelGGL(lmh_reduce_kernel, dim3((unsigned)af3_cdiv(M, 16)), dim3(256), 0, stream, partials, M, nv, zlab,
                      labels, V, logprobs, entropy, lse, ez);
   return af3::check_launch("lm_head_logprobs (reduce)");
 }
@@ -404,4 +542,50 @@ extern "C" int af3_lm_head_dlogits(const uint16_t* hidden, int64_t ldh, const ui
                                    const float* dentropy, uint16_t* dz, int64_t lddz, void* stream) {
   return af3_lm_head_dlogits_range(hidden, ldh, weight, ldw, M, 0, V, H, labels, temperature, lse, ez, dlogprobs,
                                    dlp_stride, dlp_scale, dentropy, dz, lddz, stream);
+}
+
+extern "C" int af3_lm_head_chunk_stats(const float* logits, int64_t ldl, int M, int v_begin, int v_count,
+                                       const int64_t* labels, float temperature, void* partial, float* zlab,
+                                       void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  AF3_REQUIRE(M >= 0 && v_begin >= 0 && v_count > 0 && ldl >= v_count, "lm_head_chunk_stats: bad shape");
+  if (M == 0) return 0;
+  AF3_REQUIRE(logits && labels && partial && zlab, "lm_head_chunk_stats: null pointer");
+  AF3_REQUIRE(temperature > 0.f, "lm_head_chunk_stats: temperature must be positive");
+  AF3_REQUIRE(((uintptr_t)partial & 15) == 0, "lm_head_chunk_stats: partials must be 16-byte aligned");
+  const bool vec = ((uintptr_t)logits & 15) == 0 && ldl % 4 == 0;
+  hipLaunchKernelGGL(lmh_chunk_stats_kernel, dim3((unsigned)af3_cdiv(M, 4)), dim3(256), 0, stream, logits, ldl, M,
+                     v_count, v_begin, labels, 1.f / temperature, vec, (float4*)partial, zlab);
+  return af3::check_launch("lm_head_chunk_stats");
+}
+
+extern "C" int af3_lm_head_reduce(const void* partials, int M, int n_parts, const float* zlab, const int64_t* labels,
+                                  int V, float* logprobs, float* entropy, float* lse, float* ez, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  AF3_REQUIRE(M >= 0 && n_parts > 0 && V > 0, "lm_head_reduce: bad shape");
+  if (M == 0) return 0;
+  AF3_REQUIRE(partials && zlab && labels && logprobs && entropy && lse && ez, "lm_head_reduce: null pointer");
+  AF3_REQUIRE(((uintptr_t)partials & 15) == 0, "lm_head_reduce: partials must be 16-byte aligned");
+  hipLaunchKernelGGL(lmh_reduce_kernel, dim3((unsigned)af3_cdiv(M, 16)), dim3(256), 0, stream,
+                     (const float4*)partials, M, n_parts, zlab, labels, V, logprobs, entropy, lse, ez);
+  return af3::check_launch("lm_head_reduce");
+}
+
+extern "C" int af3_lm_head_dz_chunk(const float* logits, int64_t ldl, int M, int v_begin, int v_count,
+                                    const int64_t* labels, float temperature, const float* lse, const float* ez,
+                                    const float* dlogprobs, int64_t dlp_stride, float dlp_scale,
+                                    const float* dentropy, uint16_t* dz, int64_t lddz, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  AF3_REQUIRE(M >= 0 && v_begin >= 0 && v_count > 0 && ldl >= v_count && lddz >= v_count,
+              "lm_head_dz_chunk: bad shape");
+  if (M == 0) return 0;
+  AF3_REQUIRE(logits && labels && lse && ez && dlogprobs && dentropy && dz, "lm_head_dz_chunk: null pointer");
+  AF3_REQUIRE(temperature > 0.f, "lm_head_dz_chunk: temperature must be positive");
+  const int n_cb = (int)af3_cdiv(v_count, 2048);
+  AF3_REQUIRE((int64_t)M * n_cb <= 0x7fffffffLL, "lm_head_dz_chunk: too many rows");
+  const bool vec = ((uintptr_t)logits & 15) == 0 && ldl % 4 == 0 && ((uintptr_t)dz & 15) == 0 && lddz % 8 == 0;
+  hipLaunchKernelGGL(lmh_chunk_dz_kernel, dim3((unsigned)(M * n_cb)), dim3(256), 0, stream, logits, ldl, v_count,
+                     v_begin, n_cb, labels, 1.f / temperature, lse, ez, dlogprobs, dlp_stride, dlp_scale, dentropy, dz,
+                     lddz, vec);
+  return af3::check_launch("lm_head_dz_chunk");
 }

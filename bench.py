@@ -323,10 +323,15 @@ def gamma_extras(torch, dev, workloads, inp_cpu, k, steps=10):
 
 
 def lm_head_extras(torch, dev, M=8192, H=2880, V=201088, reps=3):
-    """The fused LM-head log-probabilities / entropy at the gpt-oss vocabulary:
-    forward kernel (GEMM + softmax statistics, no logits written), the
-    logits-gradient kernel, the whole forward + backward, and a plain hipBLASLt
-    bf16 GEMM of the same shape (logits written) for comparison."""
+    """The LM-head log-probabilities / entropy at the gpt-oss vocabulary, in the
+    default modes (``linear_cross_entropy.LOGITS_GEMM`` for the forward,
+    ``DLOGITS_GEMM`` for the backward: "library" = fp32 logits of each
+    vocabulary chunk from a plain GEMM, then the statistics / gradient kernels;
+    "fused" = the GEMM kernel with the softmax statistics or the logits
+    gradient in its epilogue, no logits written) and with both library / both
+    fused: the forward, the backward alone (split logits gradient, two GEMMs
+    per split), forward + backward; the whole-vocabulary logits gradient, and a
+    plain hipBLASLt bf16 GEMM of the same shape (logits written) for comparison."""
     from agent_factory_3_amd import linear_cross_entropy as lce
     g = torch.Generator().manual_seed(3)
     h = torch.randn(M, H, generator=g).to(torch.bfloat16).to(dev)
@@ -346,35 +351,51 @@ def lm_head_extras(torch, dev, M=8192, H=2880, V=201088, reps=3):
         torch.cuda.synchronize()
         return t0.elapsed_time(t1) / reps
 
-    res = {"shape": {"tokens": M, "hidden": H, "vocab": V}}
-    ms = timed(lambda: lce.lm_head_forward(h, w, lab, 1.0))
-    res["forward"] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12}
-    _, _, lse, ez = lce.lm_head_forward(h, w, lab, 1.0)
     dlp = torch.randn(M, device=dev)
     dent = torch.randn(M, device=dev)
-    ms = timed(lambda: lce.lm_head_dlogits(h, w, lab, 1.0, lse, ez, dlp, dent))
-    res["dlogits"] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12}
     hh = h.detach().requires_grad_(True)
     ww = w.detach().requires_grad_(True)
 
     def fwd_bwd():
         lp, ent = lce.linear_cross_entropy(hh, ww, lab, 1.0, "none")
         torch.autograd.backward([lp, ent], [dlp, dent])
-    ms = timed(fwd_bwd)
-    res["fwd_bwd"] = {"ms": ms, "tflops": 4 * flops / (ms * 1e-3) / 1e12}
-    # the backward alone (logits recomputed, split gradient, two GEMMs per split) and its
-    # memory beyond the inputs, against forming the whole [M, V] gradient first
-    torch.cuda.synchronize()
-    base = torch.cuda.memory_allocated(dev)
-    torch.cuda.reset_peak_memory_stats(dev)
-    ms = timed(lambda: lce.lm_head_backward(h, w, lab, 1.0, lse, ez, dlp, dent))
-    res["backward_split"] = {"ms": ms, "tflops": 3 * flops / (ms * 1e-3) / 1e12, "split": lce.vocab_split(M, V),
-                             "peak_extra_bytes": torch.cuda.max_memory_allocated(dev) - base}
+
+    def mode_figures():
+        r = {}
+        ms = timed(lambda: lce.lm_head_forward(h, w, lab, 1.0))
+        r["forward"] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12}
+        _, _, lse, ez = lce.lm_head_forward(h, w, lab, 1.0)
+        ms = timed(fwd_bwd)
+        r["fwd_bwd"] = {"ms": ms, "tflops": 4 * flops / (ms * 1e-3) / 1e12}
+        # the backward alone and its memory beyond the inputs
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated(dev)
+        torch.cuda.reset_peak_memory_stats(dev)
+        ms = timed(lambda: lce.lm_head_backward(h, w, lab, 1.0, lse, ez, dlp, dent))
+        r["backward_split"] = {"ms": ms, "tflops": 3 * flops / (ms * 1e-3) / 1e12, "split": lce.vocab_split(M, V),
+                               "peak_extra_bytes": torch.cuda.max_memory_allocated(dev) - base}
+        return r, lse, ez
+
+    default = (lce.LOGITS_GEMM, lce.DLOGITS_GEMM)
+    res = {"shape": {"tokens": M, "hidden": H, "vocab": V}, "mode": "/".join(default),
+           "logits_chunk": lce.logits_chunk(M, V)}
+    r, lse, ez = mode_figures()
+    res.update(r)
+    try:
+        for modes in (("library", "library"), ("fused", "fused")):
+            if modes != default:
+                lce.LOGITS_GEMM, lce.DLOGITS_GEMM = modes
+                res["/".join(modes)], _, _ = mode_figures()
+    finally:
+        lce.LOGITS_GEMM, lce.DLOGITS_GEMM = default
+    ms = timed(lambda: lce.lm_head_dlogits(h, w, lab, 1.0, lse, ez, dlp, dent))
+    res["dlogits_whole_vocab"] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12}
 
     def whole():
         dz = lce.lm_head_dlogits(h, w, lab, 1.0, lse, ez, dlp, dent)
         return torch.mm(dz, w), torch.mm(dz.t(), h)
     torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated(dev)
     torch.cuda.reset_peak_memory_stats(dev)
     ms = timed(whole)
     res["backward_whole_vocab"] = {"ms": ms, "tflops": 3 * flops / (ms * 1e-3) / 1e12,

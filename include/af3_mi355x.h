@@ -322,6 +322,30 @@ int af3_lm_head_dlogits_range(const uint16_t* hidden, int64_t ldh, const uint16_
                               const float* lse, const float* ez, const float* dlogprobs, int64_t dlp_stride,
                               float dlp_scale, const float* dentropy, uint16_t* dz, int64_t lddz, void* stream);
 
+/* The forward's statistics when the logits of a vocabulary chunk come from a
+ * library GEMM (fp32 output): the per-row softmax partial of the columns
+ * v_begin .. v_begin + v_count - 1 of z = logits [M][ldl] / temperature, the
+ * online max / sum-exp of the reference's forward kernel (trainer/losses/
+ * kernels.py:296-385) over one chunk: partial [M] float4 = (max, sum exp(z -
+ * max), sum exp(z - max) z, 0); zlab[m] = z[m][labels[m]] for the rows whose
+ * label lies in the chunk (other rows untouched).  af3_lm_head_reduce combines
+ * n_parts such partials per row ([n_parts][M] float4) into logprobs, entropy,
+ * lse and ez exactly as af3_lm_head_logprobs does (a label outside [0, V)
+ * contributes z = 0). */
+int af3_lm_head_chunk_stats(const float* logits, int64_t ldl, int M, int v_begin, int v_count, const int64_t* labels,
+                            float temperature, void* partial, float* zlab, void* stream);
+int af3_lm_head_reduce(const void* partials, int M, int n_parts, const float* zlab, const int64_t* labels, int V,
+                       float* logprobs, float* entropy, float* lse, float* ez, void* stream);
+
+/* af3_lm_head_dlogits_range's logits gradient from precomputed fp32 logits of
+ * the chunk (logits [M][ldl], column j = entry v_begin + j): the d_logits of
+ * trainer/losses/kernels.py:829-839 per split (1528-1585) when a library GEMM
+ * recomputed the split's logits. */
+int af3_lm_head_dz_chunk(const float* logits, int64_t ldl, int M, int v_begin, int v_count, const int64_t* labels,
+                         float temperature, const float* lse, const float* ez, const float* dlogprobs,
+                         int64_t dlp_stride, float dlp_scale, const float* dentropy, uint16_t* dz, int64_t lddz,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

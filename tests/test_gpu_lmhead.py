@@ -1,10 +1,13 @@
-"""Fused LM-head log-probabilities / entropy (linear_cross_entropy) on the GPU
-against oracle/lmhead.py on the same bf16 inputs: forward values (the GEMM
-accumulates in fp32, so only summation order separates it from float64),
-the logits gradient per vocabulary split (bit-equal to the whole-vocabulary
-kernel), gradients of hidden and weight through the split backward, the three
-reductions, out-of-range labels, partial row / vocabulary tiles and the full
-gpt-oss vocabulary (201,088)."""
+"""LM-head log-probabilities / entropy (linear_cross_entropy) on the GPU
+against oracle/lmhead.py on the same bf16 inputs, in both logits modes
+(library: fp32 logits of each vocabulary chunk from a plain GEMM, then the
+statistics / gradient kernels; fused: the GEMM kernel with them in its
+epilogue): forward values (the GEMMs accumulate in fp32, so only summation
+order separates them from float64), the fused logits gradient per vocabulary
+split (bit-equal to the whole-vocabulary kernel), gradients of hidden and
+weight through the split backward, the three reductions, out-of-range labels,
+partial row / vocabulary tiles, chunks that split the vocabulary raggedly and
+rows the vector loads cannot take, and the full gpt-oss vocabulary (201,088)."""
 import pytest
 import torch
 
@@ -26,7 +29,9 @@ def _inputs(M, H, V, seed, scale=0.05):
 
 
 def _close(got, ref, atol, rtol):
+    """Fraction of elements outside atol + rtol |ref| (a non-finite value fails)."""
     got = got.detach().float().cpu().double()
+    assert torch.isfinite(got).all(), "non-finite values"
     return float(((got - ref).abs() > atol + rtol * ref.abs()).float().mean())
 
 
@@ -36,12 +41,26 @@ def _split(monkeypatch, M, cols):
     assert lce.vocab_split(M, 10 ** 6) == cols
 
 
+def _mode(monkeypatch, mode, M, chunk):
+    """Logits modes "forward/backward"; library chunks of ``chunk`` vocabulary columns."""
+    fwd, bwd = mode.split("/")
+    monkeypatch.setattr(lce, "LOGITS_GEMM", fwd)
+    monkeypatch.setattr(lce, "DLOGITS_GEMM", bwd)
+    if chunk:
+        monkeypatch.setattr(lce, "CHUNK_BYTES", 4 * M * chunk)
+        assert lce.logits_chunk(M, 10 ** 6) == chunk
+
+
+MODES = [("library/library", 256), ("library/fused", 0), ("fused/fused", 0), ("fused/library", 0)]
+
+
 def _check_grads(hd, wd, h, w, lab, T, dlp, dent, hr, wr, lse, ez, what):
     """d_hidden / d_weight against (1) the exact float64 gradients, within the
     north-star tolerance scaled to the gradient's size (the bf16 logits gradient
     is the only rounding that separates them), and (2) the same GEMMs in float64
-    over the GPU's own bf16 logits gradient (whole-vocabulary kernel), within a
-    bf16 output rounding plus the fp32 accumulation allowance."""
+    over the GPU's own bf16 logits gradient (the mode's lm_head_dlogits, which
+    forms the values the backward forms), within a bf16 output rounding plus
+    the fp32 accumulation allowance."""
     for got, ref in ((hd.grad, hr.grad), (wd.grad, wr.grad)):
         scale = float(ref.abs().max())
         check_close(got, ref, rtol=2e-2, atol=1e-2 * scale, what=f"{what} vs float64")
@@ -55,14 +74,16 @@ def _check_grads(hd, wd, h, w, lab, T, dlp, dent, hr, wr, lse, ez, what):
                 what=f"{what} d_weight vs the GEMM over the GPU logits gradient")
 
 
+@pytest.mark.parametrize("mode,chunk", MODES)
 @pytest.mark.parametrize("M,H,V,T,cols", [(300, 128, 1000, 1.0, 256), (257, 96, 513, 0.7, 512),
                                           (64, 64, 256, 1.3, 256), (300, 128, 1000, 1.0, 1024)])
-def test_forward_and_backward(dev, monkeypatch, M, H, V, T, cols):
+def test_forward_and_backward(dev, monkeypatch, M, H, V, T, cols, mode, chunk):
     h, w, lab = _inputs(M, H, V, seed=M + V)
     lab[5] = -100
     lab[6], lab[7], lab[8] = 255, 256, V - 1  # the last and first column of two splits, the last entry
     _split(monkeypatch, M, cols)
-    print(f"lm_head M={M} H={H} V={V} T={T} split={cols}", flush=True)
+    _mode(monkeypatch, mode, M, chunk)
+    print(f"lm_head M={M} H={H} V={V} T={T} split={cols} {mode} chunk={chunk}", flush=True)
     hd = h.to(dev).requires_grad_(True)
     wd = w.to(dev).requires_grad_(True)
     lp, ent = linear_cross_entropy(hd, wd, lab.to(dev), T, "none")
@@ -82,10 +103,11 @@ def test_forward_and_backward(dev, monkeypatch, M, H, V, T, cols):
     _check_grads(hd, wd, h, w, lab, T, dlp, dent, hr, wr, lse, ez, f"M={M} V={V} split={cols}")
 
 
-def test_dlogits_range_equals_whole_vocabulary_columns(dev):
+def test_dlogits_range_equals_whole_vocabulary_columns(dev, monkeypatch):
     """The per-split kernel reproduces the whole-vocabulary logits gradient's
     columns bit for bit (same 256-column tiles, same k order), labels mapped
     into the split, for splits that start on any 256-column tile."""
+    monkeypatch.setattr(lce, "DLOGITS_GEMM", "fused")
     M, H, V, T = 200, 96, 1300, 0.9
     h, w, lab = _inputs(M, H, V, seed=21)
     lab[:6] = torch.tensor([0, 255, 256, 511, 512, V - 1])
@@ -105,11 +127,13 @@ def test_dlogits_range_equals_whole_vocabulary_columns(dev):
         assert (dz[:, n:] == 7.0).all(), "columns past the split untouched"
 
 
+@pytest.mark.parametrize("mode,chunk", MODES)
 @pytest.mark.parametrize("reduction", ["sum", "mean"])
-def test_reductions(dev, monkeypatch, reduction):
+def test_reductions(dev, monkeypatch, reduction, mode, chunk):
     M, H, V = 200, 64, 700
     h, w, lab = _inputs(M, H, V, seed=9)
     _split(monkeypatch, M, 256)
+    _mode(monkeypatch, mode, M, chunk)
     hd = h.to(dev).requires_grad_(True)
     wd = w.to(dev).requires_grad_(True)
     lp, ent = linear_cross_entropy(hd, wd, lab.to(dev), 1.0, reduction)
@@ -125,14 +149,18 @@ def test_reductions(dev, monkeypatch, reduction):
         check_close(got, ref, rtol=2e-2, atol=1e-2 * float(ref.abs().max()), what=f"{reduction} gradients")
 
 
-def test_full_vocabulary(dev, monkeypatch):
+@pytest.mark.parametrize("mode,chunk", [("library/library", 4096), ("library/fused", 0), ("fused/fused", 0)])
+def test_full_vocabulary(dev, monkeypatch, mode, chunk):
     """Forward and backward over the whole gpt-oss vocabulary, the backward in
-    22 splits of 9472 columns (the last one ragged)."""
+    22 splits of 9472 columns (the last one ragged); library chunks of 4096
+    columns (forward: 50, the last one ragged; backward: three per split, the
+    third ragged)."""
     M, H, V = 96, 256, 201088
     h, w, lab = _inputs(M, H, V, seed=4, scale=0.1)
     lab[:3] = torch.tensor([9471, 9472, V - 1])
     _split(monkeypatch, M, 9472)
-    print("lm_head full vocabulary", flush=True)
+    _mode(monkeypatch, mode, M, chunk)
+    print(f"lm_head full vocabulary {mode}", flush=True)
     hd = h.to(dev).requires_grad_(True)
     wd = w.to(dev).requires_grad_(True)
     lp, ent = linear_cross_entropy(hd, wd, lab.to(dev), 1.0, "none")
@@ -149,3 +177,59 @@ def test_full_vocabulary(dev, monkeypatch):
     assert _close(ent, entr.detach(), 2e-3, 1e-3) == 0.0
     _, _, lse, ez = lce.lm_head_forward(hd.detach(), wd.detach(), lab.to(dev), 1.0)
     _check_grads(hd, wd, h, w, lab, 1.0, dlp, dent, hr, wr, lse, ez, "full vocabulary")
+
+
+def test_library_statistics_and_gradient_kernels_on_given_logits(dev):
+    """af3_lm_head_chunk_stats / _reduce / _dz_chunk on fp32 logits given
+    directly (no GEMM): per-row statistics over chunks that split the
+    vocabulary raggedly, rows of odd length (no vector loads) and aligned ones,
+    against float64 softmax statistics and the closed-form logits gradient."""
+    M, V, T = 70, 1037, 0.8
+    g = torch.Generator().manual_seed(11)
+    z = torch.randn(M, V, generator=g) * 4
+    lab = torch.randint(0, V, (M,), generator=g)
+    lab[:4] = torch.tensor([-1, V, 0, V - 1])
+    zd, labd = z.to(dev), lab.to(dev)
+    stream = _capi.stream_of(dev)
+    for ch in (1037, 256, 255):  # one chunk; 4 + a ragged one; odd widths (scalar loads)
+        parts = (V + ch - 1) // ch
+        ws = torch.zeros(parts * M * 4 + M, dtype=torch.float32, device=dev)
+        zlab = ws.data_ptr() + parts * M * 16
+        for j, v0 in enumerate(range(0, V, ch)):
+            n = min(ch, V - v0)
+            zc = zd[:, v0:v0 + n].contiguous()
+            _capi.call("af3_lm_head_chunk_stats", zc.data_ptr(), n, M, v0, n, labd.data_ptr(), T,
+                       ws.data_ptr() + j * M * 16, zlab, stream)
+        outs = [torch.empty(M, dtype=torch.float32, device=dev) for _ in range(4)]
+        _capi.call("af3_lm_head_reduce", ws.data_ptr(), M, parts, zlab, labd.data_ptr(), V,
+                   *[o.data_ptr() for o in outs], stream)
+        torch.cuda.synchronize()
+        x = z.double() / T
+        lse = torch.logsumexp(x, 1)
+        p = torch.softmax(x, 1)
+        ez = (p * x).sum(1)
+        zl = torch.where((lab >= 0) & (lab < V), x.gather(1, lab.clamp(0, V - 1)[:, None])[:, 0], torch.zeros(M,
+                         dtype=torch.float64))
+        for got, ref, name in ((outs[0], zl - lse, "logprobs"), (outs[1], lse - ez, "entropy"), (outs[2], lse, "lse"),
+                               (outs[3], ez, "ez")):
+            err = float((got.cpu().double() - ref).abs().max())
+            assert err <= 1e-5 * max(1.0, float(ref.abs().max())), (ch, name, err)
+        # the gradient from the same statistics
+        dlp = torch.randn(M, generator=g)
+        dent = torch.randn(M, generator=g)
+        dlpd, dentd = dlp.to(dev), dent.to(dev)   # held: the kernel reads them after the call returns
+        dz = torch.full((M, V + 3), 9.0, dtype=torch.bfloat16, device=dev)
+        for v0 in range(0, V, ch):
+            n = min(ch, V - v0)
+            zc = zd[:, v0:v0 + n].contiguous()
+            _capi.call("af3_lm_head_dz_chunk", zc.data_ptr(), n, M, v0, n, labd.data_ptr(), T, outs[2].data_ptr(),
+                       outs[3].data_ptr(), dlpd.data_ptr(), 1, 1.0, dentd.data_ptr(),
+                       dz.data_ptr() + 2 * v0, dz.stride(0), stream)
+        torch.cuda.synchronize()
+        onehot = torch.zeros(M, V, dtype=torch.float64)
+        ok = (lab >= 0) & (lab < V)
+        onehot[ok.nonzero()[:, 0], lab[ok]] = 1.0
+        ref = (dlp.double()[:, None] * (onehot - p) - dent.double()[:, None] * p * (x - ez[:, None])) / T
+        got = dz[:, :V].float().cpu().double()
+        assert float((got - ref).abs().max()) <= 2.0 ** -8 * float(ref.abs().max()) + 1e-6, ch
+        assert (dz[:, V:] == 9.0).all()
