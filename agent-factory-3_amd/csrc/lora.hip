@@ -50,7 +50,9 @@ __device__ __forceinline__ int l_swz(int row) { return (row ^ (row >> 3)) & 7; }
 // Block = 128 expert-sorted rows (tile map of 128-row blocks), 4 waves of
 // 32 rows x 32 columns.  X k-steps (128 rows x 64 k, 16-byte chunks swizzled
 // as the GEMMs) and the Wl k-step ([32 j][64 k], or [64 k][SR bytes] when
-// TRANS) go global->LDS through a 3-stage ring, two k-steps ahead.
+// TRANS) go global->LDS through a 2-stage ring, one k-step ahead: 40 KB of
+// LDS, so four blocks fit a CU and the ~640 blocks of a 65,536-row layer run
+// in one round instead of 1.25 rounds of two blocks per CU.
 // ---------------------------------------------------------------------------
 struct LrParams {
   const uint16_t* x;
@@ -71,9 +73,11 @@ constexpr int kLrA = 128 * 64 * 2;  // A bytes per stage
 constexpr int kLrB = 64 * 64;       // B bytes per stage (<= 32 x 64 bf16)
 constexpr int kLrStage = kLrA + kLrB;
 
+constexpr int kLrStages = 2;
+
 template <bool TRANS, int SR>
 __global__ __launch_bounds__(256) void lrows_kernel(LrParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * kLrStage];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kLrStages * kLrStage];
   const int32_t ent = p.tile_map[blockIdx.x];
   if (ent < 0) return;
   const int e = ent & 0xFFFF, blk = ent >> 16;
@@ -112,7 +116,7 @@ __global__ __launch_bounds__(256) void lrows_kernel(LrParams p) {
   const int64_t bstep = TRANS ? (int64_t)64 * p.r * 2 : 128;
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(l_lds_addr(lds));
   auto issue = [&](int kt) {
-    const uint32_t st = lds0 + (uint32_t)((kt % 3) * kLrStage);
+    const uint32_t st = lds0 + (uint32_t)((kt % kLrStages) * kLrStage);
 #pragma unroll
     for (int i = 0; i < 4; ++i) l_dma16(arow[i] + kt * 64, st + (uint32_t)((wave * 4 + i) * 1024));
     if (has_b) l_dma16(bsrc + kt * bstep, st + (uint32_t)(kLrA + wave * 1024));
@@ -122,19 +126,13 @@ __global__ __launch_bounds__(256) void lrows_kernel(LrParams p) {
   for (int q = 0; q < 16; ++q) acc[q] = 0.f;
 
   issue(0);
-  if (nk > 1) issue(1);
   for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 1 < nk) {
-      if (has_b)
-        L_WAIT_VM(5);
-      else
-        L_WAIT_VM(4);
-    } else {
-      L_WAIT_VM(0);
-    }
+    // this k-step's copies are the only ones in flight; the barrier also orders
+    // every wave's reads of the other stage (k-step kt - 1) before its refill
+    L_WAIT_VM(0);
     L_BARRIER();
-    if (kt + 2 < nk) issue(kt + 2);
-    const uint8_t* as = lds + (kt % 3) * kLrStage;
+    if (kt + 1 < nk) issue(kt + 1);
+    const uint8_t* as = lds + (kt % kLrStages) * kLrStage;
     const uint8_t* bs = as + kLrA;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
