@@ -53,7 +53,7 @@ from . import _capi, kernels
 from .kernels import mxfp4_to_bf16_hip, swiglu_backward_raw, swiglu_forward
 from .routing import (  # noqa: F401  (re-exported names of the routing layer)
     ExptData, GatherIndx, RoutingData, ScatterIndx, compute_expt_data, compute_expt_data_torch,
-    dense_routing, max_tiles, router_linear, routing, routing_replay,
+    dense_routing, gemm_order_for, max_tiles, router_linear, routing, routing_replay,
 )
 
 GEMM_BLOCK_M = 128
@@ -233,7 +233,7 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
             bm = GEMM_TILE.get("fwd_block_m", 128)
         elif trans_w and GEMM_TILE["tile_cfg"] % 100 in (0, 28):
             bm = GEMM_TILE.get("dx_block_m", 128)
-    pid_map = getattr(ed, "gemm_order", {}).get(bm) if GEMM_TILE.get("order", True) else None
+    pid_map = gemm_order_for(ed, bm) if GEMM_TILE.get("order", True) else None
     if pid_map is None:
         pid_map = ed.block_pid_map[bm]
     offs = ed.token_offs_raw
@@ -336,7 +336,7 @@ def moe_rows_f8(codes, a_row_scale, blocks, scales, bias, routing_data, gather_i
     routing_data, k_act = _expt_data(routing_data, R, dev)
     ed = routing_data.expt_data
     bm = 256
-    pid_map = getattr(ed, "gemm_order", {}).get(bm) if GEMM_TILE.get("order", True) else None
+    pid_map = gemm_order_for(ed, bm) if GEMM_TILE.get("order", True) else None
     if pid_map is None:
         pid_map = ed.block_pid_map[bm]
     y = torch.empty(R, N, dtype=torch.bfloat16, device=dev)
@@ -517,7 +517,7 @@ def _lora_rows(x, gather, k_act, wl, trans_b, scale, ed, n_out, K):
     out = torch.empty(R, n_out, dtype=torch.bfloat16, device=dev)
     # full tiles first: the tiles past one round of resident blocks are then the
     # partial ones, whose clamped rows are cache hits
-    pid_map = getattr(ed, "gemm_order", {}).get(GEMM_BLOCK_M)
+    pid_map = gemm_order_for(ed, GEMM_BLOCK_M)
     if pid_map is None:
         pid_map = ed.block_pid_map[GEMM_BLOCK_M]
     if R and pid_map.numel():
@@ -880,6 +880,19 @@ class Mxfp4Bf16DequantGptOssExperts(nn.Module):
         return DequantMoEMatmul.apply(x, blocks, scales, bias, routing_data, fg, fs, fgam, bg, bs, bgam,
                                       self.dequant_dtype, routing_data.n_expts_act, self, proj)
 
+    def _bias_f32(self, proj):
+        """The projection's bias in fp32 (the GEMM epilogue's operand), cast once
+        per parameter storage and version instead of every call (the expert
+        biases are frozen: the grouped GEMMs return no bias gradient)."""
+        b = getattr(self, f"{proj}_bias")
+        cache = self.__dict__.setdefault("_bias_f32_cache", {})
+        hit = cache.get(proj)
+        # same tensor object (held by the cache, so its storage cannot be reused
+        # by another one), same storage, no in-place change since
+        if hit is None or hit[0] is not b or hit[1] != (b.data_ptr(), b._version):
+            hit = cache[proj] = (b, (b.data_ptr(), b._version), b.detach().float())
+        return hit[2]
+
     def forward(self, hidden_states: torch.Tensor, routing_data, gather_idx, scatter_idx) -> torch.Tensor:
         if FUSED_SWIGLU and self.dequant_dtype == "bf16":
             lora = self.expert_lora_r > 0
@@ -887,17 +900,17 @@ class Mxfp4Bf16DequantGptOssExperts(nn.Module):
             gu_blocks, gu_scales = self._get_uint8_weights("gate_up_proj")
             gate_up, act = _GateUpSwiGLU.apply(
                 hidden_states, la("gate_up_proj", "A"), la("gate_up_proj", "B"), self.expert_lora_scaling,
-                gu_blocks, gu_scales, self.gate_up_proj_bias.float(), routing_data, gather_idx, scatter_idx,
+                gu_blocks, gu_scales, self._bias_f32("gate_up_proj"), routing_data, gather_idx, scatter_idx,
                 self.alpha, self.limit, self, "gate_up_proj")
             dn_blocks, dn_scales = self._get_uint8_weights("down_proj")
             return _SwiGLUDown.apply(
                 gate_up, act, la("down_proj", "A"), la("down_proj", "B"), self.expert_lora_scaling, dn_blocks,
-                dn_scales, self.down_proj_bias.float(), routing_data, scatter_idx, routing_data.gate_scal,
+                dn_scales, self._bias_f32("down_proj"), routing_data, scatter_idx, routing_data.gate_scal,
                 gather_idx, self.alpha, self.limit, self, "down_proj")
-        gate_up_raw = self._proj(hidden_states, "gate_up_proj", self.gate_up_proj_bias.float(), routing_data,
+        gate_up_raw = self._proj(hidden_states, "gate_up_proj", self._bias_f32("gate_up_proj"), routing_data,
                                  gather_idx, None, None, None, scatter_idx, None)
         intermediate = SwiGLUFunction.apply(gate_up_raw, self.alpha, self.limit)
-        return self._proj(intermediate, "down_proj", self.down_proj_bias.float(), routing_data,
+        return self._proj(intermediate, "down_proj", self._bias_f32("down_proj"), routing_data,
                           None, scatter_idx, routing_data.gate_scal, gather_idx, None, routing_data.gate_scal)
 
 

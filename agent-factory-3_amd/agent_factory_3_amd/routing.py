@@ -26,7 +26,8 @@ from . import _capi
 # block sizes for which tile maps are built: 128- and 256-row GEMM tiles and
 # the 512-row chunks of the LoRA weight-gradient reduction
 BLOCK_MS = (128, 256, 512)
-GEMM_ORDER_BMS = (128, 256)  # tile sizes with a full-first work order (LoRA row tiles, GEMM tiles)
+GEMM_ORDER_BMS = (128,)  # tile sizes whose full-first work order is made with the routing (the
+# default GEMMs and the LoRA row tiles); other sizes get theirs on first use (gemm_order_for)
 
 
 @dataclass
@@ -51,8 +52,9 @@ class ExptData:
     block_pid_map: dict = field(default_factory=dict)   # BM -> [max_tiles] int32 (b<<16)|e or -1
     # BM -> the block_pid_map entries in grouped-GEMM work order (full tiles
     # first, then partial tiles by decreasing rows); not part of the
-    # reference's ExptData, filled for GEMM_ORDER_BMS
+    # reference's ExptData, filled for GEMM_ORDER_BMS and by gemm_order_for
     gemm_order: dict = field(default_factory=dict)
+    n_gates: int = 0                        # routed rows (for the work orders made on first use)
 
 
 @dataclass
@@ -95,18 +97,30 @@ def compute_expt_data(hist: torch.Tensor, n_expts_tot: int, n_gates: int,
     pid_map = torch.empty(len(BLOCK_MS), max(mt, 1), dtype=torch.int32, device=dev)
     _capi.call("af3_expt_data", hist.data_ptr(), n_expts_tot, bms.data_ptr(), len(BLOCK_MS), mt,
                offs_pad.data_ptr(), pid_map.data_ptr(), _capi.stream_of(dev))
-    ed = ExptData(hist, token_offs_raw)
+    ed = ExptData(hist, token_offs_raw, n_gates=int(n_gates))
     for i, bm in enumerate(BLOCK_MS):
         ed.token_offs_pad[bm] = offs_pad[i]
         ed.block_pid_map[bm] = pid_map[i, :mt]
-    if n_expts_tot <= 4096:
-        for bm in GEMM_ORDER_BMS:
-            n = max_tiles(n_gates, n_expts_tot, bm)
-            order = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
-            _capi.call("af3_tile_order", hist.data_ptr(), n_expts_tot, bm, ed.token_offs_pad[bm].data_ptr(), n,
-                       order.data_ptr(), _capi.stream_of(dev))
-            ed.gemm_order[bm] = order[:n]
+    for bm in GEMM_ORDER_BMS:
+        gemm_order_for(ed, bm)
     return ed
+
+
+def gemm_order_for(ed: ExptData, bm: int):
+    """The grouped-GEMM work order of the bm-row tiles (af3_tile_order), made
+    on first use and kept in ed.gemm_order; None where it cannot be made
+    (more than 4096 experts, or an ExptData built without n_gates), and the
+    callers then take block_pid_map's order."""
+    order = ed.gemm_order.get(bm)
+    n_expts_tot = ed.hist.numel()
+    if order is not None or ed.n_gates <= 0 or n_expts_tot > 4096 or bm not in ed.token_offs_pad:
+        return order
+    n = max_tiles(ed.n_gates, n_expts_tot, bm)
+    order = torch.empty(max(n, 1), dtype=torch.int32, device=ed.hist.device)
+    _capi.call("af3_tile_order", ed.hist.data_ptr(), n_expts_tot, bm, ed.token_offs_pad[bm].data_ptr(), n,
+               order.data_ptr(), _capi.stream_of(ed.hist.device))
+    ed.gemm_order[bm] = order[:n]
+    return ed.gemm_order[bm]
 
 
 # the reference's name (triton_kernels.routing.compute_expt_data_torch)
