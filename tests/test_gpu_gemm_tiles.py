@@ -113,7 +113,7 @@ def test_forward_tiles(dev, cfg, nout, gather, lora, odd):
 @pytest.mark.parametrize("cfg,nout", [(0, NOUT), (0, 640), (4, NOUT), (23, NOUT), (23, 640), (228, NOUT)])
 @pytest.mark.parametrize("gather,lora,odd", CASES)
 def test_dgrad_tiles(dev, cfg, nout, gather, lora, odd):
-    """N = 576 / 640 end in a 64- / 128-column n-tile, which the default kernel
+    """N = 576 / 640 end in a 64- / 128-column n-tile, which the 256-row kernel
     (tile_cfg 23) runs with the tile's rows split over the waves; the default
     (tile_cfg 0 = 28: 128 x 256 items on the 128-row map, two blocks per CU)
     sees tails of 10, 44, 50, 60, 100 and 104 rows; 228 is it with two m-tiles
