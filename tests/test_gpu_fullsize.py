@@ -1,4 +1,5 @@
-"""Configurations 2, 3 and 4 at their full size, through the drop-in module API.
+"""Configurations 2, 3 and 4 at their full size, through the drop-in module API
+(and cfg3 again with well-conditioned scales).
 
 The expert module (``Mxfp4Bf16DequantGptOssExperts``, with expert LoRA where
 the configuration has it) runs forward, and backward for cfg3 / cfg4, at the
@@ -34,11 +35,18 @@ from tests._tol import check_close, check_equal
 pytestmark = [pytest.mark.gpu, pytest.mark.timeout(600)]
 
 
-@pytest.fixture(scope="module", params=[2, 3, 4], ids=lambda c: f"cfg{c}")
+@pytest.fixture(scope="module", params=[2, 3, 4, "3wc"], ids=lambda c: f"cfg{c}")
 def run(request, dev):
+    """cfg3wc: cfg3 with e8m0 scales 118..122 instead of 118..130 (the
+    well-conditioned variant: pre-activations mostly inside the SwiGLU clamp,
+    so its non-saturated gradients are checked at full size too)."""
     cfg = request.param
-    r = S.LayerRun(workloads.layer(cfg), dev)
-    r.cfg = cfg
+    if cfg == "3wc":
+        r = S.LayerRun(workloads.layer(3, scale_lo=118, scale_hi=122), dev)
+        r.cfg = 3
+    else:
+        r = S.LayerRun(workloads.layer(cfg), dev)
+        r.cfg = cfg
     yield r
 
 
