@@ -65,6 +65,14 @@ GEMM_BLOCK_M = 128
 # the 128-row map.
 GEMM_TILE = {"block_m": 256, "tile_cfg": 0, "fwd_block_m": 128, "dx_block_m": 128}
 
+# The expert module's forward GEMMs read a forward-tiled copy of each frozen
+# projection's packed weights (af3_mxfp4_tile_fwd: the words one k-step of a
+# wave needs from 32 weight rows are one contiguous KB), made on first use and
+# kept per weight storage and version: one more copy of the packed blocks on
+# the device (1.6 GB for a gpt-oss-120b layer's 128 experts).  The input
+# gradient, the checkpoint format and the scales use the blocks as stored.
+FWD_TILED_WEIGHTS = True
+
 # Optional launch timer for the grouped GEMM (set by benchmark harnesses):
 # callable(tag: str, flops: int, detail: str) -> context manager wrapping the launch.
 KERNEL_TIMER = None
@@ -196,8 +204,27 @@ def _weight_dims(blocks, trans_w):
     return (E, G * 32, rows) if trans_w else (E, rows, G * 32)
 
 
+def mxfp4_tile_fwd(blocks):
+    """Forward-tiled copy of packed MXFP4 weights ``blocks`` [E, N, K/32, 16]
+    (uint8, N % 32 == 0, K % 64 == 0): the same bytes permuted so that
+    ``out.view(E, N/32, K/64, 2, 32, 16)[e, n // 32, kt, h, n % 32] ==
+    blocks[e, n, 2 kt + h]``; ``moe_rows(..., w_fwd=out)`` reads it in the
+    forward.  No counterpart in the reference (its matmul_ogs reads the stored
+    layout, quantization.py:358-362)."""
+    if not blocks.is_cuda:
+        raise RuntimeError("blocks must be a GPU tensor (the MI355X path has no CPU implementation)")
+    b = blocks if blocks.dim() == 4 else blocks.unsqueeze(0)
+    if b.dtype != torch.uint8 or b.shape[-1] != 16:
+        raise TypeError(f"blocks must be uint8 [E, N, K/32, 16] (got {b.dtype} {tuple(b.shape)})")
+    E, N, G, _ = b.shape
+    b = b if b.is_contiguous() and b.data_ptr() % 16 == 0 else b.contiguous()
+    out = torch.empty(b.shape, dtype=torch.uint8, device=b.device)
+    _capi.call("af3_mxfp4_tile_fwd", b.data_ptr(), E, N, G * 32, out.data_ptr(), _capi.stream_of(b.device))
+    return out.view(blocks.shape)
+
+
 def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=None, trans_w=False,
-             lora_l=None, lora_b=None, swiglu=None, a_row_scale=None):
+             lora_l=None, lora_b=None, swiglu=None, a_row_scale=None, w_fwd=None):
     """Expert-sorted output rows of the grouped GEMM (no scatter).
 
     ``trans_w=False``: ``Y[r] = X[a(r)] @ W[e]^T`` with W = dequant(blocks) [E, N, K]
@@ -212,6 +239,8 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
     interleaved pre-activation ``gate_up`` [R, 2N], i.e. dGU [R, 2N].  Both are
     fused into the GEMM epilogue; None is returned when the selected kernel
     has no fused epilogue (the caller then runs the two steps separately).
+    ``w_fwd``: the ``mxfp4_tile_fwd`` copy of ``blocks``, read instead of them
+    by the default forward kernel (ignored by the others).
     """
     if not x.is_cuda:
         raise RuntimeError("x must be a GPU tensor (the MI355X path has no CPU implementation)")
@@ -257,6 +286,9 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
     if R == 0 or pid_map.numel() == 0:
         return y if epi == 0 else (y, glu) if epi == 2 else y
     blocks = blocks if blocks.data_ptr() % 16 == 0 else blocks.clone()
+    if w_fwd is not None and (w_fwd.shape != blocks.shape or w_fwd.dtype != torch.uint8 or not w_fwd.is_contiguous()
+                              or w_fwd.data_ptr() % 16):
+        raise ValueError("w_fwd must be the mxfp4_tile_fwd copy of blocks (same shape, contiguous uint8)")
     b = None
     if bias is not None:
         b = bias.to(torch.float32).contiguous()
@@ -283,12 +315,26 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
             raise ValueError("a row scale cannot be combined with the LoRA segment or a fused SwiGLU")
         a_row_scale = a_row_scale.to(torch.float32).contiguous()
 
+    # the forward-tiled weights go to the default forward kernel; any other
+    # selection declines them (nothing launched) and the stored blocks are used
+    targs = None
+    if w_fwd is not None and not trans_w and a_row_scale is None and bm == 128 \
+            and GEMM_TILE["tile_cfg"] % 100 in (0, 26):
+        targs = list(args)
+        targs[4], targs[19] = w_fwd.data_ptr(), GEMM_TILE["tile_cfg"] | _capi.W_FWD_TILED
+
     def launch():
         if a_row_scale is not None:
             rargs = args[:10] + args[14:]   # without the LoRA operands
             if not _capi.try_call("af3_moe_gemm_rowscale", *rargs, a_row_scale.data_ptr(), stream):
                 raise RuntimeError("moe_gemm: the A row scale needs the default tile configurations (20-23)")
             return True
+        if targs is not None:
+            if epi == 0 and _capi.try_call("af3_moe_gemm", *targs, stream):
+                return True
+            if epi == 2 and _capi.try_call("af3_moe_gemm_swiglu", *targs, epi, glu.data_ptr(), ld_glu, alpha, limit,
+                                           stream):
+                return True
         if epi == 0:
             _capi.call("af3_moe_gemm", *args, stream)
             return True
@@ -437,9 +483,11 @@ class DequantMoEMatmul(torch.autograd.Function):
                                  a_row_scale=xs)
                 k = routing_data.n_expts_act if routing_data is not None else 1
                 out = y if fwd_scatter_indx is None else moe_combine(y, fwd_scatter_indx, k)
-            else:
-                out = matmul_ogs(x, (blocks, scales), bias, routing_data, fwd_gather_indx, fwd_scatter_indx,
-                                 fwd_gammas, trans_w=False)
+            else:  # matmul_ogs(x, (blocks, scales), ...) with the module's forward-tiled weights
+                y = moe_rows(x, blocks, scales, bias, routing_data, fwd_gather_indx, fwd_gammas, False,
+                             w_fwd=_fwd_weights(experts_module, proj_name))
+                k = routing_data.n_expts_act if routing_data is not None else 1
+                out = y if fwd_scatter_indx is None else moe_combine(y, fwd_scatter_indx, k)
         ctx.experts_module = experts_module
         ctx.proj_name = proj_name
         if experts_module is None:  # no module to re-derive from: keep the (view) tensors
@@ -616,7 +664,8 @@ class LoraDequantMoEMatmul(torch.autograd.Function):
         r = A.shape[1]
         with on_device(dev):
             L = _lora_rows(xg, g, k_act, A, 0, scaling, ed, r, K)
-            y = moe_rows(xg, blocks, scales, bias, routing_data, fwd_gather_indx, fwd_gammas, False, L, B)
+            y = moe_rows(xg, blocks, scales, bias, routing_data, fwd_gather_indx, fwd_gammas, False, L, B,
+                         w_fwd=_fwd_weights(experts_module, proj_name))
             if fwd_scatter_indx is not None:
                 y = moe_combine(y, fwd_scatter_indx, k_act)
         ctx.save_for_backward(xg, A, B, L)
@@ -686,6 +735,14 @@ def _weights_of(ctx):
     return ctx.weights
 
 
+def _fwd_weights(experts_module, proj_name):
+    """The module's forward-tiled copy of ``proj_name``'s packed weights (None
+    without a module or with FWD_TILED_WEIGHTS off)."""
+    if experts_module is None or not FWD_TILED_WEIGHTS:
+        return None
+    return experts_module._fwd_tiled(proj_name)
+
+
 def _bf16c(t):
     return None if t is None else t.to(torch.bfloat16).contiguous()
 
@@ -710,10 +767,11 @@ class _GateUpSwiGLU(torch.autograd.Function):
         with on_device(dev):
             if A is not None:
                 L = _lora_rows(xg, g, k_act, A, 0, scaling, ed, A.shape[1], K)
+            wf = _fwd_weights(experts_module, proj_name)
             res = moe_rows(xg, blocks, scales, bias, routing_data, gather_indx, None, False, L, B,
-                           swiglu=("fwd", alpha, limit))
+                           swiglu=("fwd", alpha, limit), w_fwd=wf)
             if res is None:
-                gu = moe_rows(xg, blocks, scales, bias, routing_data, gather_indx, None, False, L, B)
+                gu = moe_rows(xg, blocks, scales, bias, routing_data, gather_indx, None, False, L, B, w_fwd=wf)
                 act = swiglu_forward(gu, alpha, limit)
             else:
                 gu, act = res
@@ -776,7 +834,8 @@ class _SwiGLUDown(torch.autograd.Function):
         with on_device(dev):
             if A is not None:
                 L = _lora_rows(act, None, 1, A, 0, scaling, ed, A.shape[1], K)
-            y = moe_rows(act, blocks, scales, bias, routing_data, None, gammas, False, L, B)
+            y = moe_rows(act, blocks, scales, bias, routing_data, None, gammas, False, L, B,
+                         w_fwd=_fwd_weights(experts_module, proj_name))
             if scatter_indx is not None:
                 y = moe_combine(y, scatter_indx, k_act)
         # gate_up (the SwiGLU's input, the same bytes as the reference's saved
@@ -891,6 +950,27 @@ class Mxfp4Bf16DequantGptOssExperts(nn.Module):
         # by another one), same storage, no in-place change since
         if hit is None or hit[0] is not b or hit[1] != (b.data_ptr(), b._version):
             hit = cache[proj] = (b, (b.data_ptr(), b._version), b.detach().float())
+        return hit[2]
+
+    def _fwd_tiled(self, proj):
+        """The forward-tiled copy of the projection's packed weights
+        (``mxfp4_tile_fwd``), made once per weight storage and version (the
+        expert weights are frozen); None where the forward cannot read one."""
+        blocks, _ = self._get_uint8_weights(proj)
+        if not blocks.is_cuda or blocks.dim() != 4 or blocks.shape[1] % 32 or blocks.shape[2] % 2:
+            return None
+        src = getattr(self, f"{proj}_blocks", None)
+        if src is None:
+            return None
+        cache = self.__dict__.setdefault("_fwd_tiled_cache", {})
+        key = (blocks.data_ptr(), src._version, tuple(blocks.shape))
+        hit = cache.get(proj)
+        # same parameter object (held by the cache, so its storage cannot be
+        # reused by another one), same storage, no in-place change since
+        if hit is None or hit[0] is not src or hit[1] != key:
+            cache.pop(proj, None)  # the old copy goes before the new one is made
+            with torch.no_grad():
+                hit = cache[proj] = (src, key, mxfp4_tile_fwd(blocks))
         return hit[2]
 
     def forward(self, hidden_states: torch.Tensor, routing_data, gather_idx, scatter_idx) -> torch.Tensor:

@@ -33,6 +33,10 @@ int lora_wgrad_fast(const uint16_t* big, int64_t ld_big, const int32_t* big_gath
 // argument errors are negative, HIP errors positive (the hipError_t value)
 #define AF3_EINVAL (-1)
 #define AF3_EUNSUPPORTED (-2)
+// OR-ed into af3_moe_gemm's tile_cfg: w_blocks is the af3_mxfp4_tile_fwd copy
+#ifndef AF3_W_FWD_TILED
+#define AF3_W_FWD_TILED 0x10000
+#endif
 
 #define AF3_REQUIRE(cond, ...)            \
   do {                                    \

@@ -85,6 +85,11 @@ struct Params {
   // indexed like the A rows (gather[r] / gdiv, or r); the default epilogues
   // then store (acc * ascale + bias) * gammas
   const float* ascale;
+  // forward weights (gemm7): 0 = the packed blocks row-major [E][N][K/32][16];
+  // 1 = the forward-tiled copy of af3_mxfp4_tile_fwd, [E][N/32][K/64][2][32][16]
+  // (one KB per 32 weight rows and 64-deep k-step, in the order the wave's
+  // lanes take them)
+  int b_tiled;
 };
 
 // scale of A row a(r) for output row r (1 without a row scale)
@@ -946,17 +951,28 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
   // bq[parity]; the loads are issued by inline assembly like the copies (so the k-step waits stay
   // exact) and each k-step's registers pass through an empty asm after the vmcnt wait, so no use of
   // them can be scheduled before it.  Rows past the tile read row 0 (their sub-tiles are skipped).
+  // With the forward-tiled copy (p.b_tiled) the words of one k-step of the
+  // wave's 32 rows of sub-tile tn are one contiguous KB, lane l's at 16 l, so
+  // each load instruction reads 8 whole 128-byte lines (row-major, it takes 32
+  // bytes of 32 different lines, each line re-read over four k-steps).
   af3_u32x4 bq[2][TN];
   const uint8_t* bgp[TN];
+  const int bstep = BG && p.b_tiled ? 1024 : 32;  // bytes between a lane's words of consecutive k-steps
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) {
-    int nr = wn0 + tn * 32 + lr;
-    if (nr >= ncols) nr = 0;
-    bgp[tn] = (const uint8_t*)p.b.ptr + e * p.b.estride + (int64_t)(n0 + nr) * p.b.ld + lh * 16;
+    const uint8_t* eb = (const uint8_t*)p.b.ptr + e * p.b.estride;
+    if (BG && p.b_tiled) {  // ncols % 32 == 0: a 32-row group is live or dead as a whole
+      const int nb = wn0 + tn * 32 < ncols ? n0 + wn0 + tn * 32 : 0;
+      bgp[tn] = eb + (int64_t)nb * p.b.ld + lane * 16;  // the group's tiles start at row nb's byte offset
+    } else {
+      int nr = wn0 + tn * 32 + lr;
+      if (nr >= ncols) nr = 0;
+      bgp[tn] = eb + (int64_t)(n0 + nr) * p.b.ld + lh * 16;
+    }
     bq[0][tn] = zero4();
     bq[1][tn] = zero4();
   }
-  auto load_b = [&](int kt, auto par) { g7_load_words<TN>(bq[decltype(par)::value], bgp, kt * 32); };
+  auto load_b = [&](int kt, auto par) { g7_load_words<TN>(bq[decltype(par)::value], bgp, kt * bstep); };
   const bool live = tm_live > 0 && tn_live > 0;
 
   af3_f32x16 acc[TM][TN];
@@ -2496,6 +2512,9 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
                          int K, uint16_t* y, int64_t ldy, int epi, void* glu, int64_t ld_glu, float alpha,
                          float limit, const float* a_row_scale, void* stream_, int a_fp8 = 0) {
   hipStream_t stream = (hipStream_t)stream_;
+  const bool w_tiled = (tile_cfg & AF3_W_FWD_TILED) != 0;  // w_blocks is the af3_mxfp4_tile_fwd copy
+  tile_cfg &= ~AF3_W_FWD_TILED;
+  AF3_REQUIRE(tile_cfg >= 0, "moe_gemm: bad tile_cfg %d", tile_cfg);
   AF3_REQUIRE(N > 0 && K > 0 && n_expts > 0 && max_tiles >= 0, "moe_gemm: bad sizes N=%d K=%d E=%d", N, K, n_expts);
   if (max_tiles == 0) return 0;
   AF3_REQUIRE(x && w_blocks && w_scales && token_offs && block_pid_map && tile_offs && y, "moe_gemm: null pointer");
@@ -2581,6 +2600,14 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
   }
   const bool bm_ok = (cfg == 4 || cfg == 22 || cfg == 23) ? block_m == 256 : block_m == 128;
   AF3_REQUIRE(bm_ok, "moe_gemm: tile_cfg %d does not match block_m %d", cfg, block_m);
+  if (w_tiled) {  // only the two-blocks-per-CU forward reads the forward-tiled weights
+    if (a_fp8 || trans || cfg != 26 || K % kBK != 0) {
+      af3::set_error("moe_gemm: forward-tiled weights need the tile_cfg 26 forward (got cfg %d, trans_w %d)", cfg,
+                     trans_w);
+      return AF3_EUNSUPPORTED;
+    }
+    p.b_tiled = 1;
+  }
   if (a_fp8) {  // E4M3 activations x MXFP4 weights on the block-scaled MFMA (256-row map)
     if (trans) {  // input gradient: the weights converted to E5M2 in registers
       if (block_m != 256 || K % kBK != 0 || N % 64 != 0 || !al16(y) || ldy % 8 != 0 || ldx % 16 != 0 || !al16(x) ||
@@ -2606,7 +2633,7 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
     hipLaunchKernelGGL((gemm4_fwd_f8_kernel<NONE>), grid, dim3(512), 0, stream, p);
     return af3::check_launch("moe_gemm_f8");
   }
-  if (K % kBK != 0) cfg = 9;  // direct A loads need whole 64-deep k-steps
+  if (K % kBK != 0) cfg = 9;  // direct A loads need whole 64-deep k-steps (never with forward-tiled weights)
   if (epi != 0) {
     AF3_REQUIRE(glu && (epi == 1 || epi == 2), "moe_gemm: bad SwiGLU epilogue %d", epi);
     const bool ok = epi == 1 ? (trans && (cfg == 23 || cfg == 28) && ld_glu % 8 == 0 && al16(glu) && ldy >= 2LL * N)
@@ -2857,6 +2884,39 @@ extern "C" int af3_lora_wgrad(const uint16_t* a, int64_t lda, const int32_t* a_g
 }
 
 // out[t][:] = sum_{j<K} rows[src[t*K+j]][:]  (the scatter-sum of matmul_ogs)
+// Forward-tiled copy of packed MXFP4 weights (Params::b_tiled): 16-byte unit
+// u of out [n_mats * N / 32][K / 64][2][32][16] is block 2 kt + h of row
+// 32 (u >> 6) / nk + r, with r = u & 31, h = (u >> 5) & 1, kt = (u >> 6) % nk.
+// One wave writes one KB tile; its 32 rows are read 32 bytes each, and the
+// tiles of consecutive k-steps of the same rows follow each other, so every
+// 128-byte line of the source comes from HBM once and is re-read from L2.
+__global__ __launch_bounds__(256) void tile_fwd_kernel(const uint8_t* __restrict__ in, uint8_t* __restrict__ out,
+                                                       int64_t n_units, int nk, int64_t ld) {
+  for (int64_t u = blockIdx.x * 256LL + threadIdx.x; u < n_units; u += (int64_t)gridDim.x * 256) {
+    const int l = (int)(u & 63);
+    const int64_t t = u >> 6;
+    const int64_t row = (t / nk) * 32 + (l & 31);  // t / nk = the 32-row group over all matrices
+    const int kt = (int)(t % nk);
+    *(af3_u32x4*)(out + u * 16) = *(const af3_u32x4*)(in + row * ld + (2 * kt + (l >> 5)) * 16);
+  }
+}
+
+extern "C" int af3_mxfp4_tile_fwd(const uint8_t* blocks, int64_t n_mats, int N, int K, uint8_t* out, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  AF3_REQUIRE(n_mats >= 0 && N > 0 && K > 0, "mxfp4_tile_fwd: bad sizes E=%lld N=%d K=%d", (long long)n_mats, N, K);
+  AF3_REQUIRE(N % 32 == 0 && K % 64 == 0, "mxfp4_tile_fwd: needs N %% 32 == 0 and K %% 64 == 0 (N=%d K=%d)", N, K);
+  if (n_mats == 0) return 0;
+  AF3_REQUIRE(blocks && out && al16(blocks) && al16(out), "mxfp4_tile_fwd: blocks / out must be 16-byte aligned");
+  const int64_t n_units = n_mats * N * (int64_t)(K / 32);
+  const int64_t bytes = n_units * 16;
+  AF3_REQUIRE(out + bytes <= blocks || blocks + bytes <= out, "mxfp4_tile_fwd: out must not overlap blocks");
+  const int64_t nblk = af3_cdiv(n_units, 256);
+  const unsigned grid = (unsigned)(nblk < 16384 ? nblk : 16384);
+  hipLaunchKernelGGL(tile_fwd_kernel, dim3(grid), dim3(256), 0, stream, blocks, out, n_units, K / 64,
+                     (int64_t)(K / 2));
+  return af3::check_launch("mxfp4_tile_fwd");
+}
+
 extern "C" int af3_moe_combine(const uint16_t* rows, int64_t ld_rows, const int32_t* src_indx, int64_t n_tokens,
                                int K, int N, uint16_t* out, int64_t ld_out, void* stream_) {
   hipStream_t stream = (hipStream_t)stream_;

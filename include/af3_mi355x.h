@@ -138,13 +138,31 @@ int af3_tile_order(const int32_t* hist, int n_expts_tot, int block_m, const int3
  * 28 (input gradient, same shape); block_m 256 -> 22 / 23 (256 x 256); the
  * general fallbacks 4 / 2 / 9 where a default's alignment or K % 64 == 0
  * requirement fails.  tile_cfg / 100 = m-tiles per work group of the
- * 22 / 23 / 26 / 28 order (default 4; 2 for 26 / 28). */
+ * 22 / 23 / 26 / 28 order (default 4; 2 for 26 / 28).  tile_cfg |
+ * AF3_W_FWD_TILED: w_blocks is the af3_mxfp4_tile_fwd copy of the weights
+ * (trans_w 0, the tile_cfg 26 forward only; AF3_EUNSUPPORTED, nothing
+ * launched, when another kernel is selected: the caller then passes the
+ * row-major blocks). */
+#ifndef AF3_W_FWD_TILED
+#define AF3_W_FWD_TILED 0x10000
+#endif
 int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
                  const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
                  const void* gammas, int gammas_f32, const uint16_t* lora_l, int64_t ld_l, const uint16_t* lora_b,
                  int lora_r, const int32_t* token_offs, const int32_t* block_pid_map, const int32_t* tile_offs,
                  int max_tiles, int block_m, int tile_cfg, int n_expts, int N, int K, uint16_t* y, int64_t ldy,
                  void* stream);
+
+/* Forward-tiled copy of packed MXFP4 weights for the tile_cfg 26 forward.
+ * No counterpart in the reference (its matmul_ogs reads the weights as
+ * stored, quantization.py:358-362); a byte permutation made once per frozen
+ * weight: blocks [n_mats][N][K/32][16] -> out [n_mats][N/32][K/64][2][32][16],
+ * out[e][n/32][kt][h][n%32] = blocks[e][n][2 kt + h], so the words one
+ * k-step of the forward's wave needs from 32 weight rows are one contiguous
+ * KB (row-major they are 32 bytes of 32 different 128-byte lines).  The
+ * scales stay as they are.  N % 32 == 0, K % 64 == 0, 16-byte aligned, out
+ * the same size as blocks and not overlapping it. */
+int af3_mxfp4_tile_fwd(const uint8_t* blocks, int64_t n_mats, int N, int K, uint8_t* out, void* stream);
 
 /* af3_moe_gemm with the gpt-oss clamped SwiGLU (kernels.py:394-582 math)
  * fused into the epilogue, so the activation never makes a separate pass

@@ -1,0 +1,118 @@
+"""Forward-tiled weights (af3_mxfp4_tile_fwd): the byte permutation itself, and
+the default forward kernel reading it gives the same bits as reading the
+blocks as stored, on the shapes of test_gpu_gemm_tiles (full and partial
+tiles, 64- / 128-column tail n-tiles, gathered rows, the LoRA segment, scale
+bytes outside [2, 252], the fused SwiGLU forward).  Kernels that do not read
+the tiled copy decline it and run on the stored blocks."""
+import pytest
+import torch
+
+from agent_factory_3_amd import _capi
+from agent_factory_3_amd import quantization as Q
+from test_gpu_gemm_tiles import CASES, E, KRED, T, TOPK, _routing, _weights
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("shape", [(3, 96, 6), (1, 32, 2), (5, 640, 20)])
+def test_tile_fwd_permutation(dev, shape):
+    """out[e, n // 32, kt, h, n % 32] == blocks[e, n, 2 kt + h] for every byte."""
+    En, N, G = shape
+    g = torch.Generator().manual_seed(N + G)
+    blocks = torch.randint(0, 256, (En, N, G, 16), generator=g).to(torch.uint8)
+    out = Q.mxfp4_tile_fwd(blocks.to(dev)).cpu()
+    assert out.shape == blocks.shape
+    want = blocks.view(En, N // 32, 32, G // 2, 2, 16).permute(0, 1, 3, 4, 2, 5).contiguous()
+    assert torch.equal(out.view(En, N // 32, G // 2, 2, 32, 16), want)
+    # spot check of the indexing rule itself on a few bytes
+    t = out.view(En, N // 32, G // 2, 2, 32, 16)
+    for e, n, j in [(0, 0, 0), (En - 1, N - 1, G - 1), (En // 2, N // 2 + 1, G // 2)]:
+        assert torch.equal(t[e, n // 32, j // 2, j % 2, n % 32], blocks[e, n, j])
+
+
+def test_tile_fwd_rejects_bad_shapes(dev):
+    with pytest.raises(RuntimeError, match="N % 32"):
+        Q.mxfp4_tile_fwd(torch.zeros(2, 48, 4, 16, dtype=torch.uint8, device=dev))
+    with pytest.raises(RuntimeError, match="K % 64"):
+        Q.mxfp4_tile_fwd(torch.zeros(2, 64, 3, 16, dtype=torch.uint8, device=dev))
+
+
+@pytest.mark.parametrize("cfg,nout", [(0, 576), (0, 640), (126, 576), (22, 640), (4, 576)])
+@pytest.mark.parametrize("gather,lora,odd", CASES)
+def test_forward_tiled_bit_equal(dev, cfg, nout, gather, lora, odd):
+    """moe_rows with w_fwd equals moe_rows on the stored blocks bit for bit
+    (tile_cfg 0 / 126 read the tiled copy; 22 and 4 decline it)."""
+    g, ref, rd, gi = _routing(dev, 21)
+    blocks, scales = _weights(g, nout, KRED, odd)
+    Rr = T * TOPK
+    x = torch.randn(T if gather else Rr, KRED, generator=g).to(torch.bfloat16).to(dev)
+    bias = (torch.randn(E, nout, generator=g) * 0.1).float().to(dev)
+    gam = rd.gate_scal if gather else None
+    L = (torch.randn(Rr, 32, generator=g) * 0.3).to(torch.bfloat16).to(dev) if lora else None
+    Bx = (torch.randn(E, nout, 32, generator=g) * 0.3).to(torch.bfloat16).to(dev) if lora else None
+    wb, ws = blocks.to(dev), scales.to(dev)
+    wt = Q.mxfp4_tile_fwd(wb)
+    old = dict(Q.GEMM_TILE)
+    Q.GEMM_TILE.update(block_m=256, tile_cfg=cfg)
+    try:
+        y_ref = Q.moe_rows(x, wb, ws, bias, rd, gi if gather else None, gam, False, L, Bx)
+        y = Q.moe_rows(x, wb, ws, bias, rd, gi if gather else None, gam, False, L, Bx, w_fwd=wt)
+    finally:
+        Q.GEMM_TILE.clear()
+        Q.GEMM_TILE.update(old)
+    assert torch.isfinite(y.float()).all()
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("lora", [False, True])
+def test_forward_tiled_swiglu_bit_equal(dev, lora):
+    """The gate_up forward with its fused SwiGLU (epi 2) on the tiled copy."""
+    g, ref, rd, gi = _routing(dev, 22)
+    alpha, limit, I_ = 1.702, 7.0, 320
+    blocks, scales = _weights(g, 2 * I_, KRED, False)
+    Rr = T * TOPK
+    x = torch.randn(T, KRED, generator=g).to(torch.bfloat16).to(dev)
+    bias = (torch.randn(E, 2 * I_, generator=g) * 0.5).float().to(dev)
+    L = (torch.randn(Rr, 32, generator=g) * 0.3).to(torch.bfloat16).to(dev) if lora else None
+    Bx = (torch.randn(E, 2 * I_, 32, generator=g) * 0.3).to(torch.bfloat16).to(dev) if lora else None
+    wb, ws = blocks.to(dev), scales.to(dev)
+    gu_ref, act_ref = Q.moe_rows(x, wb, ws, bias, rd, gi, None, False, L, Bx, swiglu=("fwd", alpha, limit))
+    gu, act = Q.moe_rows(x, wb, ws, bias, rd, gi, None, False, L, Bx, swiglu=("fwd", alpha, limit),
+                         w_fwd=Q.mxfp4_tile_fwd(wb))
+    assert torch.equal(gu.view(torch.int16), gu_ref.view(torch.int16))
+    assert torch.equal(act.view(torch.int16), act_ref.view(torch.int16))
+
+
+def test_tiled_flag_declined_by_other_kernels(dev):
+    """The C entry point returns AF3_EUNSUPPORTED (nothing launched) for the
+    tiled flag on the input gradient."""
+    g, ref, rd, gi = _routing(dev, 23)
+    blocks, scales = _weights(g, KRED, 576, False)
+    wb, ws = blocks.to(dev), scales.to(dev)
+    x = torch.randn(T, KRED, generator=g).to(torch.bfloat16).to(dev)
+    ed = rd.expt_data
+    y = torch.zeros(T * TOPK, 576, dtype=torch.bfloat16, device=dev)
+    pid = ed.block_pid_map[128]
+    gp = Q._gather_ptr(gi)
+    ok = _capi.try_call("af3_moe_gemm", x.data_ptr(), KRED, gp.data_ptr(), TOPK, wb.data_ptr(),
+                        ws.data_ptr(), 1, None, None, 0, None, 0, None, 0, ed.token_offs_raw.data_ptr(),
+                        pid.data_ptr(), ed.token_offs_pad[128].data_ptr(), pid.numel(), 128, _capi.W_FWD_TILED,
+                        E, 576, KRED, y.data_ptr(), 576, _capi.stream_of(dev))
+    torch.cuda.synchronize()
+    assert not ok
+    assert int(y.view(torch.int16).abs().sum()) == 0
+
+
+def test_module_cache(dev):
+    """The expert module makes the tiled copy once per weight version."""
+    from agent_factory_3_amd import workloads
+    m = workloads.make_experts(workloads.layer(2, T=64, E=4, H=256, I=128), dev)
+    a = m._fwd_tiled("gate_up_proj")
+    assert a is not None and m._fwd_tiled("gate_up_proj") is a
+    blocks, _ = m._get_uint8_weights("gate_up_proj")
+    assert torch.equal(a, Q.mxfp4_tile_fwd(blocks))
+    with torch.no_grad():
+        w = getattr(m, "gate_up_proj_blocks")
+        w.copy_(w.clone())  # an in-place write (same bytes) bumps the version
+    b = m._fwd_tiled("gate_up_proj")
+    assert b is not a and torch.equal(b, a)
