@@ -854,10 +854,11 @@ __device__ __forceinline__ void g7_landed(af3_u32x4 (&r)[TN]) {
 // The 8 waves are WM x WN (NARROW: 1 x 8) of the same 128 x 64 wave tile.
 // SHAPE 0: 256 x 256 (WM x WN waves), 1 (NARROW): 128 x 512 (8 waves side by
 // side), 2 (HALF): 128 x 256 (4 waves side by side; two blocks per CU)
-template <int WM, int WN, int BXK, int SHAPE, bool BG = false>
+template <int WM, int WN, int BXK, int SHAPE, bool BG = false, int NB = 2>
 __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, int row_lo, int nrows, int n0,
                                          int ncols) {
   constexpr bool NARROW = SHAPE == 1, HALF = SHAPE == 2;
+  static_assert(NB == 2 || (NB == 3 && BG), "weight register buffers: 2, or 3 (BG, k-steps a multiple of 3)");
   static_assert(!HALF || BG, "the 128 x 256 shape takes the packed weights from registers");
   constexpr int NW = HALF ? 4 : WM * WN, NT = NW * 64;
   constexpr int RM = (NARROW || HALF) ? 128 : kG4Rows, CN = NARROW ? 512 : kG4Rows;
@@ -947,15 +948,16 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
       AF3_ASM_WAIT_VM(2);
   };
   // BG: the lane's packed weight words of a k-step (row wn0 + 32 tn + lr, MXFP4 block 2 kt + lh: the
-  // 16 bytes of its B fragments for the whole k-step) go global -> registers one k-step ahead, into
-  // bq[parity]; the loads are issued by inline assembly like the copies (so the k-step waits stay
-  // exact) and each k-step's registers pass through an empty asm after the vmcnt wait, so no use of
-  // them can be scheduled before it.  Rows past the tile read row 0 (their sub-tiles are skipped).
+  // 16 bytes of its B fragments for the whole k-step) go global -> registers NB - 1 k-steps ahead,
+  // into bq[kt % NB] (NB = 3 needs nk % 3 == 0, so the loop runs whole triples); the loads are
+  // issued by inline assembly like the copies (so the k-step waits stay exact) and each k-step's
+  // registers pass through an empty asm after the vmcnt wait, so no use of them can be scheduled
+  // before it.  Rows past the tile read row 0 (their sub-tiles are skipped).
   // With the forward-tiled copy (p.b_tiled) the words of one k-step of the
   // wave's 32 rows of sub-tile tn are one contiguous KB, lane l's at 16 l, so
   // each load instruction reads 8 whole 128-byte lines (row-major, it takes 32
   // bytes of 32 different lines, each line re-read over four k-steps).
-  af3_u32x4 bq[2][TN];
+  af3_u32x4 bq[NB][TN];
   const uint8_t* bgp[TN];
   const int bstep = BG && p.b_tiled ? 1024 : 32;  // bytes between a lane's words of consecutive k-steps
 #pragma unroll
@@ -969,8 +971,8 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
       if (nr >= ncols) nr = 0;
       bgp[tn] = eb + (int64_t)(n0 + nr) * p.b.ld + lh * 16;
     }
-    bq[0][tn] = zero4();
-    bq[1][tn] = zero4();
+#pragma unroll
+    for (int b = 0; b < NB; ++b) bq[b][tn] = zero4();
   }
   auto load_b = [&](int kt, auto par) { g7_load_words<TN>(bq[decltype(par)::value], bgp, kt * bstep); };
   const bool live = tm_live > 0 && tn_live > 0;
@@ -983,10 +985,16 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+  // BG: the weight words of k-step 0 (NB = 3: and 1), each before its
+  // k-step's copies (the order every later k-step keeps: its weight loads
+  // first, then its copies)
   if constexpr (BG) {
     if (live) load_b(0, std::integral_constant<int, 0>{});
   }
   issue(0);
+  if constexpr (NB == 3) {
+    if (live) load_b(1, std::integral_constant<int, 1>{});
+  }
   if (BG || nk > 1) issue(1);
   // does the tile hold a scale byte outside [2, 252]?  (then the whole work
   // item takes the exact integer dequantisation)
@@ -1005,12 +1013,18 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
   }
   odd = __syncthreads_or(odd);
 
-  auto kloop = [&](auto full_c, auto exact_c) {
+  // FULL: every sub-tile of the wave's first TMV row groups is live (TMV < TM:
+  // a partial m-tile whose columns are all live, compiled per row-group count
+  // so the k-loop holds no registers for the dead row groups); otherwise the
+  // live sub-tiles are chosen at run time
+  auto kloop = [&](auto full_c, auto exact_c, auto rows_c) {
     constexpr bool FULL = decltype(full_c)::value, EXACT = decltype(exact_c)::value;
-    af3_bf16x8 af[2][TM], bf[2][TN];
+    constexpr int TMV = decltype(rows_c)::value;
+    static_assert(FULL || TMV == TM, "run-time sub-tile selection covers all row groups");
+    af3_bf16x8 af[2][TMV], bf[2][TN];
     const af3_bf16x8 zf = __builtin_bit_cast(af3_bf16x8, zero4());
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm) af[1][tm] = zf;
+    for (int tm = 0; tm < TMV; ++tm) af[1][tm] = zf;
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) bf[1][tn] = zf;
     // the barrier after the wait also orders the carried fragment reads of
@@ -1023,19 +1037,26 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
       constexpr int P = decltype(par)::value;
       constexpr bool last = decltype(last_c)::value;
       if constexpr (BG) {
-        // uniform k-steps: API copies and TN weight loads were issued by every
-        // earlier k-step, so this k-step's data is everything but the newest API
-        wait_stage(false);
+        // uniform k-steps: every earlier k-step issued TN weight loads (for
+        // NB - 1 k-steps later) and then API copies (for two k-steps later), so
+        // this k-step's data is everything but the newest API operations (NB =
+        // 2) or the newest TN + API (NB = 3: the previous k-step's loads too)
+        if constexpr (NB == 3) {
+          static_assert(DPW + TN == 6, "wait count");
+          AF3_ASM_WAIT_VM(6);
+        } else {
+          wait_stage(false);
+        }
         g7_landed<TN>(bq[P]);
         AF3_ASM_LDS_BARRIER();
-        load_b(min(kt + 1, nk - 1), std::integral_constant<int, 1 - P>{});
+        load_b(min(kt + NB - 1, nk - 1), std::integral_constant<int, (P + NB - 1) % NB>{});
       } else {
         wait_stage(last);
         AF3_ASM_LDS_BARRIER();
       }
       const int st = kt % kG4Stages;
-      g4_kstep<TM, TN, DPW, FULL, EXACT, BG>(As + st * ASTAGE, Bs + st * BSTAGE, bq[P], Ss, G, kt, BG || !last, wm0,
-                                             wn0, tm_live, tn_live, acc, af, bf, sc, dma);
+      g4_kstep<TMV, TN, DPW, FULL, EXACT, BG>(As + st * ASTAGE, Bs + st * BSTAGE, bq[P], Ss, G, kt, BG || !last,
+                                              wm0, wn0, tm_live, tn_live, acc, af, bf, sc, dma);
     };
     constexpr std::integral_constant<int, 0> I0{};
     constexpr std::integral_constant<int, 1> I1{};
@@ -1043,18 +1064,28 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
     constexpr std::true_type LAST{};
     int kt = 0;
     if constexpr (BG) {
-      // pairs of k-steps (the register parity is static)
-      for (; kt < nk; kt += 2) {
-        step(kt, MORE, I0, [&](int j) { issue_one(kt + 2, j); });
-        if (kt + 1 < nk) step(kt + 1, MORE, I1, [&](int j) { issue_one(kt + 3, j); });
+      if constexpr (NB == 3) {
+        // whole triples (nk % 3 == 0; the register buffer of each k-step is
+        // static and no path of the compiled loop skips a k-step)
+        for (; kt < nk; kt += 3) {
+          step(kt, MORE, I0, [&](int j) { issue_one(kt + 2, j); });
+          step(kt + 1, MORE, I1, [&](int j) { issue_one(kt + 3, j); });
+          step(kt + 2, MORE, std::integral_constant<int, 2>{}, [&](int j) { issue_one(kt + 4, j); });
+        }
+      } else {
+        // pairs of k-steps (the register parity is static)
+        for (; kt < nk; kt += 2) {
+          step(kt, MORE, I0, [&](int j) { issue_one(kt + 2, j); });
+          if (kt + 1 < nk) step(kt + 1, MORE, I1, [&](int j) { issue_one(kt + 3, j); });
+        }
       }
       // the redundant copies and weight loads past the end have landed before
-      // the LDS is reused; both weight-register buffers stay allocated until
+      // the LDS is reused; all weight-register buffers stay allocated until
       // this wait (a dead load's registers handed to another value before its
       // data lands would be overwritten by it)
       AF3_ASM_WAIT_VM(0);
-      g7_landed<TN>(bq[0]);
-      g7_landed<TN>(bq[1]);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) g7_landed<TN>(bq[b]);
     } else {
       for (; kt + 2 < nk; ++kt) step(kt, MORE, I0, [&](int j) { issue_one(kt + 2, j); });
       if (nk - kt == 2) step(kt++, MORE, I0, [](int) {});
@@ -1062,18 +1093,48 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
     }
     // the last k-step's sub-step 3
 #pragma unroll
-    for (int i = 0; i < TM * TN; ++i) {
+    for (int i = 0; i < TMV * TN; ++i) {
       const int tm = i / TN, tn = i % TN;
       if (FULL || (tm < tm_live && tn < tn_live))
         acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[1][tm], bf[1][tn], acc[tm][tn], 0, 0, 0);
     }
   };
-  if (odd) {
-    kloop(std::false_type{}, std::true_type{});
-  } else if (full) {
-    kloop(std::true_type{}, std::false_type{});
-  } else if (tm_live > 0 && tn_live > 0) {
-    kloop(std::false_type{}, std::false_type{});
+  constexpr std::integral_constant<int, TM> ALL_ROWS{};
+  // NB = 3 (N % 64 == 0: a live wave's columns are all live): every k-loop
+  // is compiled for its wave's live row groups, with the exact conversion or
+  // without, and none selects sub-tiles at run time
+  auto by_rows = [&](auto exact_c) {
+    if constexpr (NB == 3 && TM == 4) {
+      if (tm_live >= 4)
+        kloop(std::true_type{}, exact_c, ALL_ROWS);
+      else if (tm_live == 3)
+        kloop(std::true_type{}, exact_c, std::integral_constant<int, 3>{});
+      else if (tm_live == 2)
+        kloop(std::true_type{}, exact_c, std::integral_constant<int, 2>{});
+      else
+        kloop(std::true_type{}, exact_c, std::integral_constant<int, 1>{});
+    }
+  };
+  if (NB == 3 && tm_live > 0 && tn_live > 0) {
+    if (odd)
+      by_rows(std::true_type{});
+    else
+      by_rows(std::false_type{});
+  } else if (NB == 2 && odd) {
+    if constexpr (NB == 2) kloop(std::false_type{}, std::true_type{}, ALL_ROWS);
+  } else if (NB == 2 && full) {
+    if constexpr (NB == 2) kloop(std::true_type{}, std::false_type{}, ALL_ROWS);
+  } else if (NB == 2 && BG && TM == 4 && tn_live == TN && tm_live > 0) {  // tm_live < TM: a partial m-tile
+    if constexpr (NB == 2 && BG && TM == 4) {
+      if (tm_live == 3)
+        kloop(std::true_type{}, std::false_type{}, std::integral_constant<int, 3>{});
+      else if (tm_live == 2)
+        kloop(std::true_type{}, std::false_type{}, std::integral_constant<int, 2>{});
+      else
+        kloop(std::true_type{}, std::false_type{}, std::integral_constant<int, 1>{});
+    }
+  } else if (NB == 2 && tm_live > 0 && tn_live > 0) {
+    if constexpr (NB == 2) kloop(std::false_type{}, std::false_type{}, ALL_ROWS);
   } else {
     // a wave with no live sub-tile (rows or columns past the end of a
     // partial tile) only keeps the copy / barrier protocol of the k-loop, so
@@ -1146,7 +1207,7 @@ constexpr int kG7MaxG = 96;  // scale bytes per weight row (K <= 3072)
 constexpr int kG7LdsBytes = kG4Stages * 128 * kBK * 2 + 256 * kG7MaxG;  // 72 KB
 static_assert(kG7LdsBytes >= 128 * 256 * 2 + 1024, "the epilogue reuses the LDS for the bf16 tile + row gammas / scales");
 
-template <int BXK>
+template <int BXK, int NB>
 __global__ __launch_bounds__(256, 2) void gemm7_fwd_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kG7LdsBytes];
   int mt, nt;
@@ -1158,7 +1219,7 @@ __global__ __launch_bounds__(256, 2) void gemm7_fwd_kernel(Params p) {
   const int nrows = min(128, p.offs[e + 1] - row_lo);
   if (nrows <= 0) return;
   const int n0 = nt * 256;
-  g4f_tile<1, 4, BXK, 2, true>(p, lds, e, row_lo, nrows, n0, min(256, p.N - n0));
+  g4f_tile<1, 4, BXK, 2, true, NB>(p, lds, e, row_lo, nrows, n0, min(256, p.N - n0));
 }
 
 // ---------------------------------------------------------------------------
@@ -2482,7 +2543,12 @@ static void launch_gemm4_fwd(int max_tiles, int N, hipStream_t stream, Params p)
 static void launch_gemm7_fwd(int max_tiles, int N, hipStream_t stream, Params p) {
   p.n_nblk = (N + 255) / 256;
   dim3 grid(g4_grid(max_tiles, p.n_nblk, p.group_m));
-  hipLaunchKernelGGL((gemm7_fwd_kernel<ROWS_BF16>), grid, dim3(256), 0, stream, p);
+  // weight words two k-steps ahead where the k-steps come in whole triples
+  // and every n-tile's columns come in whole 64-column wave slices
+  if ((p.K / kBK) % 3 == 0 && N % 64 == 0)
+    hipLaunchKernelGGL((gemm7_fwd_kernel<ROWS_BF16, 3>), grid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((gemm7_fwd_kernel<ROWS_BF16, 2>), grid, dim3(256), 0, stream, p);
 }
 
 template <int BM, int BN, int WM, int WN>

@@ -9,7 +9,10 @@ import torch
 
 from agent_factory_3_amd import _capi
 from agent_factory_3_amd import quantization as Q
-from test_gpu_gemm_tiles import CASES, E, KRED, T, TOPK, _routing, _weights
+from agent_factory_3_amd import routing as R
+from oracle import moe, mxfp4
+from oracle import routing as O
+from test_gpu_gemm_tiles import ATOL, CASES, E, KRED, RTOL, T, TOPK, _routing, _weights
 
 pytestmark = pytest.mark.gpu
 
@@ -116,3 +119,54 @@ def test_module_cache(dev):
         w.copy_(w.clone())  # an in-place write (same bytes) bumps the version
     b = m._fwd_tiled("gate_up_proj")
     assert b is not a and torch.equal(b, a)
+
+
+# rows per expert whose last 128-row tile has 2, 3, 1, 1, 4 and 4 live 32-row
+# groups (tails of 60, 74, 20, 10, 100 and 104 rows) and an idle expert
+COUNTS_NB3 = [700, 330, 660, 650, 100, 360, 0]
+
+
+def _routing_counts(dev, seed, counts):
+    g = torch.Generator().manual_seed(seed)
+    assert sum(counts) == T * TOPK and max(counts) <= T
+    order = sorted(range(len(counts)), key=lambda e: -counts[e])
+    multiset = [e for e in order for _ in range(counts[e])]
+    ids = torch.empty(T, TOPK, dtype=torch.int32)
+    for j, e in enumerate(multiset):
+        ids[j % T, j // T] = e
+    ids = ids[torch.randperm(T, generator=g)].sort(dim=1).values
+    logits = torch.randn(T, len(counts), generator=g).to(torch.bfloat16)
+    ref = O.routing_replay(logits, ids, TOPK)
+    rd, gi, si = R.routing_replay(logits.to(dev), ids.to(dev), TOPK)
+    assert ref["hist"].tolist() == counts
+    return g, ref, rd, gi
+
+
+@pytest.mark.parametrize("nout", [576, 640])
+@pytest.mark.parametrize("gather,lora,odd", CASES)
+def test_forward_three_weight_buffers(dev, nout, gather, lora, odd):
+    """K = 576 (nine k-steps, a multiple of three) with N % 64 == 0 runs the
+    forward with the weight words two k-steps ahead and a k-loop compiled per
+    count of live row groups (tails of 1, 2, 3 and 4 groups, the exact
+    conversion for out-of-range scale bytes among them): against the oracle,
+    with the stored and with the tiled weights."""
+    K = 576
+    g, ref, rd, gi = _routing_counts(dev, 31, COUNTS_NB3)
+    blocks, scales = _weights(g, nout, K, odd)
+    Rr = T * TOPK
+    x = torch.randn(T if gather else Rr, K, generator=g).to(torch.bfloat16)
+    bias = (torch.randn(E, nout, generator=g) * 0.1).to(torch.bfloat16)
+    L = (torch.randn(Rr, 32, generator=g) * 0.3).to(torch.bfloat16) if lora else None
+    Bx = (torch.randn(E, nout, 32, generator=g) * 0.3).to(torch.bfloat16) if lora else None
+    wb, ws = blocks.to(dev), scales.to(dev)
+    args = (x.to(dev), wb, ws, bias.float().to(dev), rd, gi if gather else None, None, False,
+            L.to(dev) if lora else None, Bx.to(dev) if lora else None)
+    y = Q.moe_rows(*args)
+    yt = Q.moe_rows(*args, w_fwd=Q.mxfp4_tile_fwd(wb))
+    assert torch.equal(y.view(torch.int16), yt.view(torch.int16))
+    W = mxfp4.dequant_f32(blocks, scales)
+    yr = moe.rows(x, W, ref["offs"], ref["topk_indx"] if gather else None, TOPK, bias=bias, lora_l=L, lora_b=Bx)
+    a = y.float().cpu().double()
+    assert torch.isfinite(a).all()
+    bad = (a - yr.double()).abs() > ATOL + RTOL * yr.double().abs()
+    assert not bad.any(), float(bad.float().mean())

@@ -13,11 +13,13 @@ from tests import isa_hazards as H
 ROOT = Path(__file__).resolve().parents[1]
 CSRC = ROOT / "agent-factory-3_amd" / "csrc"
 HIPCC = shutil.which("hipcc") or ("/opt/rocm/bin/hipcc" if Path("/opt/rocm/bin/hipcc").exists() else None)
-SYMBOL = "_ZN12_GLOBAL__N_116gemm7_fwd_kernelILi0EEEvNS_6ParamsE"
+# the forward kernel with two weight-register buffers and with three (k-steps a multiple of 3)
+SYMBOLS = ["_ZN12_GLOBAL__N_116gemm7_fwd_kernelILi0ELi2EEEvNS_6ParamsE",
+           "_ZN12_GLOBAL__N_116gemm7_fwd_kernelILi0ELi3EEEvNS_6ParamsE"]
 
 
 @pytest.fixture(scope="module")
-def gemm7_asm(tmp_path_factory):
+def moe_gemm_asm(tmp_path_factory):
     if HIPCC is None:
         pytest.skip("hipcc not available")
     from agent_factory_3_amd import build
@@ -25,12 +27,13 @@ def gemm7_asm(tmp_path_factory):
     flags = [f for f in build.HIPCC_FLAGS if f not in ("-fPIC",)]
     subprocess.run([HIPCC, *flags, "-I", str(CSRC), "--cuda-device-only", "-S", str(CSRC / "moe_gemm.hip"),
                     "-o", str(out)], check=True, capture_output=True)
-    return H.function_body(out.read_text(), SYMBOL)
+    return out.read_text()
 
 
 @pytest.mark.timeout(600)
-def test_forward_weight_loads_have_no_register_hazard(gemm7_asm):
-    n, bad = H.violations(gemm7_asm)
+@pytest.mark.parametrize("symbol", SYMBOLS)
+def test_forward_weight_loads_have_no_register_hazard(moe_gemm_asm, symbol):
+    n, bad = H.violations(H.function_body(moe_gemm_asm, symbol))
     assert n >= 4, "expected the k-loop's inline-assembly weight loads"
     assert not bad, bad[:5]
 
