@@ -65,7 +65,7 @@ GEMM_BLOCK_M = 128
 # the 128-row map.
 GEMM_TILE = {"block_m": 256, "tile_cfg": 0, "fwd_block_m": 128, "dx_block_m": 128}
 
-# The expert module's forward GEMMs read a forward-tiled copy of each frozen
+# The expert module's forward GEMMs read a tiled copy of each frozen
 # projection's packed weights (af3_mxfp4_tile_fwd: the words one k-step of a
 # wave needs from 32 weight rows are one contiguous KB), made on first use and
 # kept per weight storage and version: one more copy of the packed blocks on
@@ -208,7 +208,7 @@ def mxfp4_tile_fwd(blocks):
     """Forward-tiled copy of packed MXFP4 weights ``blocks`` [E, N, K/32, 16]
     (uint8, N % 32 == 0, K % 64 == 0): the same bytes permuted so that
     ``out.view(E, N/32, K/64, 2, 32, 16)[e, n // 32, kt, h, n % 32] ==
-    blocks[e, n, 2 kt + h]``; ``moe_rows(..., w_fwd=out)`` reads it in the
+    blocks[e, n, 2 kt + h]``; ``moe_rows(..., w_tiled=out)`` reads it in the
     forward.  No counterpart in the reference (its matmul_ogs reads the stored
     layout, quantization.py:358-362)."""
     if not blocks.is_cuda:
@@ -224,7 +224,7 @@ def mxfp4_tile_fwd(blocks):
 
 
 def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=None, trans_w=False,
-             lora_l=None, lora_b=None, swiglu=None, a_row_scale=None, w_fwd=None):
+             lora_l=None, lora_b=None, swiglu=None, a_row_scale=None, w_tiled=None):
     """Expert-sorted output rows of the grouped GEMM (no scatter).
 
     ``trans_w=False``: ``Y[r] = X[a(r)] @ W[e]^T`` with W = dequant(blocks) [E, N, K]
@@ -239,8 +239,8 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
     interleaved pre-activation ``gate_up`` [R, 2N], i.e. dGU [R, 2N].  Both are
     fused into the GEMM epilogue; None is returned when the selected kernel
     has no fused epilogue (the caller then runs the two steps separately).
-    ``w_fwd``: the ``mxfp4_tile_fwd`` copy of ``blocks``, read instead of them
-    by the default forward kernel (ignored by the others).
+    ``w_tiled``: the ``mxfp4_tile_fwd`` copy of ``blocks``, read instead of
+    them by the default forward kernel (ignored by the others).
     """
     if not x.is_cuda:
         raise RuntimeError("x must be a GPU tensor (the MI355X path has no CPU implementation)")
@@ -286,9 +286,9 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
     if R == 0 or pid_map.numel() == 0:
         return y if epi == 0 else (y, glu) if epi == 2 else y
     blocks = blocks if blocks.data_ptr() % 16 == 0 else blocks.clone()
-    if w_fwd is not None and (w_fwd.shape != blocks.shape or w_fwd.dtype != torch.uint8 or not w_fwd.is_contiguous()
-                              or w_fwd.data_ptr() % 16):
-        raise ValueError("w_fwd must be the mxfp4_tile_fwd copy of blocks (same shape, contiguous uint8)")
+    if w_tiled is not None and (w_tiled.shape != blocks.shape or w_tiled.dtype != torch.uint8 or not w_tiled.is_contiguous()
+                              or w_tiled.data_ptr() % 16):
+        raise ValueError("w_tiled must be the mxfp4_tile_fwd copy of blocks (same shape, contiguous uint8)")
     b = None
     if bias is not None:
         b = bias.to(torch.float32).contiguous()
@@ -315,13 +315,13 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
             raise ValueError("a row scale cannot be combined with the LoRA segment or a fused SwiGLU")
         a_row_scale = a_row_scale.to(torch.float32).contiguous()
 
-    # the forward-tiled weights go to the default forward kernel; any other
-    # selection declines them (nothing launched) and the stored blocks are used
+    # the tiled weights go to the default forward kernel; any other selection
+    # declines them (nothing launched) and the stored blocks are used
     targs = None
-    if w_fwd is not None and not trans_w and a_row_scale is None and bm == 128 \
+    if w_tiled is not None and not trans_w and a_row_scale is None and bm == 128 \
             and GEMM_TILE["tile_cfg"] % 100 in (0, 26):
         targs = list(args)
-        targs[4], targs[19] = w_fwd.data_ptr(), GEMM_TILE["tile_cfg"] | _capi.W_FWD_TILED
+        targs[4], targs[19] = w_tiled.data_ptr(), GEMM_TILE["tile_cfg"] | _capi.W_FWD_TILED
 
     def launch():
         if a_row_scale is not None:
@@ -332,8 +332,8 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
         if targs is not None:
             if epi == 0 and _capi.try_call("af3_moe_gemm", *targs, stream):
                 return True
-            if epi == 2 and _capi.try_call("af3_moe_gemm_swiglu", *targs, epi, glu.data_ptr(), ld_glu, alpha, limit,
-                                           stream):
+            if epi and _capi.try_call("af3_moe_gemm_swiglu", *targs, epi, glu.data_ptr(), ld_glu, alpha, limit,
+                                      stream):
                 return True
         if epi == 0:
             _capi.call("af3_moe_gemm", *args, stream)
@@ -485,7 +485,7 @@ class DequantMoEMatmul(torch.autograd.Function):
                 out = y if fwd_scatter_indx is None else moe_combine(y, fwd_scatter_indx, k)
             else:  # matmul_ogs(x, (blocks, scales), ...) with the module's forward-tiled weights
                 y = moe_rows(x, blocks, scales, bias, routing_data, fwd_gather_indx, fwd_gammas, False,
-                             w_fwd=_fwd_weights(experts_module, proj_name))
+                             w_tiled=_fwd_weights(experts_module, proj_name))
                 k = routing_data.n_expts_act if routing_data is not None else 1
                 out = y if fwd_scatter_indx is None else moe_combine(y, fwd_scatter_indx, k)
         ctx.experts_module = experts_module
@@ -665,7 +665,7 @@ class LoraDequantMoEMatmul(torch.autograd.Function):
         with on_device(dev):
             L = _lora_rows(xg, g, k_act, A, 0, scaling, ed, r, K)
             y = moe_rows(xg, blocks, scales, bias, routing_data, fwd_gather_indx, fwd_gammas, False, L, B,
-                         w_fwd=_fwd_weights(experts_module, proj_name))
+                         w_tiled=_fwd_weights(experts_module, proj_name))
             if fwd_scatter_indx is not None:
                 y = moe_combine(y, fwd_scatter_indx, k_act)
         ctx.save_for_backward(xg, A, B, L)
@@ -769,9 +769,9 @@ class _GateUpSwiGLU(torch.autograd.Function):
                 L = _lora_rows(xg, g, k_act, A, 0, scaling, ed, A.shape[1], K)
             wf = _fwd_weights(experts_module, proj_name)
             res = moe_rows(xg, blocks, scales, bias, routing_data, gather_indx, None, False, L, B,
-                           swiglu=("fwd", alpha, limit), w_fwd=wf)
+                           swiglu=("fwd", alpha, limit), w_tiled=wf)
             if res is None:
-                gu = moe_rows(xg, blocks, scales, bias, routing_data, gather_indx, None, False, L, B, w_fwd=wf)
+                gu = moe_rows(xg, blocks, scales, bias, routing_data, gather_indx, None, False, L, B, w_tiled=wf)
                 act = swiglu_forward(gu, alpha, limit)
             else:
                 gu, act = res
@@ -835,7 +835,7 @@ class _SwiGLUDown(torch.autograd.Function):
             if A is not None:
                 L = _lora_rows(act, None, 1, A, 0, scaling, ed, A.shape[1], K)
             y = moe_rows(act, blocks, scales, bias, routing_data, None, gammas, False, L, B,
-                         w_fwd=_fwd_weights(experts_module, proj_name))
+                         w_tiled=_fwd_weights(experts_module, proj_name))
             if scatter_indx is not None:
                 y = moe_combine(y, scatter_indx, k_act)
         # gate_up (the SwiGLU's input, the same bytes as the reference's saved

@@ -1,9 +1,9 @@
-"""Forward-tiled weights (af3_mxfp4_tile_fwd): the byte permutation itself, and
-the default forward kernel reading it gives the same bits as reading the
-blocks as stored, on the shapes of test_gpu_gemm_tiles (full and partial
-tiles, 64- / 128-column tail n-tiles, gathered rows, the LoRA segment, scale
-bytes outside [2, 252], the fused SwiGLU forward).  Kernels that do not read
-the tiled copy decline it and run on the stored blocks."""
+"""Tiled weights (af3_mxfp4_tile_fwd): the byte permutation itself, and the
+default forward kernel reading it gives the same bits as reading the blocks
+as stored, on the shapes of test_gpu_gemm_tiles (full and partial tiles, 64- /
+128-column tail n-tiles, tails of 1 to 4 row groups, gathered rows, the LoRA
+segment, scale bytes outside [2, 252], the fused SwiGLU forward).  Kernels that
+do not read the tiled copy decline it and run on the stored blocks."""
 import pytest
 import torch
 
@@ -43,7 +43,7 @@ def test_tile_fwd_rejects_bad_shapes(dev):
 @pytest.mark.parametrize("cfg,nout", [(0, 576), (0, 640), (126, 576), (22, 640), (4, 576)])
 @pytest.mark.parametrize("gather,lora,odd", CASES)
 def test_forward_tiled_bit_equal(dev, cfg, nout, gather, lora, odd):
-    """moe_rows with w_fwd equals moe_rows on the stored blocks bit for bit
+    """moe_rows with w_tiled equals moe_rows on the stored blocks bit for bit
     (tile_cfg 0 / 126 read the tiled copy; 22 and 4 decline it)."""
     g, ref, rd, gi = _routing(dev, 21)
     blocks, scales = _weights(g, nout, KRED, odd)
@@ -59,7 +59,7 @@ def test_forward_tiled_bit_equal(dev, cfg, nout, gather, lora, odd):
     Q.GEMM_TILE.update(block_m=256, tile_cfg=cfg)
     try:
         y_ref = Q.moe_rows(x, wb, ws, bias, rd, gi if gather else None, gam, False, L, Bx)
-        y = Q.moe_rows(x, wb, ws, bias, rd, gi if gather else None, gam, False, L, Bx, w_fwd=wt)
+        y = Q.moe_rows(x, wb, ws, bias, rd, gi if gather else None, gam, False, L, Bx, w_tiled=wt)
     finally:
         Q.GEMM_TILE.clear()
         Q.GEMM_TILE.update(old)
@@ -81,7 +81,7 @@ def test_forward_tiled_swiglu_bit_equal(dev, lora):
     wb, ws = blocks.to(dev), scales.to(dev)
     gu_ref, act_ref = Q.moe_rows(x, wb, ws, bias, rd, gi, None, False, L, Bx, swiglu=("fwd", alpha, limit))
     gu, act = Q.moe_rows(x, wb, ws, bias, rd, gi, None, False, L, Bx, swiglu=("fwd", alpha, limit),
-                         w_fwd=Q.mxfp4_tile_fwd(wb))
+                         w_tiled=Q.mxfp4_tile_fwd(wb))
     assert torch.equal(gu.view(torch.int16), gu_ref.view(torch.int16))
     assert torch.equal(act.view(torch.int16), act_ref.view(torch.int16))
 
@@ -162,7 +162,7 @@ def test_forward_three_weight_buffers(dev, nout, gather, lora, odd):
     args = (x.to(dev), wb, ws, bias.float().to(dev), rd, gi if gather else None, None, False,
             L.to(dev) if lora else None, Bx.to(dev) if lora else None)
     y = Q.moe_rows(*args)
-    yt = Q.moe_rows(*args, w_fwd=Q.mxfp4_tile_fwd(wb))
+    yt = Q.moe_rows(*args, w_tiled=Q.mxfp4_tile_fwd(wb))
     assert torch.equal(y.view(torch.int16), yt.view(torch.int16))
     W = mxfp4.dequant_f32(blocks, scales)
     yr = moe.rows(x, W, ref["offs"], ref["topk_indx"] if gather else None, TOPK, bias=bias, lora_l=L, lora_b=Bx)
@@ -170,3 +170,4 @@ def test_forward_three_weight_buffers(dev, nout, gather, lora, odd):
     assert torch.isfinite(a).all()
     bad = (a - yr.double()).abs() > ATOL + RTOL * yr.double().abs()
     assert not bad.any(), float(bad.float().mean())
+
