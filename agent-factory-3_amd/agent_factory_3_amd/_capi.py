@@ -116,6 +116,7 @@ def call(name: str, *args) -> None:
 
 EUNSUPPORTED = -2
 W_FWD_TILED = 0x10000  # tile_cfg flag: the weights are the af3_mxfp4_tile_fwd copy
+X_OFFSETS_32 = 0x20000  # tile_cfg flag: every row of x the call reads lies within 4 GiB of x
 
 
 def try_call(name: str, *args) -> bool:

@@ -62,7 +62,8 @@ GEMM_BLOCK_M = 128
 # default).  The default kernels take the map of fwd_block_m (forward, tile_cfg
 # 26) and dx_block_m (input gradient, tile_cfg 28), both 128; 256 there selects
 # the 256 x 256 kernels (tile_cfg 22 / 23).  The LoRA row products always use
-# the 128-row map.
+# the 128-row map.  x_off32: tell the library when x lies within 4 GiB (the
+# forward then addresses it by a scalar base and 32-bit offsets).
 GEMM_TILE = {"block_m": 256, "tile_cfg": 0, "fwd_block_m": 128, "dx_block_m": 128}
 
 # The expert module's forward GEMMs read a tiled copy of each frozen
@@ -303,11 +304,14 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
         lr = lora_l.shape[-1]
         lora_l = lora_l.contiguous()
         lora_b = lora_b.to(torch.bfloat16).contiguous()
-    args = (x.data_ptr(), x.stride(0) if x.shape[0] > 1 else K, _capi.ptr(g), k_act if g is not None else 1,
+    ldx = x.stride(0) if x.shape[0] > 1 else K
+    # every row of x lies within 4 GiB of x: the kernels may address it by 32-bit offsets
+    off32 = GEMM_TILE.get("x_off32", True) and ((x.shape[0] - 1) * ldx + K) * 2 <= 1 << 32
+    cfg = GEMM_TILE["tile_cfg"] | (_capi.X_OFFSETS_32 if off32 else 0)
+    args = (x.data_ptr(), ldx, _capi.ptr(g), k_act if g is not None else 1,
             blocks.data_ptr(), scales.data_ptr(), 1 if trans_w else 0, _capi.ptr(b), _capi.ptr(gm), gm_f32,
             _capi.ptr(lora_l), lr, _capi.ptr(lora_b), lr, offs.data_ptr(), pid_map.data_ptr(),
-            ed.token_offs_pad[bm].data_ptr(), pid_map.numel(), bm, GEMM_TILE["tile_cfg"], E, N, K, y.data_ptr(),
-            y.shape[1])
+            ed.token_offs_pad[bm].data_ptr(), pid_map.numel(), bm, cfg, E, N, K, y.data_ptr(), y.shape[1])
     stream = _capi.stream_of(dev)
 
     if a_row_scale is not None:  # fp8 mode: (acc * a_row_scale[a(r)] + bias) * gammas
@@ -321,7 +325,7 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
     if w_tiled is not None and not trans_w and a_row_scale is None and bm == 128 \
             and GEMM_TILE["tile_cfg"] % 100 in (0, 26):
         targs = list(args)
-        targs[4], targs[19] = w_tiled.data_ptr(), GEMM_TILE["tile_cfg"] | _capi.W_FWD_TILED
+        targs[4], targs[19] = w_tiled.data_ptr(), cfg | _capi.W_FWD_TILED
 
     def launch():
         if a_row_scale is not None:

@@ -37,6 +37,11 @@ int lora_wgrad_fast(const uint16_t* big, int64_t ld_big, const int32_t* big_gath
 #ifndef AF3_W_FWD_TILED
 #define AF3_W_FWD_TILED 0x10000
 #endif
+// OR-ed into af3_moe_gemm's tile_cfg: every row of x the call reads lies
+// within 4 GiB of x (row * ldx * 2 + K * 2 <= 2^32)
+#ifndef AF3_X_OFFSETS_32
+#define AF3_X_OFFSETS_32 0x20000
+#endif
 
 #define AF3_REQUIRE(cond, ...)            \
   do {                                    \

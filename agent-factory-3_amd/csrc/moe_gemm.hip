@@ -90,6 +90,9 @@ struct Params {
   // (one KB per 32 weight rows and 64-deep k-step, in the order the wave's
   // lanes take them)
   int b_tiled;
+  // the caller's guarantee that every A row the call reads lies within 4 GiB
+  // of a.ptr (tile_cfg | AF3_X_OFFSETS_32)
+  int a_off32;
 };
 
 // scale of A row a(r) for output row r (1 without a row scale)
@@ -721,6 +724,14 @@ __device__ __forceinline__ int g4_b_off(int n, int h) {
 __device__ __forceinline__ void g4_dma16(const void* gptr, uint32_t lds_byte_addr) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(lds_byte_addr) : "memory");
 }
+// The same with the address split into a wave-uniform 64-bit base (SGPRs) and
+// a per-lane 32-bit byte offset: the k-loop advances only the scalar base, so
+// the lanes' offsets stay in the same registers for the whole work item (no
+// per-copy 64-bit address arithmetic, and no register the copy has yet to read
+// is rewritten right after it is issued).
+__device__ __forceinline__ void g4_dma16_s(const void* sbase, uint32_t voff, uint32_t lds_byte_addr) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_byte_addr) : "memory");
+}
 #define AF3_ASM_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
 #define AF3_ASM_BARRIER() asm volatile("s_barrier" ::: "memory")
 // the same after this wave's own LDS stores have completed
@@ -843,6 +854,12 @@ __device__ __forceinline__ void g7_load_words(af3_u32x4 (&dst)[TN], const uint8_
     asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(dst[tn]) : "v"(src[tn] + off) : "memory");
 }
 template <int TN>
+__device__ __forceinline__ void g7_load_words_s(af3_u32x4 (&dst)[TN], const uint32_t (&voff)[TN], const void* sbase) {
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn)
+    asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(dst[tn]) : "v"(voff[tn]), "s"(sbase) : "memory");
+}
+template <int TN>
 __device__ __forceinline__ void g7_landed(af3_u32x4 (&r)[TN]) {
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) asm volatile("" : "+v"(r[tn]));
@@ -854,11 +871,14 @@ __device__ __forceinline__ void g7_landed(af3_u32x4 (&r)[TN]) {
 // The 8 waves are WM x WN (NARROW: 1 x 8) of the same 128 x 64 wave tile.
 // SHAPE 0: 256 x 256 (WM x WN waves), 1 (NARROW): 128 x 512 (8 waves side by
 // side), 2 (HALF): 128 x 256 (4 waves side by side; two blocks per CU)
-template <int WM, int WN, int BXK, int SHAPE, bool BG = false, int NB = 2>
+template <int WM, int WN, int BXK, int SHAPE, bool BG = false, int NB = 2, bool SA = false>
 __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, int row_lo, int nrows, int n0,
                                          int ncols) {
   constexpr bool NARROW = SHAPE == 1, HALF = SHAPE == 2;
   static_assert(NB == 2 || (NB == 3 && BG), "weight register buffers: 2, or 3 (BG, k-steps a multiple of 3)");
+  // SA (BG): the k-loop's A copies and weight loads address a scalar base
+  // plus a 32-bit per-lane offset (a_off32; the expert's packed weights < 4 GiB)
+  static_assert(!SA || BG, "scalar-base addressing in the register-weight kernel");
   static_assert(!HALF || BG, "the 128 x 256 shape takes the packed weights from registers");
   constexpr int NW = HALF ? 4 : WM * WN, NT = NW * 64;
   constexpr int RM = (NARROW || HALF) ? 128 : kG4Rows, CN = NARROW ? 512 : kG4Rows;
@@ -885,14 +905,18 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
   const int tn_live = min(TN, max(0, (ncols - wn0 + 31) >> 5));
   const bool full = tm_live == TM && tn_live == TN;
 
-  // DMA sources: A rows (API instructions per wave per stage, 8 rows each)
+  // DMA sources: A rows (API instructions per wave per stage, 8 rows each);
+  // SA: byte offsets from a.ptr
   const uint16_t* arow[API];
+  uint32_t aoff[API];
 #pragma unroll
   for (int i = 0; i < API; ++i) {
     const int row = (wave * API + i) * 8 + (lane >> 3);
     int64_t src = row_lo + (row < nrows ? row : 0);
     if (p.a.gather) src = p.a.gather[src] / p.a.gdiv;
-    arow[i] = (const uint16_t*)p.a.ptr + src * p.a.ld + (((lane & 7) ^ swz(row)) << 3);
+    const int64_t el = src * p.a.ld + (((lane & 7) ^ swz(row)) << 3);
+    arow[i] = (const uint16_t*)p.a.ptr + el;
+    aoff[i] = (uint32_t)(el * 2);
   }
   // packed B (BPI instructions per wave per stage, 32 weight rows each)
   const uint8_t* bsrc[BPI > 0 ? BPI : 1];
@@ -921,9 +945,13 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
     const int st = kt % kG4Stages;
     // BG: the k-steps past the end copy the last k-step's rows again (into a stage no wave reads again)
     const int ks = BG ? min(kt, nk - 1) : kt;
-    if (j < API)
-      g4_dma16(arow[j] + ks * kBK, lds0 + (uint32_t)(st * ASTAGE * 2 + (wave * API + j) * 8 * kBK * 2));
-    else if constexpr (BPI > 0)
+    if (j < API) {
+      const uint32_t dst = lds0 + (uint32_t)(st * ASTAGE * 2 + (wave * API + j) * 8 * kBK * 2);
+      if constexpr (SA)
+        g4_dma16_s((const uint8_t*)p.a.ptr + (int64_t)ks * kBK * 2, aoff[j], dst);
+      else
+        g4_dma16(arow[j] + ks * kBK, dst);
+    } else if constexpr (BPI > 0)
       g4_dma16(bsrc[j - API] + kt * 32,
                lds0 + (uint32_t)(kG4Stages * ASTAGE * 2 + st * BSTAGE + (wave * BPI + j - API) * 1024));
   };
@@ -959,22 +987,32 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
   // bytes of 32 different lines, each line re-read over four k-steps).
   af3_u32x4 bq[NB][TN];
   const uint8_t* bgp[TN];
+  uint32_t boff[TN];  // SA: byte offsets from the expert's weights
   const int bstep = BG && p.b_tiled ? 1024 : 32;  // bytes between a lane's words of consecutive k-steps
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) {
     const uint8_t* eb = (const uint8_t*)p.b.ptr + e * p.b.estride;
+    int64_t o;
     if (BG && p.b_tiled) {  // ncols % 32 == 0: a 32-row group is live or dead as a whole
       const int nb = wn0 + tn * 32 < ncols ? n0 + wn0 + tn * 32 : 0;
-      bgp[tn] = eb + (int64_t)nb * p.b.ld + lane * 16;  // the group's tiles start at row nb's byte offset
+      o = (int64_t)nb * p.b.ld + lane * 16;  // the group's tiles start at row nb's byte offset
     } else {
       int nr = wn0 + tn * 32 + lr;
       if (nr >= ncols) nr = 0;
-      bgp[tn] = eb + (int64_t)(n0 + nr) * p.b.ld + lh * 16;
+      o = (int64_t)(n0 + nr) * p.b.ld + lh * 16;
     }
+    bgp[tn] = eb + o;
+    boff[tn] = (uint32_t)o;
 #pragma unroll
     for (int b = 0; b < NB; ++b) bq[b][tn] = zero4();
   }
-  auto load_b = [&](int kt, auto par) { g7_load_words<TN>(bq[decltype(par)::value], bgp, kt * bstep); };
+  auto load_b = [&](int kt, auto par) {
+    if constexpr (SA)
+      g7_load_words_s<TN>(bq[decltype(par)::value], boff,
+                          (const uint8_t*)p.b.ptr + e * p.b.estride + (int64_t)kt * bstep);
+    else
+      g7_load_words<TN>(bq[decltype(par)::value], bgp, kt * bstep);
+  };
   const bool live = tm_live > 0 && tn_live > 0;
 
   af3_f32x16 acc[TM][TN];
@@ -1207,7 +1245,7 @@ constexpr int kG7MaxG = 96;  // scale bytes per weight row (K <= 3072)
 constexpr int kG7LdsBytes = kG4Stages * 128 * kBK * 2 + 256 * kG7MaxG;  // 72 KB
 static_assert(kG7LdsBytes >= 128 * 256 * 2 + 1024, "the epilogue reuses the LDS for the bf16 tile + row gammas / scales");
 
-template <int BXK, int NB>
+template <int BXK, int NB, bool SA>
 __global__ __launch_bounds__(256, 2) void gemm7_fwd_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kG7LdsBytes];
   int mt, nt;
@@ -1219,7 +1257,7 @@ __global__ __launch_bounds__(256, 2) void gemm7_fwd_kernel(Params p) {
   const int nrows = min(128, p.offs[e + 1] - row_lo);
   if (nrows <= 0) return;
   const int n0 = nt * 256;
-  g4f_tile<1, 4, BXK, 2, true, NB>(p, lds, e, row_lo, nrows, n0, min(256, p.N - n0));
+  g4f_tile<1, 4, BXK, 2, true, NB, SA>(p, lds, e, row_lo, nrows, n0, min(256, p.N - n0));
 }
 
 // ---------------------------------------------------------------------------
@@ -2544,11 +2582,18 @@ static void launch_gemm7_fwd(int max_tiles, int N, hipStream_t stream, Params p)
   p.n_nblk = (N + 255) / 256;
   dim3 grid(g4_grid(max_tiles, p.n_nblk, p.group_m));
   // weight words two k-steps ahead where the k-steps come in whole triples
-  // and every n-tile's columns come in whole 64-column wave slices
-  if ((p.K / kBK) % 3 == 0 && N % 64 == 0)
-    hipLaunchKernelGGL((gemm7_fwd_kernel<ROWS_BF16, 3>), grid, dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL((gemm7_fwd_kernel<ROWS_BF16, 2>), grid, dim3(256), 0, stream, p);
+  // and every n-tile's columns come in whole 64-column wave slices; scalar-base
+  // addressing where the caller vouches for 32-bit A offsets and an expert's
+  // packed weights are below 4 GiB
+  const bool sa = p.a_off32 && (int64_t)N * (p.K / 2) < (1LL << 32);
+  if ((p.K / kBK) % 3 == 0 && N % 64 == 0) {
+    if (sa)
+      hipLaunchKernelGGL((gemm7_fwd_kernel<ROWS_BF16, 3, true>), grid, dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL((gemm7_fwd_kernel<ROWS_BF16, 3, false>), grid, dim3(256), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((gemm7_fwd_kernel<ROWS_BF16, 2, false>), grid, dim3(256), 0, stream, p);
+  }
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -2579,7 +2624,8 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
                          float limit, const float* a_row_scale, void* stream_, int a_fp8 = 0) {
   hipStream_t stream = (hipStream_t)stream_;
   const bool w_tiled = (tile_cfg & AF3_W_FWD_TILED) != 0;  // w_blocks is the af3_mxfp4_tile_fwd copy
-  tile_cfg &= ~AF3_W_FWD_TILED;
+  const bool x_off32 = (tile_cfg & AF3_X_OFFSETS_32) != 0;  // x's rows within 4 GiB of x (caller's word)
+  tile_cfg &= ~(AF3_W_FWD_TILED | AF3_X_OFFSETS_32);
   AF3_REQUIRE(tile_cfg >= 0, "moe_gemm: bad tile_cfg %d", tile_cfg);
   AF3_REQUIRE(N > 0 && K > 0 && n_expts > 0 && max_tiles >= 0, "moe_gemm: bad sizes N=%d K=%d E=%d", N, K, n_expts);
   if (max_tiles == 0) return 0;
@@ -2595,6 +2641,7 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
   Params p{};
   const int G_k = K / 32, G_n = N / 32;
   p.a = make_bf16(x, ldx, 0, gather_indx, gather_div);
+  p.a_off32 = x_off32;
   p.b.ptr = w_blocks;
   p.b.scales = w_scales;
   if (trans_w == 0) {

@@ -142,9 +142,16 @@ int af3_tile_order(const int32_t* hist, int n_expts_tot, int block_m, const int3
  * AF3_W_FWD_TILED: w_blocks is the af3_mxfp4_tile_fwd copy of the weights
  * (trans_w 0, the tile_cfg 26 forward only; AF3_EUNSUPPORTED, nothing
  * launched, when another kernel is selected: the caller then passes the
- * row-major blocks). */
+ * row-major blocks).  tile_cfg | AF3_X_OFFSETS_32: the caller vouches that
+ * every row of x the call reads lies within 4 GiB of x (a(r) * ldx * 2 + K * 2
+ * <= 2^32), so the tile_cfg 26 forward may address x by a scalar base and
+ * 32-bit lane offsets (the Python layer sets it when x's whole extent is
+ * below 4 GiB); without it every address is 64-bit. */
 #ifndef AF3_W_FWD_TILED
 #define AF3_W_FWD_TILED 0x10000
+#endif
+#ifndef AF3_X_OFFSETS_32
+#define AF3_X_OFFSETS_32 0x20000
 #endif
 int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
                  const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,

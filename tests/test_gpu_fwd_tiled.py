@@ -149,7 +149,8 @@ def test_forward_three_weight_buffers(dev, nout, gather, lora, odd):
     forward with the weight words two k-steps ahead and a k-loop compiled per
     count of live row groups (tails of 1, 2, 3 and 4 groups, the exact
     conversion for out-of-range scale bytes among them): against the oracle,
-    with the stored and with the tiled weights."""
+    with the stored and with the tiled weights, and with scalar-base (x within
+    4 GiB, the default) and 64-bit addressing."""
     K = 576
     g, ref, rd, gi = _routing_counts(dev, 31, COUNTS_NB3)
     blocks, scales = _weights(g, nout, K, odd)
@@ -162,8 +163,18 @@ def test_forward_three_weight_buffers(dev, nout, gather, lora, odd):
     args = (x.to(dev), wb, ws, bias.float().to(dev), rd, gi if gather else None, None, False,
             L.to(dev) if lora else None, Bx.to(dev) if lora else None)
     y = Q.moe_rows(*args)
-    yt = Q.moe_rows(*args, w_tiled=Q.mxfp4_tile_fwd(wb))
+    wt = Q.mxfp4_tile_fwd(wb)
+    yt = Q.moe_rows(*args, w_tiled=wt)
     assert torch.equal(y.view(torch.int16), yt.view(torch.int16))
+    # the same kernel with 64-bit addresses (no 32-bit offset guarantee from the caller)
+    old = dict(Q.GEMM_TILE)
+    Q.GEMM_TILE["x_off32"] = False
+    try:
+        y64 = Q.moe_rows(*args, w_tiled=wt)
+    finally:
+        Q.GEMM_TILE.clear()
+        Q.GEMM_TILE.update(old)
+    assert torch.equal(y.view(torch.int16), y64.view(torch.int16))
     W = mxfp4.dequant_f32(blocks, scales)
     yr = moe.rows(x, W, ref["offs"], ref["topk_indx"] if gather else None, TOPK, bias=bias, lora_l=L, lora_b=Bx)
     a = y.float().cpu().double()

@@ -13,9 +13,11 @@ from tests import isa_hazards as H
 ROOT = Path(__file__).resolve().parents[1]
 CSRC = ROOT / "agent-factory-3_amd" / "csrc"
 HIPCC = shutil.which("hipcc") or ("/opt/rocm/bin/hipcc" if Path("/opt/rocm/bin/hipcc").exists() else None)
-# the forward kernel with two weight-register buffers and with three (k-steps a multiple of 3)
-SYMBOLS = ["_ZN12_GLOBAL__N_116gemm7_fwd_kernelILi0ELi2EEEvNS_6ParamsE",
-           "_ZN12_GLOBAL__N_116gemm7_fwd_kernelILi0ELi3EEEvNS_6ParamsE"]
+# the forward kernel with two weight-register buffers and with three (k-steps a
+# multiple of 3), the latter with 64-bit addresses and with a scalar base
+SYMBOLS = ["_ZN12_GLOBAL__N_116gemm7_fwd_kernelILi0ELi2ELb0EEEvNS_6ParamsE",
+           "_ZN12_GLOBAL__N_116gemm7_fwd_kernelILi0ELi3ELb0EEEvNS_6ParamsE",
+           "_ZN12_GLOBAL__N_116gemm7_fwd_kernelILi0ELi3ELb1EEEvNS_6ParamsE"]
 
 
 @pytest.fixture(scope="module")
