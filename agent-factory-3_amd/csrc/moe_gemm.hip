@@ -1680,7 +1680,9 @@ __device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f
 // RG > 0 (SPLIT = 1): only the first RG row groups of the tile hold rows (an
 // expert's last, partial m-tile), so the waves run the MFMAs and A reads of
 // those alone; the rows past them are never stored either way.
-template <bool NARROW, int BXK, int SPLIT = 1, int RG = 0, bool HALF = false>
+// SADDR: the copies address a scalar base plus 32-bit lane offsets (A: a_off32;
+// the expert's packed weights and scales below 4 GiB), advancing only the base.
+template <bool NARROW, int BXK, int SPLIT = 1, int RG = 0, bool HALF = false, bool SADDR = false>
 __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, int row_lo, int nrows, int n0, int ncols) {
   static_assert(!(NARROW && HALF), "one item shape");
   static_assert(SPLIT == 1 || (!NARROW && !HALF && (SPLIT == 2 || SPLIT == 4)), "row split only for 256-row tiles");
@@ -1714,29 +1716,38 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
   const int pg_live = min(PG, max(0, (ncols - wn0) >> 6));  // ncols is a multiple of 64
   const bool wave_live = pg_live > 0;
 
-  // ---- global -> LDS copy sources ----
+  // ---- global -> LDS copy sources (SA: byte offsets from the scalar bases) ----
   const uint16_t* arow[AI];
+  uint32_t aoff32[AI];
 #pragma unroll
   for (int i = 0; i < AI; ++i) {
     const int row = (wave * AI + i) * 8 + (lane >> 3);
     int64_t src = row_lo + (row < nrows ? row : 0);
     if (p.a.gather) src = p.a.gather[src] / p.a.gdiv;
-    arow[i] = (const uint16_t*)p.a.ptr + src * p.a.ld + (((lane & 7) ^ swz(row)) << 3);
+    const int64_t el = src * p.a.ld + (((lane & 7) ^ swz(row)) << 3);
+    arow[i] = (const uint16_t*)p.a.ptr + el;
+    aoff32[i] = (uint32_t)(el * 2);
   }
   const uint8_t* bsrc[BI];  // 1 KB of weight rows per copy: 1024 / BRB rows, LDS slot lane % NCH
+  uint32_t boff32[BI];
 #pragma unroll
   for (int j = 0; j < BI; ++j) {
     const int kr = (wave * BI + j) * (1024 / BRB) + lane / NCH;
     int c = (lane % NCH) ^ bswz(kr);
     if (c * 32 >= ncols) c = 0;  // columns past the tile: any valid bytes (never read)
-    bsrc[j] = (const uint8_t*)p.b.ptr + e * p.b.estride + (int64_t)kr * p.b.ld + (n0 >> 1) + c * 16;
+    const int64_t o = (int64_t)kr * p.b.ld + (n0 >> 1) + c * 16;
+    bsrc[j] = (const uint8_t*)p.b.ptr + e * p.b.estride + o;
+    boff32[j] = (uint32_t)o;
   }
   const uint8_t* ssrc[SI];  // block q = SI w + j, k row = lane
+  uint32_t soff32[SI];
 #pragma unroll
   for (int j = 0; j < SI; ++j) {
     int q = wave * SI + j;
     if (q * 32 >= ncols) q = 0;
-    ssrc[j] = p.b.scales + e * p.b.sestride + (int64_t)lane * p.b.sld + (n0 >> 5) + q;
+    const int64_t o = (int64_t)lane * p.b.sld + (n0 >> 5) + q;
+    ssrc[j] = p.b.scales + e * p.b.sestride + o;
+    soff32[j] = (uint32_t)o;
   }
   const int64_t bstep = (int64_t)kBK * p.b.ld, sstep = (int64_t)kBK * p.b.sld;
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
@@ -1744,11 +1755,24 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
   auto issue_one = [&](int kc, int j) {
     const uint32_t st = lds0 + (uint32_t)((kc % kD5Stages) * STAGE);
     if (j < AI) {
-      g4_dma16(arow[j] + kc * kBK, st + (uint32_t)(AOFF + (wave * AI + j) * 1024));
+      const uint32_t dst = st + (uint32_t)(AOFF + (wave * AI + j) * 1024);
+      if constexpr (SADDR)
+        g4_dma16_s((const uint8_t*)p.a.ptr + (int64_t)kc * kBK * 2, aoff32[j], dst);
+      else
+        g4_dma16(arow[j] + kc * kBK, dst);
     } else if (j < AI + BI) {
-      g4_dma16(bsrc[j - AI] + kc * bstep, st + (uint32_t)(BOFF + (wave * BI + j - AI) * 1024));
+      const uint32_t dst = st + (uint32_t)(BOFF + (wave * BI + j - AI) * 1024);
+      if constexpr (SADDR)
+        g4_dma16_s((const uint8_t*)p.b.ptr + e * p.b.estride + kc * bstep, boff32[j - AI], dst);
+      else
+        g4_dma16(bsrc[j - AI] + kc * bstep, dst);
     } else {
-      asm volatile("s_nop 0\n\tglobal_load_lds_ubyte %0, off" ::"v"(ssrc[j - AI - BI] + kc * sstep), "{m0}"(st + (uint32_t)(SOFF + (wave * SI + j - AI - BI) * 256)) : "memory");
+      const uint32_t dst = st + (uint32_t)(SOFF + (wave * SI + j - AI - BI) * 256);
+      if constexpr (SADDR)
+        asm volatile("s_nop 0\n\tglobal_load_lds_ubyte %0, %1" ::"v"(soff32[j - AI - BI]),
+                     "s"(p.b.scales + e * p.b.sestride + kc * sstep), "{m0}"(dst) : "memory");
+      else
+        asm volatile("s_nop 0\n\tglobal_load_lds_ubyte %0, off" ::"v"(ssrc[j - AI - BI] + kc * sstep), "{m0}"(dst) : "memory");
     }
   };
   auto issue = [&](int kc) {
@@ -2044,7 +2068,7 @@ __global__ __launch_bounds__(256) void gemm5_dgrad_kernel(Params p) {
 // waves of 128 x 64 (each weight byte converted once per 128 rows), two blocks
 // per CU, so one block's epilogue (the fused SwiGLU backward's VALU work in
 // the down projection) overlaps the other block's k-loop.
-template <int BXK>
+template <int BXK, bool SA>
 __global__ __launch_bounds__(256, 2) void gemm8_dgrad_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kD5HLdsBytes];
   int mt, nt;
@@ -2058,13 +2082,13 @@ __global__ __launch_bounds__(256, 2) void gemm8_dgrad_kernel(Params p) {
   const int n0 = nt * 256;
   const int ncols = min(256, p.N - n0);
   if (nrows <= 32)
-    d5_tile<false, BXK, 1, 1, true>(p, lds, e, row_lo, nrows, n0, ncols);
+    d5_tile<false, BXK, 1, 1, true, SA>(p, lds, e, row_lo, nrows, n0, ncols);
   else if (nrows <= 64)
-    d5_tile<false, BXK, 1, 2, true>(p, lds, e, row_lo, nrows, n0, ncols);
+    d5_tile<false, BXK, 1, 2, true, SA>(p, lds, e, row_lo, nrows, n0, ncols);
   else if (nrows <= 96)
-    d5_tile<false, BXK, 1, 3, true>(p, lds, e, row_lo, nrows, n0, ncols);
+    d5_tile<false, BXK, 1, 3, true, SA>(p, lds, e, row_lo, nrows, n0, ncols);
   else
-    d5_tile<false, BXK, 1, 0, true>(p, lds, e, row_lo, nrows, n0, ncols);
+    d5_tile<false, BXK, 1, 0, true, SA>(p, lds, e, row_lo, nrows, n0, ncols);
 }
 
 // ---------------------------------------------------------------------------
@@ -2562,7 +2586,12 @@ inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 static void launch_gemm8_dgrad(int max_tiles, int N, hipStream_t stream, Params p) {
   p.n_nblk = (N + 255) / 256;
   dim3 grid(g4_grid(max_tiles, p.n_nblk, p.group_m));
-  hipLaunchKernelGGL(gemm8_dgrad_kernel<COLS_BF16>, grid, dim3(256), 0, stream, p);
+  // scalar-base addressing where the caller vouches for 32-bit A offsets and
+  // an expert's packed weights (K x N / 2 bytes) are below 4 GiB
+  if (p.a_off32 && (int64_t)p.K * (N / 2) < (1LL << 32))
+    hipLaunchKernelGGL((gemm8_dgrad_kernel<COLS_BF16, true>), grid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((gemm8_dgrad_kernel<COLS_BF16, false>), grid, dim3(256), 0, stream, p);
 }
 
 static void launch_gemm5_dgrad(int max_tiles, int N, hipStream_t stream, Params p) {
