@@ -28,6 +28,11 @@ typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 __device__ __forceinline__ void l_dma16(const void* gptr, uint32_t lds_byte_addr) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(lds_byte_addr) : "memory");
 }
+// the same from a wave-uniform base (SGPRs) plus a 32-bit lane offset: the
+// 32-bit offset arithmetic replaces a 64-bit address per copy
+__device__ __forceinline__ void l_dma16_s(const void* sbase, uint32_t voff, uint32_t lds_byte_addr) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_byte_addr) : "memory");
+}
 #define L_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
 #define L_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
 
@@ -238,6 +243,7 @@ __global__ __launch_bounds__(256, 2) void lwg_kernel(LwParams p) {
   const int nsteps = (kend + kLwRows - 1) / kLwRows;
   const bool big_rs = MODE == 0 && p.rowscale != nullptr;
   const bool small_rs = MODE == 1 && p.rowscale != nullptr;
+  bool wide = false;
   for (int i = threadIdx.x; i < nsteps * kLwRows; i += 256) {
     const bool valid = i < kend;
     const int64_t src = kb + (valid ? i : 0);  // rows past the chunk read its first row
@@ -245,8 +251,11 @@ __global__ __launch_bounds__(256, 2) void lwg_kernel(LwParams p) {
     const float rs = p.rowscale ? af3_bf16_to_f32(p.rowscale[src]) : 1.f;
     rs_small[i] = valid ? (small_rs ? rs : 1.f) : 0.f;
     rs_big[i] = rs;
+    wide |= ((int64_t)gsrc[i] * p.ld_big + p.W) * 2 > (1LL << 32);
   }
-  __syncthreads();
+  // every copy of the block addresses Big and Small by 32-bit byte offsets
+  // from their bases unless a row lies beyond 4 GiB
+  wide = __syncthreads_or(wide) || (int64_t)(kb + kend) * SR > (1LL << 32);
   const int c0 = bb * 256;
   const int ncols = min(256, p.W - c0);
   const int lane = threadIdx.x & 63;
@@ -271,13 +280,21 @@ __global__ __launch_bounds__(256, 2) void lwg_kernel(LwParams p) {
     for (int i = 0; i < NB; ++i) {
       const int rr = (wave * NB + i) * 2 + (lane >> 5);
       const int64_t src = gsrc[st_i * kLwRows + rr];
-      l_dma16(bcol[i] + src * p.ld_big, st + (uint32_t)((wave * NB + i) * 1024));
+      const uint32_t dst = st + (uint32_t)((wave * NB + i) * 1024);
+      if (wide)
+        l_dma16(bcol[i] + src * p.ld_big, dst);
+      else
+        l_dma16_s(p.big, (uint32_t)(bcol[i] - p.big) * 2u + (uint32_t)src * (uint32_t)(p.ld_big * 2), dst);
     }
     if (has_s) {
       const int off = wave * 1024 + lane * 16;  // byte offset inside the step's Small rows
       const int rl = st_i * kLwRows + off / SR;
       const int64_t srow = kb + (rl < kend ? rl : 0);
-      l_dma16(ssrc + srow * SR + (off % SR), st + (uint32_t)(kLwBig + wave * 1024));
+      const uint32_t dst = st + (uint32_t)(kLwBig + wave * 1024);
+      if (wide)
+        l_dma16(ssrc + srow * SR + (off % SR), dst);
+      else
+        l_dma16_s(ssrc, (uint32_t)srow * SR + (off % SR), dst);
     }
   };
   af3_f32x16 acc[2];
@@ -484,14 +501,18 @@ __global__ __launch_bounds__(256, kLuMinBlocks) void lug_kernel(LuParams p) {
   const int nsteps = (kend + kLwRows - 1) / kLwRows;
   const int NT = nsteps * kLuG;  // ring steps
   const bool big_rs = p.rowscale != nullptr;
+  bool wide = false;
   for (int i = threadIdx.x; i < nsteps * kLwRows; i += 256) {
     const bool valid = i < kend;
     const int64_t src = kb + (valid ? i : 0);  // rows past the chunk read its first row
     gsrc[i] = p.big_gather ? p.big_gather[src] / p.big_div : (int32_t)src;
     rs_small[i] = valid ? 1.f : 0.f;
     rs_big[i] = big_rs ? af3_bf16_to_f32(p.rowscale[src]) : 1.f;
+    wide |= ((int64_t)gsrc[i] * p.ld_big + p.W) * 2 > (1LL << 32);
   }
-  __syncthreads();  // gsrc / rs_* published
+  // gsrc / rs_* published; every copy of the block addresses Big and Small by
+  // 32-bit byte offsets from their bases unless a row lies beyond 4 GiB
+  wide = __syncthreads_or(wide) || (int64_t)(kb + kend) * SR > (1LL << 32);
   const int gc0 = cg * (kLuG * 256);  // first column of the group (< W)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -517,13 +538,21 @@ __global__ __launch_bounds__(256, kLuMinBlocks) void lug_kernel(LuParams p) {
       const int64_t src = gsrc[s * kLwRows + rr];
       int col = gc0 + j * 256 + lcs[i] * 8;
       col = col < p.W ? col : 0;
-      l_dma16(p.big + src * p.ld_big + col, st + (uint32_t)((wave * NB + i) * 1024));
+      const uint32_t dst = st + (uint32_t)((wave * NB + i) * 1024);
+      if (wide)
+        l_dma16(p.big + src * p.ld_big + col, dst);
+      else
+        l_dma16_s(p.big, (uint32_t)src * (uint32_t)(p.ld_big * 2) + (uint32_t)col * 2u, dst);
     }
     if (has_s) {
       const int off = wave * 1024 + lane * 16;  // byte offset inside the step's Small rows
       const int rl = s * kLwRows + off / SR;
       const int64_t srow = kb + (rl < kend ? rl : 0);
-      l_dma16(ssrc + srow * SR + (off % SR), st + (uint32_t)(kLwBig + wave * 1024));
+      const uint32_t dst = st + (uint32_t)(kLwBig + wave * 1024);
+      if (wide)
+        l_dma16(ssrc + srow * SR + (off % SR), dst);
+      else
+        l_dma16_s(ssrc, (uint32_t)srow * SR + (off % SR), dst);
     }
   };
 

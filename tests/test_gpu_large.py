@@ -242,3 +242,41 @@ def test_whole_stack_dequant_past_2_31_elements(dev):
         assert (got == ref.numpy().view(np.uint32)).all(), f"expert {e}"   # bits: -0.0 is not +0.0
     del out, blocks, scales
     torch.cuda.empty_cache()
+
+
+def test_lora_passes_gather_rows_past_4_gib(dev):
+    """The one-pass LoRA backward (u and dB) and the dA pass read the wide
+    operand through 32-bit offsets from its base unless a row of the block lies
+    past 4 GiB: here each expert's rows are gathered from both sides of 4 GiB
+    of a 4.4 GB tensor (so its blocks take the 64-bit addresses), against the
+    oracle on the gathered rows."""
+    W, r, Ec = 2880, 16, 2
+    rows_big = 760_000                                  # 760,000 rows x 5,760 B = 4.38 GB
+    first_past = (1 << 32) // (W * 2) + 1               # first row that starts past 4 GiB
+    counts = [700, 324]
+    Rr = sum(counts)
+    g = torch.Generator().manual_seed(7)
+    low = torch.randperm(4096, generator=g)[: Rr // 2]
+    high = first_past + torch.randperm(rows_big - first_past, generator=g)[: Rr - Rr // 2]
+    idx = torch.cat([low, high])[torch.randperm(Rr, generator=g)]
+    vals = torch.randn(Rr, W, generator=g).to(torch.bfloat16)
+    big = torch.zeros(rows_big, W, dtype=torch.bfloat16, device=dev)
+    big[idx.to(dev)] = vals.to(dev)
+    gather = idx.to(torch.int32).to(dev)
+    hist = torch.tensor(counts, dtype=torch.int32, device=dev)
+    ed = R.compute_expt_data(hist, Ec, Rr)
+    L = (torch.randn(Rr, r, generator=g) * 0.5).to(torch.bfloat16)
+    Bw = (torch.randn(Ec, W, r, generator=g) * 0.05).to(torch.bfloat16)
+    u, dB = Q._lora_u_and_dB(big, gather, 1, None, L.to(dev), Bw.to(dev), 0.5, ed, Ec, W)
+    dA = Q._lora_wgrad(L.to(dev), None, 1, None, big, gather, 1, ed, Ec, r, W)
+    torch.cuda.synchronize()
+    del big
+    offs = [0, counts[0], Rr]
+    for e in range(Ec):
+        lo, hi = offs[e], offs[e + 1]
+        ref, mag = moe.expert_lora_rows(vals[lo:hi], Bw[e], torch.arange(hi - lo), 0.5, trans=True)
+        check_close(u[lo:hi].cpu(), ref, mag=mag, n=W, what=f"u e{e}")
+        ref, mag = moe.expert_wgrad(vals[lo:hi], L[lo:hi], None)
+        check_close(dB[e].cpu(), ref, mag=mag, n=hi - lo, what=f"dB e{e}")
+        ref, mag = moe.expert_wgrad(L[lo:hi], vals[lo:hi], None)
+        check_close(dA[e].cpu(), ref, mag=mag, n=hi - lo, what=f"dA e{e}")
