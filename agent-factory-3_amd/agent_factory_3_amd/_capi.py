@@ -38,6 +38,7 @@ _SIGNATURES = {
     "af3_router_logits": (_i32, [_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _p, _i64, _p]),
     "af3_tile_order": (_i32, [_p, _i32, _i32, _p, _i32, _p, _p]),
     "af3_mxfp4_tile_fwd": (_i32, [_p, _i64, _i32, _i32, _p, _p]),
+    "af3_mxfp4_tile_dx_scales": (_i32, [_p, _i64, _i32, _i32, _p, _p]),
     "af3_moe_gemm": (_i32, [_p, _i64, _p, _i32, _p, _p, _i32, _p, _p, _i32, _p, _i64, _p, _i32,
                             _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p]),
     "af3_moe_gemm_swiglu": (_i32, [_p, _i64, _p, _i32, _p, _p, _i32, _p, _p, _i32, _p, _i64, _p, _i32,
@@ -117,6 +118,7 @@ def call(name: str, *args) -> None:
 EUNSUPPORTED = -2
 W_FWD_TILED = 0x10000  # tile_cfg flag: the weights are the af3_mxfp4_tile_fwd copy
 X_OFFSETS_32 = 0x20000  # tile_cfg flag: every row of x the call reads lies within 4 GiB of x
+S_DX_TILED = 0x40000  # tile_cfg flag: the scales are the af3_mxfp4_tile_dx_scales copy
 
 
 def try_call(name: str, *args) -> bool:

@@ -73,6 +73,11 @@ GEMM_TILE = {"block_m": 256, "tile_cfg": 0, "fwd_block_m": 128, "dx_block_m": 12
 # the device (1.6 GB for a gpt-oss-120b layer's 128 experts).  The input
 # gradient, the checkpoint format and the scales use the blocks as stored.
 FWD_TILED_WEIGHTS = True
+# The input-gradient GEMMs read a tiled copy of each projection's e8m0 scales
+# (af3_mxfp4_tile_dx_scales: a wave's scale bytes of a k-step are 128
+# contiguous bytes), made on first use and kept like the tiled weights (1/16
+# of the packed blocks' size, ~0.1 GB for a gpt-oss-120b layer).
+DX_TILED_SCALES = True
 
 # Optional launch timer for the grouped GEMM (set by benchmark harnesses):
 # callable(tag: str, flops: int, detail: str) -> context manager wrapping the launch.
@@ -224,8 +229,29 @@ def mxfp4_tile_fwd(blocks):
     return out.view(blocks.shape)
 
 
+def mxfp4_tile_dx_scales(scales):
+    """Tiled copy of the e8m0 scales ``scales`` [E, K, N/32] of trans_w=True
+    weights (K % 64 == 0) for the input-gradient kernel, flat uint8:
+    ``out[:E*K/64*NT*512].view(E, K/64, NT, 8, 64)[e, k // 64, n // 256,
+    (n // 32) % 8, k % 64] == scales[e, k, n // 32]`` (NT = ceil(N/256), 127
+    past N/32), then ``out[-E*NT:].view(E, NT)``: 1 where a scale byte of the
+    n-tile lies outside [2, 252]; ``moe_rows(..., trans_w=True, s_tiled=out)``
+    reads it.  No counterpart in the reference."""
+    if not scales.is_cuda:
+        raise RuntimeError("scales must be a GPU tensor (the MI355X path has no CPU implementation)")
+    s = scales if scales.dim() == 3 else scales.unsqueeze(0)
+    if s.dtype != torch.uint8:
+        raise TypeError(f"scales must be uint8 [E, K, N/32] (got {s.dtype})")
+    E, K, G = s.shape
+    s = s.contiguous()
+    nt = (G * 32 + 255) // 256
+    out = torch.empty(E * nt * ((K // 64) * 512 + 1), dtype=torch.uint8, device=s.device)
+    _capi.call("af3_mxfp4_tile_dx_scales", s.data_ptr(), E, K, G * 32, out.data_ptr(), _capi.stream_of(s.device))
+    return out
+
+
 def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=None, trans_w=False,
-             lora_l=None, lora_b=None, swiglu=None, a_row_scale=None, w_tiled=None):
+             lora_l=None, lora_b=None, swiglu=None, a_row_scale=None, w_tiled=None, s_tiled=None):
     """Expert-sorted output rows of the grouped GEMM (no scatter).
 
     ``trans_w=False``: ``Y[r] = X[a(r)] @ W[e]^T`` with W = dequant(blocks) [E, N, K]
@@ -241,7 +267,9 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
     fused into the GEMM epilogue; None is returned when the selected kernel
     has no fused epilogue (the caller then runs the two steps separately).
     ``w_tiled``: the ``mxfp4_tile_fwd`` copy of ``blocks``, read instead of
-    them by the default forward kernel (ignored by the others).
+    them by the default forward kernel (ignored by the others); ``s_tiled``:
+    the ``mxfp4_tile_dx_scales`` copy of ``scales``, read instead of them by
+    the default input-gradient kernel.
     """
     if not x.is_cuda:
         raise RuntimeError("x must be a GPU tensor (the MI355X path has no CPU implementation)")
@@ -319,13 +347,21 @@ def moe_rows(x, blocks, scales, bias, routing_data, gather_indx=None, gammas=Non
             raise ValueError("a row scale cannot be combined with the LoRA segment or a fused SwiGLU")
         a_row_scale = a_row_scale.to(torch.float32).contiguous()
 
-    # the tiled weights go to the default forward kernel; any other selection
-    # declines them (nothing launched) and the stored blocks are used
+    # the tiled weights go to the default forward kernel, the tiled scales to
+    # the default input-gradient kernel; any other selection declines them
+    # (nothing launched) and the stored blocks / scales are used
     targs = None
     if w_tiled is not None and not trans_w and a_row_scale is None and bm == 128 \
             and GEMM_TILE["tile_cfg"] % 100 in (0, 26):
         targs = list(args)
         targs[4], targs[19] = w_tiled.data_ptr(), cfg | _capi.W_FWD_TILED
+    if s_tiled is not None and trans_w and a_row_scale is None and bm == 128 \
+            and GEMM_TILE["tile_cfg"] % 100 in (0, 28):
+        if s_tiled.dtype != torch.uint8 or not s_tiled.is_contiguous() \
+                or s_tiled.numel() != E * ((N + 255) // 256) * ((K // 64) * 512 + 1):
+            raise ValueError("s_tiled must be the mxfp4_tile_dx_scales copy of scales")
+        targs = list(args)
+        targs[5], targs[19] = s_tiled.data_ptr(), cfg | _capi.S_DX_TILED
 
     def launch():
         if a_row_scale is not None:
@@ -530,9 +566,11 @@ class DequantMoEMatmul(torch.autograd.Function):
                     _, gs, gq = kernels.quantize_per_token_e4m3(g, with_bf16=True)
                     grad_x = matmul_ogs(gq, (blocks, scales), None, ctx.routing_data, ctx.bwd_gather_indx,
                                         ctx.bwd_scatter_indx, ctx.bwd_gammas, trans_w=True, a_row_scale=gs)
-            else:
-                grad_x = matmul_ogs(g, (blocks, scales), None, ctx.routing_data, ctx.bwd_gather_indx,
-                                    ctx.bwd_scatter_indx, ctx.bwd_gammas, trans_w=True)
+            else:  # matmul_ogs(g, (blocks, scales), ..., trans_w=True) with the module's tiled scales
+                y = moe_rows(g, blocks, scales, None, ctx.routing_data, ctx.bwd_gather_indx, ctx.bwd_gammas, True,
+                             s_tiled=_dx_scales(ctx.experts_module, ctx.proj_name))
+                k = ctx.routing_data.n_expts_act if ctx.routing_data is not None else 1
+                grad_x = y if ctx.bwd_scatter_indx is None else moe_combine(y, ctx.bwd_scatter_indx, k)
             d_gam = None
             if ctx.needs_input_grad[7]:
                 x, gam = ctx.saved_tensors
@@ -705,7 +743,8 @@ class LoraDequantMoEMatmul(torch.autograd.Function):
             gam = gam.to(torch.bfloat16).contiguous()
         with on_device(dY.device):
             u, dB = _lora_u_and_dB(dY, bg, k_act if bg is not None else 1, gam, L, B, ctx.scaling, ed, E, N)
-            dx = moe_rows(dY, blocks, scales, None, ctx.routing_data, ctx.bwd_gather_indx, gam, True, u, A)
+            dx = moe_rows(dY, blocks, scales, None, ctx.routing_data, ctx.bwd_gather_indx, gam, True, u, A,
+                          s_tiled=_dx_scales(ctx.experts_module, ctx.proj_name))
             if ctx.bwd_scatter_indx is not None:
                 dx = moe_combine(dx, ctx.bwd_scatter_indx, k_act)
             dA = _lora_wgrad(u, None, 1, gam, xg, ctx.fwd_gather, k_act if ctx.fwd_gather is not None else 1,
@@ -745,6 +784,14 @@ def _fwd_weights(experts_module, proj_name):
     if experts_module is None or not FWD_TILED_WEIGHTS:
         return None
     return experts_module._fwd_tiled(proj_name)
+
+
+def _dx_scales(experts_module, proj_name):
+    """The module's tiled copy of ``proj_name``'s scales for the input
+    gradient (None without a module or with DX_TILED_SCALES off)."""
+    if experts_module is None or not DX_TILED_SCALES:
+        return None
+    return experts_module._dx_tiled_scales(proj_name)
 
 
 def _bf16c(t):
@@ -809,7 +856,8 @@ class _GateUpSwiGLU(torch.autograd.Function):
             if A is not None:
                 u, dB = _lora_u_and_dB(dGU, None, 1, None, L, B, ctx.scaling, ed, E, N)
                 dB = dB.to(ctx.lora_dtypes[1])
-            dx = moe_rows(dGU, blocks, scales, None, ctx.routing_data, None, None, True, u, A)
+            dx = moe_rows(dGU, blocks, scales, None, ctx.routing_data, None, None, True, u, A,
+                          s_tiled=_dx_scales(ctx.experts_module, ctx.proj_name))
             if ctx.scatter_indx is not None:
                 dx = moe_combine(dx, ctx.scatter_indx, k_act)
             if A is not None:
@@ -880,9 +928,11 @@ class _SwiGLUDown(torch.autograd.Function):
             want_gam = ctx.needs_input_grad[10]  # routing-weight gradient (routing.GAMMA_GRAD)
             if FUSED_SWIGLU_BWD and not want_gam:
                 dgu = moe_rows(dY, blocks, scales, None, ctx.routing_data, ctx.bwd_gather_indx, gam, True, u, A,
-                               swiglu=("bwd", gate_up, ctx.alpha, ctx.limit))
+                               swiglu=("bwd", gate_up, ctx.alpha, ctx.limit),
+                               s_tiled=_dx_scales(ctx.experts_module, ctx.proj_name))
             if dgu is None:
-                d_act = moe_rows(dY, blocks, scales, None, ctx.routing_data, ctx.bwd_gather_indx, gam, True, u, A)
+                d_act = moe_rows(dY, blocks, scales, None, ctx.routing_data, ctx.bwd_gather_indx, gam, True, u, A,
+                                 s_tiled=_dx_scales(ctx.experts_module, ctx.proj_name))
                 if want_gam:
                     d_gam = _gamma_grad(d_act, act, dY, ctx.bwd_gather_indx, k_act, ctx.gamma_bias,
                                         ctx.routing_data, ctx.gammas)
@@ -975,6 +1025,25 @@ class Mxfp4Bf16DequantGptOssExperts(nn.Module):
             cache.pop(proj, None)  # the old copy goes before the new one is made
             with torch.no_grad():
                 hit = cache[proj] = (src, key, mxfp4_tile_fwd(blocks))
+        return hit[2]
+
+    def _dx_tiled_scales(self, proj):
+        """The input gradient's tiled copy of the projection's scales
+        (``mxfp4_tile_dx_scales``), made once per scale storage and version;
+        None where the input-gradient kernel cannot read one."""
+        _, scales = self._get_uint8_weights(proj)
+        if not scales.is_cuda or scales.dim() != 3 or scales.shape[1] % 64:
+            return None
+        src = getattr(self, f"{proj}_scales", None)
+        if src is None:
+            return None
+        cache = self.__dict__.setdefault("_dx_scales_cache", {})
+        key = (scales.data_ptr(), src._version, tuple(scales.shape))
+        hit = cache.get(proj)
+        if hit is None or hit[0] is not src or hit[1] != key:
+            cache.pop(proj, None)
+            with torch.no_grad():
+                hit = cache[proj] = (src, key, mxfp4_tile_dx_scales(scales))
         return hit[2]
 
     def forward(self, hidden_states: torch.Tensor, routing_data, gather_idx, scatter_idx) -> torch.Tensor:

@@ -42,6 +42,10 @@ int lora_wgrad_fast(const uint16_t* big, int64_t ld_big, const int32_t* big_gath
 #ifndef AF3_X_OFFSETS_32
 #define AF3_X_OFFSETS_32 0x20000
 #endif
+// OR-ed into af3_moe_gemm's tile_cfg: w_scales is the af3_mxfp4_tile_dx_scales copy
+#ifndef AF3_S_DX_TILED
+#define AF3_S_DX_TILED 0x40000
+#endif
 
 #define AF3_REQUIRE(cond, ...)            \
   do {                                    \

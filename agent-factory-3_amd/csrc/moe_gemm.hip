@@ -93,6 +93,9 @@ struct Params {
   // the caller's guarantee that every A row the call reads lies within 4 GiB
   // of a.ptr (tile_cfg | AF3_X_OFFSETS_32)
   int a_off32;
+  // input gradient (gemm8): b.scales is the af3_mxfp4_tile_dx_scales copy,
+  // [E][K/64][s_nt][8][64] bytes (s_nt = 256-column n-tiles)
+  int s_tiled, s_nt;
 };
 
 // scale of A row a(r) for output row r (1 without a row scale)
@@ -1682,9 +1685,14 @@ __device__ __forceinline__ void d5_epilogue(const Params& p, uint8_t* lds, af3_f
 // those alone; the rows past them are never stored either way.
 // SADDR: the copies address a scalar base plus 32-bit lane offsets (A: a_off32;
 // the expert's packed weights and scales below 4 GiB), advancing only the base.
-template <bool NARROW, int BXK, int SPLIT = 1, int RG = 0, bool HALF = false, bool SADDR = false>
+// TS (HALF): the scales are the af3_mxfp4_tile_dx_scales copy: a wave's two
+// blocks x 64 rows of a k-step are 128 contiguous bytes, taken by one 2-byte
+// copy per lane (rows 2 l, 2 l + 1 of block l / 32 in lane l's LDS dword)
+// instead of two 1-byte copies that read 64 rows each.
+template <bool NARROW, int BXK, int SPLIT = 1, int RG = 0, bool HALF = false, bool SADDR = false, bool TS = false>
 __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, int row_lo, int nrows, int n0, int ncols) {
   static_assert(!(NARROW && HALF), "one item shape");
+  static_assert(!TS || HALF, "tiled input-gradient scales on the 128 x 256 items");
   static_assert(SPLIT == 1 || (!NARROW && !HALF && (SPLIT == 2 || SPLIT == 4)), "row split only for 256-row tiles");
   static_assert(RG == 0 || (SPLIT == 1 && RG >= 1 && RG <= ((NARROW || HALF) ? 4 : 8)), "row groups of a tile");
   constexpr int RM = (NARROW || HALF) ? 128 : 256;  // tile rows
@@ -1750,8 +1758,11 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
     soff32[j] = (uint32_t)o;
   }
   const int64_t bstep = (int64_t)kBK * p.b.ld, sstep = (int64_t)kBK * p.b.sld;
+  // TS: the wave's 128 bytes of k-step kc are at tsb + kc * tstep
+  const uint8_t* const tsb = p.b.scales + ((int64_t)e * nk * p.s_nt + (n0 >> 8)) * 512 + wave * 128;
+  const int64_t tstep = (int64_t)p.s_nt * 512;
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
-  // copy j (0..11) of k-step kc: A, then B, then S
+  // copy j (0..11) of k-step kc: A, then B, then S (TS: one S copy, j = AI + BI)
   auto issue_one = [&](int kc, int j) {
     const uint32_t st = lds0 + (uint32_t)((kc % kD5Stages) * STAGE);
     if (j < AI) {
@@ -1766,6 +1777,10 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
         g4_dma16_s((const uint8_t*)p.b.ptr + e * p.b.estride + kc * bstep, boff32[j - AI], dst);
       else
         g4_dma16(bsrc[j - AI] + kc * bstep, dst);
+    } else if constexpr (TS) {
+      if (j == AI + BI)
+        asm volatile("s_nop 0\n\tglobal_load_lds_ushort %0, %1" ::"v"((uint32_t)(lane * 2)), "s"(tsb + kc * tstep),
+                     "{m0}"(st + (uint32_t)(SOFF + wave * 256)) : "memory");
     } else {
       const uint32_t dst = st + (uint32_t)(SOFF + (wave * SI + j - AI - BI) * 256);
       if constexpr (SADDR)
@@ -1798,10 +1813,13 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
     const int chunk = wn0 / 32 + 2 * pg + (gg & 1);
     const int kr = 32 * (gg >> 1) + (gi >> 1);
     boff[pg] = BOFF + kr * BRB + ((chunk ^ bswz(kr)) << 4) + (gi & 1) * 8;  // + 8 BRB s
-    soff[pg] = SOFF + (chunk * 64 + 32 * (gg >> 1)) * 4;                   // + 32 s
+    if constexpr (TS)  // the wave's dwords: block chunk - 2 wave, rows in pairs from 32 (gg / 2) + 8 s
+      soff[pg] = SOFF + wave * 256 + (gg & 1) * 128 + (gg >> 1) * 64;       // + 16 s
+    else
+      soff[pg] = SOFF + (chunk * 64 + 32 * (gg >> 1)) * 4;                   // + 32 s
   }
   constexpr int CW = WC / 32;  // scale dwords per lane for the wave's check (its blocks x 64 k / 64 lanes)
-  const int coff = SOFF + (wn0 / 32 * 64 + CW * lane) * 4;
+  const int coff = TS ? SOFF + wave * 256 + lane * 4 : SOFF + (wn0 / 32 * 64 + CW * lane) * 4;
 
   af3_f32x16 acc[TMW][TN];
 #pragma unroll
@@ -1814,8 +1832,13 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
   issue(0);
   if (nk > 1) issue(1);
 
-  auto kloop = [&](auto full_c) {
+  // TS: the exact conversion is chosen per work item (the tiled scales carry a
+  // flag per expert and n-tile: any scale byte outside [2, 252]), so the
+  // k-loop of the usual items holds no range check and no exact path;
+  // otherwise each k-step checks the wave's scale bytes (XC: run time)
+  auto kloop = [&](auto full_c, auto exact_c) {
     constexpr bool FULL = decltype(full_c)::value;
+    constexpr int XC = decltype(exact_c)::value;  // 0: never exact, 1: always, 2: per k-step check
     af3_bf16x8 af[2][TMW], bf[2][TN];
     // one k-step: iterations s = -1 (the carried sub-step of the previous
     // k-step, skipped at kt = 0) and 0..2; iteration s runs the MFMAs of
@@ -1863,12 +1886,27 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
               w[pg][1] = (uint32_t)wv[1];
             } else if (i < SC) {
               const int pg = (i - SB) >> 1, h = (i - SB) & 1;
-              const af3_u32x4 sv = *(const af3_u32x4*)(stg + soff[pg] + 32 * o + 16 * h);
+              if constexpr (TS) {  // 4 dwords = the 8 rows' bytes, two per dword
+                if (h == 0) {
+                  const af3_u32x4 sv = *(const af3_u32x4*)(stg + soff[pg] + 16 * o);
 #pragma unroll
-              for (int q = 0; q < 4; ++q) sc[pg][4 * h + q] = sv[q];
+                  for (int q = 0; q < 4; ++q) {
+                    sc[pg][2 * q] = sv[q] & 0xFFu;
+                    sc[pg][2 * q + 1] = (sv[q] >> 8) & 0xFFu;
+                  }
+                }
+              } else {
+                const af3_u32x4 sv = *(const af3_u32x4*)(stg + soff[pg] + 32 * o + 16 * h);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) sc[pg][4 * h + q] = sv[q];
+              }
             } else if (i == SC) {
-              if (s < 0) {
-                if constexpr (CW == 2) {
+              if (s < 0 && XC == 2) {
+                if constexpr (TS) {  // the lane's dword: two of the wave's scale bytes
+                  const uint32_t cv = *(const uint32_t*)(stg + coff);
+                  chk[0] = cv & 0xFFu;
+                  chk[1] = (cv >> 8) & 0xFFu;
+                } else if constexpr (CW == 2) {
                   const uint2 cv = *(const uint2*)(stg + coff);
                   chk[0] = cv.x;
                   chk[1] = cv.y;
@@ -1924,13 +1962,13 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
           __builtin_amdgcn_sched_barrier(0);
         }
         if (FULL || wave_live) {
-          if (s < 0) {  // does this wave's part of k-step kt hold a scale byte outside [2, 252]?
+          if (XC == 2 && s < 0) {  // does this wave's part of k-step kt hold a scale byte outside [2, 252]?
             bool lane_odd = false;
 #pragma unroll
             for (int q = 0; q < CW; ++q) lane_odd |= chk[q] - 2u > 250u;
             odd = __builtin_amdgcn_ballot_w64(lane_odd) != 0;
           }
-          if (odd) {
+          if (XC == 1 || (XC == 2 && odd)) {
 #pragma unroll
             for (int pg = 0; pg < PG; ++pg)
               if (FULL || pg < pg_live) d5_cvt_exact(w[pg][0], w[pg][1], sc[pg], bf[nx][2 * pg], bf[nx][2 * pg + 1]);
@@ -1944,8 +1982,13 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) bf[1][tn] = zf;
     // a k-step's stage is complete once this wave's copies for it have landed
-    // (NCP newer ones outstanding, none for the last k-step)
-    if constexpr (HALF) {
+    // (NCP newer ones outstanding (TS: 7), none for the last k-step)
+    if constexpr (HALF && TS) {
+      if (nk > 1)
+        AF3_ASM_WAIT_VM(7);
+      else
+        AF3_ASM_WAIT_VM(0);
+    } else if constexpr (HALF) {
       if (nk > 1)
         AF3_ASM_WAIT_VM(8);
       else
@@ -1960,7 +2003,12 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
     kstep(0, true, nk > 2);
 #pragma nounroll
     for (int kt = 1; kt < nk; ++kt) {
-      if constexpr (HALF) {
+      if constexpr (HALF && TS) {
+        if (kt + 1 < nk)
+          AF3_ASM_WAIT_VM(7);
+        else
+          AF3_ASM_WAIT_VM(0);
+      } else if constexpr (HALF) {
         if (kt + 1 < nk)
           AF3_ASM_WAIT_VM(8);
         else
@@ -1986,7 +2034,15 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
   // valid addresses and are never stored (the k-step is not MFMA-bound, and a
   // variant that skips dead sub-tiles needs more scalar registers than a wave
   // has)
-  kloop(std::true_type{});
+  if constexpr (TS) {
+    const int64_t flags = (int64_t)p.E * nk * p.s_nt * 512;  // the per-(expert, n-tile) flags after the bytes
+    if (p.b.scales[flags + (int64_t)e * p.s_nt + (n0 >> 8)])
+      kloop(std::true_type{}, std::integral_constant<int, 1>{});
+    else
+      kloop(std::true_type{}, std::integral_constant<int, 0>{});
+  } else {
+    kloop(std::true_type{}, std::integral_constant<int, 2>{});
+  }
 
   if constexpr (BXK != NONE) {
     if (p.kx > 0) {  // expert-LoRA segment: + L[r] . Bx[e][:, n] (Bx [r][N], n contiguous)
@@ -2068,7 +2124,7 @@ __global__ __launch_bounds__(256) void gemm5_dgrad_kernel(Params p) {
 // waves of 128 x 64 (each weight byte converted once per 128 rows), two blocks
 // per CU, so one block's epilogue (the fused SwiGLU backward's VALU work in
 // the down projection) overlaps the other block's k-loop.
-template <int BXK, bool SA>
+template <int BXK, bool SA, bool TS>
 __global__ __launch_bounds__(256, 2) void gemm8_dgrad_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kD5HLdsBytes];
   int mt, nt;
@@ -2082,13 +2138,13 @@ __global__ __launch_bounds__(256, 2) void gemm8_dgrad_kernel(Params p) {
   const int n0 = nt * 256;
   const int ncols = min(256, p.N - n0);
   if (nrows <= 32)
-    d5_tile<false, BXK, 1, 1, true, SA>(p, lds, e, row_lo, nrows, n0, ncols);
+    d5_tile<false, BXK, 1, 1, true, SA, TS>(p, lds, e, row_lo, nrows, n0, ncols);
   else if (nrows <= 64)
-    d5_tile<false, BXK, 1, 2, true, SA>(p, lds, e, row_lo, nrows, n0, ncols);
+    d5_tile<false, BXK, 1, 2, true, SA, TS>(p, lds, e, row_lo, nrows, n0, ncols);
   else if (nrows <= 96)
-    d5_tile<false, BXK, 1, 3, true, SA>(p, lds, e, row_lo, nrows, n0, ncols);
+    d5_tile<false, BXK, 1, 3, true, SA, TS>(p, lds, e, row_lo, nrows, n0, ncols);
   else
-    d5_tile<false, BXK, 1, 0, true, SA>(p, lds, e, row_lo, nrows, n0, ncols);
+    d5_tile<false, BXK, 1, 0, true, SA, TS>(p, lds, e, row_lo, nrows, n0, ncols);
 }
 
 // ---------------------------------------------------------------------------
@@ -2588,10 +2644,15 @@ static void launch_gemm8_dgrad(int max_tiles, int N, hipStream_t stream, Params 
   dim3 grid(g4_grid(max_tiles, p.n_nblk, p.group_m));
   // scalar-base addressing where the caller vouches for 32-bit A offsets and
   // an expert's packed weights (K x N / 2 bytes) are below 4 GiB
-  if (p.a_off32 && (int64_t)p.K * (N / 2) < (1LL << 32))
-    hipLaunchKernelGGL((gemm8_dgrad_kernel<COLS_BF16, true>), grid, dim3(256), 0, stream, p);
+  const bool sa = p.a_off32 && (int64_t)p.K * (N / 2) < (1LL << 32);
+  if (sa && p.s_tiled)
+    hipLaunchKernelGGL((gemm8_dgrad_kernel<COLS_BF16, true, true>), grid, dim3(256), 0, stream, p);
+  else if (sa)
+    hipLaunchKernelGGL((gemm8_dgrad_kernel<COLS_BF16, true, false>), grid, dim3(256), 0, stream, p);
+  else if (p.s_tiled)
+    hipLaunchKernelGGL((gemm8_dgrad_kernel<COLS_BF16, false, true>), grid, dim3(256), 0, stream, p);
   else
-    hipLaunchKernelGGL((gemm8_dgrad_kernel<COLS_BF16, false>), grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((gemm8_dgrad_kernel<COLS_BF16, false, false>), grid, dim3(256), 0, stream, p);
 }
 
 static void launch_gemm5_dgrad(int max_tiles, int N, hipStream_t stream, Params p) {
@@ -2654,7 +2715,8 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
   hipStream_t stream = (hipStream_t)stream_;
   const bool w_tiled = (tile_cfg & AF3_W_FWD_TILED) != 0;  // w_blocks is the af3_mxfp4_tile_fwd copy
   const bool x_off32 = (tile_cfg & AF3_X_OFFSETS_32) != 0;  // x's rows within 4 GiB of x (caller's word)
-  tile_cfg &= ~(AF3_W_FWD_TILED | AF3_X_OFFSETS_32);
+  const bool s_tiled = (tile_cfg & AF3_S_DX_TILED) != 0;    // w_scales is the af3_mxfp4_tile_dx_scales copy
+  tile_cfg &= ~(AF3_W_FWD_TILED | AF3_X_OFFSETS_32 | AF3_S_DX_TILED);
   AF3_REQUIRE(tile_cfg >= 0, "moe_gemm: bad tile_cfg %d", tile_cfg);
   AF3_REQUIRE(N > 0 && K > 0 && n_expts > 0 && max_tiles >= 0, "moe_gemm: bad sizes N=%d K=%d E=%d", N, K, n_expts);
   if (max_tiles == 0) return 0;
@@ -2749,6 +2811,15 @@ static int moe_gemm_impl(const uint16_t* x, int64_t ldx, const int32_t* gather_i
       return AF3_EUNSUPPORTED;
     }
     p.b_tiled = 1;
+  }
+  if (s_tiled) {  // only the two-blocks-per-CU input gradient reads the tiled scales
+    if (a_fp8 || !trans || cfg != 28 || K % kBK != 0 || N % 64 != 0) {
+      af3::set_error("moe_gemm: tiled input-gradient scales need tile_cfg 28 with trans_w 1 (got cfg %d, trans_w %d)",
+                     cfg, trans_w);
+      return AF3_EUNSUPPORTED;
+    }
+    p.s_tiled = 1;
+    p.s_nt = (N + 255) / 256;
   }
   if (a_fp8) {  // E4M3 activations x MXFP4 weights on the block-scaled MFMA (256-row map)
     if (trans) {  // input gradient: the weights converted to E5M2 in registers
@@ -3057,6 +3128,61 @@ extern "C" int af3_mxfp4_tile_fwd(const uint8_t* blocks, int64_t n_mats, int N, 
   hipLaunchKernelGGL(tile_fwd_kernel, dim3(grid), dim3(256), 0, stream, blocks, out, n_units, K / 64,
                      (int64_t)(K / 2));
   return af3::check_launch("mxfp4_tile_fwd");
+}
+
+// Tiled input-gradient scales (Params::s_tiled): byte (e, kc, nt, b, r) of out
+// [n_mats][K/64][NT][8][64] is scale byte (row 64 kc + r, block 8 nt + b) of
+// matrix e, [n_mats][K][N/32] row-major; blocks past N/32 (the last n-tile of
+// N % 256 != 0) hold 127 (a unit scale, never used).
+__global__ __launch_bounds__(256) void tile_dx_scales_kernel(const uint8_t* __restrict__ in, uint8_t* __restrict__ out,
+                                                             int64_t n_out, int nk, int nt, int G) {
+  for (int64_t o = blockIdx.x * 256LL + threadIdx.x; o < n_out; o += (int64_t)gridDim.x * 256) {
+    const int r = (int)(o & 63), b = (int)((o >> 6) & 7);
+    const int64_t t = o >> 9;  // (e nk + kc) nt + n
+    const int n = (int)(t % nt);
+    const int64_t ek = t / nt;  // e nk + kc
+    const int blk = n * 8 + b;
+    out[o] = blk < G ? in[(ek * 64 + r) * G + blk] : (uint8_t)127;
+  }
+}
+
+// flag (e, nt) of the tiled scales: 1 when a scale byte of matrix e in the
+// columns of n-tile nt lies outside [2, 252] (the input gradient then runs
+// the exact integer conversion for that work item)
+__global__ __launch_bounds__(256) void tile_dx_flags_kernel(const uint8_t* __restrict__ in, uint8_t* __restrict__ flags,
+                                                            int K, int nt, int G) {
+  const int e = blockIdx.x / nt, n = blockIdx.x % nt;
+  const int b0 = n * 8, nb = min(8, G - b0);
+  bool odd = false;
+  for (int i = threadIdx.x; i < K * nb; i += 256) {
+    const uint8_t v = in[((int64_t)e * K + i / nb) * G + b0 + i % nb];
+    odd |= (uint32_t)v - 2u > 250u;
+  }
+  odd = __syncthreads_or(odd);
+  if (threadIdx.x == 0) flags[blockIdx.x] = odd ? 1 : 0;
+}
+
+extern "C" int af3_mxfp4_tile_dx_scales(const uint8_t* scales, int64_t n_mats, int K, int N, uint8_t* out,
+                                        void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  AF3_REQUIRE(n_mats >= 0 && N > 0 && K > 0, "mxfp4_tile_dx_scales: bad sizes E=%lld K=%d N=%d", (long long)n_mats,
+              K, N);
+  AF3_REQUIRE(K % 64 == 0 && N % 32 == 0, "mxfp4_tile_dx_scales: needs K %% 64 == 0 and N %% 32 == 0 (K=%d N=%d)", K,
+              N);
+  if (n_mats == 0) return 0;
+  AF3_REQUIRE(scales && out, "mxfp4_tile_dx_scales: null pointer");
+  const int nt = (N + 255) / 256;
+  const int64_t n_out = n_mats * (K / 64) * (int64_t)nt * 512;
+  const int64_t n_in = n_mats * (int64_t)K * (N / 32);
+  AF3_REQUIRE(out + n_out + n_mats * nt <= scales || scales + n_in <= out,
+              "mxfp4_tile_dx_scales: out must not overlap scales");
+  AF3_REQUIRE(n_mats * nt < 0x7fffffffLL, "mxfp4_tile_dx_scales: too many matrices");
+  const int64_t nblk = af3_cdiv(n_out, 256);
+  hipLaunchKernelGGL(tile_dx_scales_kernel, dim3((unsigned)(nblk < 16384 ? nblk : 16384)), dim3(256), 0, stream, scales,
+                     out, n_out, K / 64, nt, N / 32);
+  hipLaunchKernelGGL(tile_dx_flags_kernel, dim3((unsigned)(n_mats * nt)), dim3(256), 0, stream, scales, out + n_out, K,
+                     nt, N / 32);
+  return af3::check_launch("mxfp4_tile_dx_scales");
 }
 
 extern "C" int af3_moe_combine(const uint16_t* rows, int64_t ld_rows, const int32_t* src_indx, int64_t n_tokens,

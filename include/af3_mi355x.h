@@ -153,6 +153,12 @@ int af3_tile_order(const int32_t* hist, int n_expts_tot, int block_m, const int3
 #ifndef AF3_X_OFFSETS_32
 #define AF3_X_OFFSETS_32 0x20000
 #endif
+/* tile_cfg | AF3_S_DX_TILED (trans_w 1, the tile_cfg 28 input gradient only,
+ * else AF3_EUNSUPPORTED with nothing launched): w_scales is the
+ * af3_mxfp4_tile_dx_scales copy of the scales. */
+#ifndef AF3_S_DX_TILED
+#define AF3_S_DX_TILED 0x40000
+#endif
 int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int gather_div,
                  const uint8_t* w_blocks, const uint8_t* w_scales, int trans_w, const float* bias,
                  const void* gammas, int gammas_f32, const uint16_t* lora_l, int64_t ld_l, const uint16_t* lora_b,
@@ -170,6 +176,19 @@ int af3_moe_gemm(const uint16_t* x, int64_t ldx, const int32_t* gather_indx, int
  * scales stay as they are.  N % 32 == 0, K % 64 == 0, 16-byte aligned, out
  * the same size as blocks and not overlapping it. */
 int af3_mxfp4_tile_fwd(const uint8_t* blocks, int64_t n_mats, int N, int K, uint8_t* out, void* stream);
+
+/* Tiled copy of the e8m0 scales for the tile_cfg 28 input gradient.  No
+ * counterpart in the reference (its matmul_ogs reads the stored scales,
+ * quantization.py:409-418); a byte permutation made once per frozen weight:
+ * scales [n_mats][K][N/32] (the trans_w 1 view: K = the reduction rows) ->
+ * out [n_mats][K/64][ceil(N/256)][8][64], out[e][k/64][n/256][(n/32)%8][k%64]
+ * = scales[e][k][n/32], 127 past N/32, so the scale bytes one wave needs for
+ * a 64-deep k-step (its two 32-column blocks x 64 rows) are 128 contiguous
+ * bytes; then one flag byte per (matrix, 256-column n-tile): 1 when a scale
+ * byte of its columns lies outside [2, 252] (the kernel then takes the exact
+ * integer conversion for that n-tile).  K % 64 == 0, N % 32 == 0; out holds
+ * n_mats * ceil(N/256) * (K/64 * 512 + 1) bytes and does not overlap scales. */
+int af3_mxfp4_tile_dx_scales(const uint8_t* scales, int64_t n_mats, int K, int N, uint8_t* out, void* stream);
 
 /* af3_moe_gemm with the gpt-oss clamped SwiGLU (kernels.py:394-582 math)
  * fused into the epilogue, so the activation never makes a separate pass

@@ -182,3 +182,96 @@ def test_forward_three_weight_buffers(dev, nout, gather, lora, odd):
     bad = (a - yr.double()).abs() > ATOL + RTOL * yr.double().abs()
     assert not bad.any(), float(bad.float().mean())
 
+
+
+@pytest.mark.parametrize("shape", [(3, 128, 18), (2, 64, 8), (1, 192, 20)])
+def test_tile_dx_scales_permutation(dev, shape):
+    """out[e, k // 64, n // 256, (n // 32) % 8, k % 64] == scales[e, k, n // 32],
+    127 past N / 32, for every byte; then one flag per (matrix, n-tile): 1 when
+    a byte of its columns lies outside [2, 252]."""
+    En, K, G = shape
+    g = torch.Generator().manual_seed(K + G)
+    scales = torch.randint(2, 253, (En, K, G), generator=g).to(torch.uint8)
+    scales[0, K - 1, G - 1] = 255                       # odd byte in the last n-tile of matrix 0
+    if En > 1:
+        scales[1, 3, 0] = 1                             # and in the first n-tile of matrix 1
+    out = Q.mxfp4_tile_dx_scales(scales.to(dev)).cpu()
+    nt = (G * 32 + 255) // 256
+    nbytes = En * (K // 64) * nt * 512
+    assert out.shape == (nbytes + En * nt,)
+    padded = torch.full((En, K, nt * 8), 127, dtype=torch.uint8)
+    padded[:, :, :G] = scales
+    want = padded.view(En, K // 64, 64, nt, 8).permute(0, 1, 3, 4, 2)
+    assert torch.equal(out[:nbytes].view(En, K // 64, nt, 8, 64), want)
+    flags = torch.zeros(En, nt, dtype=torch.uint8)
+    flags[0, nt - 1] = 1
+    if En > 1:
+        flags[1, 0] = 1
+    assert torch.equal(out[nbytes:].view(En, nt), flags)
+
+
+@pytest.mark.parametrize("nout", [576, 640])
+@pytest.mark.parametrize("gather,lora,odd", CASES)
+def test_dgrad_tiled_scales_bit_equal(dev, nout, gather, lora, odd):
+    """The default input-gradient kernel (tile_cfg 28) reading the tiled
+    scales equals it on the stored scales bit for bit (scale bytes outside
+    [2, 252] included: the exact conversion), and the oracle; tails of 1, 2
+    and 3 row groups take its row-group variants."""
+    g, ref, rd, gi = _routing_counts(dev, 32, COUNTS_NB3)
+    blocks, scales = _weights(g, KRED, nout, odd)          # W [E, K, N] packed along N
+    Rr = T * TOPK
+    x = torch.randn(T if gather else Rr, KRED, generator=g).to(torch.bfloat16)
+    L = (torch.randn(Rr, 32, generator=g) * 0.3).to(torch.bfloat16) if lora else None
+    Ax = (torch.randn(E, 32, nout, generator=g) * 0.3).to(torch.bfloat16) if lora else None
+    gam = rd.gate_scal if gather else None
+    wb, ws = blocks.to(dev), scales.to(dev)
+    args = (x.to(dev), wb, ws, None, rd, gi if gather else None, gam, True, L.to(dev) if lora else None,
+            Ax.to(dev) if lora else None)
+    y = Q.moe_rows(*args)
+    yt = Q.moe_rows(*args, s_tiled=Q.mxfp4_tile_dx_scales(ws))
+    assert torch.equal(y.view(torch.int16), yt.view(torch.int16))
+    W = mxfp4.dequant_f32(blocks, scales)
+    yr = moe.rows(x, W, ref["offs"], ref["topk_indx"] if gather else None, TOPK,
+                  gammas=gam.cpu() if gather else None, trans=True, lora_l=L, lora_b=Ax)
+    a = yt.float().cpu().double()
+    assert torch.isfinite(a).all()
+    bad = (a - yr.double()).abs() > ATOL + RTOL * yr.double().abs()
+    assert not bad.any(), float(bad.float().mean())
+
+
+def test_dgrad_tiled_scales_swiglu_bit_equal(dev):
+    """The down projection's input gradient with the fused SwiGLU backward
+    (epi 1) on the tiled scales."""
+    g, ref, rd, gi = _routing_counts(dev, 33, COUNTS_NB3)
+    alpha, limit, I_ = 1.702, 7.0, 320
+    Rr = T * TOPK
+    gu = (torch.randn(Rr, 2 * I_, generator=g) * 3).to(torch.bfloat16).to(dev)
+    blocks, scales = _weights(g, KRED, I_, True)           # down W [E, H, I] read transposed
+    dy = torch.randn(T, KRED, generator=g).to(torch.bfloat16).to(dev)
+    u = (torch.randn(Rr, 32, generator=g) * 0.3).to(torch.bfloat16).to(dev)
+    Ax = (torch.randn(E, 32, I_, generator=g) * 0.3).to(torch.bfloat16).to(dev)
+    wb, ws = blocks.to(dev), scales.to(dev)
+    args = (dy, wb, ws, None, rd, gi, rd.gate_scal, True, u, Ax)
+    dgu = Q.moe_rows(*args, swiglu=("bwd", gu, alpha, limit))
+    dgu_t = Q.moe_rows(*args, swiglu=("bwd", gu, alpha, limit), s_tiled=Q.mxfp4_tile_dx_scales(ws))
+    assert dgu is not None and dgu_t is not None
+    assert torch.equal(dgu.view(torch.int16), dgu_t.view(torch.int16))
+
+
+def test_tiled_scales_declined_by_the_forward(dev):
+    """AF3_S_DX_TILED on a forward call: AF3_EUNSUPPORTED, nothing launched."""
+    g, ref, rd, gi = _routing(dev, 24)
+    blocks, scales = _weights(g, 576, KRED, False)
+    wb, ws = blocks.to(dev), scales.to(dev)
+    x = torch.randn(T, KRED, generator=g).to(torch.bfloat16).to(dev)
+    ed = rd.expt_data
+    y = torch.zeros(T * TOPK, 576, dtype=torch.bfloat16, device=dev)
+    pid = ed.block_pid_map[128]
+    gp = Q._gather_ptr(gi)
+    ok = _capi.try_call("af3_moe_gemm", x.data_ptr(), KRED, gp.data_ptr(), TOPK, wb.data_ptr(),
+                        ws.data_ptr(), 0, None, None, 0, None, 0, None, 0, ed.token_offs_raw.data_ptr(),
+                        pid.data_ptr(), ed.token_offs_pad[128].data_ptr(), pid.numel(), 128, _capi.S_DX_TILED,
+                        E, 576, KRED, y.data_ptr(), 576, _capi.stream_of(dev))
+    torch.cuda.synchronize()
+    assert not ok
+    assert int(y.view(torch.int16).abs().sum()) == 0
