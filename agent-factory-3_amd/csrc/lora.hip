@@ -34,6 +34,43 @@ __device__ __forceinline__ void l_dma16_s(const void* sbase, uint32_t voff, uint
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_byte_addr) : "memory");
 }
 #define L_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 31] (the count is an immediate)
+__device__ __forceinline__ void l_wait_vm(int n) {
+  switch (n) {
+    case 1: L_WAIT_VM(1); break;
+    case 2: L_WAIT_VM(2); break;
+    case 3: L_WAIT_VM(3); break;
+    case 4: L_WAIT_VM(4); break;
+    case 5: L_WAIT_VM(5); break;
+    case 6: L_WAIT_VM(6); break;
+    case 7: L_WAIT_VM(7); break;
+    case 8: L_WAIT_VM(8); break;
+    case 9: L_WAIT_VM(9); break;
+    case 10: L_WAIT_VM(10); break;
+    case 11: L_WAIT_VM(11); break;
+    case 12: L_WAIT_VM(12); break;
+    case 13: L_WAIT_VM(13); break;
+    case 14: L_WAIT_VM(14); break;
+    case 15: L_WAIT_VM(15); break;
+    case 16: L_WAIT_VM(16); break;
+    case 17: L_WAIT_VM(17); break;
+    case 18: L_WAIT_VM(18); break;
+    case 19: L_WAIT_VM(19); break;
+    case 20: L_WAIT_VM(20); break;
+    case 21: L_WAIT_VM(21); break;
+    case 22: L_WAIT_VM(22); break;
+    case 23: L_WAIT_VM(23); break;
+    case 24: L_WAIT_VM(24); break;
+    case 25: L_WAIT_VM(25); break;
+    case 26: L_WAIT_VM(26); break;
+    case 27: L_WAIT_VM(27); break;
+    case 28: L_WAIT_VM(28); break;
+    case 29: L_WAIT_VM(29); break;
+    case 30: L_WAIT_VM(30); break;
+    case 31: L_WAIT_VM(31); break;
+    default: L_WAIT_VM(0); break;
+  }
+}
 #define L_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
 
 __device__ __forceinline__ uint32_t l_lds_addr(const void* p) {
@@ -523,6 +560,7 @@ __global__ __launch_bounds__(256, kLuMinBlocks) void lug_kernel(LuParams p) {
 
   constexpr int NS = (kLwRows * SR) / 1024;  // Small copies per step (block)
   constexpr int NB = kLwBig / 1024 / 4;      // Big copies per step and wave
+  static_assert((kLuStages - 2) * (NB + 1) + 4 <= 31, "wait counts within l_wait_vm");
   const bool has_s = wave < NS;
   int lcs[NB];  // logical 16-byte chunk of each Big copy of this lane
 #pragma unroll
@@ -603,26 +641,11 @@ __global__ __launch_bounds__(256, kLuMinBlocks) void lug_kernel(LuParams p) {
       const int g = s * kLuG + j;
       // this step's copies are in once at most those of the later issued steps are outstanding
       // (NB + has_s copies per step and wave; stores issued since only make the wait stricter)
+      // (plus the previous row step's 4 u stores, issued after every copy of
+      // the steps waited for in this row step: vmcnt counts stores too)
       const int ahead = min(D - 1, NT - 1 - g);
-      if (has_s) {
-        switch (ahead) {
-          case 5: L_WAIT_VM(25); break;
-          case 4: L_WAIT_VM(20); break;
-          case 3: L_WAIT_VM(15); break;
-          case 2: L_WAIT_VM(10); break;
-          case 1: L_WAIT_VM(5); break;
-          default: L_WAIT_VM(0); break;
-        }
-      } else {
-        switch (ahead) {
-          case 5: L_WAIT_VM(20); break;
-          case 4: L_WAIT_VM(16); break;
-          case 3: L_WAIT_VM(12); break;
-          case 2: L_WAIT_VM(8); break;
-          case 1: L_WAIT_VM(4); break;
-          default: L_WAIT_VM(0); break;
-        }
-      }
+      const bool stored = s > 0 && (R32 || (wave >> 1) == ((s - 1) & 1));
+      l_wait_vm(__builtin_amdgcn_readfirstlane(ahead * (NB + (has_s ? 1 : 0)) + (stored ? 4 : 0)));
       L_BARRIER();
       // the slot of step g + D is the one step g - 1 read (all waves are past it)
       const int prev = slot == 0 ? D : slot - 1;
