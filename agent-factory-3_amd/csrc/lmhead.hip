@@ -64,6 +64,11 @@ struct LmRing {
 __device__ __forceinline__ void lm_dma16(const void* gptr, uint32_t lds_byte_addr) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(lds_byte_addr) : "memory");
 }
+// the same from a wave-uniform base (SGPRs) plus a 32-bit lane offset that stays
+// in its register for the whole tile (only the scalar base advances per k-step)
+__device__ __forceinline__ void lm_dma16_s(const void* sbase, uint32_t voff, uint32_t lds_byte_addr) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_byte_addr) : "memory");
+}
 template <int N>
 __device__ __forceinline__ void lm_wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -100,7 +105,9 @@ __device__ __forceinline__ float wave32_sum(float v) {
   return v + lm_xor16(v);
 }
 
-template <int MODE, int BK>
+// SA: hidden's and weight's rows lie within 4 GiB of their bases (the host
+// checks), so the copies take 32-bit lane offsets from scalar bases
+template <int MODE, int BK, bool SA>
 __global__ __launch_bounds__(kLmThreads, 1) void lmh_gemm_kernel(
     const uint16_t* __restrict__ hidden, int64_t ldh, const uint16_t* __restrict__ weight, int64_t ldw, int M, int V,
     int H, float rcp_t, const int64_t* __restrict__ labels, int n_mtiles, int n_vtiles, int per_xcd,
@@ -126,14 +133,19 @@ __global__ __launch_bounds__(kLmThreads, 1) void lmh_gemm_kernel(
   // global -> LDS copies: stage slot q (16 bytes) of the A (B) half holds row q / 4,
   // chunk (q % 4) ^ swizzle(row); wave w copies slots (w * kLmCopies + j) * 64 + lane
   const uint16_t* src[2 * kLmCopies];
+  uint32_t soff[2 * kLmCopies];  // SA: byte offsets from hidden / weight
   uint32_t dst_off[2 * kLmCopies];
 #pragma unroll
   for (int j = 0; j < kLmCopies; ++j) {
     const int q = (w * kLmCopies + j) * 64 + lane;
     const int row = q / kLmCh;
     const int ch = Ring::swz(row, q % kLmCh);  // the swizzle is an involution
-    src[j] = hidden + (int64_t)min(m0 + row, M - 1) * ldh + ch * 8;             // clamped rows: results never stored
-    src[kLmCopies + j] = weight + (int64_t)min(v0 + row, V - 1) * ldw + ch * 8;
+    const int64_t ea = (int64_t)min(m0 + row, M - 1) * ldh + ch * 8;  // clamped rows: results never stored
+    const int64_t eb = (int64_t)min(v0 + row, V - 1) * ldw + ch * 8;
+    src[j] = hidden + ea;
+    src[kLmCopies + j] = weight + eb;
+    soff[j] = (uint32_t)(ea * 2);
+    soff[kLmCopies + j] = (uint32_t)(eb * 2);
     dst_off[j] = (uint32_t)((w * kLmCopies + j) * 1024);
     dst_off[kLmCopies + j] = (uint32_t)(kLmBM * kLmRowB + (w * kLmCopies + j) * 1024);
   }
@@ -142,8 +154,13 @@ __global__ __launch_bounds__(kLmThreads, 1) void lmh_gemm_kernel(
   auto issue = [&](int kt) {
     const uint32_t base = lds0 + (uint32_t)((kt % kLmStages) * kLmStage);
 #pragma unroll
-    for (int j = 0; j < 2 * kLmCopies; ++j)
-      lm_dma16(src[j] + kt * kLmBK, __builtin_amdgcn_readfirstlane(base + dst_off[j]));  // wave-uniform
+    for (int j = 0; j < 2 * kLmCopies; ++j) {
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(base + dst_off[j]);  // wave-uniform
+      if constexpr (SA)
+        lm_dma16_s((const uint8_t*)(j < kLmCopies ? hidden : weight) + (int64_t)kt * kLmBK * 2, soff[j], dst);
+      else
+        lm_dma16(src[j] + kt * kLmBK, dst);
+    }
   };
 
   af3_f32x16 acc[4][kLmTN];
@@ -461,6 +478,12 @@ __global__ __launch_bounds__(256) void lmh_chunk_dz_kernel(const float* __restri
   }
 }
 
+// every copy of `rows` rows of stride ld (H columns) lies within 4 GiB of the base:
+// the copies' lane offsets fit 32 bits
+bool lm_off32(int rows, int64_t ld, int H) {
+  return rows <= 0 || ((int64_t)(rows - 1) * ld + H) * 2 <= ((int64_t)1 << 32);
+}
+
 int lmh_grid(int M, int V, int& n_mtiles, int& n_vtiles, int& per_xcd) {
   n_mtiles = (int)af3_cdiv(M, kLmBM);
   n_vtiles = (int)af3_cdiv(V, kLmBN);
@@ -493,14 +516,17 @@ extern "C" int af3_lm_head_logprobs(const uint16_t* hidden, int64_t ldh, const u
   const int grid = lmh_grid(M, V, nm, nv, px);
   float4* partials = (float4*)workspace;
   float* zlab = (float*)((uint8_t*)workspace + (size_t)nv * M * sizeof(float4));
-  if (H % 64 == 0)
-    hipLaunchKernelGGL((lmh_gemm_kernel<0, 64>), dim3(grid), dim3(kLmThreads), 0, stream, hidden, ldh, weight, ldw, M, V, H,
-                       1.f / temperature, labels, nm, nv, px, partials, zlab, nullptr, nullptr, nullptr, 0, 0.f,
-                       nullptr, nullptr, 0, 0);
-  else
-    hipLaunchKernelGGL((lmh_gemm_kernel<0, 32>), dim3(grid), dim3(kLmThreads), 0, stream, hidden, ldh, weight, ldw, M, V, H,
-                       1.f / temperature, labels, nm, nv, px, partials, zlab, nullptr, nullptr, nullptr, 0, 0.f,
-                       nullptr, nullptr, 0, 0);
+  const bool sa = lm_off32(M, ldh, H) && lm_off32(V, ldw, H);
+#define AF3_LMH_FWD(BK, SA)                                                                                          \
+  hipLaunchKernelGGL((lmh_gemm_kernel<0, BK, SA>), dim3(grid), dim3(kLmThreads), 0, stream, hidden, ldh, weight, ldw, M, \
+                     V, H, 1.f / temperature, labels, nm, nv, px, partials, zlab, nullptr, nullptr, nullptr, 0, 0.f,  \
+                     nullptr, nullptr, 0, 0)
+  if (H % 64 == 0) {
+    if (sa) AF3_LMH_FWD(64, true); else AF3_LMH_FWD(64, false);
+  } else {
+    if (sa) AF3_LMH_FWD(32, true); else AF3_LMH_FWD(32, false);
+  }
+#undef AF3_LMH_FWD
   int rc = af3::check_launch("lm_head_logprobs (gemm)");
   if (rc) return rc;
   hipLaunchKernelGGL(lmh_reduce_kernel, dim3((unsigned)af3_cdiv(M, 16)), dim3(256), 0, stream, partials, M, nv, zlab,
@@ -525,14 +551,17 @@ extern "C" int af3_lm_head_dlogits_range(const uint16_t* hidden, int64_t ldh, co
   const uint16_t* wr = weight + (int64_t)v_begin * ldw;  // vocabulary rows v_begin .. v_begin + v_count - 1
   int nm, nv, px;
   const int grid = lmh_grid(M, v_count, nm, nv, px);
-  if (H % 64 == 0)
-    hipLaunchKernelGGL((lmh_gemm_kernel<1, 64>), dim3(grid), dim3(kLmThreads), 0, stream, hidden, ldh, wr, ldw, M,
-                       v_count, H, 1.f / temperature, labels, nm, nv, px, nullptr, nullptr, lse, ez, dlogprobs,
-                       dlp_stride, dlp_scale, dentropy, dz, lddz, (int64_t)v_begin);
-  else
-    hipLaunchKernelGGL((lmh_gemm_kernel<1, 32>), dim3(grid), dim3(kLmThreads), 0, stream, hidden, ldh, wr, ldw, M,
-                       v_count, H, 1.f / temperature, labels, nm, nv, px, nullptr, nullptr, lse, ez, dlogprobs,
-                       dlp_stride, dlp_scale, dentropy, dz, lddz, (int64_t)v_begin);
+  const bool sa = lm_off32(M, ldh, H) && lm_off32(v_count, ldw, H);
+#define AF3_LMH_DZ(BK, SA)                                                                                         \
+  hipLaunchKernelGGL((lmh_gemm_kernel<1, BK, SA>), dim3(grid), dim3(kLmThreads), 0, stream, hidden, ldh, wr, ldw, M, \
+                     v_count, H, 1.f / temperature, labels, nm, nv, px, nullptr, nullptr, lse, ez, dlogprobs,       \
+                     dlp_stride, dlp_scale, dentropy, dz, lddz, (int64_t)v_begin)
+  if (H % 64 == 0) {
+    if (sa) AF3_LMH_DZ(64, true); else AF3_LMH_DZ(64, false);
+  } else {
+    if (sa) AF3_LMH_DZ(32, true); else AF3_LMH_DZ(32, false);
+  }
+#undef AF3_LMH_DZ
   return af3::check_launch("lm_head_dlogits");
 }
 

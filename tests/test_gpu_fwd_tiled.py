@@ -1,9 +1,11 @@
-"""Tiled weights (af3_mxfp4_tile_fwd): the byte permutation itself, and the
-default forward kernel reading it gives the same bits as reading the blocks
-as stored, on the shapes of test_gpu_gemm_tiles (full and partial tiles, 64- /
-128-column tail n-tiles, tails of 1 to 4 row groups, gathered rows, the LoRA
-segment, scale bytes outside [2, 252], the fused SwiGLU forward).  Kernels that
-do not read the tiled copy decline it and run on the stored blocks."""
+"""Tiled weights (af3_mxfp4_tile_fwd) and tiled input-gradient scales
+(af3_mxfp4_tile_dx_scales): the byte permutations themselves, and the default
+forward / input-gradient kernels reading them give the same bits as reading
+the blocks and scales as stored, on the shapes of test_gpu_gemm_tiles (full
+and partial tiles, 64- / 128-column tail n-tiles, tails of 1 to 4 row groups,
+gathered rows, the LoRA segment, scale bytes outside [2, 252], the fused
+SwiGLU forward and backward), and against the oracle.  Kernels that do not
+read a tiled copy decline it and run on the stored bytes."""
 import pytest
 import torch
 
@@ -107,7 +109,8 @@ def test_tiled_flag_declined_by_other_kernels(dev):
 
 
 def test_module_cache(dev):
-    """The expert module makes the tiled copy once per weight version."""
+    """The expert module makes the tiled weights and the tiled scales once per
+    weight version."""
     from agent_factory_3_amd import workloads
     m = workloads.make_experts(workloads.layer(2, T=64, E=4, H=256, I=128), dev)
     a = m._fwd_tiled("gate_up_proj")
@@ -119,6 +122,16 @@ def test_module_cache(dev):
         w.copy_(w.clone())  # an in-place write (same bytes) bumps the version
     b = m._fwd_tiled("gate_up_proj")
     assert b is not a and torch.equal(b, a)
+    # the input gradient's tiled scales, the same way
+    s1 = m._dx_tiled_scales("down_proj")
+    assert s1 is not None and m._dx_tiled_scales("down_proj") is s1
+    _, scales = m._get_uint8_weights("down_proj")
+    assert torch.equal(s1, Q.mxfp4_tile_dx_scales(scales))
+    with torch.no_grad():
+        w = getattr(m, "down_proj_scales")
+        w.copy_(w.clone())
+    s2 = m._dx_tiled_scales("down_proj")
+    assert s2 is not s1 and torch.equal(s2, s1)
 
 
 # rows per expert whose last 128-row tile has 2, 3, 1, 1, 4 and 4 live 32-row

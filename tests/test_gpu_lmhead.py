@@ -7,7 +7,8 @@ order separates them from float64), the fused logits gradient per vocabulary
 split (bit-equal to the whole-vocabulary kernel), gradients of hidden and
 weight through the split backward, the three reductions, out-of-range labels,
 partial row / vocabulary tiles, chunks that split the vocabulary raggedly and
-rows the vector loads cannot take, and the full gpt-oss vocabulary (201,088)."""
+rows the vector loads cannot take, the full gpt-oss vocabulary (201,088), and
+rows more than 4 GiB past the fused kernel's bases (its 64-bit copy addresses)."""
 import pytest
 import torch
 
@@ -233,3 +234,51 @@ def test_library_statistics_and_gradient_kernels_on_given_logits(dev):
         got = dz[:, :V].float().cpu().double()
         assert float((got - ref).abs().max()) <= 2.0 ** -8 * float(ref.abs().max()) + 1e-6, ch
         assert (dz[:, V:] == 9.0).all()
+
+
+def test_fused_kernels_with_rows_past_4_gib(dev):
+    """Rows of hidden and weight more than 4 GiB past their bases (strided views
+    of two 5 GiB buffers) make the fused GEMM kernel copy through 64-bit lane
+    addresses; its log-probabilities, entropy, statistics and logits gradient
+    (whole vocabulary and a split starting at column 256) equal, bit for bit,
+    those of contiguous copies, whose copies take 32-bit offsets from scalar
+    bases.  Both are checked against the float64 oracle as well."""
+    M, H, V, T = 300, 128, 600, 0.9
+    h, w, lab = _inputs(M, H, V, seed=5)
+    lab[:2] = torch.tensor([V - 1, -100])
+    ldh, ldw = (1 << 23) + 64, (1 << 22) + 64
+    assert (M - 1) * ldh * 2 > 1 << 32 and (V - 1) * ldw * 2 > 1 << 32
+    hb = torch.empty((M - 1) * ldh + H, dtype=torch.bfloat16, device=dev)
+    wb = torch.empty((V - 1) * ldw + H, dtype=torch.bfloat16, device=dev)
+    hs, ws_ = hb.as_strided((M, H), (ldh, 1)), wb.as_strided((V, H), (ldw, 1))
+    hs.copy_(h.to(dev))
+    ws_.copy_(w.to(dev))
+    hc, wc, labd = h.to(dev), w.to(dev), lab.to(dev)
+    stream = _capi.stream_of(dev)
+    ws_n = int(_capi.load().af3_lm_head_workspace_bytes(M, V))
+    g = torch.Generator().manual_seed(6)
+    dlp, dent = torch.randn(M, generator=g).to(dev), torch.randn(M, generator=g).to(dev)
+    res = []
+    for hh, ww in ((hs, ws_), (hc, wc)):
+        print(f"lm_head fused ldh={hh.stride(0)} ldw={ww.stride(0)}", flush=True)
+        outs = [torch.empty(M, dtype=torch.float32, device=dev) for _ in range(4)]
+        wsp = torch.empty(ws_n, dtype=torch.uint8, device=dev)
+        _capi.call("af3_lm_head_logprobs", hh.data_ptr(), hh.stride(0), ww.data_ptr(), ww.stride(0), M, V, H,
+                   labd.data_ptr(), T, *[o.data_ptr() for o in outs], wsp.data_ptr(), ws_n, stream)
+        dz = torch.empty(M, V, dtype=torch.bfloat16, device=dev)
+        _capi.call("af3_lm_head_dlogits", hh.data_ptr(), hh.stride(0), ww.data_ptr(), ww.stride(0), M, V, H,
+                   labd.data_ptr(), T, outs[2].data_ptr(), outs[3].data_ptr(), dlp.data_ptr(), 1, 1.0,
+                   dent.data_ptr(), dz.data_ptr(), dz.stride(0), stream)
+        dzs = torch.empty(M, V - 256, dtype=torch.bfloat16, device=dev)
+        _capi.call("af3_lm_head_dlogits_range", hh.data_ptr(), hh.stride(0), ww.data_ptr(), ww.stride(0), M, 256,
+                   V - 256, H, labd.data_ptr(), T, outs[2].data_ptr(), outs[3].data_ptr(), dlp.data_ptr(), 1, 1.0,
+                   dent.data_ptr(), dzs.data_ptr(), dzs.stride(0), stream)
+        torch.cuda.synchronize()
+        res.append(outs + [dz, dzs])
+    for a, b in zip(*res):
+        assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a.view(torch.int32),
+                           b.view(torch.int16) if b.dtype == torch.bfloat16 else b.view(torch.int32))
+    assert torch.equal(res[0][5].view(torch.int16), res[0][4][:, 256:].view(torch.int16))
+    lpr, entr = lmhead.lm_head(h.double(), w.double(), lab, T)
+    assert _close(res[0][0], lpr, 1e-3, 1e-3) == 0.0
+    assert _close(res[0][1], entr, 1e-3, 1e-3) == 0.0
