@@ -63,8 +63,13 @@ typedef __attribute__((ext_vector_type(8))) __bf16 af3_bf16x8;
 typedef __attribute__((ext_vector_type(16))) float af3_f32x16;
 typedef __attribute__((ext_vector_type(4))) unsigned int af3_u32x4;
 
+// bf16 bits (the low 16 of h) -> fp32: exact, a shift.  Written as the bf16
+// -> float conversion so the compiler treats the result as canonical and
+// drops the quieting v_max it otherwise puts before every fminf / fmaxf of a
+// loaded value (a signaling-NaN input then clamps to NaN instead of to the
+// bound; such inputs never come out of the kernels that write these operands)
 __device__ __forceinline__ float af3_bf16_to_f32(uint32_t h) {
-  return __uint_as_float(h << 16);
+  return (float)__builtin_bit_cast(__bf16, (unsigned short)(h & 0xFFFFu));
 }
 
 // fp32 -> bf16 bits, round to nearest even (hardware v_cvt_pk_bf16_f32 on gfx950)
@@ -73,8 +78,11 @@ __device__ __forceinline__ uint32_t af3_f32_to_bf16(float f) {
   return (uint32_t)__builtin_bit_cast(unsigned short, b);
 }
 
+// two fp32 -> one dword of bf16 (lo in bits 0-15), round to nearest even:
+// one v_cvt_pk_bf16_f32 (bit-identical to two af3_f32_to_bf16)
 __device__ __forceinline__ uint32_t af3_pack_bf16x2(float lo, float hi) {
-  return af3_f32_to_bf16(lo) | (af3_f32_to_bf16(hi) << 16);
+  typedef __attribute__((ext_vector_type(2))) float f32x2;
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, af3_bf16x2));
 }
 
 // One e2m1 nibble + e8m0 scale byte -> bf16 bits, integer-only.
@@ -166,5 +174,5 @@ __device__ __forceinline__ void af3_swiglu_bwd_elem(float dout, float g, float u
   dg = dout * (u + 1.0f) * s * (1.0f + alpha * g * (1.0f - s));
   dg = (g < limit) ? dg : 0.0f;
   du = dout * g * s;
-  du = (u > -limit && u < limit) ? du : 0.0f;
+  du = (fabsf(u) < limit) ? du : 0.0f;  // -limit < u < limit (false for NaN either way)
 }
