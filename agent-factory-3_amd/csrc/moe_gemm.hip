@@ -1026,6 +1026,9 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+  // two blocks share each CU: while one runs its epilogue (VALU and memory
+  // work), the other's k-loop keeps issue priority for its MFMAs and copies
+  if constexpr (HALF) __builtin_amdgcn_s_setprio(2);
   // BG: the weight words of k-step 0 (NB = 3: and 1), each before its
   // k-step's copies (the order every later k-step keeps: its weight loads
   // first, then its copies)
@@ -1212,6 +1215,7 @@ __device__ __forceinline__ void g4f_tile(const Params& p, uint8_t* lds, int e, i
     }
   }
 
+  if constexpr (HALF) __builtin_amdgcn_s_setprio(0);  // the k-loop's waves first (see the k-loop's start)
   g4_epilogue<false, TM, TN, NT, CN, RM>(p, lds, acc, e, row_lo, nrows, n0, ncols, wm0, wn0);
 }
 
@@ -1829,6 +1833,9 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+  // two blocks share each CU: while one runs its epilogue (VALU and memory
+  // work), the other's k-loop keeps issue priority for its MFMAs and copies
+  if constexpr (HALF) __builtin_amdgcn_s_setprio(2);
   issue(0);
   if (nk > 1) issue(1);
 
@@ -2079,6 +2086,7 @@ __device__ __forceinline__ void d5_tile(const Params& p, uint8_t* lds, int e, in
     }
   }
   // (HALF: smaller batches of the SwiGLU-backward prefetch, within 256 registers)
+  if constexpr (HALF) __builtin_amdgcn_s_setprio(0);  // the k-loop's waves first (see the k-loop's start)
   d5_epilogue<RM, CN, TMW, HALF ? 4 : 16>(p, lds, acc, e, row_lo, nrows, n0, ncols, wn0, rb);
 }
 
